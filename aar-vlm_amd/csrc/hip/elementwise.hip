@@ -1,0 +1,106 @@
+// Elementwise fp32 kernels.  aar_add_f32 is the device leg of add_grads
+// (reference add_kernel, cppsrc/ops/elementwise.cu:11-14, launched from
+// add_cuda at cppsrc/ops/elementwise.cu:107-118): c = a + b.
+// 128-bit loads/stores, grid-stride over a grid sized to the chip.
+#include <hip/hip_runtime.h>
+
+#include "common.hpp"
+
+namespace aar {
+namespace {
+
+__global__ void __launch_bounds__(256)
+add_vec_kernel(const f32x4* __restrict__ a, const f32x4* __restrict__ b, f32x4* __restrict__ c,
+               int64_t n4) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += stride) c[i] = a[i] + b[i];
+}
+
+__global__ void __launch_bounds__(256)
+add_scalar_kernel(const float* __restrict__ a, const float* __restrict__ b, float* __restrict__ c,
+                  int64_t n) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) c[i] = a[i] + b[i];
+}
+
+struct StridedDesc {
+  int ndim;
+  int64_t shape[8];
+  int64_t src[8];
+  int64_t dst[8];
+};
+
+// dst[off_dst(idx)] = src[off_src(idx)] for the row-major linear index i of
+// `shape`; the index is decomposed from the last dim (fastest) outward.
+__global__ void __launch_bounds__(256)
+strided_copy_kernel(const float* __restrict__ src, float* __restrict__ dst, StridedDesc desc,
+                    int64_t n) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+    int64_t rem = i, so = 0, dof = 0;
+    for (int dim = desc.ndim - 1; dim >= 0; --dim) {
+      const int64_t ext = desc.shape[dim];
+      const int64_t idx = rem % ext;
+      rem /= ext;
+      so += idx * desc.src[dim];
+      dof += idx * desc.dst[dim];
+    }
+    dst[dof] = src[so];
+  }
+}
+
+unsigned grid_for(int64_t work) {
+  const int64_t cap = (int64_t)device_cu_count() * 16;
+  int64_t g = (work + 255) / 256;
+  if (g > cap) g = cap;
+  return (unsigned)(g > 0 ? g : 1);
+}
+
+}  // namespace
+}  // namespace aar
+
+using namespace aar;
+
+extern "C" int aar_add_f32(const float* a, const float* b, float* c, int64_t n, void* stream) {
+  if (n < 0) return AAR_EINVAL;
+  if (n == 0) return AAR_OK;
+  if (!a || !b || !c) return AAR_EINVAL;
+  hipStream_t st = as_stream(stream);
+  if (aligned16(a) && aligned16(b) && aligned16(c)) {
+    const int64_t n4 = n / 4;
+    if (n4 > 0) {
+      add_vec_kernel<<<dim3(grid_for(n4)), dim3(256), 0, st>>>(reinterpret_cast<const f32x4*>(a),
+                                                              reinterpret_cast<const f32x4*>(b),
+                                                              reinterpret_cast<f32x4*>(c), n4);
+      const int rc = launch_status();
+      if (rc != AAR_OK) return rc;
+    }
+    const int64_t done = n4 * 4;
+    if (done < n) {
+      add_scalar_kernel<<<dim3(1), dim3(256), 0, st>>>(a + done, b + done, c + done, n - done);
+    }
+  } else {
+    add_scalar_kernel<<<dim3(grid_for(n)), dim3(256), 0, st>>>(a, b, c, n);
+  }
+  return launch_status();
+}
+
+extern "C" int aar_strided_copy_f32(const float* src, float* dst, int ndim, const int64_t* shape,
+                                    const int64_t* src_strides, const int64_t* dst_strides,
+                                    void* stream) {
+  if (ndim < 0 || ndim > 8) return AAR_EINVAL;
+  int64_t n = 1;
+  StridedDesc desc;
+  desc.ndim = ndim;
+  for (int i = 0; i < ndim; ++i) {
+    if (!shape || !src_strides || !dst_strides || shape[i] < 0) return AAR_EINVAL;
+    desc.shape[i] = shape[i];
+    desc.src[i] = src_strides[i];
+    desc.dst[i] = dst_strides[i];
+    n *= shape[i];
+  }
+  if (n == 0) return AAR_OK;
+  if (!src || !dst) return AAR_EINVAL;
+  strided_copy_kernel<<<dim3(grid_for(n)), dim3(256), 0, as_stream(stream)>>>(src, dst, desc, n);
+  return launch_status();
+}

@@ -1,0 +1,626 @@
+// fp32 flash attention on CDNA4 matrix cores (v_mfma_f32_32x32x2f32).
+// Reference semantics: flash_attn_fwd_kernel / flash_attn_bwd_kernel
+// (cppsrc/ops/flash_attention.cu:13-224): O = softmax(scale*Q K^T, causal
+// mask j <= i) V, lse = m + ln(l); backward dQ, dK, dV.
+//
+// Layout trick: every product is issued "transposed" so that the dimension a
+// wave owns (its 32 queries in forward / dQ, its 32 keys in dK/dV) is the MFMA
+// output *column*, i.e. the lane index (lane % 32), while the reduced-over
+// dimension sits in the 16 accumulator registers of that lane:
+//   forward   S^T = K Q^T        lane = query, regs = 16 keys of the tile
+//             O^T += V^T P^T     lane = query, regs = head-dim entries
+// so the online-softmax row max / row sum are 16 in-register ops plus one
+// exchange with lane ^ 32, and the rescale of O by alpha is lane-local.  The
+// P tile produced by the first MFMA is consumed directly, register s of the
+// S^T accumulator, as the B operand of the second MFMA: P never touches LDS.
+//
+// In a 32x32x2 MFMA, lane (r = lane%32, h = lane/32) supplies A[r][k], B[k][r]
+// for k = h; accumulator register i of that lane is row 8*(i/4) + 4h + (i%4),
+// column r.  Over a chunk of 8 contraction steps we let step s in 0..3 use
+// k = 4h + s for the head-dim contractions (so one ds_read_b128 feeds 4
+// MFMAs) and k = 8*(s/4) + 4h + (s%4) for the key/query contractions (so the
+// accumulator register s is exactly the operand of step s).
+//
+// Backward (no float atomics, deterministic):
+//   pass 0  D[i] = sum_d dO[i][d] O[i][d]
+//   pass 1  workgroup per 128 keys (wave per 32 keys, K and V in registers),
+//           loop over query tiles:  S = Q K^T, dP = dO V^T (lane = key),
+//           P = exp(S*scale - lse), dS = P (dP - D),
+//           dV^T += dO^T P,  dK^T += Q^T dS   (lane = key, accumulated in regs)
+//   pass 2  workgroup per 128 queries (wave per 32 queries, Q and dO in regs),
+//           loop over key tiles: S^T, dP^T (lane = query), dS^T,
+//           dQ^T += K^T dS^T.
+#include <hip/hip_runtime.h>
+#include <math.h>
+
+#include "common.hpp"
+
+namespace aar {
+namespace {
+
+constexpr int kFaThreads = 256;  // 4 waves
+constexpr int kTile = 32;        // keys (or queries) per inner tile
+constexpr int kBlock = 128;      // queries (or keys) per workgroup
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+__device__ __forceinline__ f32x16 mfma32(float a, float b, const f32x16& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ f32x16 zero16() {
+  f32x16 z;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) z[i] = 0.f;
+  return z;
+}
+
+// Row index (within a 32-row tile) of accumulator register r for lane half h.
+__device__ __forceinline__ int acc_row(int r, int h) { return 8 * (r >> 2) + 4 * h + (r & 3); }
+
+// 4 consecutive floats p[0..3] of a row with `valid` leading entries (zeros
+// past it).  VEC: the row is 16-byte aligned and valid is 0 or >= 4.
+template <bool VEC>
+__device__ __forceinline__ f32x4 load4(const float* __restrict__ p, int valid) {
+  f32x4 v = {0.f, 0.f, 0.f, 0.f};
+  if (VEC) {
+    if (valid >= 4) v = *reinterpret_cast<const f32x4*>(p);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      if (e < valid) v[e] = p[e];
+  }
+  return v;
+}
+
+template <bool VEC>
+__device__ __forceinline__ void store4(float* __restrict__ p, f32x4 v, int valid) {
+  if (VEC) {
+    if (valid >= 4) *reinterpret_cast<f32x4*>(p) = v;
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      if (e < valid) p[e] = v[e];
+  }
+}
+
+// Cooperative copy of a [32][DP] tile (rows row0.., head dim padded to DP with
+// zeros, rows past T zero) from global into registers, then into LDS with row
+// stride LD.
+template <int DP, bool VEC>
+struct TileCopy {
+  static constexpr int kUnits = kTile * DP / 4;
+  static constexpr int kPer = (kUnits + kFaThreads - 1) / kFaThreads;
+  f32x4 reg[kPer];
+
+  __device__ __forceinline__ void load(const float* __restrict__ base, int row0, int T, int d, int tid) {
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int u = tid + i * kFaThreads;
+      const int r = u / (DP / 4);
+      const int c = (u % (DP / 4)) * 4;
+      f32x4 v = {0.f, 0.f, 0.f, 0.f};
+      if (u < kUnits && row0 + r < T) v = load4<VEC>(base + (int64_t)(row0 + r) * d + c, d - c);
+      reg[i] = v;
+    }
+  }
+
+  template <int LD>
+  __device__ __forceinline__ void store(float* __restrict__ s, int tid) const {
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int u = tid + i * kFaThreads;
+      if (u < kUnits) {
+        const int r = u / (DP / 4);
+        const int c = (u % (DP / 4)) * 4;
+        *reinterpret_cast<f32x4*>(s + r * LD + c) = reg[i];
+      }
+    }
+  }
+};
+
+// ------------------------------------------------------------------ forward
+
+template <int DP, bool CAUSAL, bool VEC>
+__global__ void __launch_bounds__(kFaThreads)
+flash_fwd_kernel(const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
+                 float* __restrict__ O, float* __restrict__ Lse, int T, int d, int nqb, int BH,
+                 float scale_log2) {
+  constexpr int NC = DP / 8;   // head-dim chunks
+  constexpr int NB = DP / 32;  // head-dim output blocks
+  constexpr int KLD = DP + 4;
+  constexpr int VLD = DP + 4;
+  __shared__ __attribute__((aligned(16))) float ks[2][kTile * KLD];
+  __shared__ __attribute__((aligned(16))) float vs[2][kTile * VLD];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int lr = lane & 31, h = lane >> 5;
+  // Longest work first: the last query blocks have the most key tiles.
+  const int qb = CAUSAL ? nqb - 1 - (int)(blockIdx.x / BH) : (int)(blockIdx.x / BH);
+  const int bh = blockIdx.x % BH;
+  const int64_t off = (int64_t)bh * T * d;
+  const int q0 = qb * kBlock + wave * kTile;  // first query of this wave
+  const int qi = q0 + lr;                     // this lane's query
+
+  f32x4 qr[NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const int dd = 8 * c + 4 * h;
+    qr[c] = qi < T ? load4<VEC>(Q + off + (int64_t)qi * d + dd, d - dd) : f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  f32x16 o[NB];
+#pragma unroll
+  for (int b = 0; b < NB; ++b) o[b] = zero16();
+  float m = -INFINITY, l = 0.f;
+
+  const int kv_end = CAUSAL ? min(T, qb * kBlock + kBlock) : T;
+  const int ntiles = (kv_end + kTile - 1) / kTile;
+
+  TileCopy<DP, VEC> kc, vc;
+  kc.load(K + off, 0, T, d, tid);
+  vc.load(V + off, 0, T, d, tid);
+  kc.template store<KLD>(ks[0], tid);
+  vc.template store<VLD>(vs[0], tid);
+  __syncthreads();
+
+  for (int t = 0; t < ntiles; ++t) {
+    const int cur = t & 1;
+    const int kv0 = t * kTile;
+    const bool has_next = t + 1 < ntiles;
+    if (has_next) {
+      kc.load(K + off, kv0 + kTile, T, d, tid);
+      vc.load(V + off, kv0 + kTile, T, d, tid);
+    }
+    if (!CAUSAL || kv0 <= q0 + kTile - 1) {
+      const float* kt = ks[cur];
+      const float* vt = vs[cur];
+      f32x16 s = zero16();
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        const f32x4 kf = *reinterpret_cast<const f32x4*>(kt + lr * KLD + 8 * c + 4 * h);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) s = mfma32(kf[e], qr[c][e], s);
+      }
+      float mx = -INFINITY;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int key = kv0 + acc_row(r, h);
+        float v = s[r] * scale_log2;
+        if (key >= T || (CAUSAL && key > qi)) v = -INFINITY;
+        s[r] = v;
+        mx = fmaxf(mx, v);
+      }
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      const float m_new = fmaxf(m, mx);
+      const float m_use = m_new == -INFINITY ? 0.f : m_new;
+      const float alpha = exp2f(m - m_use);
+      float ps = 0.f;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float p = exp2f(s[r] - m_use);
+        s[r] = p;
+        ps += p;
+      }
+      ps += __shfl_xor(ps, 32, 64);
+      l = l * alpha + ps;
+      m = m_new;
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[b][r] *= alpha;
+      }
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+#pragma unroll
+        for (int st = 0; st < 16; ++st) {
+          const float vf = vt[acc_row(st, h) * VLD + b * 32 + lr];
+          o[b] = mfma32(vf, s[st], o[b]);
+        }
+      }
+    }
+    if (has_next) {
+      kc.template store<KLD>(ks[cur ^ 1], tid);
+      vc.template store<VLD>(vs[cur ^ 1], tid);
+    }
+    __syncthreads();
+  }
+
+  if (qi < T) {
+    const float inv_l = 1.0f / l;
+    float* orow = O + off + (int64_t)qi * d;
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int dd = b * 32 + 8 * g + 4 * h;
+        f32x4 v = {o[b][4 * g] * inv_l, o[b][4 * g + 1] * inv_l, o[b][4 * g + 2] * inv_l,
+                   o[b][4 * g + 3] * inv_l};
+        if (dd < d) store4<VEC>(orow + dd, v, d - dd);
+      }
+    }
+    if (h == 0) Lse[(int64_t)bh * T + qi] = (m + log2f(l)) * kLn2;
+  }
+}
+
+// ------------------------------------------------------------- backward 0
+
+// D[row] = sum_d dO[row][d] * O[row][d]; 16 lanes per row.
+__global__ void __launch_bounds__(256)
+flash_bwd_dot_kernel(const float* __restrict__ dO, const float* __restrict__ O, float* __restrict__ D,
+                     int64_t rows, int d) {
+  const int64_t row = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 4;
+  const int sub = threadIdx.x & 15;
+  float acc = 0.f;
+  if (row < rows) {
+    const float* a = dO + row * d;
+    const float* b = O + row * d;
+    for (int c = sub; c < d; c += 16) acc += a[c] * b[c];
+  }
+  acc += dpp_quad_xor1(acc);
+  acc += dpp_quad_xor2(acc);
+  acc += dpp_half_mirror(acc);
+  acc += dpp_row_mirror(acc);
+  if (row < rows && sub == 0) D[row] = acc;
+}
+
+// ------------------------------------------------------------- backward 1
+
+template <int DP, bool CAUSAL, bool VEC>
+__global__ void __launch_bounds__(kFaThreads)
+flash_bwd_dkdv_kernel(const float* __restrict__ Q, const float* __restrict__ K,
+                      const float* __restrict__ V, const float* __restrict__ dO,
+                      const float* __restrict__ Lse, const float* __restrict__ Dv,
+                      float* __restrict__ dK, float* __restrict__ dV, int T, int d, int nkb, int BH,
+                      float scale, float scale_log2) {
+  constexpr int NC = DP / 8;
+  constexpr int NB = DP / 32;
+  constexpr int LD = DP + 4;
+  __shared__ __attribute__((aligned(16))) float qs[2][kTile * LD];
+  __shared__ __attribute__((aligned(16))) float dos[2][kTile * LD];
+  __shared__ __attribute__((aligned(16))) float ls[2][kTile];
+  __shared__ __attribute__((aligned(16))) float dsum[2][kTile];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int lr = lane & 31, h = lane >> 5;
+  // Longest work first: under the causal mask the first key blocks see the
+  // most query tiles.
+  const int kb = (int)(blockIdx.x / BH);
+  const int bh = blockIdx.x % BH;
+  const int64_t off = (int64_t)bh * T * d;
+  const int k0 = kb * kBlock + wave * kTile;  // first key of this wave
+  const int kj = k0 + lr;                     // this lane's key
+
+  f32x4 kr[NC], vr[NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const int dd = 8 * c + 4 * h;
+    const bool ok = kj < T;
+    kr[c] = ok ? load4<VEC>(K + off + (int64_t)kj * d + dd, d - dd) : f32x4{0.f, 0.f, 0.f, 0.f};
+    vr[c] = ok ? load4<VEC>(V + off + (int64_t)kj * d + dd, d - dd) : f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  f32x16 dk[NB], dv[NB];
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    dk[b] = zero16();
+    dv[b] = zero16();
+  }
+
+  const int q_begin = CAUSAL ? kb * kBlock : 0;  // first query tile with work
+  const int t0 = q_begin / kTile;
+  const int ntiles = (T + kTile - 1) / kTile;
+  const float* Lb = Lse + (int64_t)bh * T;
+  const float* Db = Dv + (int64_t)bh * T;
+
+  TileCopy<DP, VEC> qc, dc;
+  float lreg = 0.f, dreg = 0.f;
+  auto load_tile = [&](int t) {
+    qc.load(Q + off, t * kTile, T, d, tid);
+    dc.load(dO + off, t * kTile, T, d, tid);
+    if (tid < kTile) {
+      const int q = t * kTile + tid;
+      // Past-the-end queries get lse = +inf so that their P is exactly 0.
+      lreg = q < T ? Lb[q] * kLog2e : INFINITY;
+      dreg = q < T ? Db[q] : 0.f;
+    }
+  };
+  auto store_tile = [&](int buf) {
+    qc.template store<LD>(qs[buf], tid);
+    dc.template store<LD>(dos[buf], tid);
+    if (tid < kTile) {
+      ls[buf][tid] = lreg;
+      dsum[buf][tid] = dreg;
+    }
+  };
+  if (t0 < ntiles) {
+    load_tile(t0);
+    store_tile(0);
+  }
+  __syncthreads();
+
+  for (int t = t0; t < ntiles; ++t) {
+    const int cur = (t - t0) & 1;
+    const int qt0 = t * kTile;
+    const bool has_next = t + 1 < ntiles;
+    if (has_next) load_tile(t + 1);
+    if (!CAUSAL || qt0 + kTile - 1 >= k0) {
+      const float* qt = qs[cur];
+      const float* dot = dos[cur];
+      f32x16 s = zero16(), dp = zero16();
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        const f32x4 qf = *reinterpret_cast<const f32x4*>(qt + lr * LD + 8 * c + 4 * h);
+        const f32x4 df = *reinterpret_cast<const f32x4*>(dot + lr * LD + 8 * c + 4 * h);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          s = mfma32(qf[e], kr[c][e], s);
+          dp = mfma32(df[e], vr[c][e], dp);
+        }
+      }
+      // s, dp: lane = key kj, register r = query qt0 + acc_row(r, h).
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const f32x4 l4 = *reinterpret_cast<const f32x4*>(&ls[cur][8 * g + 4 * h]);
+        const f32x4 d4 = *reinterpret_cast<const f32x4*>(&dsum[cur][8 * g + 4 * h]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int r = 4 * g + e;
+          float p = exp2f(s[r] * scale_log2 - l4[e]);
+          if (CAUSAL && kj > qt0 + acc_row(r, h)) p = 0.f;
+          s[r] = p;
+          dp[r] = p * (dp[r] - d4[e]);
+        }
+      }
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+#pragma unroll
+        for (int st = 0; st < 16; ++st) {
+          const int q = acc_row(st, h);
+          dv[b] = mfma32(dot[q * LD + b * 32 + lr], s[st], dv[b]);
+          dk[b] = mfma32(qt[q * LD + b * 32 + lr], dp[st], dk[b]);
+        }
+      }
+    }
+    if (has_next) store_tile(cur ^ 1);
+    __syncthreads();
+  }
+
+  if (kj < T) {
+    float* krow = dK + off + (int64_t)kj * d;
+    float* vrow = dV + off + (int64_t)kj * d;
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int dd = b * 32 + 8 * g + 4 * h;
+        if (dd >= d) continue;
+        f32x4 a = {dk[b][4 * g] * scale, dk[b][4 * g + 1] * scale, dk[b][4 * g + 2] * scale,
+                   dk[b][4 * g + 3] * scale};
+        f32x4 c = {dv[b][4 * g], dv[b][4 * g + 1], dv[b][4 * g + 2], dv[b][4 * g + 3]};
+        store4<VEC>(krow + dd, a, d - dd);
+        store4<VEC>(vrow + dd, c, d - dd);
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------- backward 2
+
+template <int DP, bool CAUSAL, bool VEC>
+__global__ void __launch_bounds__(kFaThreads)
+flash_bwd_dq_kernel(const float* __restrict__ Q, const float* __restrict__ K,
+                    const float* __restrict__ V, const float* __restrict__ dO,
+                    const float* __restrict__ Lse, const float* __restrict__ Dv,
+                    float* __restrict__ dQ, int T, int d, int nqb, int BH, float scale,
+                    float scale_log2) {
+  constexpr int NC = DP / 8;
+  constexpr int NB = DP / 32;
+  constexpr int LD = DP + 4;
+  __shared__ __attribute__((aligned(16))) float ks[2][kTile * LD];
+  __shared__ __attribute__((aligned(16))) float vs[2][kTile * LD];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int lr = lane & 31, h = lane >> 5;
+  const int qb = CAUSAL ? nqb - 1 - (int)(blockIdx.x / BH) : (int)(blockIdx.x / BH);
+  const int bh = blockIdx.x % BH;
+  const int64_t off = (int64_t)bh * T * d;
+  const int q0 = qb * kBlock + wave * kTile;
+  const int qi = q0 + lr;
+
+  f32x4 qr[NC], dor[NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const int dd = 8 * c + 4 * h;
+    const bool ok = qi < T;
+    qr[c] = ok ? load4<VEC>(Q + off + (int64_t)qi * d + dd, d - dd) : f32x4{0.f, 0.f, 0.f, 0.f};
+    dor[c] = ok ? load4<VEC>(dO + off + (int64_t)qi * d + dd, d - dd) : f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  const float l2 = qi < T ? Lse[(int64_t)bh * T + qi] * kLog2e : INFINITY;
+  const float dq_sum = qi < T ? Dv[(int64_t)bh * T + qi] : 0.f;
+  f32x16 dq[NB];
+#pragma unroll
+  for (int b = 0; b < NB; ++b) dq[b] = zero16();
+
+  const int kv_end = CAUSAL ? min(T, qb * kBlock + kBlock) : T;
+  const int ntiles = (kv_end + kTile - 1) / kTile;
+
+  TileCopy<DP, VEC> kc, vc;
+  kc.load(K + off, 0, T, d, tid);
+  vc.load(V + off, 0, T, d, tid);
+  kc.template store<LD>(ks[0], tid);
+  vc.template store<LD>(vs[0], tid);
+  __syncthreads();
+
+  for (int t = 0; t < ntiles; ++t) {
+    const int cur = t & 1;
+    const int kv0 = t * kTile;
+    const bool has_next = t + 1 < ntiles;
+    if (has_next) {
+      kc.load(K + off, kv0 + kTile, T, d, tid);
+      vc.load(V + off, kv0 + kTile, T, d, tid);
+    }
+    if (!CAUSAL || kv0 <= q0 + kTile - 1) {
+      const float* kt = ks[cur];
+      const float* vt = vs[cur];
+      f32x16 s = zero16(), dp = zero16();
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        const f32x4 kf = *reinterpret_cast<const f32x4*>(kt + lr * LD + 8 * c + 4 * h);
+        const f32x4 vf = *reinterpret_cast<const f32x4*>(vt + lr * LD + 8 * c + 4 * h);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          s = mfma32(kf[e], qr[c][e], s);
+          dp = mfma32(vf[e], dor[c][e], dp);
+        }
+      }
+      // s, dp: lane = query qi, register r = key kv0 + acc_row(r, h).
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int key = kv0 + acc_row(r, h);
+        float p = exp2f(s[r] * scale_log2 - l2);
+        if (key >= T || (CAUSAL && key > qi)) p = 0.f;
+        dp[r] = p * (dp[r] - dq_sum);
+      }
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+#pragma unroll
+        for (int st = 0; st < 16; ++st) {
+          dq[b] = mfma32(kt[acc_row(st, h) * LD + b * 32 + lr], dp[st], dq[b]);
+        }
+      }
+    }
+    if (has_next) {
+      kc.template store<LD>(ks[cur ^ 1], tid);
+      vc.template store<LD>(vs[cur ^ 1], tid);
+    }
+    __syncthreads();
+  }
+
+  if (qi < T) {
+    float* qrow = dQ + off + (int64_t)qi * d;
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int dd = b * 32 + 8 * g + 4 * h;
+        if (dd >= d) continue;
+        f32x4 v = {dq[b][4 * g] * scale, dq[b][4 * g + 1] * scale, dq[b][4 * g + 2] * scale,
+                   dq[b][4 * g + 3] * scale};
+        store4<VEC>(qrow + dd, v, d - dd);
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------ dispatching
+
+int pad_dim(int64_t d) { return d <= 32 ? 32 : (d <= 64 ? 64 : 128); }
+
+template <template <int, bool, bool> class Launcher, typename... Args>
+int dispatch_fa(int dp, bool causal, bool vec, Args... args) {
+#define AAR_FA_CASE(DPV)                                                      \
+  if (dp == DPV) {                                                            \
+    if (causal) {                                                             \
+      return vec ? Launcher<DPV, true, true>::run(args...)                    \
+                 : Launcher<DPV, true, false>::run(args...);                  \
+    }                                                                         \
+    return vec ? Launcher<DPV, false, true>::run(args...)                     \
+               : Launcher<DPV, false, false>::run(args...);                   \
+  }
+  AAR_FA_CASE(32)
+  AAR_FA_CASE(64)
+  AAR_FA_CASE(128)
+#undef AAR_FA_CASE
+  return AAR_EUNSUPPORTED;
+}
+
+struct FwdArgs {
+  const float *q, *k, *v;
+  float *o, *lse;
+  int T, d, BH;
+  float scale;
+  hipStream_t st;
+};
+
+template <int DP, bool C, bool VEC>
+struct FwdLaunch {
+  static int run(const FwdArgs& a) {
+    const int nqb = (a.T + kBlock - 1) / kBlock;
+    flash_fwd_kernel<DP, C, VEC><<<dim3((unsigned)(nqb * a.BH)), dim3(kFaThreads), 0, a.st>>>(
+        a.q, a.k, a.v, a.o, a.lse, a.T, a.d, nqb, a.BH, a.scale * kLog2e);
+    return launch_status();
+  }
+};
+
+struct BwdArgs {
+  const float *q, *k, *v, *dout, *lse, *D;
+  float *dq, *dk, *dv;
+  int T, d, BH;
+  float scale;
+  hipStream_t st;
+};
+
+template <int DP, bool C, bool VEC>
+struct BwdLaunch {
+  static int run(const BwdArgs& a) {
+    const int nb = (a.T + kBlock - 1) / kBlock;
+    flash_bwd_dkdv_kernel<DP, C, VEC><<<dim3((unsigned)(nb * a.BH)), dim3(kFaThreads), 0, a.st>>>(
+        a.q, a.k, a.v, a.dout, a.lse, a.D, a.dk, a.dv, a.T, a.d, nb, a.BH, a.scale, a.scale * kLog2e);
+    int rc = launch_status();
+    if (rc != AAR_OK) return rc;
+    flash_bwd_dq_kernel<DP, C, VEC><<<dim3((unsigned)(nb * a.BH)), dim3(kFaThreads), 0, a.st>>>(
+        a.q, a.k, a.v, a.dout, a.lse, a.D, a.dq, a.T, a.d, nb, a.BH, a.scale, a.scale * kLog2e);
+    return launch_status();
+  }
+};
+
+bool fa_shape_ok(int64_t bh, int64_t T, int64_t d) {
+  return bh > 0 && T > 0 && d > 0 && d <= 128 && T <= (1 << 24) && bh <= (1 << 24) &&
+         bh * ((T + kBlock - 1) / kBlock) < (int64_t)INT32_MAX;
+}
+
+}  // namespace
+}  // namespace aar
+
+using namespace aar;
+
+extern "C" int aar_flash_fwd_f32(const float* q, const float* k, const float* v, float* o, float* lse,
+                                 int64_t bh, int64_t T, int64_t d, int causal, float scale,
+                                 void* stream) {
+  if (bh < 0 || T < 0 || d <= 0) return AAR_EINVAL;
+  if (d > 128) return AAR_EINVAL;
+  if (bh == 0 || T == 0) return AAR_OK;
+  if (!q || !k || !v || !o || !lse) return AAR_EINVAL;
+  if (!fa_shape_ok(bh, T, d)) return AAR_EUNSUPPORTED;
+  const bool vec = d % 4 == 0 && aligned16(q) && aligned16(k) && aligned16(v) && aligned16(o);
+  FwdArgs a{q, k, v, o, lse, (int)T, (int)d, (int)bh, scale, as_stream(stream)};
+  return dispatch_fa<FwdLaunch>(pad_dim(d), causal != 0, vec, a);
+}
+
+extern "C" size_t aar_flash_bwd_workspace_bytes(int64_t bh, int64_t T, int64_t d) {
+  (void)d;
+  if (bh <= 0 || T <= 0) return 0;
+  return (size_t)bh * (size_t)T * sizeof(float);
+}
+
+extern "C" int aar_flash_bwd_f32(const float* q, const float* k, const float* v, const float* o,
+                                 const float* lse, const float* dout, float* dq, float* dk, float* dv,
+                                 int64_t bh, int64_t T, int64_t d, int causal, float scale,
+                                 void* workspace, size_t workspace_bytes, void* stream) {
+  if (bh < 0 || T < 0 || d <= 0) return AAR_EINVAL;
+  if (d > 128) return AAR_EINVAL;
+  if (bh == 0 || T == 0) return AAR_OK;
+  if (!q || !k || !v || !o || !lse || !dout || !dq || !dk || !dv) return AAR_EINVAL;
+  if (!fa_shape_ok(bh, T, d)) return AAR_EUNSUPPORTED;
+  if (!workspace || workspace_bytes < aar_flash_bwd_workspace_bytes(bh, T, d)) return AAR_EWORKSPACE;
+  hipStream_t st = as_stream(stream);
+  float* D = static_cast<float*>(workspace);
+  const int64_t rows = bh * T;
+  flash_bwd_dot_kernel<<<dim3((unsigned)ceil_div(rows * 16, 256)), dim3(256), 0, st>>>(dout, o, D, rows,
+                                                                                     (int)d);
+  int rc = launch_status();
+  if (rc != AAR_OK) return rc;
+  const bool vec = d % 4 == 0 && aligned16(q) && aligned16(k) && aligned16(v) && aligned16(dout) &&
+                   aligned16(dq) && aligned16(dk) && aligned16(dv);
+  BwdArgs a{q, k, v, dout, lse, D, dq, dk, dv, (int)T, (int)d, (int)bh, scale, st};
+  return dispatch_fa<BwdLaunch>(pad_dim(d), causal != 0, vec, a);
+}

@@ -1,0 +1,631 @@
+// Row-wise fp32 kernels over the last dim: softmax fwd/bwd and layernorm
+// fwd (with or without stats) / bwd.  Reference semantics:
+//   softmax_cpu / softmax_backward_cpu   cppsrc/ops/softmax.cpp:15-55
+//   layernorm_cpu / _with_stats / _bwd   cppsrc/ops/layernorm.cpp:20-134
+//
+// HBM-bound design:
+//  * A row is held in VGPRs for the whole op, so x (and g, y) cross HBM once:
+//    softmax fwd moves 8*cols bytes per row, bwd 12*cols, layernorm fwd
+//    8*cols (+8 for stats), bwd 12*cols (+8).
+//  * Each row is owned by W waves (W = 1 up to 2048 columns, else 4); a lane
+//    holds NV slots of 4 consecutive floats (one 128-bit load each) laid out
+//    so every slot is a contiguous 1 KB segment across the wave.
+//  * Reductions are wave64 DPP/ds_swizzle butterflies; with W = 4 the four
+//    wave partials meet in LDS and are summed in a fixed order.
+//  * Workgroups are persistent (a few per CU) and stride over rows, so gamma/
+//    beta stay in registers and layernorm's dgamma/dbeta accumulate per lane
+//    in registers; each workgroup writes one partial row to a workspace and a
+//    second kernel sums the partials in a fixed order.  No float atomics: the
+//    result is bit-reproducible on a given device.
+#include <hip/hip_runtime.h>
+#include <math.h>
+
+#include "common.hpp"
+
+namespace aar {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / kWave;
+
+// One lane's share of a row: NV slots of 4 floats (VEC: 128-bit accesses, the
+// row must be 16-byte aligned with cols % 4 == 0) or NV single floats.
+template <int NV, int W, bool VEC>
+struct RowSlots {
+  static constexpr int kElem = VEC ? 4 : 1;
+  static constexpr int kN = NV * kElem;
+  float v[kN];
+
+  // Column of element e (0..kElem-1) of slot i for lane `lane` of wave `wr`.
+  __device__ __forceinline__ static int col(int i, int e, int wr, int lane) {
+    return ((i * W + wr) * kWave + lane) * kElem + e;
+  }
+
+  __device__ __forceinline__ void load(const float* __restrict__ row, int cols, int wr, int lane) {
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int c0 = col(i, 0, wr, lane);
+      if (VEC) {
+        f32x4 t = {0.f, 0.f, 0.f, 0.f};
+        if (c0 < cols) t = *reinterpret_cast<const f32x4*>(row + c0);
+        v[4 * i + 0] = t[0];
+        v[4 * i + 1] = t[1];
+        v[4 * i + 2] = t[2];
+        v[4 * i + 3] = t[3];
+      } else {
+        v[i] = c0 < cols ? row[c0] : 0.f;
+      }
+    }
+  }
+
+  __device__ __forceinline__ void store(float* __restrict__ row, int cols, int wr, int lane) const {
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int c0 = col(i, 0, wr, lane);
+      if (c0 >= cols) continue;
+      if (VEC) {
+        f32x4 t = {v[4 * i + 0], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]};
+        *reinterpret_cast<f32x4*>(row + c0) = t;
+      } else {
+        row[c0] = v[i];
+      }
+    }
+  }
+
+  __device__ __forceinline__ bool valid(int k, int cols, int wr, int lane) const {
+    return col(k / kElem, k % kElem, wr, lane) < cols;
+  }
+};
+
+// Row-group reduction: full wave reduction, then (W > 1) a fixed-order sum of
+// the W wave partials through LDS.  `slot` selects a private LDS cell set; all
+// waves of the workgroup must call this uniformly.
+template <int W, bool MAX>
+__device__ __forceinline__ float group_reduce(float v, float* red, int slot, int grp, int wr,
+                                              int lane) {
+  v = MAX ? wave_max(v) : wave_sum(v);
+  if (W == 1) return v;
+  float* cell = red + (slot * kWaves + grp * W);
+  if (lane == 0) cell[wr] = v;
+  __syncthreads();
+  float r = cell[0];
+#pragma unroll
+  for (int i = 1; i < W; ++i) r = MAX ? fmaxf(r, cell[i]) : r + cell[i];
+  return r;
+}
+
+// Number of row-groups each workgroup iteration covers, and persistent grid.
+inline int rows_grid(int64_t rows, int W) {
+  const int64_t per_iter = kWaves / W;
+  const int64_t need = ceil_div(rows, per_iter);
+  const int64_t cap = (int64_t)device_cu_count() * 8;
+  return (int)(need < cap ? need : cap);
+}
+
+// ------------------------------------------------------------------ softmax
+
+template <int NV, int W, bool VEC>
+__global__ void __launch_bounds__(kThreads)
+softmax_fwd_kernel(const float* __restrict__ x, float* __restrict__ y, int64_t rows, int cols) {
+  __shared__ float red[4 * kWaves];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int grp = wave / W, wr = wave % W;
+  constexpr int per_iter = kWaves / W;
+  const int64_t iters = ceil_div(rows, (int64_t)gridDim.x * per_iter);
+  using RS = RowSlots<NV, W, VEC>;
+  for (int64_t it = 0; it < iters; ++it) {
+    const int64_t row = (it * gridDim.x + blockIdx.x) * per_iter + grp;
+    const bool live = row < rows;
+    RS s;
+    if (live) s.load(x + row * cols, cols, wr, lane);
+    float mx = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < RS::kN; ++k)
+      if (live && s.valid(k, cols, wr, lane)) mx = fmaxf(mx, s.v[k]);
+    mx = group_reduce<W, true>(mx, red, (int)(it & 1) * 2 + 0, grp, wr, lane);
+    float sum = 0.f;
+#pragma unroll
+    for (int k = 0; k < RS::kN; ++k) {
+      const float e = (live && s.valid(k, cols, wr, lane)) ? expf(s.v[k] - mx) : 0.f;
+      s.v[k] = e;
+      sum += e;
+    }
+    sum = group_reduce<W, false>(sum, red, (int)(it & 1) * 2 + 1, grp, wr, lane);
+    const float inv = 1.0f / sum;
+#pragma unroll
+    for (int k = 0; k < RS::kN; ++k) s.v[k] *= inv;
+    if (live) s.store(y + row * cols, cols, wr, lane);
+  }
+}
+
+template <int NV, int W, bool VEC>
+__global__ void __launch_bounds__(kThreads)
+softmax_bwd_kernel(const float* __restrict__ g, const float* __restrict__ y, float* __restrict__ dx,
+                   int64_t rows, int cols) {
+  __shared__ float red[4 * kWaves];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int grp = wave / W, wr = wave % W;
+  constexpr int per_iter = kWaves / W;
+  const int64_t iters = ceil_div(rows, (int64_t)gridDim.x * per_iter);
+  using RS = RowSlots<NV, W, VEC>;
+  for (int64_t it = 0; it < iters; ++it) {
+    const int64_t row = (it * gridDim.x + blockIdx.x) * per_iter + grp;
+    const bool live = row < rows;
+    RS sg, sy;
+    if (live) {
+      sg.load(g + row * cols, cols, wr, lane);
+      sy.load(y + row * cols, cols, wr, lane);
+    }
+    float dot = 0.f;
+#pragma unroll
+    for (int k = 0; k < RS::kN; ++k) dot += sg.v[k] * sy.v[k];  // padding slots are zero
+    dot = group_reduce<W, false>(dot, red, (int)(it & 1), grp, wr, lane);
+#pragma unroll
+    for (int k = 0; k < RS::kN; ++k) sg.v[k] = sy.v[k] * (sg.v[k] - dot);
+    if (live) sg.store(dx + row * cols, cols, wr, lane);
+  }
+}
+
+// ---------------------------------------------------------------- layernorm
+
+template <int NV, int W, bool VEC, bool STATS>
+__global__ void __launch_bounds__(kThreads)
+layernorm_fwd_kernel(const float* __restrict__ x, const float* __restrict__ w,
+                     const float* __restrict__ b, float* __restrict__ y, float* __restrict__ mean,
+                     float* __restrict__ rstd, int64_t rows, int cols, float eps) {
+  __shared__ float red[4 * kWaves];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int grp = wave / W, wr = wave % W;
+  constexpr int per_iter = kWaves / W;
+  const int64_t iters = ceil_div(rows, (int64_t)gridDim.x * per_iter);
+  using RS = RowSlots<NV, W, VEC>;
+  RS sw, sb;
+  sw.load(w, cols, wr, lane);
+  sb.load(b, cols, wr, lane);
+  const float inv_d = 1.0f / (float)cols;
+  for (int64_t it = 0; it < iters; ++it) {
+    const int64_t row = (it * gridDim.x + blockIdx.x) * per_iter + grp;
+    const bool live = row < rows;
+    RS s;
+    if (live) s.load(x + row * cols, cols, wr, lane);
+    float sum = 0.f;
+#pragma unroll
+    for (int k = 0; k < RS::kN; ++k) sum += s.v[k];
+    sum = group_reduce<W, false>(sum, red, (int)(it & 1) * 2 + 0, grp, wr, lane);
+    const float mu = sum * inv_d;
+    float sq = 0.f;
+#pragma unroll
+    for (int k = 0; k < RS::kN; ++k) {
+      const float dlt = s.valid(k, cols, wr, lane) ? s.v[k] - mu : 0.f;
+      sq += dlt * dlt;
+    }
+    sq = group_reduce<W, false>(sq, red, (int)(it & 1) * 2 + 1, grp, wr, lane);
+    const float var = sq * inv_d;
+    const float r = 1.0f / sqrtf(var + eps);
+#pragma unroll
+    for (int k = 0; k < RS::kN; ++k) s.v[k] = (s.v[k] - mu) * r * sw.v[k] + sb.v[k];
+    if (live) {
+      s.store(y + row * cols, cols, wr, lane);
+      if (STATS && wr == 0 && lane == 0) {
+        mean[row] = mu;
+        rstd[row] = r;
+      }
+    }
+  }
+}
+
+// Stage 1 of layernorm backward: dx per row, plus per-workgroup partial
+// column sums of gy*xhat (dgamma) and gy (dbeta) written to
+// part[blockIdx.x][2][cols].
+template <int NV, int W, bool VEC>
+__global__ void __launch_bounds__(kThreads)
+layernorm_bwd_kernel(const float* __restrict__ gy, const float* __restrict__ x,
+                     const float* __restrict__ w, const float* __restrict__ mean,
+                     const float* __restrict__ rstd, float* __restrict__ dx,
+                     float* __restrict__ part, int64_t rows, int cols) {
+  __shared__ float red[4 * kWaves];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int grp = wave / W, wr = wave % W;
+  constexpr int per_iter = kWaves / W;
+  const int64_t iters = ceil_div(rows, (int64_t)gridDim.x * per_iter);
+  using RS = RowSlots<NV, W, VEC>;
+  RS sw, dwacc, dbacc;
+  sw.load(w, cols, wr, lane);
+#pragma unroll
+  for (int k = 0; k < RS::kN; ++k) {
+    dwacc.v[k] = 0.f;
+    dbacc.v[k] = 0.f;
+  }
+  const float inv_d = 1.0f / (float)cols;
+  for (int64_t it = 0; it < iters; ++it) {
+    const int64_t row = (it * gridDim.x + blockIdx.x) * per_iter + grp;
+    const bool live = row < rows;
+    RS sg, sx;
+    float mu = 0.f, r = 0.f;
+    if (live) {
+      sg.load(gy + row * cols, cols, wr, lane);
+      sx.load(x + row * cols, cols, wr, lane);
+      mu = mean[row];
+      r = rstd[row];
+    } else {
+#pragma unroll
+      for (int k = 0; k < RS::kN; ++k) {
+        sg.v[k] = 0.f;
+        sx.v[k] = 0.f;
+      }
+    }
+    float sum_g = 0.f, sum_gn = 0.f;
+#pragma unroll
+    for (int k = 0; k < RS::kN; ++k) {
+      const float n = (sx.v[k] - mu) * r;
+      const float gg = sg.v[k] * sw.v[k];
+      sum_g += gg;
+      sum_gn += gg * n;
+      dwacc.v[k] += sg.v[k] * n;
+      dbacc.v[k] += sg.v[k];
+      sx.v[k] = n;  // keep xhat
+    }
+    sum_g = group_reduce<W, false>(sum_g, red, (int)(it & 1) * 2 + 0, grp, wr, lane);
+    sum_gn = group_reduce<W, false>(sum_gn, red, (int)(it & 1) * 2 + 1, grp, wr, lane);
+#pragma unroll
+    for (int k = 0; k < RS::kN; ++k) {
+      const float gg = sg.v[k] * sw.v[k];
+      sg.v[k] = r * (gg - sum_g * inv_d - sx.v[k] * sum_gn * inv_d);
+    }
+    if (live) sg.store(dx + row * cols, cols, wr, lane);
+  }
+  // Combine the row groups of this workgroup in a fixed order: group 0 seeds
+  // the LDS accumulator, groups 1.. add in turn, then group 0's waves write
+  // the workgroup's partial row.
+  __shared__ float stage[2][RS::kN * kWave * W];
+  constexpr int ngrp = kWaves / W;
+#pragma unroll
+  for (int gi = 0; gi < ngrp; ++gi) {
+    if (grp == gi) {
+#pragma unroll
+      for (int k = 0; k < RS::kN; ++k) {
+        const int o = (k * W + wr) * kWave + lane;
+        stage[0][o] = gi == 0 ? dwacc.v[k] : stage[0][o] + dwacc.v[k];
+        stage[1][o] = gi == 0 ? dbacc.v[k] : stage[1][o] + dbacc.v[k];
+      }
+    }
+    __syncthreads();
+  }
+  if (grp == 0) {
+#pragma unroll
+    for (int k = 0; k < RS::kN; ++k) {
+      const int o = (k * W + wr) * kWave + lane;
+      dwacc.v[k] = stage[0][o];
+      dbacc.v[k] = stage[1][o];
+    }
+    float* pw = part + (int64_t)blockIdx.x * 2 * cols;
+    dwacc.store(pw, cols, wr, lane);
+    dbacc.store(pw + cols, cols, wr, lane);
+  }
+}
+
+// Stage 2: dw[c] = sum_p part[p][0][c], db[c] = sum_p part[p][1][c] (fixed order).
+__global__ void __launch_bounds__(256)
+layernorm_bwd_reduce_kernel(const float* __restrict__ part, float* __restrict__ dw,
+                            float* __restrict__ db, int nparts, int cols) {
+  const int c = blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= cols) return;
+  float a = 0.f, b = 0.f;
+  for (int p = 0; p < nparts; ++p) {
+    a += part[(int64_t)p * 2 * cols + c];
+    b += part[(int64_t)p * 2 * cols + cols + c];
+  }
+  dw[c] = a;
+  db[c] = b;
+}
+
+// ------------------------------------------------------- generic wide rows
+// Rows wider than the register-resident kernels cover: one workgroup per row,
+// three passes over the row (re-reads hit L2).
+
+__device__ __forceinline__ float block_sum(float v, float* red) {
+  v = wave_sum(v);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  __syncthreads();
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  float r = red[0];
+  for (int i = 1; i < kWaves; ++i) r += red[i];
+  return r;
+}
+
+__device__ __forceinline__ float block_max(float v, float* red) {
+  v = wave_max(v);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  __syncthreads();
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  float r = red[0];
+  for (int i = 1; i < kWaves; ++i) r = fmaxf(r, red[i]);
+  return r;
+}
+
+__global__ void __launch_bounds__(kThreads)
+softmax_fwd_wide_kernel(const float* __restrict__ x, float* __restrict__ y, int64_t cols) {
+  __shared__ float red[kWaves];
+  const float* xr = x + (int64_t)blockIdx.x * cols;
+  float* yr = y + (int64_t)blockIdx.x * cols;
+  float mx = -INFINITY;
+  for (int64_t c = threadIdx.x; c < cols; c += kThreads) mx = fmaxf(mx, xr[c]);
+  mx = block_max(mx, red);
+  float s = 0.f;
+  for (int64_t c = threadIdx.x; c < cols; c += kThreads) {
+    const float e = expf(xr[c] - mx);
+    yr[c] = e;
+    s += e;
+  }
+  s = block_sum(s, red);
+  const float inv = 1.0f / s;
+  for (int64_t c = threadIdx.x; c < cols; c += kThreads) yr[c] *= inv;
+}
+
+__global__ void __launch_bounds__(kThreads)
+softmax_bwd_wide_kernel(const float* __restrict__ g, const float* __restrict__ y,
+                        float* __restrict__ dx, int64_t cols) {
+  __shared__ float red[kWaves];
+  const int64_t off = (int64_t)blockIdx.x * cols;
+  float dot = 0.f;
+  for (int64_t c = threadIdx.x; c < cols; c += kThreads) dot += g[off + c] * y[off + c];
+  dot = block_sum(dot, red);
+  for (int64_t c = threadIdx.x; c < cols; c += kThreads) dx[off + c] = y[off + c] * (g[off + c] - dot);
+}
+
+__global__ void __launch_bounds__(kThreads)
+layernorm_fwd_wide_kernel(const float* __restrict__ x, const float* __restrict__ w,
+                          const float* __restrict__ b, float* __restrict__ y,
+                          float* __restrict__ mean, float* __restrict__ rstd, int64_t cols,
+                          float eps) {
+  __shared__ float red[kWaves];
+  const int64_t off = (int64_t)blockIdx.x * cols;
+  float s = 0.f;
+  for (int64_t c = threadIdx.x; c < cols; c += kThreads) s += x[off + c];
+  const float mu = block_sum(s, red) / (float)cols;
+  float q = 0.f;
+  for (int64_t c = threadIdx.x; c < cols; c += kThreads) {
+    const float d = x[off + c] - mu;
+    q += d * d;
+  }
+  const float var = block_sum(q, red) / (float)cols;
+  const float r = 1.0f / sqrtf(var + eps);
+  for (int64_t c = threadIdx.x; c < cols; c += kThreads) y[off + c] = (x[off + c] - mu) * r * w[c] + b[c];
+  if (mean && threadIdx.x == 0) {
+    mean[blockIdx.x] = mu;
+    rstd[blockIdx.x] = r;
+  }
+}
+
+// One workgroup per row for dx; dgamma/dbeta partials: workgroup p covers rows
+// p, p + gridDim.x, ... and accumulates per column in a strided loop.
+__global__ void __launch_bounds__(kThreads)
+layernorm_bwd_wide_kernel(const float* __restrict__ gy, const float* __restrict__ x,
+                          const float* __restrict__ w, const float* __restrict__ mean,
+                          const float* __restrict__ rstd, float* __restrict__ dx, int64_t cols) {
+  __shared__ float red[kWaves];
+  const int64_t off = (int64_t)blockIdx.x * cols;
+  const float mu = mean[blockIdx.x], r = rstd[blockIdx.x];
+  float sg = 0.f, sgn = 0.f;
+  for (int64_t c = threadIdx.x; c < cols; c += kThreads) {
+    const float n = (x[off + c] - mu) * r;
+    const float gg = gy[off + c] * w[c];
+    sg += gg;
+    sgn += gg * n;
+  }
+  sg = block_sum(sg, red);
+  sgn = block_sum(sgn, red);
+  const float inv_d = 1.0f / (float)cols;
+  for (int64_t c = threadIdx.x; c < cols; c += kThreads) {
+    const float n = (x[off + c] - mu) * r;
+    const float gg = gy[off + c] * w[c];
+    dx[off + c] = r * (gg - sg * inv_d - n * sgn * inv_d);
+  }
+}
+
+__global__ void __launch_bounds__(kThreads)
+layernorm_bwd_wide_cols_kernel(const float* __restrict__ gy, const float* __restrict__ x,
+                               const float* __restrict__ mean, const float* __restrict__ rstd,
+                               float* __restrict__ part, int64_t rows, int64_t cols) {
+  // part[blockIdx.y][2][cols]: rows blockIdx.y, blockIdx.y + gridDim.y, ...
+  const int64_t c = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (c >= cols) return;
+  float a = 0.f, b = 0.f;
+  for (int64_t r = blockIdx.y; r < rows; r += gridDim.y) {
+    const float g = gy[r * cols + c];
+    a += g * ((x[r * cols + c] - mean[r]) * rstd[r]);
+    b += g;
+  }
+  part[(int64_t)blockIdx.y * 2 * cols + c] = a;
+  part[(int64_t)blockIdx.y * 2 * cols + cols + c] = b;
+}
+
+// ------------------------------------------------------------ dispatching
+
+struct RowPlan {
+  int nv;   // slots per lane: 1, 2, 4 or 8 (0 = use the wide kernels)
+  int w;    // waves per row: 1 or 4
+  bool vec;
+};
+
+RowPlan plan_rows(int64_t cols, bool vec) {
+  const int64_t units = vec ? cols / 4 : cols;  // slots needed per row
+  RowPlan p{0, 1, vec};
+  for (int w : {1, 4}) {
+    for (int nv : {1, 2, 4, 8}) {
+      if (units <= (int64_t)nv * kWave * w) {
+        if (w == 4 && nv < 2) continue;
+        p.nv = nv;
+        p.w = w;
+        return p;
+      }
+    }
+  }
+  return p;
+}
+
+#define AAR_ROW_DISPATCH(PLAN, LAUNCH)                 \
+  do {                                                  \
+    if ((PLAN).vec) {                                   \
+      if ((PLAN).w == 1) {                              \
+        switch ((PLAN).nv) {                            \
+          case 1: LAUNCH(1, 1, true); break;            \
+          case 2: LAUNCH(2, 1, true); break;            \
+          case 4: LAUNCH(4, 1, true); break;            \
+          default: LAUNCH(8, 1, true); break;           \
+        }                                               \
+      } else {                                          \
+        switch ((PLAN).nv) {                            \
+          case 2: LAUNCH(2, 4, true); break;            \
+          case 4: LAUNCH(4, 4, true); break;            \
+          default: LAUNCH(8, 4, true); break;           \
+        }                                               \
+      }                                                 \
+    } else {                                            \
+      if ((PLAN).w == 1) {                              \
+        switch ((PLAN).nv) {                            \
+          case 1: LAUNCH(1, 1, false); break;           \
+          case 2: LAUNCH(2, 1, false); break;           \
+          case 4: LAUNCH(4, 1, false); break;           \
+          default: LAUNCH(8, 1, false); break;          \
+        }                                               \
+      } else {                                          \
+        switch ((PLAN).nv) {                            \
+          case 2: LAUNCH(2, 4, false); break;           \
+          case 4: LAUNCH(4, 4, false); break;           \
+          default: LAUNCH(8, 4, false); break;          \
+        }                                               \
+      }                                                 \
+    }                                                   \
+  } while (0)
+
+// Number of dgamma/dbeta partial rows (= workgroups of the backward kernel).
+int ln_bwd_parts(int64_t rows) {
+  const int64_t cap = (int64_t)device_cu_count() * 2;
+  const int64_t p = rows < cap ? rows : cap;
+  return (int)(p > 0 ? p : 1);
+}
+
+}  // namespace
+}  // namespace aar
+
+using namespace aar;
+
+extern "C" int aar_softmax_fwd_f32(const float* x, float* y, int64_t rows, int64_t cols, void* stream) {
+  if (rows < 0 || cols <= 0) return AAR_EINVAL;
+  if (rows == 0) return AAR_OK;
+  if (!x || !y || cols > INT32_MAX) return AAR_EINVAL;
+  hipStream_t st = as_stream(stream);
+  const RowPlan p = plan_rows(cols, cols % 4 == 0 && aligned16(x) && aligned16(y));
+  if (p.nv == 0) {
+    softmax_fwd_wide_kernel<<<dim3((unsigned)rows), dim3(kThreads), 0, st>>>(x, y, cols);
+    return launch_status();
+  }
+  const int grid = rows_grid(rows, p.w);
+#define L(NV, W, V) softmax_fwd_kernel<NV, W, V><<<dim3(grid), dim3(kThreads), 0, st>>>(x, y, rows, (int)cols)
+  AAR_ROW_DISPATCH(p, L);
+#undef L
+  return launch_status();
+}
+
+extern "C" int aar_softmax_bwd_f32(const float* g, const float* y, float* dx, int64_t rows, int64_t cols,
+                                   void* stream) {
+  if (rows < 0 || cols <= 0) return AAR_EINVAL;
+  if (rows == 0) return AAR_OK;
+  if (!g || !y || !dx || cols > INT32_MAX) return AAR_EINVAL;
+  hipStream_t st = as_stream(stream);
+  const RowPlan p = plan_rows(cols, cols % 4 == 0 && aligned16(g) && aligned16(y) && aligned16(dx));
+  if (p.nv == 0) {
+    softmax_bwd_wide_kernel<<<dim3((unsigned)rows), dim3(kThreads), 0, st>>>(g, y, dx, cols);
+    return launch_status();
+  }
+  const int grid = rows_grid(rows, p.w);
+#define L(NV, W, V) \
+  softmax_bwd_kernel<NV, W, V><<<dim3(grid), dim3(kThreads), 0, st>>>(g, y, dx, rows, (int)cols)
+  AAR_ROW_DISPATCH(p, L);
+#undef L
+  return launch_status();
+}
+
+extern "C" int aar_layernorm_fwd_f32(const float* x, const float* w, const float* b, float* y,
+                                     float* mean, float* rstd, int64_t rows, int64_t cols, float eps,
+                                     void* stream) {
+  if (rows < 0 || cols <= 0 || !(eps > 0.f)) return AAR_EINVAL;
+  if (rows == 0) return AAR_OK;
+  if (!x || !w || !b || !y || cols > INT32_MAX) return AAR_EINVAL;
+  const bool stats = mean && rstd;
+  hipStream_t st = as_stream(stream);
+  const bool vec = cols % 4 == 0 && aligned16(x) && aligned16(y) && aligned16(w) && aligned16(b);
+  const RowPlan p = plan_rows(cols, vec);
+  if (p.nv == 0) {
+    layernorm_fwd_wide_kernel<<<dim3((unsigned)rows), dim3(kThreads), 0, st>>>(
+        x, w, b, y, stats ? mean : nullptr, stats ? rstd : nullptr, cols, eps);
+    return launch_status();
+  }
+  const int grid = rows_grid(rows, p.w);
+  if (stats) {
+#define L(NV, W, V)                                                                              \
+  layernorm_fwd_kernel<NV, W, V, true><<<dim3(grid), dim3(kThreads), 0, st>>>(x, w, b, y, mean, \
+                                                                              rstd, rows,       \
+                                                                              (int)cols, eps)
+    AAR_ROW_DISPATCH(p, L);
+#undef L
+  } else {
+#define L(NV, W, V)                                                                    \
+  layernorm_fwd_kernel<NV, W, V, false><<<dim3(grid), dim3(kThreads), 0, st>>>(       \
+      x, w, b, y, nullptr, nullptr, rows, (int)cols, eps)
+    AAR_ROW_DISPATCH(p, L);
+#undef L
+  }
+  return launch_status();
+}
+
+extern "C" size_t aar_layernorm_bwd_workspace_bytes(int64_t rows, int64_t cols) {
+  if (rows <= 0 || cols <= 0) return 0;
+  return (size_t)ln_bwd_parts(rows) * 2 * (size_t)cols * sizeof(float);
+}
+
+extern "C" int aar_layernorm_bwd_f32(const float* gy, const float* x, const float* w,
+                                     const float* mean, const float* rstd, float* dx, float* dw,
+                                     float* db, int64_t rows, int64_t cols, void* workspace,
+                                     size_t workspace_bytes, void* stream) {
+  if (rows < 0 || cols <= 0) return AAR_EINVAL;
+  if (!dw || !db || cols > INT32_MAX) return AAR_EINVAL;
+  hipStream_t st = as_stream(stream);
+  if (rows == 0) {
+    int rc = aar_memset_zero(dw, cols * sizeof(float), stream);
+    if (rc == AAR_OK) rc = aar_memset_zero(db, cols * sizeof(float), stream);
+    return rc;
+  }
+  if (!gy || !x || !w || !mean || !rstd || !dx) return AAR_EINVAL;
+  const int parts = ln_bwd_parts(rows);
+  const size_t need = (size_t)parts * 2 * (size_t)cols * sizeof(float);
+  if (!workspace || workspace_bytes < need) return AAR_EWORKSPACE;
+  float* part = static_cast<float*>(workspace);
+  const bool vec = cols % 4 == 0 && aligned16(gy) && aligned16(x) && aligned16(w) &&
+                   aligned16(dx) && aligned16(workspace);
+  const RowPlan p = plan_rows(cols, vec);
+  int rc;
+  if (p.nv == 0) {
+    layernorm_bwd_wide_kernel<<<dim3((unsigned)rows), dim3(kThreads), 0, st>>>(gy, x, w, mean, rstd,
+                                                                                dx, cols);
+    rc = launch_status();
+    if (rc != AAR_OK) return rc;
+    layernorm_bwd_wide_cols_kernel<<<dim3((unsigned)ceil_div(cols, kThreads), (unsigned)parts),
+                                     dim3(kThreads), 0, st>>>(gy, x, mean, rstd, part, rows, cols);
+  } else {
+#define L(NV, W, V)                                                                           \
+  layernorm_bwd_kernel<NV, W, V><<<dim3(parts), dim3(kThreads), 0, st>>>(gy, x, w, mean, rstd, \
+                                                                         dx, part, rows,      \
+                                                                         (int)cols)
+    AAR_ROW_DISPATCH(p, L);
+#undef L
+  }
+  rc = launch_status();
+  if (rc != AAR_OK) return rc;
+  layernorm_bwd_reduce_kernel<<<dim3((unsigned)ceil_div(cols, 256)), dim3(256), 0, st>>>(
+      part, dw, db, parts, (int)cols);
+  return launch_status();
+}

@@ -1,0 +1,184 @@
+// pybind11 module aargrad._core for the MI355X backend.  Same module name,
+// classes, properties, function names, argument names and defaults as the
+// reference binding (cppsrc/python/binding.cpp:84-185); every op releases the
+// GIL.  Ops of the reference API that this build does not run on the GPU yet
+// are still bound and raise RuntimeError when called.
+#include <pybind11/numpy.h>
+#include <pybind11/pybind11.h>
+#include <pybind11/stl.h>
+
+#include <atomic>
+#include <cstring>
+#include <sstream>
+
+#include "aar_hip.h"
+#include "ops.hpp"
+#include "tensor.hpp"
+
+namespace py = pybind11;
+using namespace aar;
+using gil_release = py::call_guard<py::gil_scoped_release>;
+
+namespace {
+
+DType numpy_to_dtype(const py::dtype& dt) {
+  if (dt.is(py::dtype::of<float>())) return DType::Fp32;
+  if (dt.is(py::dtype::of<int64_t>())) return DType::Int64;
+  if (dt.kind() == 'f' && dt.itemsize() == 2) return DType::Fp16;
+  throw std::runtime_error("unsupported numpy dtype; expected float32, float16, or int64");
+}
+
+py::dtype dtype_to_numpy(DType d) {
+  switch (d) {
+    case DType::Fp32: return py::dtype::of<float>();
+    case DType::Fp16: return py::dtype("float16");
+    case DType::Int64: return py::dtype::of<int64_t>();
+    case DType::Bf16: throw std::runtime_error("bf16 has no numpy equivalent");
+  }
+  throw std::runtime_error("unknown dtype");
+}
+
+std::shared_ptr<Tensor> from_numpy(py::array arr, bool requires_grad) {
+  auto dt = numpy_to_dtype(arr.dtype());
+  py::array contig = py::array::ensure(arr, py::array::c_style);
+  std::vector<int64_t> shape(contig.shape(), contig.shape() + contig.ndim());
+  auto t = std::make_shared<Tensor>(Tensor::empty(shape, dt, Device::CPU));
+  t->set_requires_grad(requires_grad);
+  if (t->nbytes()) std::memcpy(t->data(), contig.data(), t->nbytes());
+  return t;
+}
+
+py::array to_numpy(const Tensor& t) {
+  if (t.device != Device::CPU) {
+    throw std::runtime_error("to_numpy requires CPU tensor; call .to(Device.CPU) first");
+  }
+  Tensor src = t.is_contiguous() ? t : contiguous(t);
+  std::vector<py::ssize_t> shape(src.shape.begin(), src.shape.end());
+  py::array out(dtype_to_numpy(src.dtype), shape);
+  if (src.nbytes()) std::memcpy(out.mutable_data(), src.data(), src.nbytes());
+  return out;
+}
+
+std::atomic<uint64_t> g_seed{0};
+
+[[noreturn]] void unavailable(const char* op, const Tensor& t) {
+  if (t.device == Device::CPU) throw_cpu_compute(op);
+  throw_not_on_device(op);
+}
+
+int device_count() {
+  int n = 0;
+  if (aar_device_count(&n) != AAR_OK) return 0;
+  return n;
+}
+
+}  // namespace
+
+PYBIND11_MODULE(_core, m) {
+  m.doc() = "aargrad core: fp32 tensors with autograd; compute on the MI355X (gfx950) GPU";
+
+  py::enum_<DType>(m, "DType")
+      .value("Fp32", DType::Fp32)
+      .value("Fp16", DType::Fp16)
+      .value("Bf16", DType::Bf16)
+      .value("Int64", DType::Int64);
+
+  py::enum_<Device>(m, "Device").value("CPU", Device::CPU).value("CUDA", Device::CUDA);
+
+  py::class_<Tensor, std::shared_ptr<Tensor>>(m, "Tensor")
+      .def_static("empty", &Tensor::empty, py::arg("shape"), py::arg("dtype"),
+                  py::arg("device") = Device::CPU, gil_release())
+      .def_static("zeros", &Tensor::zeros, py::arg("shape"), py::arg("dtype"),
+                  py::arg("device") = Device::CPU, gil_release())
+      .def_static("ones", &Tensor::ones, py::arg("shape"), py::arg("dtype"),
+                  py::arg("device") = Device::CPU, gil_release())
+      .def_readonly("shape", &Tensor::shape)
+      .def_readonly("strides", &Tensor::strides)
+      .def_readonly("storage_offset", &Tensor::storage_offset)
+      .def_readonly("dtype", &Tensor::dtype)
+      .def_readonly("device", &Tensor::device)
+      .def_property("requires_grad", [](const Tensor& t) { return t.requires_grad; },
+                    [](Tensor& t, bool r) { t.set_requires_grad(r); })
+      .def_property_readonly("is_leaf", &Tensor::is_leaf)
+      .def_property_readonly("numel", &Tensor::numel)
+      .def("is_contiguous", &Tensor::is_contiguous)
+      .def_property_readonly("grad", &Tensor::grad)
+      .def("to", &Tensor::to, py::arg("device"), gil_release())
+      .def("zero_grad", &Tensor::zero_grad, gil_release())
+      .def("backward", py::overload_cast<>(&Tensor::backward), gil_release())
+      .def("backward", py::overload_cast<const Tensor&>(&Tensor::backward), py::arg("grad_output"),
+           gil_release())
+      .def("__repr__", [](const Tensor& t) {
+        std::ostringstream s;
+        s << "Tensor(shape=[";
+        for (size_t i = 0; i < t.shape.size(); ++i) {
+          if (i) s << ", ";
+          s << t.shape[i];
+        }
+        s << "], dtype=" << dtype_name(t.dtype) << ", device=" << (t.device == Device::CPU ? "CPU" : "CUDA")
+          << ")";
+        return s.str();
+      });
+
+  m.def("from_numpy", &from_numpy, py::arg("array"), py::arg("requires_grad") = false);
+  m.def("to_numpy", &to_numpy, py::arg("tensor"));
+  m.def("cuda_synchronize", &device_synchronize, gil_release());
+
+  // Ops on the MI355X path.
+  m.def("add", &add, gil_release());
+  m.def("matmul", &matmul, gil_release());
+  m.def("matmul_a_bt", &matmul_a_bt, gil_release());
+  m.def("matmul_at_b", &matmul_at_b, gil_release());
+  m.def("softmax", &softmax, gil_release());
+  m.def("layernorm", &layernorm, py::arg("x"), py::arg("weight"), py::arg("bias"), py::arg("eps") = 1e-5f,
+        gil_release());
+  m.def("flash_attention", &flash_attention, py::arg("q"), py::arg("k"), py::arg("v"), py::arg("causal"),
+        gil_release());
+  m.def("reshape", &reshape, py::arg("x"), py::arg("shape"), gil_release());
+  m.def("transpose", &transpose, py::arg("x"), py::arg("dim_a"), py::arg("dim_b"), gil_release());
+  m.def("slice", &slice, py::arg("x"), py::arg("dim"), py::arg("start"), py::arg("end"), gil_release());
+  m.def("squeeze", &squeeze, py::arg("x"), py::arg("dim"), gil_release());
+  m.def("unsqueeze", &unsqueeze, py::arg("x"), py::arg("dim"), gil_release());
+  m.def("contiguous", &contiguous, py::arg("x"), gil_release());
+
+  // Reference API entries outside the MI355X hot path of this build.
+  m.def("sub", [](const Tensor& a, const Tensor&) -> Tensor { unavailable("sub", a); });
+  m.def("mul", [](const Tensor& a, const Tensor&) -> Tensor { unavailable("mul", a); });
+  m.def("relu", [](const Tensor& a) -> Tensor { unavailable("relu", a); });
+  m.def("gelu", [](const Tensor& a) -> Tensor { unavailable("gelu", a); });
+  m.def("sum_all", [](const Tensor& a) -> Tensor { unavailable("sum_all", a); });
+  m.def("add_bias", [](const Tensor& a, const Tensor&) -> Tensor { unavailable("add_bias", a); });
+  m.def("scale", [](const Tensor& x, float) -> Tensor { unavailable("scale", x); }, py::arg("x"),
+        py::arg("alpha"));
+  m.def("apply_causal_mask", [](const Tensor& x) -> Tensor { unavailable("apply_causal_mask", x); });
+  m.def("bmm", [](const Tensor& a, const Tensor&) -> Tensor { unavailable("bmm", a); });
+  m.def("bmm_a_bt", [](const Tensor& a, const Tensor&) -> Tensor { unavailable("bmm_a_bt", a); });
+  m.def("bmm_at_b", [](const Tensor& a, const Tensor&) -> Tensor { unavailable("bmm_at_b", a); });
+  m.def("embedding", [](const Tensor& w, const Tensor&) -> Tensor { unavailable("embedding", w); },
+        py::arg("weight"), py::arg("ids"));
+  m.def("cross_entropy",
+        [](const Tensor& l, const Tensor&, int64_t) -> Tensor { unavailable("cross_entropy", l); },
+        py::arg("logits"), py::arg("targets"), py::arg("ignore_index") = -100);
+  m.def("dropout", [](const Tensor& x, float) -> Tensor { unavailable("dropout", x); }, py::arg("x"),
+        py::arg("p"));
+  m.def("manual_seed", [](uint64_t seed) { g_seed.store(seed); }, py::arg("seed"));
+  m.def("scaled_add_inplace",
+        [](Tensor& dst, const Tensor&, float) { unavailable("scaled_add_inplace", dst); }, py::arg("dst"),
+        py::arg("src"), py::arg("alpha"));
+  m.def("adamw_step",
+        [](Tensor& p, const Tensor&, Tensor&, Tensor&, float, float, float, float, float, float, float) {
+          unavailable("adamw_step", p);
+        },
+        py::arg("param"), py::arg("grad"), py::arg("m"), py::arg("v"), py::arg("lr"), py::arg("beta1"),
+        py::arg("beta2"), py::arg("eps"), py::arg("weight_decay"), py::arg("bias_correction1"),
+        py::arg("bias_correction2"));
+
+  // Extensions of this build (not in the reference API).
+  m.def("_flash_attention_fwd", &flash_attention_fwd_lse, py::arg("q"), py::arg("k"), py::arg("v"),
+        py::arg("causal"), gil_release(),
+        "Forward flash attention returning (O, lse); lse = m + ln(l) per query row.");
+  m.def("_device_count", &device_count);
+  m.def("_empty_cache", &device_empty_cache, gil_release());
+  m.def("_memory_in_use", &device_bytes_in_use);
+  m.def("_memory_cached", &device_bytes_cached);
+}

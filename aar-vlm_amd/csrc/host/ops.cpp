@@ -1,0 +1,695 @@
+// Op layer of aargrad._core: validation, autograd Functions and dispatch to
+// the device kernels through the C ABI (include/aar_hip.h).
+//
+// Validation messages, exception types, contiguity handling, leading-dim
+// flattening and the Function graph follow the reference op files:
+//   matmul*      cppsrc/ops/matmul.cpp:93-257
+//   softmax      cppsrc/ops/softmax.cpp:57-96
+//   layernorm    cppsrc/ops/layernorm.cpp:136-227
+//   flash        cppsrc/ops/flash_attention.cpp:25-98
+//   views        cppsrc/ops/shape.cpp:99-374
+//   add          cppsrc/ops/elementwise.cpp:29-42, :225-231, :315-330
+// The device half replaces each reference *_cuda function; host tensors are
+// accepted by the view ops (metadata plus a host-side layout copy) but every
+// arithmetic op raises for Device.CPU: this build computes on the GPU only.
+#include "ops.hpp"
+
+#include <cmath>
+#include <cstring>
+
+#include "aar_hip.h"
+
+namespace aar {
+
+namespace {
+
+const float* fp(const Tensor& t) { return static_cast<const float*>(t.data()); }
+float* fp(Tensor& t) { return static_cast<float*>(t.data()); }
+
+Tensor as_view(const Tensor& src, std::vector<int64_t> new_shape) {
+  auto strides = compute_contiguous_strides(new_shape);
+  return make_view(src, std::move(new_shape), std::move(strides), src.storage_offset);
+}
+
+Tensor as_contig(const Tensor& t) { return t.is_contiguous() ? t : contiguous(t); }
+
+// ------------------------------------------------------------- layout copies
+
+void copy_strided_to_contiguous_host(const Tensor& src, Tensor& dst) {
+  const size_t ndim = src.shape.size();
+  const size_t total = src.numel();
+  if (total == 0) return;
+  const size_t es = dtype_size(src.dtype);
+  const char* X = static_cast<const char*>(src.data());
+  char* Y = static_cast<char*>(dst.data());
+  std::vector<int64_t> idx(ndim, 0);
+  for (size_t flat = 0; flat < total; ++flat) {
+    int64_t off = 0;
+    for (size_t d = 0; d < ndim; ++d) off += idx[d] * src.strides[d];
+    std::memcpy(Y + flat * es, X + off * (int64_t)es, es);
+    for (int d = (int)ndim - 1; d >= 0; --d) {
+      if (++idx[d] < src.shape[d]) break;
+      idx[d] = 0;
+    }
+  }
+}
+
+void device_strided_copy(const Tensor& src, Tensor& dst, const char* what) {
+  if (src.dtype != DType::Fp32) {
+    throw std::runtime_error(std::string(what) + ": only Fp32 supported on CUDA");
+  }
+  if (src.shape.size() > 8) throw std::runtime_error(std::string(what) + ": rank > 8");
+  check_status(aar_strided_copy_f32(fp(src), fp(dst), (int)src.shape.size(), src.shape.data(),
+                                    src.strides.data(), dst.strides.data(), current_stream()),
+               what);
+}
+
+void copy_contiguous_into_strided(const Tensor& src, Tensor& dst) {
+  if (src.shape != dst.shape) throw std::runtime_error("copy_contiguous_into_strided: shape mismatch");
+  if (src.dtype != dst.dtype || src.device != dst.device) {
+    throw std::runtime_error("copy_contiguous_into_strided: dtype/device mismatch");
+  }
+  if (!src.is_contiguous()) {
+    throw std::runtime_error("copy_contiguous_into_strided: src must be contiguous");
+  }
+  if (src.device == Device::CUDA) {
+    device_strided_copy(src, dst, "copy_contiguous_into_strided");
+    return;
+  }
+  // host: walk the destination view
+  const size_t ndim = src.shape.size();
+  const size_t total = src.numel();
+  if (total == 0) return;
+  const size_t es = dtype_size(src.dtype);
+  const char* X = static_cast<const char*>(src.data());
+  char* Y = static_cast<char*>(dst.data());
+  std::vector<int64_t> idx(ndim, 0);
+  for (size_t flat = 0; flat < total; ++flat) {
+    int64_t off = 0;
+    for (size_t d = 0; d < ndim; ++d) off += idx[d] * dst.strides[d];
+    std::memcpy(Y + off * (int64_t)es, X + flat * es, es);
+    for (int d = (int)ndim - 1; d >= 0; --d) {
+      if (++idx[d] < src.shape[d]) break;
+      idx[d] = 0;
+    }
+  }
+}
+
+std::vector<int64_t> resolve_new_shape(const std::vector<int64_t>& shape, size_t numel) {
+  std::vector<int64_t> out = shape;
+  int neg_pos = -1;
+  int64_t known = 1;
+  for (size_t i = 0; i < out.size(); ++i) {
+    if (out[i] == -1) {
+      if (neg_pos != -1) throw std::invalid_argument("reshape: at most one -1 dim allowed");
+      neg_pos = static_cast<int>(i);
+    } else if (out[i] < 0) {
+      throw std::invalid_argument("reshape: negative dim other than -1");
+    } else {
+      known *= out[i];
+    }
+  }
+  if (neg_pos == -1) {
+    int64_t prod = 1;
+    for (auto d : out) prod *= d;
+    if (static_cast<size_t>(prod) != numel) throw std::invalid_argument("reshape: numel mismatch");
+  } else {
+    if (known == 0 || numel % static_cast<size_t>(known) != 0) {
+      throw std::invalid_argument("reshape: cannot infer -1 dim");
+    }
+    out[neg_pos] = static_cast<int64_t>(numel) / known;
+  }
+  return out;
+}
+
+// ------------------------------------------------------------ view Functions
+
+class ReshapeFunction : public Function {
+ public:
+  std::vector<int64_t> original_shape;
+  std::vector<Tensor> backward(const Tensor& grad_output) override {
+    Tensor g = as_contig(grad_output);
+    return {make_view(g, original_shape, compute_contiguous_strides(original_shape), g.storage_offset)};
+  }
+  const char* name() const override { return "ReshapeFunction"; }
+};
+
+class TransposeFunction : public Function {
+ public:
+  int64_t dim_a = 0, dim_b = 0;
+  std::vector<Tensor> backward(const Tensor& grad_output) override {
+    std::vector<int64_t> sh = grad_output.shape, st = grad_output.strides;
+    std::swap(sh[dim_a], sh[dim_b]);
+    std::swap(st[dim_a], st[dim_b]);
+    return {as_contig(make_view(grad_output, sh, st, grad_output.storage_offset))};
+  }
+  const char* name() const override { return "TransposeFunction"; }
+};
+
+class SliceFunction : public Function {
+ public:
+  std::vector<int64_t> original_shape;
+  int64_t dim = 0, start = 0, end = 0;
+  DType dtype = DType::Fp32;
+  Device device = Device::CPU;
+  std::vector<Tensor> backward(const Tensor& grad_output) override {
+    Tensor full = Tensor::zeros(original_shape, dtype, device);
+    Tensor slot = make_view(full, grad_output.shape, full.strides,
+                            full.storage_offset + start * full.strides[dim]);
+    Tensor src = as_contig(grad_output);
+    copy_contiguous_into_strided(src, slot);
+    return {full};
+  }
+  const char* name() const override { return "SliceFunction"; }
+};
+
+class SqueezeFunction : public Function {
+ public:
+  int64_t dim = 0, inserted_size_stride = 1;
+  std::vector<Tensor> backward(const Tensor& grad_output) override {
+    std::vector<int64_t> sh = grad_output.shape, st = grad_output.strides;
+    sh.insert(sh.begin() + dim, 1);
+    st.insert(st.begin() + dim, inserted_size_stride);
+    return {as_contig(make_view(grad_output, sh, st, grad_output.storage_offset))};
+  }
+  const char* name() const override { return "SqueezeFunction"; }
+};
+
+class UnsqueezeFunction : public Function {
+ public:
+  int64_t dim = 0;
+  std::vector<Tensor> backward(const Tensor& grad_output) override {
+    std::vector<int64_t> sh = grad_output.shape, st = grad_output.strides;
+    sh.erase(sh.begin() + dim);
+    st.erase(st.begin() + dim);
+    return {as_contig(make_view(grad_output, sh, st, grad_output.storage_offset))};
+  }
+  const char* name() const override { return "UnsqueezeFunction"; }
+};
+
+class ContiguousFunction : public Function {
+ public:
+  std::vector<Tensor> backward(const Tensor& grad_output) override { return {as_contig(grad_output)}; }
+  const char* name() const override { return "ContiguousFunction"; }
+};
+
+// ------------------------------------------------------------------ GEMM
+
+Tensor gemm_device(int op, const Tensor& a, const Tensor& b, int64_t M, int64_t N, int64_t K) {
+  Tensor out = Tensor::empty({M, N}, DType::Fp32, Device::CUDA);
+  if (out.numel() == 0) return out;
+  const size_t wsb = aar_gemm_f32_workspace_bytes(op, M, N, K);
+  Workspace ws(wsb);
+  check_status(aar_gemm_f32(op, M, N, K, fp(a), fp(b), fp(out), ws.data(), ws.bytes(), current_stream()),
+               op == AAR_GEMM_NN ? "matmul" : (op == AAR_GEMM_NT ? "matmul_a_bt" : "matmul_at_b"));
+  return out;
+}
+
+// 2-D kernels (reference matmul_cuda / matmul_a_bt_cuda / matmul_at_b_cuda).
+Tensor matmul_2d(const Tensor& a, const Tensor& b) {
+  if (a.device == Device::CPU) throw_cpu_compute("matmul");
+  return gemm_device(AAR_GEMM_NN, a, b, a.shape[0], b.shape[1], a.shape[1]);
+}
+Tensor matmul_a_bt_2d(const Tensor& a, const Tensor& b) {
+  if (a.device == Device::CPU) throw_cpu_compute("matmul_a_bt");
+  return gemm_device(AAR_GEMM_NT, a, b, a.shape[0], b.shape[0], a.shape[1]);
+}
+Tensor matmul_at_b_2d(const Tensor& a, const Tensor& b) {
+  if (a.device == Device::CPU) throw_cpu_compute("matmul_at_b");
+  return gemm_device(AAR_GEMM_TN, a, b, a.shape[1], b.shape[1], a.shape[0]);
+}
+
+Tensor matmul_no_grad(const Tensor& a, const Tensor& b) {
+  if (a.shape.size() == 2) return matmul_2d(a, b);
+  const int64_t K = a.shape.back();
+  const int64_t N = b.shape[1];
+  const int64_t M_flat = K ? static_cast<int64_t>(a.numel()) / K : 0;
+  Tensor out2d = matmul_2d(as_view(a, {M_flat, K}), b);
+  std::vector<int64_t> out_shape(a.shape.begin(), a.shape.end() - 1);
+  out_shape.push_back(N);
+  return as_view(out2d, std::move(out_shape));
+}
+
+Tensor matmul_a_bt_no_grad(const Tensor& a, const Tensor& b) {
+  if (a.shape.size() == 2) return matmul_a_bt_2d(a, b);
+  const int64_t K = a.shape.back();
+  const int64_t N = b.shape[0];
+  const int64_t M_flat = K ? static_cast<int64_t>(a.numel()) / K : 0;
+  Tensor out2d = matmul_a_bt_2d(as_view(a, {M_flat, K}), b);
+  std::vector<int64_t> out_shape(a.shape.begin(), a.shape.end() - 1);
+  out_shape.push_back(N);
+  return as_view(out2d, std::move(out_shape));
+}
+
+Tensor matmul_at_b_no_grad(const Tensor& a, const Tensor& b) {
+  if (a.shape.size() == 2 && b.shape.size() == 2) return matmul_at_b_2d(a, b);
+  const int64_t M = a.shape.back();
+  const int64_t N = b.shape.back();
+  const int64_t K_flat = M ? static_cast<int64_t>(a.numel()) / M : 0;
+  return matmul_at_b_2d(as_view(a, {K_flat, M}), as_view(b, {K_flat, N}));
+}
+
+class MatmulFunction : public Function {
+ public:
+  Tensor saved_a, saved_b;
+  std::vector<Tensor> backward(const Tensor& g) override {
+    return {matmul_a_bt_no_grad(g, saved_b), matmul_at_b_no_grad(saved_a, g)};
+  }
+  const char* name() const override { return "MatmulFunction"; }
+};
+
+class MatmulABTFunction : public Function {
+ public:
+  Tensor saved_a, saved_b;
+  std::vector<Tensor> backward(const Tensor& g) override {
+    return {matmul_no_grad(g, saved_b), matmul_at_b_no_grad(g, saved_a)};
+  }
+  const char* name() const override { return "MatmulABTFunction"; }
+};
+
+class MatmulATBFunction : public Function {
+ public:
+  Tensor saved_a, saved_b;
+  std::vector<Tensor> backward(const Tensor& g) override {
+    return {matmul_a_bt_no_grad(saved_b, g), matmul_no_grad(saved_a, g)};
+  }
+  const char* name() const override { return "MatmulATBFunction"; }
+};
+
+template <typename Fn, typename NoGrad>
+Tensor with_matmul_grad(const Tensor& ac, const Tensor& bc, NoGrad no_grad) {
+  if (!ac.requires_grad && !bc.requires_grad) return no_grad(ac, bc);
+  auto fn = std::make_shared<Fn>();
+  fn->record_input(ac);
+  fn->record_input(bc);
+  fn->saved_a = ac;
+  fn->saved_b = bc;
+  Tensor out = no_grad(ac, bc);
+  out.requires_grad = true;
+  out.grad_fn = fn;
+  return out;
+}
+
+// -------------------------------------------------------------- softmax
+
+Tensor softmax_no_grad(const Tensor& x) {
+  if (x.device == Device::CPU) throw_cpu_compute("softmax");
+  Tensor out = Tensor::empty(x.shape, x.dtype, x.device);
+  const int64_t last = x.shape.back();
+  const int64_t outer = static_cast<int64_t>(x.numel()) / last;
+  check_status(aar_softmax_fwd_f32(fp(x), fp(out), outer, last, current_stream()), "softmax");
+  return out;
+}
+
+Tensor softmax_backward_no_grad(const Tensor& g, const Tensor& y) {
+  if (g.device == Device::CPU) throw_cpu_compute("softmax backward");
+  Tensor gc = as_contig(g);
+  Tensor dx = Tensor::empty(gc.shape, gc.dtype, gc.device);
+  const int64_t last = gc.shape.back();
+  const int64_t outer = static_cast<int64_t>(gc.numel()) / last;
+  check_status(aar_softmax_bwd_f32(fp(gc), fp(y), fp(dx), outer, last, current_stream()),
+               "softmax backward");
+  return dx;
+}
+
+class SoftmaxFunction : public Function {
+ public:
+  Tensor saved_y;
+  std::vector<Tensor> backward(const Tensor& g) override { return {softmax_backward_no_grad(g, saved_y)}; }
+  const char* name() const override { return "SoftmaxFunction"; }
+};
+
+// ------------------------------------------------------------- layernorm
+
+class LayerNormFunction : public Function {
+ public:
+  Tensor saved_x, saved_w, saved_mean, saved_rstd;
+  std::vector<Tensor> backward(const Tensor& grad_y) override {
+    if (saved_x.device == Device::CPU) throw_cpu_compute("layernorm backward");
+    Tensor gy = as_contig(grad_y);
+    Tensor dx = Tensor::empty(saved_x.shape, saved_x.dtype, saved_x.device);
+    Tensor dw = Tensor::empty(saved_w.shape, saved_w.dtype, saved_w.device);
+    Tensor db = Tensor::empty(saved_w.shape, saved_w.dtype, saved_w.device);
+    const int64_t last = saved_x.shape.back();
+    const int64_t outer = static_cast<int64_t>(saved_x.numel()) / last;
+    Workspace ws(aar_layernorm_bwd_workspace_bytes(outer, last));
+    check_status(aar_layernorm_bwd_f32(fp(gy), fp(saved_x), fp(saved_w), fp(saved_mean), fp(saved_rstd),
+                                       fp(dx), fp(dw), fp(db), outer, last, ws.data(), ws.bytes(),
+                                       current_stream()),
+                 "layernorm backward");
+    return {dx, dw, db};
+  }
+  const char* name() const override { return "LayerNormFunction"; }
+};
+
+// ------------------------------------------------------------- attention
+
+class FlashAttentionFunction : public Function {
+ public:
+  Tensor saved_q, saved_k, saved_v, saved_o, saved_lse;
+  bool causal = false;
+  float scale_factor = 1.0f;
+  std::vector<Tensor> backward(const Tensor& grad_output) override {
+    Tensor go = as_contig(grad_output);
+    Tensor dq = Tensor::empty(saved_q.shape, saved_q.dtype, saved_q.device);
+    Tensor dk = Tensor::empty(saved_k.shape, saved_k.dtype, saved_k.device);
+    Tensor dv = Tensor::empty(saved_v.shape, saved_v.dtype, saved_v.device);
+    const int64_t d = saved_q.shape.back();
+    const int64_t T = saved_q.shape[saved_q.shape.size() - 2];
+    const int64_t bh = T * d ? static_cast<int64_t>(saved_q.numel()) / (T * d) : 0;
+    Workspace ws(aar_flash_bwd_workspace_bytes(bh, T, d));
+    check_status(aar_flash_bwd_f32(fp(saved_q), fp(saved_k), fp(saved_v), fp(saved_o), fp(saved_lse),
+                                   fp(go), fp(dq), fp(dk), fp(dv), bh, T, d, causal ? 1 : 0,
+                                   scale_factor, ws.data(), ws.bytes(), current_stream()),
+                 "flash_attention backward");
+    return {dq, dk, dv};
+  }
+  const char* name() const override { return "FlashAttentionFunction"; }
+};
+
+void flash_check(const Tensor& q, const Tensor& k, const Tensor& v) {
+  if (q.dtype != DType::Fp32 || k.dtype != DType::Fp32 || v.dtype != DType::Fp32) {
+    throw std::invalid_argument("flash_attention: only Fp32 supported");
+  }
+  if (q.device != k.device || q.device != v.device) {
+    throw std::invalid_argument("flash_attention: device mismatch");
+  }
+  if (q.shape.size() < 3 || k.shape.size() < 3 || v.shape.size() < 3) {
+    throw std::invalid_argument("flash_attention: need at least 3 dims [..., T, d]");
+  }
+  if (q.shape != k.shape || q.shape != v.shape) {
+    throw std::invalid_argument("flash_attention: q, k, v must share shape");
+  }
+}
+
+// Forward on contiguous inputs; returns (O, lse).
+std::tuple<Tensor, Tensor> flash_forward_device(const Tensor& qc, const Tensor& kc, const Tensor& vc,
+                                                bool causal, float s) {
+  const int64_t d = qc.shape.back();
+  if (d > 128) throw std::invalid_argument("flash_attention: d_head exceeds D_MAX (128)");
+  const int64_t T = qc.shape[qc.shape.size() - 2];
+  std::vector<int64_t> lse_shape(qc.shape.begin(), qc.shape.end() - 1);
+  Tensor out = Tensor::empty(qc.shape, qc.dtype, qc.device);
+  Tensor lse = Tensor::empty(lse_shape, qc.dtype, qc.device);
+  const int64_t bh = T * d ? static_cast<int64_t>(qc.numel()) / (T * d) : 0;
+  check_status(aar_flash_fwd_f32(fp(qc), fp(kc), fp(vc), fp(out), fp(lse), bh, T, d, causal ? 1 : 0, s,
+                                 current_stream()),
+               "flash_attention");
+  return {out, lse};
+}
+
+// ------------------------------------------------------------------ add
+
+void check_binary(const Tensor& a, const Tensor& b, const char* op) {
+  if (a.shape != b.shape) throw std::invalid_argument(std::string(op) + ": shape mismatch");
+  if (a.dtype != b.dtype) throw std::invalid_argument(std::string(op) + ": dtype mismatch");
+  if (a.device != b.device) throw std::invalid_argument(std::string(op) + ": device mismatch");
+  if (a.dtype != DType::Fp32) throw std::invalid_argument(std::string(op) + ": only Fp32 supported");
+}
+
+class AddFunction : public Function {
+ public:
+  std::vector<Tensor> backward(const Tensor& g) override { return {g, g}; }
+  const char* name() const override { return "AddFunction"; }
+};
+
+Tensor add_no_grad(const Tensor& a, const Tensor& b) {
+  if (a.device == Device::CPU) throw_cpu_compute("add");
+  Tensor out = Tensor::empty(a.shape, a.dtype, a.device);
+  check_status(aar_add_f32(fp(a), fp(b), fp(out), (int64_t)a.numel(), current_stream()), "add");
+  return out;
+}
+
+}  // namespace
+
+// ======================================================================= API
+
+Tensor make_view(const Tensor& src, std::vector<int64_t> shape, std::vector<int64_t> strides,
+                 int64_t storage_offset) {
+  Tensor v;
+  v.shape = std::move(shape);
+  v.strides = std::move(strides);
+  v.storage_offset = storage_offset;
+  v.dtype = src.dtype;
+  v.device = src.device;
+  v.storage = src.storage;
+  return v;
+}
+
+void copy_strided_to_contiguous(const Tensor& src, Tensor& dst) {
+  if (src.shape != dst.shape) throw std::runtime_error("copy_strided_to_contiguous: shape mismatch");
+  if (src.dtype != dst.dtype || src.device != dst.device) {
+    throw std::runtime_error("copy_strided_to_contiguous: dtype/device mismatch");
+  }
+  if (!dst.is_contiguous()) throw std::runtime_error("copy_strided_to_contiguous: dst must be contiguous");
+  if (src.device == Device::CUDA) {
+    device_strided_copy(src, dst, "copy_strided_to_contiguous");
+    return;
+  }
+  copy_strided_to_contiguous_host(src, dst);
+}
+
+Tensor contiguous(const Tensor& x) {
+  if (x.is_contiguous()) return x;
+  Tensor out = Tensor::empty(x.shape, x.dtype, x.device);
+  copy_strided_to_contiguous(x, out);
+  if (!x.requires_grad) return out;
+  auto fn = std::make_shared<ContiguousFunction>();
+  fn->record_input(x);
+  out.requires_grad = true;
+  out.grad_fn = fn;
+  return out;
+}
+
+Tensor reshape(const Tensor& x, std::vector<int64_t> new_shape) {
+  auto resolved = resolve_new_shape(new_shape, x.numel());
+  Tensor src = as_contig(x);
+  Tensor out = make_view(src, resolved, compute_contiguous_strides(resolved), src.storage_offset);
+  if (!x.requires_grad) return out;
+  auto fn = std::make_shared<ReshapeFunction>();
+  fn->record_input(x);
+  fn->original_shape = x.shape;
+  out.requires_grad = true;
+  out.grad_fn = fn;
+  return out;
+}
+
+Tensor transpose(const Tensor& x, int64_t dim_a, int64_t dim_b) {
+  const int64_t ndim = static_cast<int64_t>(x.shape.size());
+  if (dim_a < 0 || dim_a >= ndim || dim_b < 0 || dim_b >= ndim) {
+    throw std::invalid_argument("transpose: dim out of range");
+  }
+  std::vector<int64_t> sh = x.shape, st = x.strides;
+  std::swap(sh[dim_a], sh[dim_b]);
+  std::swap(st[dim_a], st[dim_b]);
+  Tensor out = make_view(x, sh, st, x.storage_offset);
+  if (!x.requires_grad) return out;
+  auto fn = std::make_shared<TransposeFunction>();
+  fn->record_input(x);
+  fn->dim_a = dim_a;
+  fn->dim_b = dim_b;
+  out.requires_grad = true;
+  out.grad_fn = fn;
+  return out;
+}
+
+Tensor slice(const Tensor& x, int64_t dim, int64_t start, int64_t end) {
+  const int64_t ndim = static_cast<int64_t>(x.shape.size());
+  if (dim < 0 || dim >= ndim) throw std::invalid_argument("slice: dim out of range");
+  if (start < 0 || end > x.shape[dim] || start >= end) throw std::invalid_argument("slice: invalid range");
+  std::vector<int64_t> sh = x.shape;
+  sh[dim] = end - start;
+  Tensor out = make_view(x, sh, x.strides, x.storage_offset + start * x.strides[dim]);
+  if (!x.requires_grad) return out;
+  auto fn = std::make_shared<SliceFunction>();
+  fn->record_input(x);
+  fn->original_shape = x.shape;
+  fn->dim = dim;
+  fn->start = start;
+  fn->end = end;
+  fn->dtype = x.dtype;
+  fn->device = x.device;
+  out.requires_grad = true;
+  out.grad_fn = fn;
+  return out;
+}
+
+Tensor squeeze(const Tensor& x, int64_t dim) {
+  const int64_t ndim = static_cast<int64_t>(x.shape.size());
+  if (dim < 0 || dim >= ndim) throw std::invalid_argument("squeeze: dim out of range");
+  if (x.shape[dim] != 1) throw std::invalid_argument("squeeze: dim size must be 1");
+  std::vector<int64_t> sh = x.shape, st = x.strides;
+  const int64_t inserted_stride = st[dim];
+  sh.erase(sh.begin() + dim);
+  st.erase(st.begin() + dim);
+  Tensor out = make_view(x, sh, st, x.storage_offset);
+  if (!x.requires_grad) return out;
+  auto fn = std::make_shared<SqueezeFunction>();
+  fn->record_input(x);
+  fn->dim = dim;
+  fn->inserted_size_stride = inserted_stride;
+  out.requires_grad = true;
+  out.grad_fn = fn;
+  return out;
+}
+
+Tensor unsqueeze(const Tensor& x, int64_t dim) {
+  const int64_t ndim = static_cast<int64_t>(x.shape.size());
+  if (dim < 0 || dim > ndim) throw std::invalid_argument("unsqueeze: dim out of range");
+  std::vector<int64_t> sh = x.shape, st = x.strides;
+  const int64_t new_stride = (dim < ndim) ? x.strides[dim] * x.shape[dim] : 1;
+  sh.insert(sh.begin() + dim, 1);
+  st.insert(st.begin() + dim, new_stride);
+  Tensor out = make_view(x, sh, st, x.storage_offset);
+  if (!x.requires_grad) return out;
+  auto fn = std::make_shared<UnsqueezeFunction>();
+  fn->record_input(x);
+  fn->dim = dim;
+  out.requires_grad = true;
+  out.grad_fn = fn;
+  return out;
+}
+
+Tensor matmul(const Tensor& a, const Tensor& b) {
+  if (a.shape.size() < 2 || b.shape.size() != 2) {
+    throw std::invalid_argument("matmul: LHS rank must be >= 2 and RHS must be 2D");
+  }
+  if (a.dtype != b.dtype) throw std::invalid_argument("matmul: dtype mismatch");
+  if (a.device != b.device) throw std::invalid_argument("matmul: device mismatch");
+  if (a.dtype != DType::Fp32) throw std::invalid_argument("matmul: only Fp32 supported");
+  if (b.shape[0] != a.shape.back()) throw std::invalid_argument("matmul: inner dimensions mismatch");
+  return with_matmul_grad<MatmulFunction>(as_contig(a), as_contig(b), matmul_no_grad);
+}
+
+Tensor matmul_a_bt(const Tensor& a, const Tensor& b) {
+  if (a.shape.size() < 2 || b.shape.size() != 2) {
+    throw std::invalid_argument("matmul_a_bt: LHS rank must be >= 2 and RHS must be 2D");
+  }
+  if (a.dtype != b.dtype || a.device != b.device) {
+    throw std::invalid_argument("matmul_a_bt: dtype/device mismatch");
+  }
+  if (a.dtype != DType::Fp32) throw std::invalid_argument("matmul_a_bt: only Fp32 supported");
+  if (a.shape.back() != b.shape[1]) throw std::invalid_argument("matmul_a_bt: contraction dim mismatch");
+  return with_matmul_grad<MatmulABTFunction>(as_contig(a), as_contig(b), matmul_a_bt_no_grad);
+}
+
+Tensor matmul_at_b(const Tensor& a, const Tensor& b) {
+  if (a.shape.size() != 2 || b.shape.size() != 2) {
+    throw std::invalid_argument("matmul_at_b: inputs must be 2D");
+  }
+  if (a.dtype != b.dtype || a.device != b.device) {
+    throw std::invalid_argument("matmul_at_b: dtype/device mismatch");
+  }
+  if (a.dtype != DType::Fp32) throw std::invalid_argument("matmul_at_b: only Fp32 supported");
+  if (a.shape[0] != b.shape[0]) throw std::invalid_argument("matmul_at_b: contraction dim mismatch");
+  return with_matmul_grad<MatmulATBFunction>(as_contig(a), as_contig(b), matmul_at_b_no_grad);
+}
+
+Tensor softmax(const Tensor& x) {
+  if (x.shape.empty()) throw std::invalid_argument("softmax: input must have at least 1 dim");
+  if (x.dtype != DType::Fp32) throw std::invalid_argument("softmax: only Fp32 supported");
+  if (x.shape.back() == 0) throw std::invalid_argument("softmax: last dim must be > 0");
+  Tensor xc = as_contig(x);
+  if (!xc.requires_grad) return softmax_no_grad(xc);
+  auto fn = std::make_shared<SoftmaxFunction>();
+  fn->record_input(xc);
+  Tensor out = softmax_no_grad(xc);
+  fn->saved_y = out;
+  out.requires_grad = true;
+  out.grad_fn = fn;
+  return out;
+}
+
+Tensor layernorm(const Tensor& x, const Tensor& weight, const Tensor& bias, float eps) {
+  if (x.shape.empty()) throw std::invalid_argument("layernorm: input must have at least 1 dim");
+  if (x.dtype != DType::Fp32) throw std::invalid_argument("layernorm: only Fp32 supported");
+  const int64_t last = x.shape.back();
+  if (last == 0) throw std::invalid_argument("layernorm: last dim must be > 0");
+  if (weight.shape.size() != 1 || weight.shape[0] != last) {
+    throw std::invalid_argument("layernorm: weight must be 1D matching last dim");
+  }
+  if (bias.shape.size() != 1 || bias.shape[0] != last) {
+    throw std::invalid_argument("layernorm: bias must be 1D matching last dim");
+  }
+  if (weight.dtype != DType::Fp32 || bias.dtype != DType::Fp32) {
+    throw std::invalid_argument("layernorm: weight/bias must be Fp32");
+  }
+  if (x.device != weight.device || x.device != bias.device) {
+    throw std::invalid_argument("layernorm: device mismatch");
+  }
+  if (eps <= 0.0f) throw std::invalid_argument("layernorm: eps must be > 0");
+
+  Tensor xc = as_contig(x), wc = as_contig(weight), bc = as_contig(bias);
+  if (xc.device == Device::CPU) throw_cpu_compute("layernorm");
+  const int64_t outer = static_cast<int64_t>(xc.numel()) / last;
+  Tensor y = Tensor::empty(xc.shape, xc.dtype, xc.device);
+  if (!xc.requires_grad && !wc.requires_grad && !bc.requires_grad) {
+    check_status(aar_layernorm_fwd_f32(fp(xc), fp(wc), fp(bc), fp(y), nullptr, nullptr, outer, last, eps,
+                                       current_stream()),
+                 "layernorm");
+    return y;
+  }
+  Tensor mean = Tensor::empty({outer}, xc.dtype, xc.device);
+  Tensor rstd = Tensor::empty({outer}, xc.dtype, xc.device);
+  check_status(aar_layernorm_fwd_f32(fp(xc), fp(wc), fp(bc), fp(y), fp(mean), fp(rstd), outer, last, eps,
+                                     current_stream()),
+               "layernorm");
+  auto fn = std::make_shared<LayerNormFunction>();
+  fn->record_input(xc);
+  fn->record_input(wc);
+  fn->record_input(bc);
+  fn->saved_x = xc;
+  fn->saved_w = wc;
+  fn->saved_mean = mean;
+  fn->saved_rstd = rstd;
+  y.requires_grad = true;
+  y.grad_fn = fn;
+  return y;
+}
+
+Tensor flash_attention(const Tensor& q, const Tensor& k, const Tensor& v, bool causal) {
+  flash_check(q, k, v);
+  Tensor qc = as_contig(q), kc = as_contig(k), vc = as_contig(v);
+  if (qc.device == Device::CPU) throw_cpu_compute("flash_attention");
+  const float s = 1.0f / std::sqrt(static_cast<float>(qc.shape.back()));
+  auto [out, lse] = flash_forward_device(qc, kc, vc, causal, s);
+  if (!qc.requires_grad && !kc.requires_grad && !vc.requires_grad) return out;
+  auto fn = std::make_shared<FlashAttentionFunction>();
+  fn->record_input(qc);
+  fn->record_input(kc);
+  fn->record_input(vc);
+  fn->saved_q = qc;
+  fn->saved_k = kc;
+  fn->saved_v = vc;
+  fn->saved_o = out;
+  fn->saved_lse = lse;
+  fn->causal = causal;
+  fn->scale_factor = s;
+  out.requires_grad = true;
+  out.grad_fn = fn;
+  return out;
+}
+
+std::tuple<Tensor, Tensor> flash_attention_fwd_lse(const Tensor& q, const Tensor& k, const Tensor& v,
+                                                   bool causal) {
+  flash_check(q, k, v);
+  Tensor qc = as_contig(q), kc = as_contig(k), vc = as_contig(v);
+  if (qc.device == Device::CPU) throw_cpu_compute("flash_attention");
+  const float s = 1.0f / std::sqrt(static_cast<float>(qc.shape.back()));
+  return flash_forward_device(qc, kc, vc, causal, s);
+}
+
+Tensor add(const Tensor& a, const Tensor& b) {
+  check_binary(a, b, "add");
+  Tensor ac = as_contig(a), bc = as_contig(b);
+  if (!ac.requires_grad && !bc.requires_grad) return add_no_grad(ac, bc);
+  auto fn = std::make_shared<AddFunction>();
+  fn->record_input(ac);
+  fn->record_input(bc);
+  Tensor out = add_no_grad(ac, bc);
+  out.requires_grad = true;
+  out.grad_fn = fn;
+  return out;
+}
+
+}  // namespace aar

@@ -1,0 +1,39 @@
+// Public ops of aargrad._core (same names, argument meaning and exceptions as
+// the reference's namespace-vlm functions bound in cppsrc/python/binding.cpp).
+#pragma once
+
+#include <tuple>
+
+#include "tensor.hpp"
+
+namespace aar {
+
+// Views and layout (cppsrc/ops/shape.cpp:99-374).
+Tensor contiguous(const Tensor& x);
+Tensor reshape(const Tensor& x, std::vector<int64_t> new_shape);
+Tensor transpose(const Tensor& x, int64_t dim_a, int64_t dim_b);
+Tensor slice(const Tensor& x, int64_t dim, int64_t start, int64_t end);
+Tensor squeeze(const Tensor& x, int64_t dim);
+Tensor unsqueeze(const Tensor& x, int64_t dim);
+
+// GEMM (cppsrc/ops/matmul.cpp:169-257).
+Tensor matmul(const Tensor& a, const Tensor& b);
+Tensor matmul_a_bt(const Tensor& a, const Tensor& b);
+Tensor matmul_at_b(const Tensor& a, const Tensor& b);
+
+// Row-wise (cppsrc/ops/softmax.cpp:75-96, cppsrc/ops/layernorm.cpp:174-227).
+Tensor softmax(const Tensor& x);
+Tensor layernorm(const Tensor& x, const Tensor& weight, const Tensor& bias, float eps);
+
+// Attention (cppsrc/ops/flash_attention.cpp:65-98).
+Tensor flash_attention(const Tensor& q, const Tensor& k, const Tensor& v, bool causal);
+// Forward returning (O, lse) for benchmarks and parity checks; no autograd node.
+std::tuple<Tensor, Tensor> flash_attention_fwd_lse(const Tensor& q, const Tensor& k, const Tensor& v,
+                                                   bool causal);
+
+// Elementwise (cppsrc/ops/elementwise.cpp:315-330) and gradient fan-in
+// (cppsrc/autograd/backward.cpp:17-36).
+Tensor add(const Tensor& a, const Tensor& b);
+Tensor add_grads(const Tensor& a, const Tensor& b);
+
+}  // namespace aar

@@ -1,0 +1,262 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X aargrad backend on BASELINE.json's headline metric:
+fp32 matmul TFLOPS at 4096^3 (fraction of the 157.3 TFLOP/s fp32 MFMA peak),
+plus causal flash-attention fwd+bwd TFLOPS (B8 H12 T4096 d64).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+
+A step is one C = A.B at M=N=K=4096 (BASELINE config 2's square 4096 point,
+A, B ~ N(0,1)/sqrt(K), synthetic, resident in HBM), issued through the product
+path: aargrad.matmul -> aargrad._core -> aar_gemm_f32 (C ABI) -> the gfx950
+MFMA kernel, all ordered on the null stream.  W untimed steps, then exactly K
+timed steps bracketed by device synchronisation; HIP events recorded on that
+same stream time the region.  One GPU only: --gpus N > 1 exits with a message.
+
+Prints ONE JSON line on stdout; a human-readable summary goes to stderr.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import platform
+import subprocess
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+REPO = Path(__file__).resolve().parent
+sys.path.insert(0, str(REPO / "aar-vlm_amd"))
+
+PEAK_FP32_MFMA_TFLOPS = 157.3  # MI355X dense fp32 matrix peak
+PEAK_HBM_GBS = 8000.0
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+class Events:
+    """HIP events through the C ABI, recorded on the null stream (the stream
+    every aargrad op is enqueued on)."""
+
+    def __init__(self):
+        self.L = ctypes.CDLL(str(REPO / "aar-vlm_amd" / "aargrad" / "libaar_hip.so"))
+        vp = ctypes.c_void_p
+        self.L.aar_event_create.argtypes = [ctypes.POINTER(vp)]
+        self.L.aar_event_record.argtypes = [vp, vp]
+        self.L.aar_event_elapsed_ms.argtypes = [ctypes.POINTER(ctypes.c_float), vp, vp]
+        self.L.aar_event_destroy.argtypes = [vp]
+        self.a, self.b = vp(), vp()
+        assert self.L.aar_event_create(ctypes.byref(self.a)) == 0
+        assert self.L.aar_event_create(ctypes.byref(self.b)) == 0
+
+    def start(self):
+        self.L.aar_event_record(self.a, None)
+
+    def stop_ms(self):
+        self.L.aar_event_record(self.b, None)
+        ms = ctypes.c_float()
+        assert self.L.aar_event_elapsed_ms(ctypes.byref(ms), self.a, self.b) == 0
+        return float(ms.value)
+
+
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def load_traffic(name: str):
+    """HBM bytes per launch measured by rocprofv3 --pmc (FETCH_SIZE +
+    WRITE_SIZE, scaled by the copy-kernel calibration), committed under
+    profiles/ as JSON; None when not measured."""
+    p = REPO / "profiles" / f"{name}_traffic.json"
+    if not p.exists():
+        return None
+    try:
+        return float(json.loads(p.read_text())["hbm_bytes_per_launch"])
+    except (KeyError, ValueError):
+        return None
+
+
+def bench_matmul(ag, steps: int, warmup: int, ev: Events):
+    n = 4096
+    rng = np.random.default_rng(0)
+    a = (rng.standard_normal((n, n)) / np.sqrt(n)).astype(np.float32)
+    b = (rng.standard_normal((n, n)) / np.sqrt(n)).astype(np.float32)
+    ta = ag.from_numpy(a).to(ag.Device.CUDA)
+    tb = ag.from_numpy(b).to(ag.Device.CUDA)
+    for _ in range(warmup):
+        ag.matmul(ta, tb)
+    ag.cuda_synchronize()
+    t0 = time.perf_counter()
+    ev.start()
+    for _ in range(steps):
+        c = ag.matmul(ta, tb)
+    ms = ev.stop_ms()
+    ag.cuda_synchronize()
+    wall = time.perf_counter() - t0
+    # spot-check the timed output (rows sampled, float64 closed form)
+    ch = ag.to_numpy(c.to(ag.Device.CPU))
+    rows = rng.choice(n, 8, replace=False)
+    ref = a[rows].astype(np.float64) @ b.astype(np.float64)
+    err = float(np.abs(ch[rows] - ref).max() / max(np.abs(ref).max(), 1.0))
+    if not err <= 1e-4 * np.sqrt(n):
+        raise SystemExit(f"bench: matmul result check failed (err {err:.3e})")
+    return ms / steps, wall, err, (a, b)
+
+
+def bench_flash(ag, steps: int, warmup: int, ev: Events, T: int = 4096):
+    B, H, d = 8, 12, 64
+    rng = np.random.default_rng(0)
+    q, k, v, do = (rng.standard_normal((B, H, T, d)).astype(np.float32) for _ in range(4))
+    tq, tk, tv = (ag.from_numpy(x).to(ag.Device.CUDA) for x in (q, k, v))
+    tdo = ag.from_numpy(do).to(ag.Device.CUDA)
+    for t in (tq, tk, tv):
+        t.requires_grad = True
+
+    def step():
+        o = ag.flash_attention(tq, tk, tv, True)
+        o.backward(tdo)
+        for t in (tq, tk, tv):
+            t.zero_grad()
+        return o
+
+    for _ in range(warmup):
+        step()
+    ag.cuda_synchronize()
+    ev.start()
+    for _ in range(steps):
+        step()
+    ms = ev.stop_ms() / steps
+    ag.cuda_synchronize()
+    fwd_flops = 4.0 * B * H * T * T * d / 2.0
+    return ms, 3.5 * fwd_flops
+
+
+def cpu_baseline_matmul(ab, budget_s: float = 12.0):
+    """The reference CPU path (oracle/_ref: the reference's own matmul built
+    from its sources; else the C restatement) on one core, on a row band of
+    the same 4096^3 product, extrapolated to the full product."""
+    import oracle
+
+    a, b = ab
+    n = a.shape[0]
+    use_ref = oracle.ref_available()
+    kind = "reference" if use_ref else "port"
+
+    def run(rows):
+        if use_ref:
+            oracle.ref_matmul("nn", np.ascontiguousarray(a[:rows]), b)
+        else:
+            oracle.matmul("nn", a, b, rows=(0, rows))
+
+    run(2)  # warm caches / page in
+    t0 = time.perf_counter()
+    run(4)
+    per_row = (time.perf_counter() - t0) / 4
+    rows = int(max(8, min(n, budget_s / max(per_row, 1e-6))))
+    t0 = time.perf_counter()
+    run(rows)
+    t = time.perf_counter() - t0
+    tflops = 2.0 * rows * n * n / t / 1e12
+    return {
+        "value": tflops,
+        "unit": "TFLOPS",
+        "cores": 1,
+        "kind": kind,
+        "sample": f"{rows}-row band of the 4096^3 fp32 matmul (naive i-j-k reference loop, {t:.1f} s; "
+                  f"full product extrapolates to {t * n / rows:.0f} s); host {cpu_model()}, "
+                  f"{os.cpu_count()} cores visible, 1 used",
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--flash-steps", type=int, default=5)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build targets one GPU; --gpus {args.gpus} is not supported "
+              "(the hot path is single-GPU; sharding is described in DESIGN.md)", file=sys.stderr)
+        return 2
+
+    import aargrad as ag
+
+    if not ag.device_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        return 1
+    ev = Events()
+
+    step_ms, wall, err, ab = bench_matmul(ag, args.steps, args.warmup, ev)
+    n = 4096
+    flops = 2.0 * n ** 3
+    tflops = flops / (step_ms * 1e-3) / 1e12
+    log(f"matmul 4096^3: {step_ms:.4f} ms/step, {tflops:.2f} TFLOPS "
+        f"({100 * tflops / PEAK_FP32_MFMA_TFLOPS:.1f}% of fp32 MFMA peak), check err {err:.2e}")
+
+    fa_ms, fa_flops = bench_flash(ag, args.flash_steps, 2, ev)
+    fa_tflops = fa_flops / (fa_ms * 1e-3) / 1e12
+    log(f"flash causal B8 H12 T4096 d64 fwd+bwd: {fa_ms:.3f} ms, {fa_tflops:.2f} TFLOPS "
+        f"({100 * fa_tflops / PEAK_FP32_MFMA_TFLOPS:.1f}%)")
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline_matmul(ab)
+        log(f"cpu baseline ({cpu['kind']}): {cpu['value'] * 1e3:.3f} GFLOPS on 1 core")
+
+    out = {
+        "metric": "fp32 matmul TFLOPS @4096^3 (% of FP32 MFMA peak) + flash-attn fwd+bwd TFLOPS",
+        "value": round(tflops, 3),
+        "unit": "TFLOPS",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(step_ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (A, B ~ N(0,1)/sqrt(K) from seed 0, resident in HBM)",
+        "config": {
+            "workload": "fp32 matmul C=A.B, M=N=K=4096 (BASELINE config 2 square point)",
+            "op": "matmul (NN)",
+            "M": n, "N": n, "K": n,
+            "flops_per_step": flops,
+        },
+        "pct_of_fp32_mfma_peak": round(100 * tflops / PEAK_FP32_MFMA_TFLOPS, 2),
+        "flash_attn_fwd_bwd": {
+            "tflops": round(fa_tflops, 3),
+            "pct_of_fp32_mfma_peak": round(100 * fa_tflops / PEAK_FP32_MFMA_TFLOPS, 2),
+            "ms_per_step": round(fa_ms, 4),
+            "config": "causal, B8 H12 T4096 d64, fwd+bwd, flops = 3.5 * 4*B*H*T^2*d/2",
+        },
+        "roofline": {
+            "bound": "mfma",
+            "achieved": round(tflops, 3),
+            "peak": PEAK_FP32_MFMA_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(tflops / PEAK_FP32_MFMA_TFLOPS, 4),
+            "traffic": load_traffic("gemm_f32_nn_4096"),
+            "kernel": "gemm_f32_kernel<256,256,16,128,128,NN> (one launch per step)",
+            "algorithmic_flops_per_launch": flops,
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,166 @@
+/*
+ * aar_hip.h — C ABI of the MI355X (gfx950) device backend for aargrad.
+ *
+ * Plain C: pointers, sizes, an opaque stream handle (hipStream_t passed as
+ * void*; NULL is the null stream) and an int status.  No C++ or torch types.
+ *
+ * Contract for every entry point:
+ *   - Returns AAR_OK (0) on success.  A positive value is a hipError_t code;
+ *     a negative value is one of the AAR_E* codes below.
+ *     aar_error_string() turns either into text.
+ *   - Never allocates an output.  Inputs are borrowed and outputs are written
+ *     in place; the caller owns all memory.  Entry points that need scratch
+ *     memory take an explicit workspace and expose its size through a
+ *     *_workspace_bytes() query.
+ *   - All work is enqueued on `stream` and returns without waiting; results are
+ *     visible to the host after aar_stream_synchronize()/aar_synchronize() or a
+ *     device-to-host copy.
+ *   - fp32 tensors are dense row-major (C-contiguous).
+ *
+ * Each declaration names the reference (AARONKANG04/aar-vlm) interface it
+ * replaces, as file:line under the reference tree.
+ */
+#ifndef AAR_HIP_H
+#define AAR_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define AAR_OK 0
+#define AAR_EINVAL (-1)        /* bad shape / argument (maps to std::invalid_argument) */
+#define AAR_EWORKSPACE (-2)    /* workspace pointer NULL or too small */
+#define AAR_EUNSUPPORTED (-3)  /* shape outside what the kernels implement */
+#define AAR_ENOMEM (-4)        /* device allocation failed (maps to std::bad_alloc) */
+
+/* ---------------------------------------------------------------- runtime */
+
+/* Text for a status returned by any aar_* call (static storage). */
+const char* aar_error_string(int status);
+
+/* Number of visible GPUs.  Replaces the implicit lazy CUDA init that the
+ * reference probes with Tensor::zeros(..., CUDA) (tests/python/test_flash_attention.py:8-13). */
+int aar_device_count(int* count);
+
+/* Device properties used by launch heuristics and roofline reporting. */
+int aar_device_info(int* cu_count, int* clock_khz, int* lds_bytes_per_cu,
+                    char* arch_name, int arch_name_len);
+
+/* Device allocation (AAR_ENOMEM when the device is out of memory).  Replaces
+ * CUDAAllocator::alloc/free (cppsrc/core/cuda_allocator.cpp:8-22). */
+int aar_malloc(void** ptr, size_t bytes);
+int aar_free(void* ptr);
+
+/* Copies.  Replaces copy_bytes (cppsrc/core/cuda_copy.hpp:8-10).
+ * kind: 1 = host->device, 2 = device->host, 3 = device->device.
+ * Host<->device copies are synchronous with respect to the host;
+ * device->device copies are ordered on `stream`. */
+int aar_memcpy(void* dst, const void* src, size_t bytes, int kind, void* stream);
+
+/* Zero `bytes` of device memory with a fill kernel (capturable into a HIP graph).
+ * Replaces zero_bytes (cppsrc/core/cuda_copy.hpp:12). */
+int aar_memset_zero(void* ptr, size_t bytes, void* stream);
+
+/* Replaces cuda_synchronize (cppsrc/python/binding.cpp:62-69). */
+int aar_synchronize(void);
+int aar_stream_synchronize(void* stream);
+
+/* Timing events (bench harness; the reference uses cudaEvent in
+ * bench/bench_matmul.cu:66-89). */
+int aar_event_create(void** event);
+int aar_event_destroy(void* event);
+int aar_event_record(void* event, void* stream);
+int aar_event_elapsed_ms(float* ms, void* start, void* stop);
+
+/* ------------------------------------------------------------------- GEMM */
+
+#define AAR_GEMM_NN 0  /* C[M,N] = A[M,K]   . B[K,N]    matmul       */
+#define AAR_GEMM_NT 1  /* C[M,N] = A[M,K]   . B[N,K]^T  matmul_a_bt  */
+#define AAR_GEMM_TN 2  /* C[M,N] = A[K,M]^T . B[K,N]    matmul_at_b  */
+
+/* Scratch needed by aar_gemm_f32 for a split-K launch of this shape (0 when
+ * the shape runs without split-K). */
+size_t aar_gemm_f32_workspace_bytes(int op, int64_t M, int64_t N, int64_t K);
+
+/* fp32 GEMM on v_mfma_f32_32x32x2f32.  Replaces matmul_cuda /
+ * matmul_a_bt_cuda / matmul_at_b_cuda (cppsrc/ops/matmul.cpp:10-12) and the
+ * raw-pointer launchers matmul_v4_launch / matmul_a_bt_v4_launch /
+ * matmul_at_b_v4_launch (cppsrc/ops/matmul.cu:648-650).
+ * `workspace` may be NULL when aar_gemm_f32_workspace_bytes() returned 0;
+ * with a smaller workspace the call runs without split-K (same result up to
+ * summation order).  K == 0 writes zeros. */
+int aar_gemm_f32(int op, int64_t M, int64_t N, int64_t K,
+                 const float* A, const float* B, float* C,
+                 void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------- row-wise kernels */
+
+/* y = softmax(x) over the last dim; x,y [rows, cols].
+ * Replaces softmax_cuda (cppsrc/ops/softmax.cpp:11). */
+int aar_softmax_fwd_f32(const float* x, float* y, int64_t rows, int64_t cols,
+                        void* stream);
+
+/* dx = y * (g - sum(g*y)) per row.  Replaces softmax_backward_cuda
+ * (cppsrc/ops/softmax.cpp:12). */
+int aar_softmax_bwd_f32(const float* g, const float* y, float* dx,
+                        int64_t rows, int64_t cols, void* stream);
+
+/* y = (x - mean) * rstd * w + b per row; mean/rstd [rows] are written when both
+ * are non-NULL.  Replaces layernorm_cuda and layernorm_with_stats_cuda
+ * (cppsrc/ops/layernorm.cpp:12-14). */
+int aar_layernorm_fwd_f32(const float* x, const float* w, const float* b,
+                          float* y, float* mean, float* rstd,
+                          int64_t rows, int64_t cols, float eps, void* stream);
+
+size_t aar_layernorm_bwd_workspace_bytes(int64_t rows, int64_t cols);
+
+/* dx [rows,cols], dw and db [cols] (fully overwritten; deterministic two-stage
+ * column reduction through `workspace`).  Replaces layernorm_backward_cuda
+ * (cppsrc/ops/layernorm.cpp:15-17). */
+int aar_layernorm_bwd_f32(const float* gy, const float* x, const float* w,
+                          const float* mean, const float* rstd,
+                          float* dx, float* dw, float* db,
+                          int64_t rows, int64_t cols,
+                          void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------- flash attention */
+
+/* O = softmax(scale * Q K^T [+ causal mask]) V and lse = m + ln(l) per query
+ * row; q,k,v,o [bh, T, d], lse [bh, T].  d <= 128 (d % 4 == 0 for the MFMA
+ * path).  Replaces flash_attention_forward_cuda
+ * (cppsrc/ops/flash_attention.cpp:15-16). */
+int aar_flash_fwd_f32(const float* q, const float* k, const float* v,
+                      float* o, float* lse, int64_t bh, int64_t T, int64_t d,
+                      int causal, float scale, void* stream);
+
+size_t aar_flash_bwd_workspace_bytes(int64_t bh, int64_t T, int64_t d);
+
+/* dq, dk, dv [bh, T, d] (fully overwritten; no float atomics).  Replaces
+ * flash_attention_backward_cuda (cppsrc/ops/flash_attention.cpp:18-22). */
+int aar_flash_bwd_f32(const float* q, const float* k, const float* v,
+                      const float* o, const float* lse, const float* dout,
+                      float* dq, float* dk, float* dv,
+                      int64_t bh, int64_t T, int64_t d, int causal, float scale,
+                      void* workspace, size_t workspace_bytes, void* stream);
+
+/* Strided fp32 copy of an ndim <= 8 view: dst[idx] = src[idx] for every index
+ * of `shape`, element offsets given by the two stride arrays (host arrays, read
+ * during the call).  Replaces contiguous_cuda / copy_contiguous_into_strided_cuda
+ * (cppsrc/ops/shape.cpp:11-12); no per-call device allocation. */
+int aar_strided_copy_f32(const float* src, float* dst, int ndim, const int64_t* shape,
+                         const int64_t* src_strides, const int64_t* dst_strides, void* stream);
+
+/* ------------------------------------------------------------ elementwise */
+
+/* c = a + b over n floats: the device leg of add_grads.  Replaces add_cuda
+ * (cppsrc/autograd/backward.cpp:14, cppsrc/ops/elementwise.cu:107-118). */
+int aar_add_f32(const float* a, const float* b, float* c, int64_t n, void* stream);
+
+#ifdef __cplusplus
+}  /* extern "C" */
+#endif
+
+#endif /* AAR_HIP_H */

@@ -1,0 +1,85 @@
+"""Helpers for the GPU tests: move arrays through aargrad._core, and a thin
+ctypes wrapper over the C ABI (include/aar_hip.h) for direct calls."""
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+import numpy as np
+
+LIB = Path(__file__).resolve().parent.parent / "aar-vlm_amd" / "aargrad" / "libaar_hip.so"
+
+
+def dev(ag, arr, requires_grad=False):
+    t = ag.from_numpy(np.ascontiguousarray(arr, np.float32)).to(ag.Device.CUDA)
+    if requires_grad:
+        t.requires_grad = True
+    return t
+
+
+def host(ag, t):
+    return ag.to_numpy(t.to(ag.Device.CPU))
+
+
+class Abi:
+    """Direct C-ABI access with device buffers owned by this object."""
+
+    def __init__(self):
+        L = ctypes.CDLL(str(LIB))
+        vp, i64, sz = ctypes.c_void_p, ctypes.c_int64, ctypes.c_size_t
+        L.aar_error_string.restype = ctypes.c_char_p
+        L.aar_malloc.argtypes = [ctypes.POINTER(vp), sz]
+        L.aar_free.argtypes = [vp]
+        L.aar_memcpy.argtypes = [vp, vp, sz, ctypes.c_int, vp]
+        L.aar_memset_zero.argtypes = [vp, sz, vp]
+        L.aar_gemm_f32.argtypes = [ctypes.c_int, i64, i64, i64, vp, vp, vp, vp, sz, vp]
+        L.aar_gemm_f32_workspace_bytes.restype = sz
+        L.aar_gemm_f32_workspace_bytes.argtypes = [ctypes.c_int, i64, i64, i64]
+        L.aar_softmax_fwd_f32.argtypes = [vp, vp, i64, i64, vp]
+        L.aar_softmax_bwd_f32.argtypes = [vp, vp, vp, i64, i64, vp]
+        L.aar_layernorm_fwd_f32.argtypes = [vp, vp, vp, vp, vp, vp, i64, i64, ctypes.c_float, vp]
+        L.aar_layernorm_bwd_workspace_bytes.restype = sz
+        L.aar_layernorm_bwd_workspace_bytes.argtypes = [i64, i64]
+        L.aar_layernorm_bwd_f32.argtypes = [vp] * 8 + [i64, i64, vp, sz, vp]
+        L.aar_flash_fwd_f32.argtypes = [vp] * 5 + [i64, i64, i64, ctypes.c_int, ctypes.c_float, vp]
+        L.aar_flash_bwd_workspace_bytes.restype = sz
+        L.aar_flash_bwd_workspace_bytes.argtypes = [i64, i64, i64]
+        L.aar_flash_bwd_f32.argtypes = [vp] * 9 + [i64, i64, i64, ctypes.c_int, ctypes.c_float, vp, sz, vp]
+        L.aar_add_f32.argtypes = [vp, vp, vp, i64, vp]
+        L.aar_strided_copy_f32.argtypes = [vp, vp, ctypes.c_int, ctypes.POINTER(i64), ctypes.POINTER(i64),
+                                           ctypes.POINTER(i64), vp]
+        L.aar_synchronize.restype = ctypes.c_int
+        self.L = L
+        self._bufs = []
+
+    def check(self, rc):
+        if rc != 0:
+            raise RuntimeError(self.L.aar_error_string(rc).decode())
+
+    def alloc(self, nbytes):
+        p = ctypes.c_void_p()
+        self.check(self.L.aar_malloc(ctypes.byref(p), max(int(nbytes), 16)))
+        self._bufs.append(p)
+        return p.value
+
+    def put(self, arr, offset_floats=0):
+        """Upload into a fresh buffer, optionally at a float offset (misaligned)."""
+        arr = np.ascontiguousarray(arr, np.float32)
+        base = self.alloc(arr.nbytes + 4 * offset_floats + 16)
+        p = base + 4 * offset_floats
+        self.check(self.L.aar_memcpy(p, arr.ctypes.data, arr.nbytes, 1, None))
+        return p
+
+    def empty(self, n_floats, offset_floats=0):
+        return self.alloc(4 * (n_floats + offset_floats) + 16) + 4 * offset_floats
+
+    def get(self, p, shape):
+        out = np.empty(shape, np.float32)
+        self.check(self.L.aar_memcpy(out.ctypes.data, p, out.nbytes, 2, None))
+        return out
+
+    def free(self):
+        self.L.aar_synchronize()
+        for p in self._bufs:
+            self.L.aar_free(p)
+        self._bufs.clear()

@@ -1,0 +1,160 @@
+"""CPU-side checks of the boundary: the C-ABI library loads and exports every
+entry point declared in include/aar_hip.h, and the host layer (aargrad._core)
+keeps the reference API, validation errors and view semantics.  No kernel is
+launched here (no GPU in this container)."""
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+REPO = Path(__file__).resolve().parent.parent
+HEADER = REPO / "include" / "aar_hip.h"
+LIB = REPO / "aar-vlm_amd" / "aargrad" / "libaar_hip.so"
+
+
+def declared_symbols():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(aar_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_the_dispatch_surface():
+    syms = declared_symbols()
+    for s in ("aar_gemm_f32", "aar_softmax_fwd_f32", "aar_softmax_bwd_f32", "aar_layernorm_fwd_f32",
+              "aar_layernorm_bwd_f32", "aar_flash_fwd_f32", "aar_flash_bwd_f32", "aar_add_f32",
+              "aar_malloc", "aar_free", "aar_memcpy", "aar_memset_zero", "aar_synchronize",
+              "aar_error_string"):
+        assert s in syms
+
+
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(str(LIB))
+    missing = [s for s in declared_symbols() if not hasattr(lib, s)]
+    assert not missing, missing
+
+
+def test_error_strings():
+    lib = ctypes.CDLL(str(LIB))
+    lib.aar_error_string.restype = ctypes.c_char_p
+    assert lib.aar_error_string(0) == b"ok"
+    assert b"invalid" in lib.aar_error_string(-1)
+    assert b"workspace" in lib.aar_error_string(-2)
+    assert b"memory" in lib.aar_error_string(-4)
+
+
+def test_abi_validates_before_touching_the_device():
+    lib = ctypes.CDLL(str(LIB))
+    vp = ctypes.c_void_p
+    i64 = ctypes.c_int64
+    lib.aar_gemm_f32.argtypes = [ctypes.c_int, i64, i64, i64, vp, vp, vp, vp, ctypes.c_size_t, vp]
+    assert lib.aar_gemm_f32(7, 2, 2, 2, None, None, None, None, 0, None) == -1  # bad op
+    assert lib.aar_gemm_f32(0, -1, 2, 2, None, None, None, None, 0, None) == -1
+    assert lib.aar_gemm_f32(0, 0, 2, 2, None, None, None, None, 0, None) == 0  # empty is a no-op
+    lib.aar_softmax_fwd_f32.argtypes = [vp, vp, i64, i64, vp]
+    assert lib.aar_softmax_fwd_f32(None, None, 4, 0, None) == -1
+    lib.aar_flash_fwd_f32.argtypes = [vp] * 5 + [i64, i64, i64, ctypes.c_int, ctypes.c_float, vp]
+    assert lib.aar_flash_fwd_f32(None, None, None, None, None, 1, 8, 256, 1, 1.0, None) == -1  # d > 128
+    lib.aar_flash_bwd_workspace_bytes.restype = ctypes.c_size_t
+    lib.aar_flash_bwd_workspace_bytes.argtypes = [i64, i64, i64]
+    assert lib.aar_flash_bwd_workspace_bytes(96, 4096, 64) == 96 * 4096 * 4
+
+
+def test_core_exports_reference_api(ag):
+    for name in ("Tensor", "DType", "Device", "from_numpy", "to_numpy", "add", "sub", "mul", "relu",
+                 "gelu", "sum_all", "add_bias", "scale", "matmul", "matmul_a_bt", "matmul_at_b",
+                 "softmax", "layernorm", "apply_causal_mask", "reshape", "transpose", "slice",
+                 "squeeze", "unsqueeze", "contiguous", "bmm", "bmm_a_bt", "bmm_at_b", "embedding",
+                 "cross_entropy", "dropout", "manual_seed", "scaled_add_inplace", "adamw_step",
+                 "flash_attention", "cuda_synchronize"):
+        assert hasattr(ag, name), name
+    assert ag.Device.CUDA is not None and ag.DType.Fp32 is not None
+
+
+def test_factories_and_numpy_round_trip(ag):
+    # tests/python/test_smoke.py:23-42 (host-side plumbing)
+    z = ag.Tensor.zeros([2, 3], ag.DType.Fp32)
+    o = ag.Tensor.ones([2, 3], ag.DType.Fp32)
+    assert z.numel == 6 and z.shape == [2, 3] and z.strides == [3, 1]
+    np.testing.assert_array_equal(ag.to_numpy(z), np.zeros((2, 3), np.float32))
+    np.testing.assert_array_equal(ag.to_numpy(o), np.ones((2, 3), np.float32))
+    x = np.arange(6, dtype=np.float16).reshape(2, 3)
+    t = ag.from_numpy(x)
+    assert t.dtype == ag.DType.Fp16
+    np.testing.assert_array_equal(ag.to_numpy(t), x)
+    assert repr(ag.from_numpy(np.zeros((2, 3), np.float32))) == "Tensor(shape=[2, 3], dtype=Fp32, device=CPU)"
+
+
+def test_views_on_host(ag):
+    a = np.arange(24, dtype=np.float32).reshape(2, 3, 4)
+    t = ag.from_numpy(a)
+    tr = ag.transpose(t, 0, 2)
+    assert not tr.is_contiguous() and tr.shape == [4, 3, 2]
+    np.testing.assert_array_equal(ag.to_numpy(tr), a.transpose(2, 1, 0))
+    s = ag.slice(t, 1, 1, 3)
+    np.testing.assert_array_equal(ag.to_numpy(s), a[:, 1:3])
+    np.testing.assert_array_equal(ag.to_numpy(ag.reshape(t, [-1, 4])), a.reshape(-1, 4))
+    np.testing.assert_array_equal(ag.to_numpy(ag.unsqueeze(t, 0)), a[None])
+    np.testing.assert_array_equal(ag.to_numpy(ag.squeeze(ag.unsqueeze(t, 3), 3)), a)
+    with pytest.raises(ValueError):
+        ag.reshape(t, [5, -1])
+    with pytest.raises(ValueError):
+        ag.transpose(t, 0, 3)
+    with pytest.raises(ValueError):
+        ag.slice(t, 1, 2, 2)
+    with pytest.raises(ValueError):
+        ag.squeeze(t, 0)
+
+
+def test_validation_errors_match_reference(ag):
+    # std::invalid_argument -> ValueError, as in the reference binding
+    f = lambda *s: ag.from_numpy(np.zeros(s, np.float32))  # noqa: E731
+    with pytest.raises(ValueError, match="inner dimensions mismatch"):
+        ag.matmul(f(2, 3), f(4, 2))  # tests/cpp/test_matmul.cpp:52-56
+    with pytest.raises(ValueError, match="dtype mismatch"):
+        ag.matmul(f(2, 2), ag.from_numpy(np.zeros((2, 2), np.float16)))
+    with pytest.raises(ValueError):
+        ag.matmul_a_bt(f(2, 3), f(2, 4))
+    with pytest.raises(ValueError):
+        ag.matmul_at_b(f(3, 2), f(4, 2))
+    with pytest.raises(ValueError):
+        ag.softmax(ag.Tensor.empty([], ag.DType.Fp32))  # tests/cpp/test_softmax.cpp:67-70
+    with pytest.raises(ValueError):
+        ag.layernorm(f(4), f(3), f(4))  # tests/cpp/test_layernorm.cpp:100-105
+    with pytest.raises(ValueError, match="eps"):
+        ag.layernorm(f(2, 4), f(4), f(4), 0.0)
+    with pytest.raises(ValueError, match="share shape"):
+        ag.flash_attention(f(1, 2, 4, 8), f(1, 2, 4, 8), f(1, 2, 5, 8), True)
+    with pytest.raises(ValueError, match="at least 3 dims"):
+        ag.flash_attention(f(4, 8), f(4, 8), f(4, 8), True)
+
+
+def test_host_compute_fails_loudly(ag):
+    f = lambda *s: ag.from_numpy(np.zeros(s, np.float32))  # noqa: E731
+    for call in (lambda: ag.matmul(f(2, 3), f(3, 2)),
+                 lambda: ag.softmax(f(2, 3)),
+                 lambda: ag.layernorm(f(2, 3), f(3), f(3)),
+                 lambda: ag.flash_attention(f(1, 4, 8), f(1, 4, 8), f(1, 4, 8), True),
+                 lambda: ag.add(f(3), f(3)),
+                 lambda: ag.sum_all(f(3))):
+        with pytest.raises(RuntimeError, match="GPU only"):
+            call()
+
+
+def test_backward_arity_and_shape_errors(ag):
+    x = ag.from_numpy(np.zeros((3,), np.float32), requires_grad=True)
+    y = ag.reshape(x, [3, 1])
+    with pytest.raises(RuntimeError, match="scalar"):
+        y.backward()
+    with pytest.raises(RuntimeError, match="shape mismatch"):
+        y.backward(ag.from_numpy(np.ones((3,), np.float32)))
+    # a view-only graph needs no arithmetic: the seed flows back to the leaf
+    y.backward(ag.from_numpy(np.arange(3, dtype=np.float32).reshape(3, 1)))
+    np.testing.assert_array_equal(ag.to_numpy(x.grad), np.arange(3, dtype=np.float32))
+    x.zero_grad()
+    assert x.grad is None
+    with pytest.raises(RuntimeError, match="non-leaf"):
+        y.requires_grad = True

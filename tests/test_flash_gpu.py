@@ -1,0 +1,199 @@
+"""Flash-attention parity on the GPU: forward O and lse, backward dQ/dK/dV,
+against the oracle (the reference's CPU composite restated, and its float64
+lse) at the reference tests' shapes, the golden vectors from the reference CPU
+build, sampled heads of BASELINE config 4 and full-size checksum identities.
+Tolerance 1e-4 on both error metrics."""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+
+import oracle as O
+from conftest import TOL, assert_close
+from devutil import Abi, dev, host
+
+pytestmark = pytest.mark.gpu
+f32 = np.float32
+GOLDEN = O.HERE.parent / "tests" / "golden"
+
+
+def run_flash(gpu, q, k, v, do, causal):
+    tq, tk, tv = dev(gpu, q, True), dev(gpu, k, True), dev(gpu, v, True)
+    o = gpu.flash_attention(tq, tk, tv, causal)
+    o.backward(dev(gpu, do))
+    return host(gpu, o), host(gpu, tq.grad), host(gpu, tk.grad), host(gpu, tv.grad)
+
+
+def lse_of(gpu, q, k, v, causal):
+    _, lse = gpu._core._flash_attention_fwd(dev(gpu, q), dev(gpu, k), dev(gpu, v), causal)
+    return host(gpu, lse)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("T", [8, 32, 33, 64])
+def test_reference_forward_shapes(gpu, causal, T):
+    # tests/python/test_flash_attention.py:29-44 (B2 H4 d16), deterministic seed
+    rng = np.random.default_rng(1000 + T + causal)
+    q, k, v = (rng.standard_normal((2, 4, T, 16)).astype(f32) for _ in range(3))
+    o = host(gpu, gpu.flash_attention(dev(gpu, q), dev(gpu, k), dev(gpu, v), causal))
+    o_ref = O.attention(q, k, v, causal)
+    np.testing.assert_allclose(o, o_ref, atol=1e-4)
+    assert_close(o, o_ref, TOL, "O")
+    assert_close(lse_of(gpu, q, k, v, causal), O.attention_lse(q, k, causal), TOL, "lse")
+
+
+def test_reference_dq_case(gpu):
+    # tests/python/test_flash_attention.py:47-77 (B1 H2 T4 d8, causal, loss = sum(out))
+    rng = np.random.default_rng(7)
+    q, k, v = (rng.standard_normal((1, 2, 4, 8)).astype(f32) for _ in range(3))
+    ones = np.ones_like(q)
+    _, dq, dk, dv = run_flash(gpu, q, k, v, ones, True)
+    rq, rk, rv = O.attention_backward(q, k, v, ones, True)
+    for got, ref, n in ((dq, rq, "dq"), (dk, rk, "dk"), (dv, rv, "dv")):
+        assert_close(got, ref, TOL, n)
+
+
+@pytest.mark.parametrize("causal", [0, 1])
+def test_golden_cpu_gpu_parity(gpu, causal):
+    # tests/python/test_flash_attention.py:80-112 inputs; outputs from the reference CPU build
+    z = np.load(GOLDEN / "attention_b2h4t64d16.npz")
+    o, dq, dk, dv = run_flash(gpu, z["q"], z["k"], z["v"], z["do"], bool(causal))
+    np.testing.assert_allclose(o, z[f"o_{causal}"], atol=1e-4)
+    for got, name in ((o, "o"), (dq, "dq"), (dk, "dk"), (dv, "dv")):
+        assert_close(got, z[f"{name}_{causal}"], TOL, name)
+
+
+@pytest.mark.parametrize("shape", [(1, 3, 100, 64), (2, 2, 257, 64), (1, 2, 130, 128), (1, 1, 70, 36),
+                                   (3, 1, 1, 32), (1, 2, 96, 48)])
+@pytest.mark.parametrize("causal", [False, True])
+def test_shapes_vs_oracle(gpu, shape, causal):
+    rng = np.random.default_rng(sum(shape) + causal)
+    q, k, v, do = (rng.standard_normal(shape).astype(f32) for _ in range(4))
+    o, dq, dk, dv = run_flash(gpu, q, k, v, do, causal)
+    assert_close(o, O.attention(q, k, v, causal), TOL, "O")
+    rq, rk, rv = O.attention_backward(q, k, v, do, causal)
+    for got, ref, n in ((dq, rq, "dq"), (dk, rk, "dk"), (dv, rv, "dv")):
+        assert_close(got, ref, TOL, n)
+    assert_close(lse_of(gpu, q, k, v, causal), O.attention_lse(q, k, causal), TOL, "lse")
+
+
+def _config4(T, seed):
+    rng = np.random.default_rng(seed)
+    return [rng.standard_normal((8, 12, T, 64)).astype(f32) for _ in range(4)]
+
+
+def _checksums(q, o, dk, dv, do):
+    """Size-independent identities over every head: sum_j dV[j] = sum_i dO[i]
+    (rows of P sum to 1) and sum_j dK[j] = 0 (rows of dS sum to 0)."""
+    sdv = dv.astype(np.float64).sum(2)
+    sdo = do.astype(np.float64).sum(2)
+    assert_close(sdv, sdo, TOL, "sum dV = sum dO")
+    sdk = np.abs(dk.astype(np.float64).sum(2)).max()
+    scale = np.abs(dk.astype(np.float64)).sum(2).max()
+    assert sdk <= TOL * scale, f"sum dK = {sdk:.3e} (scale {scale:.3e})"
+    assert np.isfinite(o).all()
+
+
+def test_config4_t1024_sampled_heads(gpu):
+    q, k, v, do = _config4(1024, 0)
+    o, dq, dk, dv = run_flash(gpu, q, k, v, do, True)
+    lse = lse_of(gpu, q, k, v, True)
+    for b, h in ((0, 0), (5, 7)):
+        sl = (slice(b, b + 1), slice(h, h + 1))
+        assert_close(o[sl], O.attention(q[sl], k[sl], v[sl], True), TOL, "O")
+        rq, rk, rv = O.attention_backward(q[sl], k[sl], v[sl], do[sl], True)
+        assert_close(dq[sl], rq, TOL, "dq")
+        assert_close(dk[sl], rk, TOL, "dk")
+        assert_close(dv[sl], rv, TOL, "dv")
+        assert_close(lse[sl], O.attention_lse(q[sl], k[sl], True), TOL, "lse")
+    _checksums(q, o, dk, dv, do)
+
+
+def _closed64(q, k, v, do):
+    q, k, v, do = (t.astype(np.float64) for t in (q, k, v, do))
+    T, d = q.shape[-2:]
+    s = q @ k.T / math.sqrt(d)
+    s = np.where(np.triu(np.ones((T, T), bool), 1), -np.inf, s)
+    m = s.max(-1, keepdims=True)
+    e = np.exp(s - m)
+    l = e.sum(-1, keepdims=True)
+    p = e / l
+    dp = do @ v.T
+    ds = p * (dp - (dp * p).sum(-1, keepdims=True))
+    return p @ v, (m + np.log(l))[:, 0], ds @ k / math.sqrt(d), ds.T @ q / math.sqrt(d), p.T @ do
+
+
+def test_config4_t4096_sampled_head(gpu):
+    q, k, v, do = _config4(4096, 1)
+    o, dq, dk, dv = run_flash(gpu, q, k, v, do, True)
+    lse = lse_of(gpu, q, k, v, True)
+    b, h = 3, 11
+    ro, rl, rq, rk, rv = _closed64(q[b, h], k[b, h], v[b, h], do[b, h])
+    for got, ref, n in ((o, ro, "O"), (lse, rl, "lse"), (dq, rq, "dq"), (dk, rk, "dk"), (dv, rv, "dv")):
+        assert_close(got[b, h], ref, TOL, n)
+    _checksums(q, o, dk, dv, do)
+
+
+def test_backward_is_reproducible(gpu):
+    rng = np.random.default_rng(2)
+    q, k, v, do = (rng.standard_normal((2, 3, 300, 64)).astype(f32) for _ in range(4))
+    r1 = run_flash(gpu, q, k, v, do, True)
+    r2 = run_flash(gpu, q, k, v, do, True)
+    for a, c in zip(r1, r2):
+        np.testing.assert_array_equal(a, c)
+
+
+def test_strided_views_like_mha(gpu):
+    """nn.MultiHeadAttention feeds slice/squeeze/transpose views of qkv
+    [B,T,3,H,d] (aargrad/nn.py:177-189); they are made contiguous first."""
+    B, T, H, d = 2, 48, 3, 16
+    rng = np.random.default_rng(9)
+    qkv = rng.standard_normal((B, T, 3, H, d)).astype(f32)
+    t = dev(gpu, qkv, True)
+
+    def take(i):
+        return gpu.transpose(gpu.squeeze(gpu.slice(t, 2, i, i + 1), 2), 1, 2)
+
+    q, k, v = take(0), take(1), take(2)
+    assert not q.is_contiguous()
+    o = gpu.flash_attention(q, k, v, True)
+    do = rng.standard_normal((B, H, T, d)).astype(f32)
+    o.backward(dev(gpu, do))
+    qn, kn, vn = (np.ascontiguousarray(qkv[:, :, i].transpose(0, 2, 1, 3)) for i in range(3))
+    assert_close(host(gpu, o), O.attention(qn, kn, vn, True), TOL, "O")
+    rq, rk, rv = O.attention_backward(qn, kn, vn, do, True)
+    g = host(gpu, t.grad)
+    for i, ref in enumerate((rq, rk, rv)):
+        assert_close(g[:, :, i].transpose(0, 2, 1, 3), ref, TOL, f"d{'qkv'[i]}")
+
+
+def test_abi_misaligned(gpu):
+    bh, T, d = 3, 77, 64
+    rng = np.random.default_rng(4)
+    q, k, v, do = (rng.standard_normal((bh, T, d)).astype(f32) for _ in range(4))
+    abi = Abi()
+    try:
+        pq, pk, pv, pdo = (abi.put(t, 1) for t in (q, k, v, do))
+        po, pl = abi.empty(bh * T * d, 1), abi.empty(bh * T)
+        s = 1.0 / math.sqrt(d)
+        abi.check(abi.L.aar_flash_fwd_f32(pq, pk, pv, po, pl, bh, T, d, 1, s, None))
+        assert_close(abi.get(po, (bh, T, d)), O.attention(q, k, v, True), TOL, "O")
+        wsb = abi.L.aar_flash_bwd_workspace_bytes(bh, T, d)
+        pdq, pdk, pdv = (abi.empty(bh * T * d, 1) for _ in range(3))
+        assert abi.L.aar_flash_bwd_f32(pq, pk, pv, po, pl, pdo, pdq, pdk, pdv, bh, T, d, 1, s,
+                                       None, 0, None) == -2
+        abi.check(abi.L.aar_flash_bwd_f32(pq, pk, pv, po, pl, pdo, pdq, pdk, pdv, bh, T, d, 1, s,
+                                          abi.alloc(wsb), wsb, None))
+        rq, rk, rv = O.attention_backward(q, k, v, do, True)
+        for p, ref, n in ((pdq, rq, "dq"), (pdk, rk, "dk"), (pdv, rv, "dv")):
+            assert_close(abi.get(p, (bh, T, d)), ref, TOL, n)
+    finally:
+        abi.free()
+
+
+def test_head_dim_limit(gpu):
+    x = dev(gpu, np.zeros((1, 4, 136), f32))
+    with pytest.raises(ValueError, match="D_MAX"):
+        gpu.flash_attention(x, x, x, True)

@@ -1,0 +1,181 @@
+"""GEMM parity on the GPU: matmul / matmul_a_bt / matmul_at_b through
+aargrad._core (and the C ABI directly for alignment and workspace cases),
+against the oracle at sizes it finishes in seconds and against float64
+closed forms on sampled rows plus full-size checksums at the BASELINE sweep.
+Tolerance: 1e-4*sqrt(K) for both error metrics (conftest.errs)."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle as O
+from conftest import assert_close, gemm_tol
+from devutil import Abi, dev, host
+
+pytestmark = pytest.mark.gpu
+f32 = np.float32
+OPFN = {"nn": "matmul", "nt": "matmul_a_bt", "tn": "matmul_at_b"}
+
+
+def operands(op, M, N, K, rng, scale=1.0):
+    a = (rng.standard_normal((M, K) if op != "tn" else (K, M)) * scale).astype(f32)
+    b = (rng.standard_normal((K, N) if op != "nt" else (N, K)) * scale).astype(f32)
+    return a, b
+
+
+def logical(op, a, b):
+    A = a.astype(np.float64) if op != "tn" else a.T.astype(np.float64)
+    B = b.astype(np.float64) if op != "nt" else b.T.astype(np.float64)
+    return A, B
+
+
+@pytest.mark.parametrize("op", ["nn", "nt", "tn"])
+def test_kat_on_device(gpu, op):
+    # tests/cpp/test_matmul.cpp:21-36, :58-88, :96-117
+    a = {"nn": [[1, 2, 3], [4, 5, 6]], "nt": [[1, 2, 3], [4, 5, 6]], "tn": [[1, 4], [2, 5], [3, 6]]}[op]
+    b = {"nn": [[7, 8], [9, 10], [11, 12]], "nt": [[7, 9, 11], [8, 10, 12]],
+         "tn": [[7, 8], [9, 10], [11, 12]]}[op]
+    c = getattr(gpu, OPFN[op])(dev(gpu, np.array(a, f32)), dev(gpu, np.array(b, f32)))
+    np.testing.assert_array_equal(host(gpu, c), [[58, 64], [139, 154]])
+
+
+@pytest.mark.parametrize("op", ["nn", "nt", "tn"])
+def test_golden_fill_64x96x48(gpu, op):
+    # tests/cpp/test_matmul.cpp:119-140 fill; outputs from the reference CPU build
+    z = np.load(O.HERE.parent / "tests" / "golden" / "gemm_64x96x48.npz")
+    c = host(gpu, getattr(gpu, OPFN[op])(dev(gpu, z[f"{op}_a"]), dev(gpu, z[f"{op}_b"])))
+    ref = z[f"{op}_c"]
+    tol = 1e-5 * np.maximum(np.abs(ref), 1.0) + 1e-6  # the reference test's own bound
+    assert np.all(np.abs(c - ref) <= tol)
+
+
+@pytest.mark.parametrize("op", ["nn", "nt", "tn"])
+def test_config1_1024_vs_oracle(gpu, op):
+    # M=N=K=1024, A then B ~ N(0,1) from seed 0, forward only
+    rng = np.random.default_rng(0)
+    a, b = operands(op, 1024, 1024, 1024, rng)
+    c = host(gpu, getattr(gpu, OPFN[op])(dev(gpu, a), dev(gpu, b)))
+    assert_close(c, O.matmul(op, a, b), gemm_tol(1024), f"{op} 1024^3")
+
+
+SWEEP = [(2048, 2048, 2048), (4096, 4096, 4096), (8192, 8192, 8192), (16384, 1536, 384), (16384, 384, 1536)]
+
+
+@pytest.mark.parametrize("shape", SWEEP, ids=lambda s: "x".join(map(str, s)))
+@pytest.mark.parametrize("op", ["nn", "nt", "tn"])
+def test_config2_sweep_fwd_bwd(gpu, op, shape):
+    """Forward plus both input-gradient GEMMs (through the autograd Functions)
+    at the BASELINE sweep sizes.  Sampled output rows are compared with float64
+    closed forms; every column is checked through the column-sum identity
+    1^T (A B) = (1^T A) B, a size-independent checksum."""
+    M, N, K = shape
+    rng = np.random.default_rng(hash(shape) % 2**32 + ord(op[0]))
+    a, b = operands(op, M, N, K, rng, 1.0 / np.sqrt(K))
+    g = rng.standard_normal((M, N)).astype(f32)
+    ta, tb = dev(gpu, a, True), dev(gpu, b, True)
+    c = getattr(gpu, OPFN[op])(ta, tb)
+    c.backward(dev(gpu, g))
+    ch, da, db = host(gpu, c), host(gpu, ta.grad), host(gpu, tb.grad)
+    A, B = logical(op, a, b)
+    G = g.astype(np.float64)
+    rows = np.sort(rng.choice(M, 48, replace=False))
+    assert_close(ch[rows], A[rows] @ B, gemm_tol(K), f"{op} fwd rows")
+    assert_close(ch.astype(np.float64).sum(0), A.sum(0) @ B, gemm_tol(K) * np.sqrt(M), f"{op} fwd colsum")
+    # logical gradients: dA = G B^T (contraction N), dB = A^T G (contraction M)
+    dA_rows = G[rows] @ B.T
+    brow = np.sort(rng.choice(K, 48, replace=False))
+    dB_rows = A[:, brow].T @ G
+    dA_log = da if op != "tn" else da.T  # tn: a is A^T
+    dB_log = db if op != "nt" else db.T  # nt: b is B^T
+    assert_close(dA_log[rows], dA_rows, gemm_tol(N), f"{op} dA rows")
+    assert_close(dB_log[brow], dB_rows, gemm_tol(M), f"{op} dB rows")
+
+
+@pytest.mark.parametrize("op", ["nn", "nt", "tn"])
+@pytest.mark.parametrize("shape", [(1, 1, 1), (1, 257, 3), (333, 65, 129), (65, 16384, 384),
+                                   (384, 384, 16384), (17, 5, 1), (128, 128, 8)])
+def test_edge_shapes_vs_oracle(gpu, op, shape):
+    M, N, K = shape
+    rng = np.random.default_rng(M + 7 * N + 13 * K)
+    a, b = operands(op, M, N, K, rng)
+    c = host(gpu, getattr(gpu, OPFN[op])(dev(gpu, a), dev(gpu, b)))
+    if M * N * K <= 2**28:
+        assert_close(c, O.matmul(op, a, b), gemm_tol(K), f"{op} {shape}")
+    else:
+        r = np.sort(rng.choice(M, 16, replace=False))
+        A, B = logical(op, a, b)
+        assert_close(c[r], A[r] @ B, gemm_tol(K), f"{op} {shape}")
+
+
+def test_zero_contraction_writes_zeros(gpu):
+    abi = Abi()
+    try:
+        c = abi.put(np.full((4, 5), 7.0, f32))
+        abi.check(abi.L.aar_gemm_f32(0, 4, 5, 0, abi.alloc(16), abi.alloc(16), c, None, 0, None))
+        np.testing.assert_array_equal(abi.get(c, (4, 5)), np.zeros((4, 5), f32))
+    finally:
+        abi.free()
+
+
+@pytest.mark.parametrize("op", [0, 1, 2])
+def test_abi_misaligned_and_no_workspace(gpu, op):
+    """Pointers offset by one float take the scalar-load path; a missing
+    workspace disables split-K.  Both must give the same parity."""
+    M, N, K = 260, 132, 2052
+    rng = np.random.default_rng(5 + op)
+    name = ["nn", "nt", "tn"][op]
+    a, b = operands(name, M, N, K, rng)
+    ref = O.matmul(name, a, b)
+    abi = Abi()
+    try:
+        pa, pb, pc = abi.put(a, 1), abi.put(b, 1), abi.empty(M * N, 1)
+        abi.check(abi.L.aar_gemm_f32(op, M, N, K, pa, pb, pc, None, 0, None))
+        assert_close(abi.get(pc, (M, N)), ref, gemm_tol(K), "misaligned")
+        pa, pb, pc = abi.put(a), abi.put(b), abi.empty(M * N)
+        wsb = abi.L.aar_gemm_f32_workspace_bytes(op, M, N, K)
+        ws = abi.alloc(wsb) if wsb else None
+        abi.check(abi.L.aar_gemm_f32(op, M, N, K, pa, pb, pc, ws, wsb, None))
+        assert_close(abi.get(pc, (M, N)), ref, gemm_tol(K), "aligned")
+    finally:
+        abi.free()
+
+
+def test_split_k_is_deterministic(gpu):
+    rng = np.random.default_rng(11)
+    a = rng.standard_normal((16384, 384)).astype(f32)
+    g = rng.standard_normal((16384, 1152)).astype(f32)
+    ta, tg = dev(gpu, a), dev(gpu, g)
+    r1 = host(gpu, gpu.matmul_at_b(tg, ta))
+    r2 = host(gpu, gpu.matmul_at_b(tg, ta))
+    np.testing.assert_array_equal(r1, r2)
+    rows = np.arange(0, 1152, 97)
+    assert_close(r1[rows], g.astype(np.float64)[:, rows].T @ a.astype(np.float64), gemm_tol(16384), "dW")
+
+
+def test_leading_dims_are_flattened(gpu):
+    # matmul / matmul_a_bt accept rank>=2 LHS (cppsrc/ops/matmul.cpp:93-120)
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((4, 7, 24)).astype(f32)
+    w = rng.standard_normal((24, 10)).astype(f32)
+    y = gpu.matmul(dev(gpu, x), dev(gpu, w))
+    assert y.shape == [4, 7, 10]
+    assert_close(host(gpu, y), x.astype(np.float64) @ w, gemm_tol(24), "3-D matmul")
+    wt = np.ascontiguousarray(w.T)
+    y2 = gpu.matmul_a_bt(dev(gpu, x), dev(gpu, wt))
+    assert_close(host(gpu, y2), x.astype(np.float64) @ w, gemm_tol(24), "3-D matmul_a_bt")
+
+
+def test_linear_layer_grads_match_oracle(gpu):
+    """nn.Linear's forward is matmul_a_bt; its backward runs matmul (dX) and
+    matmul_at_b with 3-D operands flattened (dW) (cppsrc/ops/matmul.cpp:146-155)."""
+    rng = np.random.default_rng(8)
+    x = rng.standard_normal((2, 96, 64)).astype(f32)
+    w = (0.1 * rng.standard_normal((48, 64))).astype(f32)
+    g = rng.standard_normal((2, 96, 48)).astype(f32)
+    tx, tw = dev(gpu, x, True), dev(gpu, w, True)
+    y = gpu.matmul_a_bt(tx, tw)
+    y.backward(dev(gpu, g))
+    x2, g2 = x.reshape(-1, 64), g.reshape(-1, 48)
+    assert_close(host(gpu, y).reshape(-1, 48), O.matmul("nt", x2, w), gemm_tol(64), "y")
+    assert_close(host(gpu, tx.grad).reshape(-1, 64), O.matmul("nn", g2, w), gemm_tol(48), "dx")
+    assert_close(host(gpu, tw.grad), O.matmul("tn", g2, x2), gemm_tol(192), "dw")
