@@ -182,10 +182,10 @@ def cpu_baseline_matmul(ab, budget_s: float = 12.0):
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=60)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--flash-steps", type=int, default=5)
+    ap.add_argument("--flash-steps", type=int, default=6)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build targets one GPU; --gpus {args.gpus} is not supported "
@@ -206,7 +206,7 @@ def main() -> int:
     log(f"matmul 4096^3: {step_ms:.4f} ms/step, {tflops:.2f} TFLOPS "
         f"({100 * tflops / PEAK_FP32_MFMA_TFLOPS:.1f}% of fp32 MFMA peak), check err {err:.2e}")
 
-    fa_ms, fa_flops = bench_flash(ag, args.flash_steps, 2, ev)
+    fa_ms, fa_flops = bench_flash(ag, args.flash_steps, 3, ev)
     fa_tflops = fa_flops / (fa_ms * 1e-3) / 1e12
     log(f"flash causal B8 H12 T4096 d64 fwd+bwd: {fa_ms:.3f} ms, {fa_tflops:.2f} TFLOPS "
         f"({100 * fa_tflops / PEAK_FP32_MFMA_TFLOPS:.1f}%)")
