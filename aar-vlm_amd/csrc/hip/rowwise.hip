@@ -94,47 +94,73 @@ __device__ __forceinline__ float group_reduce(float v, float* red, int slot, int
   return r;
 }
 
-// Number of row-groups each workgroup iteration covers, and persistent grid.
-inline int rows_grid(int64_t rows, int W) {
-  const int64_t per_iter = kWaves / W;
-  const int64_t need = ceil_div(rows, per_iter);
-  const int64_t cap = (int64_t)device_cu_count() * 8;
+// Rows each row group handles per iteration: their loads are all issued
+// before the first reduction, so several KB per wave are in flight (a single
+// small row leaves HBM latency exposed).
+template <int NV, int W>
+struct RowsPerIter {
+  static constexpr int value = W == 1 ? (NV <= 2 ? 4 : (NV == 4 ? 2 : 1)) : 1;
+};
+
+inline int rows_per_iter(int nv, int w) { return w == 1 ? (nv <= 2 ? 4 : (nv == 4 ? 2 : 1)) : 1; }
+
+// Persistent grid: enough workgroups to cover the rows once, capped at
+// `per_cu` workgroups per CU.
+inline int rows_grid(int64_t rows, int nv, int W, int per_cu = 8) {
+  const int64_t per_wg_iter = (int64_t)(kWaves / W) * rows_per_iter(nv, W);
+  const int64_t need = ceil_div(rows, per_wg_iter);
+  const int64_t cap = (int64_t)device_cu_count() * per_cu;
   return (int)(need < cap ? need : cap);
 }
+
+// First row of row group `grp` in iteration `it`; the group's rows are
+// row0 .. row0 + U - 1.
+__device__ __forceinline__ int64_t group_row0(int64_t it, int per_iter, int grp, int U) {
+  return ((it * gridDim.x + blockIdx.x) * per_iter + grp) * U;
+}
+
+// LDS cells used by group_reduce: 2 parities x U rows x 2 reductions x 4 waves.
+constexpr int kRedCells = 2 * 4 * 2 * kWaves;
 
 // ------------------------------------------------------------------ softmax
 
 template <int NV, int W, bool VEC>
 __global__ void __launch_bounds__(kThreads)
 softmax_fwd_kernel(const float* __restrict__ x, float* __restrict__ y, int64_t rows, int cols) {
-  __shared__ float red[4 * kWaves];
+  constexpr int U = RowsPerIter<NV, W>::value;
+  __shared__ float red[kRedCells];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int grp = wave / W, wr = wave % W;
   constexpr int per_iter = kWaves / W;
-  const int64_t iters = ceil_div(rows, (int64_t)gridDim.x * per_iter);
+  const int64_t iters = ceil_div(rows, (int64_t)gridDim.x * per_iter * U);
   using RS = RowSlots<NV, W, VEC>;
   for (int64_t it = 0; it < iters; ++it) {
-    const int64_t row = (it * gridDim.x + blockIdx.x) * per_iter + grp;
-    const bool live = row < rows;
-    RS s;
-    if (live) s.load(x + row * cols, cols, wr, lane);
-    float mx = -INFINITY;
+    const int64_t row0 = group_row0(it, per_iter, grp, U);
+    RS s[U];
 #pragma unroll
-    for (int k = 0; k < RS::kN; ++k)
-      if (live && s.valid(k, cols, wr, lane)) mx = fmaxf(mx, s.v[k]);
-    mx = group_reduce<W, true>(mx, red, (int)(it & 1) * 2 + 0, grp, wr, lane);
-    float sum = 0.f;
+    for (int u = 0; u < U; ++u)
+      if (row0 + u < rows) s[u].load(x + (row0 + u) * cols, cols, wr, lane);
 #pragma unroll
-    for (int k = 0; k < RS::kN; ++k) {
-      const float e = (live && s.valid(k, cols, wr, lane)) ? expf(s.v[k] - mx) : 0.f;
-      s.v[k] = e;
-      sum += e;
+    for (int u = 0; u < U; ++u) {
+      const bool live = row0 + u < rows;
+      float mx = -INFINITY;
+#pragma unroll
+      for (int k = 0; k < RS::kN; ++k)
+        if (live && s[u].valid(k, cols, wr, lane)) mx = fmaxf(mx, s[u].v[k]);
+      mx = group_reduce<W, true>(mx, red, (((int)(it & 1) * U + u) * 2 + 0), grp, wr, lane);
+      float sum = 0.f;
+#pragma unroll
+      for (int k = 0; k < RS::kN; ++k) {
+        const float e = (live && s[u].valid(k, cols, wr, lane)) ? expf(s[u].v[k] - mx) : 0.f;
+        s[u].v[k] = e;
+        sum += e;
+      }
+      sum = group_reduce<W, false>(sum, red, (((int)(it & 1) * U + u) * 2 + 1), grp, wr, lane);
+      const float inv = 1.0f / sum;
+#pragma unroll
+      for (int k = 0; k < RS::kN; ++k) s[u].v[k] *= inv;
+      if (live) s[u].store(y + (row0 + u) * cols, cols, wr, lane);
     }
-    sum = group_reduce<W, false>(sum, red, (int)(it & 1) * 2 + 1, grp, wr, lane);
-    const float inv = 1.0f / sum;
-#pragma unroll
-    for (int k = 0; k < RS::kN; ++k) s.v[k] *= inv;
-    if (live) s.store(y + row * cols, cols, wr, lane);
   }
 }
 
@@ -142,27 +168,36 @@ template <int NV, int W, bool VEC>
 __global__ void __launch_bounds__(kThreads)
 softmax_bwd_kernel(const float* __restrict__ g, const float* __restrict__ y, float* __restrict__ dx,
                    int64_t rows, int cols) {
-  __shared__ float red[4 * kWaves];
+  constexpr int U = RowsPerIter<NV, W>::value;
+  __shared__ float red[kRedCells];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int grp = wave / W, wr = wave % W;
   constexpr int per_iter = kWaves / W;
-  const int64_t iters = ceil_div(rows, (int64_t)gridDim.x * per_iter);
+  const int64_t iters = ceil_div(rows, (int64_t)gridDim.x * per_iter * U);
   using RS = RowSlots<NV, W, VEC>;
   for (int64_t it = 0; it < iters; ++it) {
-    const int64_t row = (it * gridDim.x + blockIdx.x) * per_iter + grp;
-    const bool live = row < rows;
-    RS sg, sy;
-    if (live) {
-      sg.load(g + row * cols, cols, wr, lane);
-      sy.load(y + row * cols, cols, wr, lane);
+    const int64_t row0 = group_row0(it, per_iter, grp, U);
+    RS sg[U], sy[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (row0 + u < rows) {
+        sg[u].load(g + (row0 + u) * cols, cols, wr, lane);
+        sy[u].load(y + (row0 + u) * cols, cols, wr, lane);
+      } else {
+#pragma unroll
+        for (int k = 0; k < RS::kN; ++k) sg[u].v[k] = sy[u].v[k] = 0.f;
+      }
     }
-    float dot = 0.f;
 #pragma unroll
-    for (int k = 0; k < RS::kN; ++k) dot += sg.v[k] * sy.v[k];  // padding slots are zero
-    dot = group_reduce<W, false>(dot, red, (int)(it & 1), grp, wr, lane);
+    for (int u = 0; u < U; ++u) {
+      float dot = 0.f;
 #pragma unroll
-    for (int k = 0; k < RS::kN; ++k) sg.v[k] = sy.v[k] * (sg.v[k] - dot);
-    if (live) sg.store(dx + row * cols, cols, wr, lane);
+      for (int k = 0; k < RS::kN; ++k) dot += sg[u].v[k] * sy[u].v[k];  // padding slots are zero
+      dot = group_reduce<W, false>(dot, red, (((int)(it & 1) * U + u) * 2), grp, wr, lane);
+#pragma unroll
+      for (int k = 0; k < RS::kN; ++k) sg[u].v[k] = sy[u].v[k] * (sg[u].v[k] - dot);
+      if (row0 + u < rows) sg[u].store(dx + (row0 + u) * cols, cols, wr, lane);
+    }
   }
 }
 
@@ -173,42 +208,54 @@ __global__ void __launch_bounds__(kThreads)
 layernorm_fwd_kernel(const float* __restrict__ x, const float* __restrict__ w,
                      const float* __restrict__ b, float* __restrict__ y, float* __restrict__ mean,
                      float* __restrict__ rstd, int64_t rows, int cols, float eps) {
-  __shared__ float red[4 * kWaves];
+  constexpr int U = RowsPerIter<NV, W>::value;
+  __shared__ float red[kRedCells];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int grp = wave / W, wr = wave % W;
   constexpr int per_iter = kWaves / W;
-  const int64_t iters = ceil_div(rows, (int64_t)gridDim.x * per_iter);
+  const int64_t iters = ceil_div(rows, (int64_t)gridDim.x * per_iter * U);
   using RS = RowSlots<NV, W, VEC>;
   RS sw, sb;
   sw.load(w, cols, wr, lane);
   sb.load(b, cols, wr, lane);
   const float inv_d = 1.0f / (float)cols;
   for (int64_t it = 0; it < iters; ++it) {
-    const int64_t row = (it * gridDim.x + blockIdx.x) * per_iter + grp;
-    const bool live = row < rows;
-    RS s;
-    if (live) s.load(x + row * cols, cols, wr, lane);
-    float sum = 0.f;
+    const int64_t row0 = group_row0(it, per_iter, grp, U);
+    RS s[U];
 #pragma unroll
-    for (int k = 0; k < RS::kN; ++k) sum += s.v[k];
-    sum = group_reduce<W, false>(sum, red, (int)(it & 1) * 2 + 0, grp, wr, lane);
-    const float mu = sum * inv_d;
-    float sq = 0.f;
+    for (int u = 0; u < U; ++u) {
+      if (row0 + u < rows) {
+        s[u].load(x + (row0 + u) * cols, cols, wr, lane);
+      } else {
 #pragma unroll
-    for (int k = 0; k < RS::kN; ++k) {
-      const float dlt = s.valid(k, cols, wr, lane) ? s.v[k] - mu : 0.f;
-      sq += dlt * dlt;
+        for (int k = 0; k < RS::kN; ++k) s[u].v[k] = 0.f;
+      }
     }
-    sq = group_reduce<W, false>(sq, red, (int)(it & 1) * 2 + 1, grp, wr, lane);
-    const float var = sq * inv_d;
-    const float r = 1.0f / sqrtf(var + eps);
 #pragma unroll
-    for (int k = 0; k < RS::kN; ++k) s.v[k] = (s.v[k] - mu) * r * sw.v[k] + sb.v[k];
-    if (live) {
-      s.store(y + row * cols, cols, wr, lane);
-      if (STATS && wr == 0 && lane == 0) {
-        mean[row] = mu;
-        rstd[row] = r;
+    for (int u = 0; u < U; ++u) {
+      const int64_t row = row0 + u;
+      float sum = 0.f;
+#pragma unroll
+      for (int k = 0; k < RS::kN; ++k) sum += s[u].v[k];
+      sum = group_reduce<W, false>(sum, red, (((int)(it & 1) * U + u) * 2 + 0), grp, wr, lane);
+      const float mu = sum * inv_d;
+      float sq = 0.f;
+#pragma unroll
+      for (int k = 0; k < RS::kN; ++k) {
+        const float dlt = s[u].valid(k, cols, wr, lane) ? s[u].v[k] - mu : 0.f;
+        sq += dlt * dlt;
+      }
+      sq = group_reduce<W, false>(sq, red, (((int)(it & 1) * U + u) * 2 + 1), grp, wr, lane);
+      const float var = sq * inv_d;
+      const float r = 1.0f / sqrtf(var + eps);
+#pragma unroll
+      for (int k = 0; k < RS::kN; ++k) s[u].v[k] = (s[u].v[k] - mu) * r * sw.v[k] + sb.v[k];
+      if (row < rows) {
+        s[u].store(y + row * cols, cols, wr, lane);
+        if (STATS && wr == 0 && lane == 0) {
+          mean[row] = mu;
+          rstd[row] = r;
+        }
       }
     }
   }
@@ -223,11 +270,12 @@ layernorm_bwd_kernel(const float* __restrict__ gy, const float* __restrict__ x,
                      const float* __restrict__ w, const float* __restrict__ mean,
                      const float* __restrict__ rstd, float* __restrict__ dx,
                      float* __restrict__ part, int64_t rows, int cols) {
-  __shared__ float red[4 * kWaves];
+  constexpr int U = RowsPerIter<NV, W>::value;
+  __shared__ float red[kRedCells];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int grp = wave / W, wr = wave % W;
   constexpr int per_iter = kWaves / W;
-  const int64_t iters = ceil_div(rows, (int64_t)gridDim.x * per_iter);
+  const int64_t iters = ceil_div(rows, (int64_t)gridDim.x * per_iter * U);
   using RS = RowSlots<NV, W, VEC>;
   RS sw, dwacc, dbacc;
   sw.load(w, cols, wr, lane);
@@ -238,47 +286,57 @@ layernorm_bwd_kernel(const float* __restrict__ gy, const float* __restrict__ x,
   }
   const float inv_d = 1.0f / (float)cols;
   for (int64_t it = 0; it < iters; ++it) {
-    const int64_t row = (it * gridDim.x + blockIdx.x) * per_iter + grp;
-    const bool live = row < rows;
-    RS sg, sx;
-    float mu = 0.f, r = 0.f;
-    if (live) {
-      sg.load(gy + row * cols, cols, wr, lane);
-      sx.load(x + row * cols, cols, wr, lane);
-      mu = mean[row];
-      r = rstd[row];
-    } else {
+    const int64_t row0 = group_row0(it, per_iter, grp, U);
+    RS sg[U], sx[U];
+    float mu[U], r[U];
 #pragma unroll
-      for (int k = 0; k < RS::kN; ++k) {
-        sg.v[k] = 0.f;
-        sx.v[k] = 0.f;
+    for (int u = 0; u < U; ++u) {
+      if (row0 + u < rows) {
+        sg[u].load(gy + (row0 + u) * cols, cols, wr, lane);
+        sx[u].load(x + (row0 + u) * cols, cols, wr, lane);
+        mu[u] = mean[row0 + u];
+        r[u] = rstd[row0 + u];
+      } else {
+#pragma unroll
+        for (int k = 0; k < RS::kN; ++k) sg[u].v[k] = sx[u].v[k] = 0.f;
+        mu[u] = 0.f;
+        r[u] = 0.f;
       }
     }
-    float sum_g = 0.f, sum_gn = 0.f;
 #pragma unroll
-    for (int k = 0; k < RS::kN; ++k) {
-      const float n = (sx.v[k] - mu) * r;
-      const float gg = sg.v[k] * sw.v[k];
-      sum_g += gg;
-      sum_gn += gg * n;
-      dwacc.v[k] += sg.v[k] * n;
-      dbacc.v[k] += sg.v[k];
-      sx.v[k] = n;  // keep xhat
-    }
-    sum_g = group_reduce<W, false>(sum_g, red, (int)(it & 1) * 2 + 0, grp, wr, lane);
-    sum_gn = group_reduce<W, false>(sum_gn, red, (int)(it & 1) * 2 + 1, grp, wr, lane);
+    for (int u = 0; u < U; ++u) {
+      float sum_g = 0.f, sum_gn = 0.f;
 #pragma unroll
-    for (int k = 0; k < RS::kN; ++k) {
-      const float gg = sg.v[k] * sw.v[k];
-      sg.v[k] = r * (gg - sum_g * inv_d - sx.v[k] * sum_gn * inv_d);
+      for (int k = 0; k < RS::kN; ++k) {
+        const float n = (sx[u].v[k] - mu[u]) * r[u];
+        const float gg = sg[u].v[k] * sw.v[k];
+        sum_g += gg;
+        sum_gn += gg * n;
+        dwacc.v[k] += sg[u].v[k] * n;
+        dbacc.v[k] += sg[u].v[k];
+        sx[u].v[k] = n;  // keep xhat
+      }
+      sum_g = group_reduce<W, false>(sum_g, red, (((int)(it & 1) * U + u) * 2 + 0), grp, wr, lane);
+      sum_gn = group_reduce<W, false>(sum_gn, red, (((int)(it & 1) * U + u) * 2 + 1), grp, wr, lane);
+#pragma unroll
+      for (int k = 0; k < RS::kN; ++k) {
+        const float gg = sg[u].v[k] * sw.v[k];
+        sg[u].v[k] = r[u] * (gg - sum_g * inv_d - sx[u].v[k] * sum_gn * inv_d);
+      }
+      if (row0 + u < rows) sg[u].store(dx + (row0 + u) * cols, cols, wr, lane);
     }
-    if (live) sg.store(dx + row * cols, cols, wr, lane);
   }
   // Combine the row groups of this workgroup in a fixed order: group 0 seeds
   // the LDS accumulator, groups 1.. add in turn, then group 0's waves write
   // the workgroup's partial row.
-  __shared__ float stage[2][RS::kN * kWave * W];
   constexpr int ngrp = kWaves / W;
+  if (ngrp == 1) {
+    float* pw = part + (int64_t)blockIdx.x * 2 * cols;
+    dwacc.store(pw, cols, wr, lane);
+    dbacc.store(pw + cols, cols, wr, lane);
+    return;
+  }
+  __shared__ float stage[2][RS::kN * kWave * W];
 #pragma unroll
   for (int gi = 0; gi < ngrp; ++gi) {
     if (grp == gi) {
@@ -503,7 +561,7 @@ RowPlan plan_rows(int64_t cols, bool vec) {
 
 // Number of dgamma/dbeta partial rows (= workgroups of the backward kernel).
 int ln_bwd_parts(int64_t rows) {
-  const int64_t cap = (int64_t)device_cu_count() * 2;
+  const int64_t cap = (int64_t)device_cu_count() * 4;
   const int64_t p = rows < cap ? rows : cap;
   return (int)(p > 0 ? p : 1);
 }
@@ -523,7 +581,7 @@ extern "C" int aar_softmax_fwd_f32(const float* x, float* y, int64_t rows, int64
     softmax_fwd_wide_kernel<<<dim3((unsigned)rows), dim3(kThreads), 0, st>>>(x, y, cols);
     return launch_status();
   }
-  const int grid = rows_grid(rows, p.w);
+  const int grid = rows_grid(rows, p.nv, p.w);
 #define L(NV, W, V) softmax_fwd_kernel<NV, W, V><<<dim3(grid), dim3(kThreads), 0, st>>>(x, y, rows, (int)cols)
   AAR_ROW_DISPATCH(p, L);
 #undef L
@@ -541,7 +599,7 @@ extern "C" int aar_softmax_bwd_f32(const float* g, const float* y, float* dx, in
     softmax_bwd_wide_kernel<<<dim3((unsigned)rows), dim3(kThreads), 0, st>>>(g, y, dx, cols);
     return launch_status();
   }
-  const int grid = rows_grid(rows, p.w);
+  const int grid = rows_grid(rows, p.nv, p.w);
 #define L(NV, W, V) \
   softmax_bwd_kernel<NV, W, V><<<dim3(grid), dim3(kThreads), 0, st>>>(g, y, dx, rows, (int)cols)
   AAR_ROW_DISPATCH(p, L);
@@ -564,7 +622,7 @@ extern "C" int aar_layernorm_fwd_f32(const float* x, const float* w, const float
         x, w, b, y, stats ? mean : nullptr, stats ? rstd : nullptr, cols, eps);
     return launch_status();
   }
-  const int grid = rows_grid(rows, p.w);
+  const int grid = rows_grid(rows, p.nv, p.w);
   if (stats) {
 #define L(NV, W, V)                                                                              \
   layernorm_fwd_kernel<NV, W, V, true><<<dim3(grid), dim3(kThreads), 0, st>>>(x, w, b, y, mean, \

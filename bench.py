@@ -21,7 +21,6 @@ import ctypes
 import json
 import os
 import platform
-import subprocess
 import sys
 import time
 from pathlib import Path
@@ -142,6 +141,112 @@ def bench_flash(ag, steps: int, warmup: int, ev: Events, T: int = 4096):
     return ms, 3.5 * fwd_flops
 
 
+class Abi:
+    """Direct C-ABI calls with preallocated buffers (kernel-level timing)."""
+
+    def __init__(self, L):
+        vp, i64, sz = ctypes.c_void_p, ctypes.c_int64, ctypes.c_size_t
+        L.aar_malloc.argtypes = [ctypes.POINTER(vp), sz]
+        L.aar_free.argtypes = [vp]
+        L.aar_memcpy.argtypes = [vp, vp, sz, ctypes.c_int, vp]
+        L.aar_softmax_fwd_f32.argtypes = [vp, vp, i64, i64, vp]
+        L.aar_softmax_bwd_f32.argtypes = [vp, vp, vp, i64, i64, vp]
+        L.aar_layernorm_fwd_f32.argtypes = [vp, vp, vp, vp, vp, vp, i64, i64, ctypes.c_float, vp]
+        L.aar_layernorm_bwd_workspace_bytes.restype = sz
+        L.aar_layernorm_bwd_workspace_bytes.argtypes = [i64, i64]
+        L.aar_layernorm_bwd_f32.argtypes = [vp] * 8 + [i64, i64, vp, sz, vp]
+        L.aar_add_f32.argtypes = [vp, vp, vp, i64, vp]
+        self.L = L
+        self.bufs = []
+
+    def alloc(self, nbytes):
+        p = ctypes.c_void_p()
+        if self.L.aar_malloc(ctypes.byref(p), max(int(nbytes), 256)) != 0:
+            raise MemoryError(nbytes)
+        self.bufs.append(p)
+        return p.value
+
+    def put(self, arr):
+        p = self.alloc(arr.nbytes)
+        assert self.L.aar_memcpy(p, arr.ctypes.data, arr.nbytes, 1, None) == 0
+        return p
+
+    def free(self):
+        self.L.aar_synchronize()
+        for p in self.bufs:
+            self.L.aar_free(p)
+        self.bufs.clear()
+
+
+def bench_rowwise(ev: Events, iters: int = 20, min_set_bytes: float = 1.2e9):
+    """Softmax / layernorm fwd+bwd at BASELINE config 3 (rows 65536,
+    cols 384/768/4096), rotating over enough buffer sets (>= 1.2 GB of
+    operands) that the 256 MB Infinity Cache cannot serve them.  Algorithmic
+    bytes: softmax fwd 8RC, bwd 12RC; layernorm fwd-with-stats 8RC+8C+8R,
+    bwd 12RC+12C+8R (dgamma/dbeta partials excluded)."""
+    abi = Abi(ev.L)
+    rows = 65536
+    out = {}
+    rng = np.random.default_rng(0)
+    try:
+        for cols in (384, 768, 4096):
+            rc_bytes = rows * cols * 4
+            nsets = max(1, int(np.ceil(min_set_bytes / (3 * rc_bytes))))
+            x = (3 * rng.standard_normal((rows, cols))).astype(np.float32)
+            w = (1 + 0.02 * rng.standard_normal(cols)).astype(np.float32)
+            b = (0.02 * rng.standard_normal(cols)).astype(np.float32)
+            sets = [(abi.put(x), abi.alloc(rc_bytes), abi.put(x)) for _ in range(nsets)]  # x, y, g
+            pw, pb = abi.put(w), abi.put(b)
+            pm, pr = abi.alloc(rows * 4), abi.alloc(rows * 4)
+            pdw, pdb = abi.alloc(cols * 4), abi.alloc(cols * 4)
+            wsb = ev.L.aar_layernorm_bwd_workspace_bytes(rows, cols)
+            pws = abi.alloc(wsb)
+            L = ev.L
+            cases = {
+                "softmax_fwd": (8.0 * rows * cols, lambda s: L.aar_softmax_fwd_f32(s[0], s[1], rows, cols, None)),
+                "softmax_bwd": (12.0 * rows * cols,
+                                lambda s: L.aar_softmax_bwd_f32(s[2], s[1], s[0], rows, cols, None)),
+                "layernorm_fwd": (8.0 * rows * cols + 8 * cols + 8 * rows,
+                                  lambda s: L.aar_layernorm_fwd_f32(s[0], pw, pb, s[1], pm, pr, rows, cols,
+                                                                    ctypes.c_float(1e-5), None)),
+                "layernorm_bwd": (12.0 * rows * cols + 12 * cols + 8 * rows,
+                                  lambda s: L.aar_layernorm_bwd_f32(s[2], s[0], pw, pm, pr, s[1], pdw, pdb, rows,
+                                                                    cols, pws, wsb, None)),
+            }
+            for name, (nbytes, fn) in cases.items():
+                for i in range(3):
+                    assert fn(sets[i % nsets]) == 0
+                ev.start()
+                for i in range(iters):
+                    assert fn(sets[i % nsets]) == 0
+                ms = ev.stop_ms() / iters
+                out[f"{name}_c{cols}"] = {"ms": round(ms, 4), "GB_s": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                                          "frac_of_hbm_peak": round(nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+                                          "buffer_sets": nsets}
+            abi.free()
+    finally:
+        abi.free()
+    return out
+
+
+def bench_copy(ev: Events, iters: int = 5, n: int = 1 << 26):
+    """Calibration kernel for the HBM byte counters: c = a + b over n floats
+    (reads 8n bytes, writes 4n bytes per launch)."""
+    abi = Abi(ev.L)
+    try:
+        a = np.ones(n, np.float32)
+        pa, pb, pc = abi.put(a), abi.put(a), abi.alloc(4 * n)
+        for _ in range(2):
+            ev.L.aar_add_f32(pa, pb, pc, n, None)
+        ev.start()
+        for _ in range(iters):
+            assert ev.L.aar_add_f32(pa, pb, pc, n, None) == 0
+        ms = ev.stop_ms() / iters
+    finally:
+        abi.free()
+    return {"n": n, "read_bytes": 8 * n, "write_bytes": 4 * n, "ms": ms, "GB_s": 12 * n / (ms * 1e-3) / 1e9}
+
+
 def cpu_baseline_matmul(ab, budget_s: float = 12.0):
     """The reference CPU path (oracle/_ref: the reference's own matmul built
     from its sources; else the C restatement) on one core, on a row band of
@@ -186,6 +291,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=60)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--flash-steps", type=int, default=6)
+    ap.add_argument("--only", choices=["all", "gemm", "flash", "rowwise", "copy"], default="all",
+                    help="run one part (profiling runs); the JSON line is printed for 'all'")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build targets one GPU; --gpus {args.gpus} is not supported "
@@ -198,18 +305,35 @@ def main() -> int:
         print("bench.py: no GPU visible", file=sys.stderr)
         return 1
     ev = Events()
-
-    step_ms, wall, err, ab = bench_matmul(ag, args.steps, args.warmup, ev)
     n = 4096
     flops = 2.0 * n ** 3
+
+    if args.only == "copy":
+        log("copy calibration:", bench_copy(ev))
+        return 0
+    if args.only == "rowwise":
+        log(json.dumps(bench_rowwise(ev)))
+        return 0
+    if args.only == "flash":
+        fa_ms, fa_flops = bench_flash(ag, args.flash_steps, 3, ev)
+        log(f"flash fwd+bwd {fa_ms:.3f} ms {fa_flops / (fa_ms * 1e-3) / 1e12:.2f} TFLOPS")
+        return 0
+
+    step_ms, wall, err, ab = bench_matmul(ag, args.steps, args.warmup, ev)
     tflops = flops / (step_ms * 1e-3) / 1e12
     log(f"matmul 4096^3: {step_ms:.4f} ms/step, {tflops:.2f} TFLOPS "
         f"({100 * tflops / PEAK_FP32_MFMA_TFLOPS:.1f}% of fp32 MFMA peak), check err {err:.2e}")
+    if args.only == "gemm":
+        return 0
 
     fa_ms, fa_flops = bench_flash(ag, args.flash_steps, 3, ev)
     fa_tflops = fa_flops / (fa_ms * 1e-3) / 1e12
     log(f"flash causal B8 H12 T4096 d64 fwd+bwd: {fa_ms:.3f} ms, {fa_tflops:.2f} TFLOPS "
         f"({100 * fa_tflops / PEAK_FP32_MFMA_TFLOPS:.1f}%)")
+
+    rowwise = bench_rowwise(ev)
+    for k, v in rowwise.items():
+        log(f"{k}: {v['GB_s']} GB/s ({100 * v['frac_of_hbm_peak']:.1f}% of HBM peak)")
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -242,6 +366,7 @@ def main() -> int:
             "ms_per_step": round(fa_ms, 4),
             "config": "causal, B8 H12 T4096 d64, fwd+bwd, flops = 3.5 * 4*B*H*T^2*d/2",
         },
+        "rowwise_hbm": rowwise,
         "roofline": {
             "bound": "mfma",
             "achieved": round(tflops, 3),
