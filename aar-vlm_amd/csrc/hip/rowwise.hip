@@ -41,13 +41,19 @@ struct RowSlots {
     return ((i * W + wr) * kWave + lane) * kElem + e;
   }
 
+  // STREAM: the data is touched once (nontemporal hint, keeps it from
+  // displacing reused lines such as gamma/beta).
+  template <bool STREAM = true>
   __device__ __forceinline__ void load(const float* __restrict__ row, int cols, int wr, int lane) {
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
       const int c0 = col(i, 0, wr, lane);
       if (VEC) {
         f32x4 t = {0.f, 0.f, 0.f, 0.f};
-        if (c0 < cols) t = *reinterpret_cast<const f32x4*>(row + c0);
+        if (c0 < cols) {
+          const f32x4* src = reinterpret_cast<const f32x4*>(row + c0);
+          t = STREAM ? __builtin_nontemporal_load(src) : *src;
+        }
         v[4 * i + 0] = t[0];
         v[4 * i + 1] = t[1];
         v[4 * i + 2] = t[2];
@@ -65,7 +71,7 @@ struct RowSlots {
       if (c0 >= cols) continue;
       if (VEC) {
         f32x4 t = {v[4 * i + 0], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]};
-        *reinterpret_cast<f32x4*>(row + c0) = t;
+        __builtin_nontemporal_store(t, reinterpret_cast<f32x4*>(row + c0));
       } else {
         row[c0] = v[i];
       }
@@ -216,8 +222,8 @@ layernorm_fwd_kernel(const float* __restrict__ x, const float* __restrict__ w,
   const int64_t iters = ceil_div(rows, (int64_t)gridDim.x * per_iter * U);
   using RS = RowSlots<NV, W, VEC>;
   RS sw, sb;
-  sw.load(w, cols, wr, lane);
-  sb.load(b, cols, wr, lane);
+  sw.template load<false>(w, cols, wr, lane);
+  sb.template load<false>(b, cols, wr, lane);
   const float inv_d = 1.0f / (float)cols;
   for (int64_t it = 0; it < iters; ++it) {
     const int64_t row0 = group_row0(it, per_iter, grp, U);
@@ -278,7 +284,7 @@ layernorm_bwd_kernel(const float* __restrict__ gy, const float* __restrict__ x,
   const int64_t iters = ceil_div(rows, (int64_t)gridDim.x * per_iter * U);
   using RS = RowSlots<NV, W, VEC>;
   RS sw, dwacc, dbacc;
-  sw.load(w, cols, wr, lane);
+  sw.template load<false>(w, cols, wr, lane);
 #pragma unroll
   for (int k = 0; k < RS::kN; ++k) {
     dwacc.v[k] = 0.f;
@@ -362,16 +368,37 @@ layernorm_bwd_kernel(const float* __restrict__ gy, const float* __restrict__ x,
   }
 }
 
-// Stage 2: dw[c] = sum_p part[p][0][c], db[c] = sum_p part[p][1][c] (fixed order).
+// Stage 2 of layernorm backward, a fixed-order two-level tree over the
+// partial rows part[p][0..2C) (dgamma in [0,C), dbeta in [C,2C)):
+//   2a: grp[g][c] = sum of part[p][c] for p in [32g, 32g+32), in order
+//   2b: dw[c] = sum_g grp[g][c], db[c] = sum_g grp[g][C+c], in order
+// Deterministic, and every level runs with full column parallelism.
+constexpr int kPartGroup = 32;
+
 __global__ void __launch_bounds__(256)
-layernorm_bwd_reduce_kernel(const float* __restrict__ part, float* __restrict__ dw,
-                            float* __restrict__ db, int nparts, int cols) {
-  const int c = blockIdx.x * blockDim.x + threadIdx.x;
+layernorm_bwd_reduce_a_kernel(const float* __restrict__ part, float* __restrict__ grp, int nparts,
+                              int64_t ncol2) {
+  const int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (c >= ncol2) return;
+  const int p0 = blockIdx.y * kPartGroup;
+  const int p1 = min(nparts, p0 + kPartGroup);
+  float s = 0.f;
+#pragma unroll 8
+  for (int p = p0; p < p1; ++p) s += part[(int64_t)p * ncol2 + c];
+  grp[(int64_t)blockIdx.y * ncol2 + c] = s;
+}
+
+__global__ void __launch_bounds__(256)
+layernorm_bwd_reduce_b_kernel(const float* __restrict__ grp, float* __restrict__ dw, float* __restrict__ db,
+                              int ngroups, int cols) {
+  const int c = blockIdx.x * 256 + threadIdx.x;
   if (c >= cols) return;
+  const int64_t ncol2 = 2 * (int64_t)cols;
   float a = 0.f, b = 0.f;
-  for (int p = 0; p < nparts; ++p) {
-    a += part[(int64_t)p * 2 * cols + c];
-    b += part[(int64_t)p * 2 * cols + cols + c];
+#pragma unroll 8
+  for (int g = 0; g < ngroups; ++g) {
+    a += grp[g * ncol2 + c];
+    b += grp[g * ncol2 + cols + c];
   }
   dw[c] = a;
   db[c] = b;
@@ -642,7 +669,9 @@ extern "C" int aar_layernorm_fwd_f32(const float* x, const float* w, const float
 
 extern "C" size_t aar_layernorm_bwd_workspace_bytes(int64_t rows, int64_t cols) {
   if (rows <= 0 || cols <= 0) return 0;
-  return (size_t)ln_bwd_parts(rows) * 2 * (size_t)cols * sizeof(float);
+  const int64_t parts = ln_bwd_parts(rows);
+  const int64_t groups = ceil_div(parts, kPartGroup);
+  return (size_t)(parts + groups) * 2 * (size_t)cols * sizeof(float);
 }
 
 extern "C" int aar_layernorm_bwd_f32(const float* gy, const float* x, const float* w,
@@ -659,9 +688,11 @@ extern "C" int aar_layernorm_bwd_f32(const float* gy, const float* x, const floa
   }
   if (!gy || !x || !w || !mean || !rstd || !dx) return AAR_EINVAL;
   const int parts = ln_bwd_parts(rows);
-  const size_t need = (size_t)parts * 2 * (size_t)cols * sizeof(float);
+  const int groups = (int)ceil_div(parts, kPartGroup);
+  const size_t need = (size_t)(parts + groups) * 2 * (size_t)cols * sizeof(float);
   if (!workspace || workspace_bytes < need) return AAR_EWORKSPACE;
   float* part = static_cast<float*>(workspace);
+  float* grp = part + (int64_t)parts * 2 * cols;
   const bool vec = cols % 4 == 0 && aligned16(gy) && aligned16(x) && aligned16(w) &&
                    aligned16(dx) && aligned16(workspace);
   const RowPlan p = plan_rows(cols, vec);
@@ -683,7 +714,12 @@ extern "C" int aar_layernorm_bwd_f32(const float* gy, const float* x, const floa
   }
   rc = launch_status();
   if (rc != AAR_OK) return rc;
-  layernorm_bwd_reduce_kernel<<<dim3((unsigned)ceil_div(cols, 256)), dim3(256), 0, st>>>(
-      part, dw, db, parts, (int)cols);
+  const int64_t ncol2 = 2 * cols;
+  layernorm_bwd_reduce_a_kernel<<<dim3((unsigned)ceil_div(ncol2, 256), (unsigned)groups), dim3(256), 0, st>>>(
+      part, grp, parts, ncol2);
+  rc = launch_status();
+  if (rc != AAR_OK) return rc;
+  layernorm_bwd_reduce_b_kernel<<<dim3((unsigned)ceil_div(cols, 256)), dim3(256), 0, st>>>(grp, dw, db, groups,
+                                                                                          (int)cols);
   return launch_status();
 }
