@@ -1,0 +1,554 @@
+// Device ops of the GPT training step around the hot path (elementwise
+// family, bias add/grad, reductions, embedding, cross entropy).  Reference
+// semantics:
+//   sub/mul/scale/neg/relu/gelu/add_bias/bias_grad/sum_all/fill/scaled_add
+//                              cppsrc/ops/elementwise.cpp:44-474, elementwise.cu:11-276
+//   embedding fwd/bwd          cppsrc/ops/embedding.cpp:9-104
+//   cross_entropy fwd/bwd      cppsrc/ops/cross_entropy.cpp:15-152
+// Design:
+//  * Streaming elementwise kernels: 128-bit loads/stores, grid-stride over a
+//    chip-sized grid, one templated body per op.
+//  * Every reduction is a fixed-order two-stage tree (bias_grad = column sums,
+//    sum_all, cross-entropy mean), so results are bit-reproducible; the
+//    reference uses float atomicAdd for bias_grad and embedding backward.
+//  * Embedding backward is dW = onehot(ids)^T . dY, run on the MFMA GEMM
+//    (matmul_at_b layout): deterministic, and at the vocabularies of the GPT
+//    step (65, 256) far cheaper than atomics into a few hot rows.
+//  * Out-of-range ids/targets cannot throw on the device: the kernels write
+//    zeros for such rows (never reading out of bounds) and raise a flag in a
+//    caller-provided int that the host checks at its next synchronisation.
+#include <hip/hip_runtime.h>
+#include <math.h>
+
+#include "common.hpp"
+
+namespace aar {
+namespace {
+
+unsigned stream_grid(int64_t work) {
+  const int64_t cap = (int64_t)device_cu_count() * 16;
+  int64_t g = (work + 255) / 256;
+  if (g > cap) g = cap;
+  return (unsigned)(g > 0 ? g : 1);
+}
+
+// ---------------------------------------------------------------- elementwise
+
+enum class Ew { Sub, Mul, Scale, Neg, Relu, ReluBwd, Gelu, GeluBwd, Fill, ScaledAdd };
+
+constexpr float kInvSqrt2 = 0.70710678118654752440f;
+constexpr float kInvSqrt2Pi = 0.39894228040143267794f;
+
+template <Ew OP>
+__device__ __forceinline__ float ew(float a, float b, float alpha) {
+  switch (OP) {
+    case Ew::Sub: return a - b;
+    case Ew::Mul: return a * b;
+    case Ew::Scale: return alpha * a;
+    case Ew::Neg: return -a;
+    case Ew::Relu: return fmaxf(0.0f, a);
+    case Ew::ReluBwd: return b > 0.0f ? a : 0.0f;  // a = grad, b = x
+    case Ew::Gelu: return 0.5f * a * (1.0f + erff(a * kInvSqrt2));
+    case Ew::GeluBwd: {  // a = grad, b = x
+      const float cdf = 0.5f * (1.0f + erff(b * kInvSqrt2));
+      const float pdf = kInvSqrt2Pi * expf(-0.5f * b * b);
+      return a * (cdf + b * pdf);
+    }
+    case Ew::Fill: return alpha;
+    case Ew::ScaledAdd: return a + alpha * b;  // a = dst, b = src
+  }
+  return 0.f;
+}
+
+template <Ew OP>
+__global__ void __launch_bounds__(256)
+ew_vec_kernel(const f32x4* __restrict__ a, const f32x4* __restrict__ b, f32x4* __restrict__ c, float alpha,
+              int64_t n4) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += stride) {
+    f32x4 x = {0.f, 0.f, 0.f, 0.f}, y = {0.f, 0.f, 0.f, 0.f};
+    if (OP != Ew::Fill) x = a[i];
+    if (OP == Ew::Sub || OP == Ew::Mul || OP == Ew::ReluBwd || OP == Ew::GeluBwd || OP == Ew::ScaledAdd) y = b[i];
+    f32x4 r;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) r[e] = ew<OP>(x[e], y[e], alpha);
+    c[i] = r;
+  }
+}
+
+template <Ew OP>
+__global__ void __launch_bounds__(256)
+ew_scalar_kernel(const float* __restrict__ a, const float* __restrict__ b, float* __restrict__ c, float alpha,
+                 int64_t n) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+    const float x = OP != Ew::Fill ? a[i] : 0.f;
+    const float y = (OP == Ew::Sub || OP == Ew::Mul || OP == Ew::ReluBwd || OP == Ew::GeluBwd ||
+                     OP == Ew::ScaledAdd)
+                        ? b[i]
+                        : 0.f;
+    c[i] = ew<OP>(x, y, alpha);
+  }
+}
+
+template <Ew OP>
+int launch_ew(const float* a, const float* b, float* c, float alpha, int64_t n, void* stream) {
+  if (n < 0) return AAR_EINVAL;
+  if (n == 0) return AAR_OK;
+  const bool needs_a = OP != Ew::Fill;
+  const bool needs_b = OP == Ew::Sub || OP == Ew::Mul || OP == Ew::ReluBwd || OP == Ew::GeluBwd ||
+                       OP == Ew::ScaledAdd;
+  if (!c || (needs_a && !a) || (needs_b && !b)) return AAR_EINVAL;
+  hipStream_t st = as_stream(stream);
+  const bool vec = aligned16(c) && (!needs_a || aligned16(a)) && (!needs_b || aligned16(b));
+  if (vec) {
+    const int64_t n4 = n / 4;
+    if (n4 > 0) {
+      ew_vec_kernel<OP><<<dim3(stream_grid(n4)), dim3(256), 0, st>>>(
+          reinterpret_cast<const f32x4*>(a), reinterpret_cast<const f32x4*>(b), reinterpret_cast<f32x4*>(c),
+          alpha, n4);
+      const int rc = launch_status();
+      if (rc != AAR_OK) return rc;
+    }
+    const int64_t done = n4 * 4;
+    if (done < n)
+      ew_scalar_kernel<OP><<<dim3(1), dim3(256), 0, st>>>(needs_a ? a + done : nullptr,
+                                                           needs_b ? b + done : nullptr, c + done, alpha,
+                                                           n - done);
+  } else {
+    ew_scalar_kernel<OP><<<dim3(stream_grid(n)), dim3(256), 0, st>>>(a, b, c, alpha, n);
+  }
+  return launch_status();
+}
+
+// ---------------------------------------------------------------- bias
+
+// y[r][c] = x[r][c] + bias[c]
+__global__ void __launch_bounds__(256)
+add_bias_kernel(const float* __restrict__ x, const float* __restrict__ bias, float* __restrict__ y, int64_t n,
+                int64_t cols) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) y[i] = x[i] + bias[i % cols];
+}
+
+__global__ void __launch_bounds__(256)
+add_bias_vec_kernel(const f32x4* __restrict__ x, const f32x4* __restrict__ bias, f32x4* __restrict__ y,
+                    int64_t n4, int64_t cols4) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += stride) y[i] = x[i] + bias[i % cols4];
+}
+
+// Column sums, stage 1: part[p][c] = sum of g[r][c] for rows r in chunk p
+// (rows p*chunk .. p*chunk+chunk-1, in order).
+__global__ void __launch_bounds__(256)
+colsum_stage1_kernel(const float* __restrict__ g, float* __restrict__ part, int64_t rows, int64_t cols,
+                     int64_t chunk) {
+  const int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (c >= cols) return;
+  const int64_t r0 = (int64_t)blockIdx.y * chunk;
+  const int64_t r1 = min(rows, r0 + chunk);
+  float s = 0.f;
+#pragma unroll 8
+  for (int64_t r = r0; r < r1; ++r) s += g[r * cols + c];
+  part[(int64_t)blockIdx.y * cols + c] = s;
+}
+
+// Stage 2: out[c] = sum_p part[p][c] in order.
+__global__ void __launch_bounds__(256)
+colsum_stage2_kernel(const float* __restrict__ part, float* __restrict__ out, int nparts, int64_t cols) {
+  const int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (c >= cols) return;
+  float s = 0.f;
+#pragma unroll 8
+  for (int p = 0; p < nparts; ++p) s += part[(int64_t)p * cols + c];
+  out[c] = s;
+}
+
+int colsum_parts(int64_t rows) {
+  const int64_t p = ceil_div(rows, 64);
+  return (int)(p < 256 ? (p > 0 ? p : 1) : 256);
+}
+
+// ---------------------------------------------------------------- sum_all
+
+constexpr int kSumBlocks = 256;
+
+// Stage 1: block b sums elements [b*chunk, (b+1)*chunk) (thread-strided,
+// then a fixed-shape block tree); stage 2 sums the block partials in order.
+__global__ void __launch_bounds__(256)
+sum_stage1_kernel(const float* __restrict__ x, float* __restrict__ part, int64_t n, int64_t chunk) {
+  __shared__ float red[4];
+  const int64_t b0 = (int64_t)blockIdx.x * chunk;
+  const int64_t b1 = min(n, b0 + chunk);
+  float s = 0.f;
+  for (int64_t i = b0 + threadIdx.x; i < b1; i += 256) s += x[i];
+  s = wave_sum(s);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
+  __syncthreads();
+  if (threadIdx.x == 0) part[blockIdx.x] = ((red[0] + red[1]) + red[2]) + red[3];
+}
+
+__global__ void __launch_bounds__(256)
+sum_stage2_kernel(const float* __restrict__ part, float* __restrict__ out, int nparts) {
+  __shared__ float red[4];
+  float s = threadIdx.x < nparts ? part[threadIdx.x] : 0.f;
+  s = wave_sum(s);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
+  __syncthreads();
+  if (threadIdx.x == 0) out[0] = ((red[0] + red[1]) + red[2]) + red[3];
+}
+
+// ---------------------------------------------------------------- embedding
+
+// out[i][:] = w[ids[i]][:]; an out-of-range id writes a zero row and sets *err.
+__global__ void __launch_bounds__(256)
+embedding_fwd_kernel(const float* __restrict__ w, const int64_t* __restrict__ ids, float* __restrict__ out,
+                     int64_t n, int64_t vocab, int64_t dim, int* __restrict__ err) {
+  const int64_t total = n * dim;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += stride) {
+    const int64_t i = e / dim, k = e - i * dim;
+    const int64_t id = ids[i];
+    float v = 0.f;
+    if (id >= 0 && id < vocab) {
+      v = w[id * dim + k];
+    } else if (k == 0 && err) {
+      *err = 1;
+    }
+    out[e] = v;
+  }
+}
+
+// onehot[i][v] = (ids[i] == v)  (row-major [n, vocab])
+__global__ void __launch_bounds__(256)
+onehot_kernel(const int64_t* __restrict__ ids, float* __restrict__ oh, int64_t n, int64_t vocab) {
+  const int64_t total = n * vocab;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += stride) {
+    const int64_t i = e / vocab, v = e - i * vocab;
+    oh[e] = ids[i] == v ? 1.0f : 0.0f;
+  }
+}
+
+// --------------------------------------------------------------- cross entropy
+
+// Row loss: lse(row) - row[t] (0 for ignored rows), active flag 1/0; one wave
+// per row, lanes strided over the vocabulary.  Mirrors cross_entropy_cpu's
+// float arithmetic (max, sum of exp(x - max), m + log(s)).
+__global__ void __launch_bounds__(256)
+ce_row_kernel(const float* __restrict__ L, const int64_t* __restrict__ T, float* __restrict__ row_loss,
+              int* __restrict__ active, int64_t n, int64_t V, int64_t ignore_index, int* __restrict__ err) {
+  const int64_t i = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (i >= n) return;
+  const int64_t t = T[i];
+  if (t == ignore_index) {
+    if (lane == 0) {
+      row_loss[i] = 0.f;
+      active[i] = 0;
+    }
+    return;
+  }
+  if (t < 0 || t >= V) {
+    if (lane == 0) {
+      row_loss[i] = 0.f;
+      active[i] = 0;
+      if (err) *err = 1;
+    }
+    return;
+  }
+  const float* row = L + i * V;
+  float m = -INFINITY;
+  for (int64_t v = lane; v < V; v += 64) m = fmaxf(m, row[v]);
+  m = wave_max(m);
+  float s = 0.f;
+  for (int64_t v = lane; v < V; v += 64) s += expf(row[v] - m);
+  s = wave_sum(s);
+  if (lane == 0) {
+    row_loss[i] = (m + logf(s)) - row[t];
+    active[i] = 1;
+  }
+}
+
+// Mean over active rows: loss and count summed in double / int64 in a fixed
+// order by one workgroup; writes the float mean (0 when no row is active) and
+// the active count.
+__global__ void __launch_bounds__(256)
+ce_mean_kernel(const float* __restrict__ row_loss, const int* __restrict__ active, int64_t n,
+               float* __restrict__ out, long long* __restrict__ count_out) {
+  __shared__ double dsum[256];
+  __shared__ long long csum[256];
+  double s = 0.0;
+  long long c = 0;
+  for (int64_t i = threadIdx.x; i < n; i += 256) {
+    s += (double)row_loss[i];
+    c += active[i];
+  }
+  dsum[threadIdx.x] = s;
+  csum[threadIdx.x] = c;
+  __syncthreads();
+  for (int w = 128; w > 0; w >>= 1) {
+    if (threadIdx.x < w) {
+      dsum[threadIdx.x] += dsum[threadIdx.x + w];
+      csum[threadIdx.x] += csum[threadIdx.x + w];
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    out[0] = csum[0] > 0 ? (float)(dsum[0] / (double)csum[0]) : 0.0f;
+    if (count_out) count_out[0] = csum[0];
+  }
+}
+
+__global__ void __launch_bounds__(256)
+ce_count_kernel(const int64_t* __restrict__ T, int64_t n, int64_t ignore_index, long long* __restrict__ count) {
+  __shared__ long long csum[256];
+  long long c = 0;
+  for (int64_t i = threadIdx.x; i < n; i += 256) c += (T[i] != ignore_index) ? 1 : 0;
+  csum[threadIdx.x] = c;
+  __syncthreads();
+  for (int w = 128; w > 0; w >>= 1) {
+    if (threadIdx.x < w) csum[threadIdx.x] += csum[threadIdx.x + w];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) count[0] = csum[0];
+}
+
+// dL[i][v] = (softmax(row)[v] - [v == t]) * go / active, zeros for ignored
+// (or out-of-range) rows.  Same float order as cross_entropy_backward_cpu.
+__global__ void __launch_bounds__(256)
+ce_bwd_kernel(const float* __restrict__ L, const int64_t* __restrict__ T, const float* __restrict__ grad,
+              const long long* __restrict__ count, float* __restrict__ dL, int64_t n, int64_t V,
+              int64_t ignore_index) {
+  const int64_t i = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (i >= n) return;
+  const int64_t t = T[i];
+  float* drow = dL + i * V;
+  const long long active = count[0];
+  if (t == ignore_index || t < 0 || t >= V || active == 0) {
+    for (int64_t v = lane; v < V; v += 64) drow[v] = 0.f;
+    return;
+  }
+  const float scale = grad[0] / (float)active;
+  const float* row = L + i * V;
+  float m = -INFINITY;
+  for (int64_t v = lane; v < V; v += 64) m = fmaxf(m, row[v]);
+  m = wave_max(m);
+  float s = 0.f;
+  for (int64_t v = lane; v < V; v += 64) s += expf(row[v] - m);
+  s = wave_sum(s);
+  const float inv_s = 1.0f / s;
+  for (int64_t v = lane; v < V; v += 64) {
+    float d = (expf(row[v] - m) * inv_s) * scale;
+    if (v == t) d -= scale;
+    drow[v] = d;
+  }
+}
+
+// ------------------------------------------------------------------- AdamW
+
+// Same per-element arithmetic as adamw_step_cpu (cppsrc/ops/adamw.cpp:22-44).
+__global__ void __launch_bounds__(256)
+adamw_kernel(float* __restrict__ p, const float* __restrict__ g, float* __restrict__ m, float* __restrict__ v,
+             int64_t n, float lr, float beta1, float beta2, float eps, float wd_factor, float bc1, float bc2) {
+  const float omb1 = 1.0f - beta1, omb2 = 1.0f - beta2;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+    const float gi = g[i];
+    const float mi = beta1 * m[i] + omb1 * gi;
+    const float vi = beta2 * v[i] + omb2 * gi * gi;
+    m[i] = mi;
+    v[i] = vi;
+    const float m_hat = mi / bc1;
+    const float v_hat = vi / bc2;
+    p[i] = p[i] * wd_factor - lr * m_hat / (sqrtf(v_hat) + eps);
+  }
+}
+
+}  // namespace
+}  // namespace aar
+
+using namespace aar;
+
+extern "C" {
+
+int aar_sub_f32(const float* a, const float* b, float* c, int64_t n, void* s) {
+  return launch_ew<Ew::Sub>(a, b, c, 0.f, n, s);
+}
+int aar_mul_f32(const float* a, const float* b, float* c, int64_t n, void* s) {
+  return launch_ew<Ew::Mul>(a, b, c, 0.f, n, s);
+}
+int aar_scale_f32(const float* x, float* y, float alpha, int64_t n, void* s) {
+  return launch_ew<Ew::Scale>(x, nullptr, y, alpha, n, s);
+}
+int aar_neg_f32(const float* x, float* y, int64_t n, void* s) { return launch_ew<Ew::Neg>(x, nullptr, y, 0.f, n, s); }
+int aar_relu_f32(const float* x, float* y, int64_t n, void* s) {
+  return launch_ew<Ew::Relu>(x, nullptr, y, 0.f, n, s);
+}
+int aar_relu_bwd_f32(const float* g, const float* x, float* dx, int64_t n, void* s) {
+  return launch_ew<Ew::ReluBwd>(g, x, dx, 0.f, n, s);
+}
+int aar_gelu_f32(const float* x, float* y, int64_t n, void* s) {
+  return launch_ew<Ew::Gelu>(x, nullptr, y, 0.f, n, s);
+}
+int aar_gelu_bwd_f32(const float* g, const float* x, float* dx, int64_t n, void* s) {
+  return launch_ew<Ew::GeluBwd>(g, x, dx, 0.f, n, s);
+}
+int aar_fill_f32(float* y, float value, int64_t n, void* s) {
+  return launch_ew<Ew::Fill>(nullptr, nullptr, y, value, n, s);
+}
+int aar_scaled_add_f32(float* dst, const float* src, float alpha, int64_t n, void* s) {
+  return launch_ew<Ew::ScaledAdd>(dst, src, dst, alpha, n, s);
+}
+
+int aar_add_bias_f32(const float* x, const float* bias, float* y, int64_t rows, int64_t cols, void* stream) {
+  if (rows < 0 || cols <= 0) return AAR_EINVAL;
+  const int64_t n = rows * cols;
+  if (n == 0) return AAR_OK;
+  if (!x || !bias || !y) return AAR_EINVAL;
+  hipStream_t st = as_stream(stream);
+  if (cols % 4 == 0 && aligned16(x) && aligned16(bias) && aligned16(y)) {
+    add_bias_vec_kernel<<<dim3(stream_grid(n / 4)), dim3(256), 0, st>>>(
+        reinterpret_cast<const f32x4*>(x), reinterpret_cast<const f32x4*>(bias), reinterpret_cast<f32x4*>(y),
+        n / 4, cols / 4);
+  } else {
+    add_bias_kernel<<<dim3(stream_grid(n)), dim3(256), 0, st>>>(x, bias, y, n, cols);
+  }
+  return launch_status();
+}
+
+size_t aar_colsum_workspace_bytes(int64_t rows, int64_t cols) {
+  if (rows <= 0 || cols <= 0) return 0;
+  return (size_t)colsum_parts(rows) * (size_t)cols * sizeof(float);
+}
+
+int aar_colsum_f32(const float* g, float* out, int64_t rows, int64_t cols, void* workspace, size_t workspace_bytes,
+                   void* stream) {
+  if (rows < 0 || cols <= 0) return AAR_EINVAL;
+  if (!out) return AAR_EINVAL;
+  if (rows == 0) return aar_memset_zero(out, (size_t)cols * sizeof(float), stream);
+  if (!g) return AAR_EINVAL;
+  const int parts = colsum_parts(rows);
+  if (!workspace || workspace_bytes < aar_colsum_workspace_bytes(rows, cols)) return AAR_EWORKSPACE;
+  hipStream_t st = as_stream(stream);
+  const int64_t chunk = ceil_div(rows, parts);
+  float* part = static_cast<float*>(workspace);
+  colsum_stage1_kernel<<<dim3((unsigned)ceil_div(cols, 256), (unsigned)parts), dim3(256), 0, st>>>(g, part, rows,
+                                                                                                  cols, chunk);
+  int rc = launch_status();
+  if (rc != AAR_OK) return rc;
+  colsum_stage2_kernel<<<dim3((unsigned)ceil_div(cols, 256)), dim3(256), 0, st>>>(part, out, parts, cols);
+  return launch_status();
+}
+
+size_t aar_sum_workspace_bytes(int64_t n) {
+  (void)n;
+  return (size_t)kSumBlocks * sizeof(float);
+}
+
+int aar_sum_f32(const float* x, float* out, int64_t n, void* workspace, size_t workspace_bytes, void* stream) {
+  if (n < 0 || !out) return AAR_EINVAL;
+  if (n > 0 && !x) return AAR_EINVAL;
+  if (!workspace || workspace_bytes < aar_sum_workspace_bytes(n)) return AAR_EWORKSPACE;
+  hipStream_t st = as_stream(stream);
+  const int64_t chunk = n > 0 ? ceil_div(n, kSumBlocks) : 1;
+  float* part = static_cast<float*>(workspace);
+  sum_stage1_kernel<<<dim3(kSumBlocks), dim3(256), 0, st>>>(x, part, n, chunk);
+  int rc = launch_status();
+  if (rc != AAR_OK) return rc;
+  sum_stage2_kernel<<<dim3(1), dim3(256), 0, st>>>(part, out, kSumBlocks);
+  return launch_status();
+}
+
+int aar_embedding_fwd_f32(const float* w, const int64_t* ids, float* out, int64_t n, int64_t vocab, int64_t dim,
+                          int* err, void* stream) {
+  if (n < 0 || vocab < 0 || dim < 0) return AAR_EINVAL;
+  if (n == 0 || dim == 0) return AAR_OK;
+  if (!ids || !out || (vocab > 0 && !w)) return AAR_EINVAL;
+  embedding_fwd_kernel<<<dim3(stream_grid(n * dim)), dim3(256), 0, as_stream(stream)>>>(w, ids, out, n, vocab, dim,
+                                                                                         err);
+  return launch_status();
+}
+
+// one-hot [n, vocab] followed by the GEMM's own workspace
+size_t aar_embedding_bwd_workspace_bytes(int64_t n, int64_t vocab, int64_t dim) {
+  if (n <= 0 || vocab <= 0 || dim <= 0) return 0;
+  const size_t oh = ((size_t)n * (size_t)vocab * sizeof(float) + 255) / 256 * 256;
+  return oh + aar_gemm_f32_workspace_bytes(AAR_GEMM_TN, vocab, dim, n);
+}
+
+int aar_embedding_bwd_f32(const float* g, const int64_t* ids, float* dw, int64_t n, int64_t vocab, int64_t dim,
+                          void* workspace, size_t workspace_bytes, void* stream) {
+  if (n < 0 || vocab < 0 || dim < 0) return AAR_EINVAL;
+  if (vocab == 0 || dim == 0) return AAR_OK;
+  if (!dw) return AAR_EINVAL;
+  if (n == 0) return aar_memset_zero(dw, (size_t)vocab * dim * sizeof(float), stream);
+  if (!g || !ids) return AAR_EINVAL;
+  if ((double)n * (double)vocab > (double)(1ll << 30)) return AAR_EUNSUPPORTED;
+  if (!workspace || workspace_bytes < aar_embedding_bwd_workspace_bytes(n, vocab, dim)) return AAR_EWORKSPACE;
+  float* oh = static_cast<float*>(workspace);
+  const size_t oh_bytes = ((size_t)n * (size_t)vocab * sizeof(float) + 255) / 256 * 256;
+  onehot_kernel<<<dim3(stream_grid(n * vocab)), dim3(256), 0, as_stream(stream)>>>(ids, oh, n, vocab);
+  int rc = launch_status();
+  if (rc != AAR_OK) return rc;
+  // dW[vocab, dim] = onehot[n, vocab]^T . g[n, dim]
+  return aar_gemm_f32(AAR_GEMM_TN, vocab, dim, n, oh, g, dw, static_cast<char*>(workspace) + oh_bytes,
+                      workspace_bytes - oh_bytes, stream);
+}
+
+// row_loss [n] floats, active [n] ints, count (int64)
+size_t aar_cross_entropy_workspace_bytes(int64_t n) {
+  if (n < 0) return 0;
+  return (size_t)n * (sizeof(float) + sizeof(int)) + 16;
+}
+
+int aar_cross_entropy_fwd_f32(const float* logits, const int64_t* targets, float* loss, int64_t n, int64_t vocab,
+                              int64_t ignore_index, int* err, void* workspace, size_t workspace_bytes,
+                              void* stream) {
+  if (n < 0 || vocab <= 0 || !loss) return AAR_EINVAL;
+  if (n > 0 && (!logits || !targets)) return AAR_EINVAL;
+  if (!workspace || workspace_bytes < aar_cross_entropy_workspace_bytes(n)) return AAR_EWORKSPACE;
+  hipStream_t st = as_stream(stream);
+  long long* count = static_cast<long long*>(workspace);
+  float* row_loss = reinterpret_cast<float*>(static_cast<char*>(workspace) + 16);
+  int* active = reinterpret_cast<int*>(row_loss + n);
+  if (n > 0) {
+    ce_row_kernel<<<dim3((unsigned)ceil_div(n, 4)), dim3(256), 0, st>>>(logits, targets, row_loss, active, n, vocab,
+                                                                          ignore_index, err);
+    const int rc = launch_status();
+    if (rc != AAR_OK) return rc;
+  }
+  ce_mean_kernel<<<dim3(1), dim3(256), 0, st>>>(row_loss, active, n, loss, count);
+  return launch_status();
+}
+
+int aar_cross_entropy_bwd_f32(const float* grad, const float* logits, const int64_t* targets, float* dlogits,
+                              int64_t n, int64_t vocab, int64_t ignore_index, void* workspace,
+                              size_t workspace_bytes, void* stream) {
+  if (n < 0 || vocab <= 0) return AAR_EINVAL;
+  if (n == 0) return AAR_OK;
+  if (!grad || !logits || !targets || !dlogits) return AAR_EINVAL;
+  if (!workspace || workspace_bytes < 16) return AAR_EWORKSPACE;
+  hipStream_t st = as_stream(stream);
+  long long* count = static_cast<long long*>(workspace);
+  ce_count_kernel<<<dim3(1), dim3(256), 0, st>>>(targets, n, ignore_index, count);
+  int rc = launch_status();
+  if (rc != AAR_OK) return rc;
+  ce_bwd_kernel<<<dim3((unsigned)ceil_div(n, 4)), dim3(256), 0, st>>>(logits, targets, grad, count, dlogits, n,
+                                                                        vocab, ignore_index);
+  return launch_status();
+}
+
+int aar_adamw_f32(float* param, const float* grad, float* m, float* v, int64_t n, float lr, float beta1,
+                  float beta2, float eps, float weight_decay, float bias_correction1, float bias_correction2,
+                  void* stream) {
+  if (n < 0) return AAR_EINVAL;
+  if (n == 0) return AAR_OK;
+  if (!param || !grad || !m || !v) return AAR_EINVAL;
+  adamw_kernel<<<dim3(stream_grid(n)), dim3(256), 0, as_stream(stream)>>>(
+      param, grad, m, v, n, lr, beta1, beta2, eps, 1.0f - lr * weight_decay, bias_correction1, bias_correction2);
+  return launch_status();
+}
+
+}  // extern "C"

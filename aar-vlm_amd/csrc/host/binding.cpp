@@ -141,37 +141,31 @@ PYBIND11_MODULE(_core, m) {
   m.def("unsqueeze", &unsqueeze, py::arg("x"), py::arg("dim"), gil_release());
   m.def("contiguous", &contiguous, py::arg("x"), gil_release());
 
-  // Reference API entries outside the MI355X hot path of this build.
-  m.def("sub", [](const Tensor& a, const Tensor&) -> Tensor { unavailable("sub", a); });
-  m.def("mul", [](const Tensor& a, const Tensor&) -> Tensor { unavailable("mul", a); });
-  m.def("relu", [](const Tensor& a) -> Tensor { unavailable("relu", a); });
-  m.def("gelu", [](const Tensor& a) -> Tensor { unavailable("gelu", a); });
-  m.def("sum_all", [](const Tensor& a) -> Tensor { unavailable("sum_all", a); });
-  m.def("add_bias", [](const Tensor& a, const Tensor&) -> Tensor { unavailable("add_bias", a); });
-  m.def("scale", [](const Tensor& x, float) -> Tensor { unavailable("scale", x); }, py::arg("x"),
-        py::arg("alpha"));
+  // Ops of the GPT training step around the path.
+  m.def("sub", &sub, gil_release());
+  m.def("mul", &mul, gil_release());
+  m.def("relu", &relu, gil_release());
+  m.def("gelu", &gelu, gil_release());
+  m.def("sum_all", &sum_all, gil_release());
+  m.def("add_bias", &add_bias, gil_release());
+  m.def("scale", &scale, py::arg("x"), py::arg("alpha"), gil_release());
+  m.def("scaled_add_inplace", &scaled_add_inplace, py::arg("dst"), py::arg("src"), py::arg("alpha"),
+        gil_release());
+  m.def("embedding", &embedding, py::arg("weight"), py::arg("ids"), gil_release());
+  m.def("cross_entropy", &cross_entropy, py::arg("logits"), py::arg("targets"), py::arg("ignore_index") = -100,
+        gil_release());
+  m.def("adamw_step", &adamw_step, py::arg("param"), py::arg("grad"), py::arg("m"), py::arg("v"), py::arg("lr"),
+        py::arg("beta1"), py::arg("beta2"), py::arg("eps"), py::arg("weight_decay"),
+        py::arg("bias_correction1"), py::arg("bias_correction2"), gil_release());
+  m.def("manual_seed", [](uint64_t seed) { g_seed.store(seed); }, py::arg("seed"));
+
+  // Reference API entries this build does not run on the GPU yet.
   m.def("apply_causal_mask", [](const Tensor& x) -> Tensor { unavailable("apply_causal_mask", x); });
   m.def("bmm", [](const Tensor& a, const Tensor&) -> Tensor { unavailable("bmm", a); });
   m.def("bmm_a_bt", [](const Tensor& a, const Tensor&) -> Tensor { unavailable("bmm_a_bt", a); });
   m.def("bmm_at_b", [](const Tensor& a, const Tensor&) -> Tensor { unavailable("bmm_at_b", a); });
-  m.def("embedding", [](const Tensor& w, const Tensor&) -> Tensor { unavailable("embedding", w); },
-        py::arg("weight"), py::arg("ids"));
-  m.def("cross_entropy",
-        [](const Tensor& l, const Tensor&, int64_t) -> Tensor { unavailable("cross_entropy", l); },
-        py::arg("logits"), py::arg("targets"), py::arg("ignore_index") = -100);
   m.def("dropout", [](const Tensor& x, float) -> Tensor { unavailable("dropout", x); }, py::arg("x"),
         py::arg("p"));
-  m.def("manual_seed", [](uint64_t seed) { g_seed.store(seed); }, py::arg("seed"));
-  m.def("scaled_add_inplace",
-        [](Tensor& dst, const Tensor&, float) { unavailable("scaled_add_inplace", dst); }, py::arg("dst"),
-        py::arg("src"), py::arg("alpha"));
-  m.def("adamw_step",
-        [](Tensor& p, const Tensor&, Tensor&, Tensor&, float, float, float, float, float, float, float) {
-          unavailable("adamw_step", p);
-        },
-        py::arg("param"), py::arg("grad"), py::arg("m"), py::arg("v"), py::arg("lr"), py::arg("beta1"),
-        py::arg("beta2"), py::arg("eps"), py::arg("weight_decay"), py::arg("bias_correction1"),
-        py::arg("bias_correction2"));
 
   // Extensions of this build (not in the reference API).
   m.def("_flash_attention_fwd", &flash_attention_fwd_lse, py::arg("q"), py::arg("k"), py::arg("v"),

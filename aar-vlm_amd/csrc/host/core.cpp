@@ -188,6 +188,37 @@ Workspace::Workspace(size_t bytes) {
 
 // --------------------------------------------------------------- transfers
 
+namespace {
+std::mutex g_err_mu;
+int* g_err_words = nullptr;  // kErrSlots ints on the device, zeroed once
+}  // namespace
+
+int* device_error_word(DeviceErrorSlot slot) {
+  std::lock_guard<std::mutex> lock(g_err_mu);
+  if (!g_err_words) {
+    void* p = device_allocator()->alloc(256);  // held for the life of the process
+    check_status(aar_memset_zero(p, 256, current_stream()), "device error word");
+    g_err_words = static_cast<int*>(p);
+  }
+  return g_err_words + slot;
+}
+
+void check_device_errors() {
+  int* words;
+  {
+    std::lock_guard<std::mutex> lock(g_err_mu);
+    words = g_err_words;
+  }
+  if (!words) return;
+  int host[kErrSlots] = {0, 0};
+  check_status(aar_memcpy(host, words, sizeof(host), 2, current_stream()), "device error word");
+  if (host[0] || host[1]) {
+    check_status(aar_memset_zero(words, sizeof(host), current_stream()), "device error word");
+    if (host[0]) throw std::out_of_range("embedding: id out of range [0, vocab_size)");
+    throw std::out_of_range("cross_entropy: target out of range [0, V)");
+  }
+}
+
 void copy_bytes(void* dst, Device dst_device, const void* src, Device src_device, size_t nbytes) {
   if (nbytes == 0) return;
   if (dst_device == Device::CPU && src_device == Device::CPU) {
@@ -198,6 +229,7 @@ void copy_bytes(void* dst, Device dst_device, const void* src, Device src_device
   if (src_device == Device::CPU) kind = 1;
   else if (dst_device == Device::CPU) kind = 2;
   check_status(aar_memcpy(dst, src, nbytes, kind, current_stream()), "copy_bytes");
+  if (kind == 2) check_device_errors();
 }
 
 void zero_bytes(void* p, Device device, size_t nbytes) {
@@ -209,7 +241,10 @@ void zero_bytes(void* p, Device device, size_t nbytes) {
   check_status(aar_memset_zero(p, nbytes, current_stream()), "zero_bytes");
 }
 
-void device_synchronize() { check_status(aar_synchronize(), "cuda_synchronize"); }
+void device_synchronize() {
+  check_status(aar_synchronize(), "cuda_synchronize");
+  check_device_errors();
+}
 
 // ------------------------------------------------------------------ tensor
 

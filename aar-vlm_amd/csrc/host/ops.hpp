@@ -36,4 +36,19 @@ std::tuple<Tensor, Tensor> flash_attention_fwd_lse(const Tensor& q, const Tensor
 Tensor add(const Tensor& a, const Tensor& b);
 Tensor add_grads(const Tensor& a, const Tensor& b);
 
+// Ops of the GPT training step around the path (cppsrc/ops/elementwise.cpp:315-474,
+// embedding.cpp:78-104, cross_entropy.cpp:121-152, adamw.cpp:47-75).
+Tensor sub(const Tensor& a, const Tensor& b);
+Tensor mul(const Tensor& a, const Tensor& b);
+Tensor scale(const Tensor& x, float alpha);
+Tensor relu(const Tensor& a);
+Tensor gelu(const Tensor& a);
+Tensor sum_all(const Tensor& a);
+Tensor add_bias(const Tensor& x, const Tensor& bias);
+void scaled_add_inplace(Tensor& dst, const Tensor& src, float alpha);
+Tensor embedding(const Tensor& weight, const Tensor& ids);
+Tensor cross_entropy(const Tensor& logits, const Tensor& targets, int64_t ignore_index);
+void adamw_step(Tensor& param, const Tensor& grad, Tensor& m, Tensor& v, float lr, float beta1, float beta2,
+                float eps, float weight_decay, float bias_correction1, float bias_correction2);
+
 }  // namespace aar

@@ -159,6 +159,70 @@ int aar_strided_copy_f32(const float* src, float* dst, int ndim, const int64_t* 
  * (cppsrc/autograd/backward.cpp:14, cppsrc/ops/elementwise.cu:107-118). */
 int aar_add_f32(const float* a, const float* b, float* c, int64_t n, void* stream);
 
+/* ------------------------------------------- GPT-step ops around the path */
+/* Elementwise over n floats; outputs may alias inputs.  Replace the reference
+ * device legs sub_cuda / mul_cuda / scale_cuda / neg_cuda / relu_cuda /
+ * relu_backward_cuda / gelu_cuda / gelu_backward_cuda / fill_cuda /
+ * scaled_add_inplace_cuda (cppsrc/ops/elementwise.cpp:8-27, kernels
+ * cppsrc/ops/elementwise.cu:16-72). */
+int aar_sub_f32(const float* a, const float* b, float* c, int64_t n, void* stream);      /* c = a - b */
+int aar_mul_f32(const float* a, const float* b, float* c, int64_t n, void* stream);      /* c = a * b */
+int aar_scale_f32(const float* x, float* y, float alpha, int64_t n, void* stream);       /* y = alpha * x */
+int aar_neg_f32(const float* x, float* y, int64_t n, void* stream);                      /* y = -x */
+int aar_relu_f32(const float* x, float* y, int64_t n, void* stream);                     /* y = max(0, x) */
+int aar_relu_bwd_f32(const float* g, const float* x, float* dx, int64_t n, void* stream);/* dx = x > 0 ? g : 0 */
+int aar_gelu_f32(const float* x, float* y, int64_t n, void* stream);                     /* exact (erf) GELU */
+int aar_gelu_bwd_f32(const float* g, const float* x, float* dx, int64_t n, void* stream);
+int aar_fill_f32(float* y, float value, int64_t n, void* stream);
+int aar_scaled_add_f32(float* dst, const float* src, float alpha, int64_t n, void* stream); /* dst += alpha*src (SGD) */
+
+/* y[r][c] = x[r][c] + bias[c].  Replaces add_bias_cuda (cppsrc/ops/elementwise.cpp:22). */
+int aar_add_bias_f32(const float* x, const float* bias, float* y, int64_t rows, int64_t cols, void* stream);
+
+/* out[c] = sum_r g[r][c], deterministic two-stage tree.  Replaces bias_grad_cuda
+ * (cppsrc/ops/elementwise.cpp:23, atomicAdd kernel elementwise.cu:79-82). */
+size_t aar_colsum_workspace_bytes(int64_t rows, int64_t cols);
+int aar_colsum_f32(const float* g, float* out, int64_t rows, int64_t cols,
+                   void* workspace, size_t workspace_bytes, void* stream);
+
+/* out[0] = sum of n floats, deterministic two-stage tree.  Replaces sum_all_cuda
+ * (cppsrc/ops/elementwise.cpp:24, single-block kernel elementwise.cu:84-100). */
+size_t aar_sum_workspace_bytes(int64_t n);
+int aar_sum_f32(const float* x, float* out, int64_t n, void* workspace, size_t workspace_bytes, void* stream);
+
+/* out[i][:] = w[ids[i]][:], w [vocab, dim], ids int64 [n].  An id outside
+ * [0, vocab) yields a zero row and sets *err = 1 (err may be NULL).
+ * Replaces embedding_cuda (cppsrc/ops/embedding.cpp:9). */
+int aar_embedding_fwd_f32(const float* w, const int64_t* ids, float* out, int64_t n, int64_t vocab,
+                          int64_t dim, int* err, void* stream);
+
+/* dw[vocab, dim] = onehot(ids)^T . g[n, dim] on the MFMA GEMM (deterministic;
+ * AAR_EUNSUPPORTED when n*vocab > 2^30).  Replaces embedding_backward_cuda
+ * (cppsrc/ops/embedding.cpp:10-11, atomicAdd kernel embedding.cu:19-26). */
+size_t aar_embedding_bwd_workspace_bytes(int64_t n, int64_t vocab, int64_t dim);
+int aar_embedding_bwd_f32(const float* g, const int64_t* ids, float* dw, int64_t n, int64_t vocab,
+                          int64_t dim, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Mean cross entropy over rows whose target != ignore_index; logits [n, vocab],
+ * targets int64 [n], loss a device scalar.  A target outside [0, vocab) (and not
+ * ignore_index) sets *err = 1 and the row is skipped.  Replaces
+ * cross_entropy_cuda / cross_entropy_backward_cuda (cppsrc/ops/cross_entropy.cpp:8-14). */
+size_t aar_cross_entropy_workspace_bytes(int64_t n);
+int aar_cross_entropy_fwd_f32(const float* logits, const int64_t* targets, float* loss, int64_t n,
+                              int64_t vocab, int64_t ignore_index, int* err,
+                              void* workspace, size_t workspace_bytes, void* stream);
+/* dlogits = (softmax(logits) - onehot(target)) * grad[0] / active, zero rows for
+ * ignored targets; grad is a device scalar (no host round trip). */
+int aar_cross_entropy_bwd_f32(const float* grad, const float* logits, const int64_t* targets,
+                              float* dlogits, int64_t n, int64_t vocab, int64_t ignore_index,
+                              void* workspace, size_t workspace_bytes, void* stream);
+
+/* Fused AdamW step over n floats (param, m, v updated in place).  Replaces
+ * adamw_step_cuda (cppsrc/ops/adamw.cpp:6-10, kernel adamw.cu:11-27). */
+int aar_adamw_f32(float* param, const float* grad, float* m, float* v, int64_t n, float lr,
+                  float beta1, float beta2, float eps, float weight_decay,
+                  float bias_correction1, float bias_correction2, void* stream);
+
 #ifdef __cplusplus
 }  /* extern "C" */
 #endif

@@ -25,6 +25,7 @@ REF_PATH = HERE / "_ref" / "libaar_ref.so"
 
 _f32p = np.ctypeslib.ndpointer(dtype=np.float32, flags="C_CONTIGUOUS")
 _f64p = np.ctypeslib.ndpointer(dtype=np.float64, flags="C_CONTIGUOUS")
+_i64p = np.ctypeslib.ndpointer(dtype=np.int64, flags="C_CONTIGUOUS")
 _i64 = ctypes.c_int64
 
 _lib = None
@@ -59,6 +60,25 @@ def lib():
         L.orc_attention_bwd.restype = ctypes.c_int
         L.orc_attention_lse.argtypes = [_f32p, _f32p, _f64p, _i64, _i64, _i64, ctypes.c_int]
         L.orc_add.argtypes = [_f32p, _f32p, _f32p, _i64]
+        for name in ("orc_sub", "orc_mul"):
+            getattr(L, name).argtypes = [_f32p, _f32p, _f32p, _i64]
+        L.orc_scale.argtypes = [_f32p, _f32p, ctypes.c_float, _i64]
+        for name in ("orc_relu", "orc_gelu"):
+            getattr(L, name).argtypes = [_f32p, _f32p, _i64]
+        for name in ("orc_relu_bwd", "orc_gelu_bwd"):
+            getattr(L, name).argtypes = [_f32p, _f32p, _f32p, _i64]
+        L.orc_add_bias.argtypes = [_f32p, _f32p, _f32p, _i64, _i64]
+        L.orc_bias_grad.argtypes = [_f32p, _f32p, _i64, _i64]
+        L.orc_sum_all.argtypes = [_f32p, _i64]
+        L.orc_sum_all.restype = ctypes.c_float
+        L.orc_scaled_add.argtypes = [_f32p, _f32p, ctypes.c_float, _i64]
+        L.orc_embedding_fwd.argtypes = [_f32p, _i64p, _f32p, _i64, _i64, _i64]
+        L.orc_embedding_fwd.restype = ctypes.c_int
+        L.orc_embedding_bwd.argtypes = [_f32p, _i64p, _f32p, _i64, _i64, _i64]
+        L.orc_cross_entropy_fwd.argtypes = [_f32p, _i64p, ctypes.POINTER(ctypes.c_float), _i64, _i64, _i64]
+        L.orc_cross_entropy_fwd.restype = ctypes.c_int
+        L.orc_cross_entropy_bwd.argtypes = [ctypes.c_float, _f32p, _i64p, _f32p, _i64, _i64, _i64]
+        L.orc_adamw.argtypes = [_f32p, _f32p, _f32p, _f32p, _i64] + [ctypes.c_float] * 7
         _lib = L
     return _lib
 
@@ -77,7 +97,15 @@ def ref():
         R.ref_softmax.argtypes = [_f32p, vp, _f32p, vp, _i64, _i64]
         R.ref_layernorm.argtypes = [_f32p, _f32p, _f32p, vp, _f32p, vp, vp, vp, _i64, _i64, ctypes.c_float]
         R.ref_attention.argtypes = [_f32p, _f32p, _f32p, vp, _f32p, vp, vp, vp, _i64, _i64, _i64, ctypes.c_int]
-        for f in (R.ref_matmul, R.ref_softmax, R.ref_layernorm, R.ref_attention):
+        R.ref_elementwise.argtypes = [ctypes.c_int, _f32p, vp, ctypes.c_float, vp, _f32p, vp, _i64]
+        R.ref_add_bias.argtypes = [_f32p, _f32p, vp, _f32p, vp, _i64, _i64]
+        R.ref_sum_all.argtypes = [_f32p, _i64, ctypes.POINTER(ctypes.c_float)]
+        R.ref_embedding.argtypes = [_f32p, _i64p, vp, _f32p, vp, _i64, _i64, _i64]
+        R.ref_cross_entropy.argtypes = [_f32p, _i64p, _i64, _i64, _i64, ctypes.c_float,
+                                        ctypes.POINTER(ctypes.c_float), vp]
+        R.ref_adamw.argtypes = [_f32p, _f32p, _f32p, _f32p, _i64] + [ctypes.c_float] * 7
+        for f in (R.ref_matmul, R.ref_softmax, R.ref_layernorm, R.ref_attention, R.ref_elementwise,
+                  R.ref_add_bias, R.ref_sum_all, R.ref_embedding, R.ref_cross_entropy, R.ref_adamw):
             f.restype = ctypes.c_int
         _ref = R
     return _ref
@@ -239,3 +267,181 @@ def ref_attention(q, k, v, causal, dout=None):
     if rc != 0:
         raise RuntimeError("reference attention failed")
     return o, dq, dk, dv
+
+
+# ------------------------------------------------------ GPT-step ops (next row)
+def sub(a, b):
+    a, b = _c(a), _c(b)
+    c = np.empty_like(a)
+    lib().orc_sub(a, b, c, a.size)
+    return c
+
+
+def mul(a, b):
+    a, b = _c(a), _c(b)
+    c = np.empty_like(a)
+    lib().orc_mul(a, b, c, a.size)
+    return c
+
+
+def scale(x, alpha):
+    x = _c(x)
+    y = np.empty_like(x)
+    lib().orc_scale(x, y, alpha, x.size)
+    return y
+
+
+def relu(x):
+    x = _c(x)
+    y = np.empty_like(x)
+    lib().orc_relu(x, y, x.size)
+    return y
+
+
+def relu_backward(g, x):
+    g, x = _c(g), _c(x)
+    d = np.empty_like(x)
+    lib().orc_relu_bwd(g, x, d, x.size)
+    return d
+
+
+def gelu(x):
+    x = _c(x)
+    y = np.empty_like(x)
+    lib().orc_gelu(x, y, x.size)
+    return y
+
+
+def gelu_backward(g, x):
+    g, x = _c(g), _c(x)
+    d = np.empty_like(x)
+    lib().orc_gelu_bwd(g, x, d, x.size)
+    return d
+
+
+def add_bias(x, bias):
+    x, bias = _c(x), _c(bias)
+    y = np.empty_like(x)
+    lib().orc_add_bias(x, bias, y, x.size, bias.size)
+    return y
+
+
+def bias_grad(g, D):
+    g = _c(g)
+    db = np.empty(D, np.float32)
+    lib().orc_bias_grad(g, db, g.size, D)
+    return db
+
+
+def sum_all(x):
+    x = _c(x)
+    return np.float32(lib().orc_sum_all(x, x.size))
+
+
+def scaled_add(dst, src, alpha):
+    dst = _c(dst).copy()
+    lib().orc_scaled_add(dst, _c(src), alpha, dst.size)
+    return dst
+
+
+def embedding(w, ids):
+    w = _c(w)
+    ids = np.ascontiguousarray(ids, np.int64)
+    V, D = w.shape
+    out = np.empty(ids.shape + (D,), np.float32)
+    if lib().orc_embedding_fwd(w, ids.reshape(-1), out.reshape(-1, D), ids.size, V, D) != 0:
+        raise IndexError("embedding: id out of range [0, vocab_size)")
+    return out
+
+
+def embedding_backward(g, ids, vocab):
+    ids = np.ascontiguousarray(ids, np.int64).reshape(-1)
+    g = _c(g).reshape(ids.size, -1)
+    dw = np.empty((vocab, g.shape[1]), np.float32)
+    lib().orc_embedding_bwd(g, ids, dw, ids.size, vocab, g.shape[1])
+    return dw
+
+
+def cross_entropy(logits, targets, ignore_index=-100):
+    logits = _c(logits)
+    targets = np.ascontiguousarray(targets, np.int64)
+    N, V = logits.shape
+    out = ctypes.c_float()
+    if lib().orc_cross_entropy_fwd(logits, targets, ctypes.byref(out), N, V, ignore_index) != 0:
+        raise IndexError("cross_entropy: target out of range [0, V)")
+    return np.float32(out.value)
+
+
+def cross_entropy_backward(go, logits, targets, ignore_index=-100):
+    logits = _c(logits)
+    targets = np.ascontiguousarray(targets, np.int64)
+    N, V = logits.shape
+    d = np.empty_like(logits)
+    lib().orc_cross_entropy_bwd(go, logits, targets, d, N, V, ignore_index)
+    return d
+
+
+def adamw(p, g, m, v, lr, b1, b2, eps, wd, bc1, bc2):
+    p, m, v = _c(p).copy(), _c(m).copy(), _c(v).copy()
+    lib().orc_adamw(p, _c(g), m, v, p.size, lr, b1, b2, eps, wd, bc1, bc2)
+    return p, m, v
+
+
+def ref_elementwise(op, a, b=None, alpha=0.0, g=None):
+    a = _c(a)
+    b = _c(b) if b is not None else None
+    g = _c(g) if g is not None else None
+    y = np.empty_like(a)
+    da = np.empty_like(a) if g is not None else None
+    code = {"sub": 0, "mul": 1, "scale": 2, "relu": 3, "gelu": 4}[op]
+    if ref().ref_elementwise(code, a, _ptr(b), alpha, _ptr(g), y, _ptr(da), a.size) != 0:
+        raise RuntimeError("reference elementwise failed")
+    return (y, da) if g is not None else y
+
+
+def ref_add_bias(x, bias, g=None):
+    x, bias = _c(x), _c(bias)
+    y = np.empty_like(x)
+    db = np.empty_like(bias) if g is not None else None
+    g = _c(g) if g is not None else None
+    if ref().ref_add_bias(x, bias, _ptr(g), y, _ptr(db), x.size // bias.size, bias.size) != 0:
+        raise RuntimeError("reference add_bias failed")
+    return (y, db) if g is not None else y
+
+
+def ref_sum_all(x):
+    x = _c(x)
+    r = ctypes.c_float()
+    if ref().ref_sum_all(x, x.size, ctypes.byref(r)) != 0:
+        raise RuntimeError("reference sum_all failed")
+    return np.float32(r.value)
+
+
+def ref_embedding(w, ids, g=None):
+    w = _c(w)
+    ids = np.ascontiguousarray(ids, np.int64).reshape(-1)
+    V, D = w.shape
+    y = np.empty((ids.size, D), np.float32)
+    dw = np.empty_like(w) if g is not None else None
+    g = _c(g) if g is not None else None
+    if ref().ref_embedding(w, ids, _ptr(g), y, _ptr(dw), ids.size, V, D) != 0:
+        raise RuntimeError("reference embedding failed")
+    return (y, dw) if g is not None else y
+
+
+def ref_cross_entropy(logits, targets, ignore_index=-100, go=None):
+    logits = _c(logits)
+    targets = np.ascontiguousarray(targets, np.int64)
+    N, V = logits.shape
+    loss = ctypes.c_float()
+    d = np.empty_like(logits) if go is not None else None
+    if ref().ref_cross_entropy(logits, targets, N, V, ignore_index, go or 0.0, ctypes.byref(loss), _ptr(d)) != 0:
+        raise RuntimeError("reference cross_entropy failed")
+    return (np.float32(loss.value), d) if go is not None else np.float32(loss.value)
+
+
+def ref_adamw(p, g, m, v, lr, b1, b2, eps, wd, bc1, bc2):
+    p, m, v = _c(p).copy(), _c(m).copy(), _c(v).copy()
+    if ref().ref_adamw(p, _c(g), m, v, p.size, lr, b1, b2, eps, wd, bc1, bc2) != 0:
+        raise RuntimeError("reference adamw failed")
+    return p, m, v

@@ -33,6 +33,11 @@
  *                       independently in numpy.
  *   orc_add             exact (c = a + b in fp32), fan-in KATs of
  *                       tests/cpp/test_autograd.cpp:169-186.
+ *   GPT-step ops        (sub, mul, scale, relu, gelu, add_bias, bias_grad,
+ *                       sum_all, scaled_add, embedding, cross_entropy, adamw):
+ *                       KATs of tests/cpp/test_elementwise.cpp and
+ *                       tests/python/test_{embedding,cross_entropy,adamw}.py,
+ *                       float64 closed forms, bit-exact vs oracle/_ref.
  */
 #include <math.h>
 #include <stdint.h>
@@ -336,4 +341,147 @@ void orc_attention_lse(const float* Q, const float* K, double* L, int64_t bh, in
 /* cppsrc/autograd/backward.cpp:28-35: c = a + b. */
 void orc_add(const float* a, const float* b, float* c, int64_t n) {
   for (int64_t i = 0; i < n; ++i) c[i] = a[i] + b[i];
+}
+
+/* ------------------------------------------------- GPT-step ops (next row) */
+
+/* cppsrc/ops/elementwise.cpp:104-112 */
+void orc_sub(const float* a, const float* b, float* c, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) c[i] = a[i] - b[i];
+}
+/* cppsrc/ops/elementwise.cpp:54-62 */
+void orc_mul(const float* a, const float* b, float* c, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) c[i] = a[i] * b[i];
+}
+/* cppsrc/ops/elementwise.cpp:64-71 */
+void orc_scale(const float* x, float* y, float alpha, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) y[i] = alpha * x[i];
+}
+/* cppsrc/ops/elementwise.cpp:73-80 (std::max(0.0f, x)) */
+void orc_relu(const float* x, float* y, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) y[i] = x[i] > 0.0f ? x[i] : 0.0f;
+}
+/* cppsrc/ops/elementwise.cpp:210-218 */
+void orc_relu_bwd(const float* g, const float* x, float* dx, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) dx[i] = x[i] > 0.0f ? g[i] : 0.0f;
+}
+/* cppsrc/ops/elementwise.cpp:131-141 (exact erf GELU) */
+void orc_gelu(const float* x, float* y, int64_t n) {
+  const float inv_sqrt2 = 0.70710678118654752440f;
+  for (int64_t i = 0; i < n; ++i) y[i] = 0.5f * x[i] * (1.0f + erff(x[i] * inv_sqrt2));
+}
+/* cppsrc/ops/elementwise.cpp:143-159 */
+void orc_gelu_bwd(const float* g, const float* x, float* dx, int64_t n) {
+  const float inv_sqrt2 = 0.70710678118654752440f;
+  const float inv_sqrt_2pi = 0.39894228040143267794f;
+  for (int64_t i = 0; i < n; ++i) {
+    const float xi = x[i];
+    const float cdf = 0.5f * (1.0f + erff(xi * inv_sqrt2));
+    const float pdf = inv_sqrt_2pi * expf(-0.5f * xi * xi);
+    dx[i] = g[i] * (cdf + xi * pdf);
+  }
+}
+/* cppsrc/ops/elementwise.cpp:180-189: y[i] = x[i] + bias[i % D] */
+void orc_add_bias(const float* x, const float* bias, float* y, int64_t n, int64_t D) {
+  for (int64_t i = 0; i < n; ++i) y[i] = x[i] + bias[i % D];
+}
+/* cppsrc/ops/elementwise.cpp:191-199: db[i % D] += g[i] in element order */
+void orc_bias_grad(const float* g, float* db, int64_t n, int64_t D) {
+  memset(db, 0, (size_t)D * sizeof(float));
+  for (int64_t i = 0; i < n; ++i) db[i % D] += g[i];
+}
+/* cppsrc/ops/elementwise.cpp:82-90: sequential fp32 sum */
+float orc_sum_all(const float* x, int64_t n) {
+  float acc = 0.0f;
+  for (int64_t i = 0; i < n; ++i) acc += x[i];
+  return acc;
+}
+/* cppsrc/ops/elementwise.cpp:473: d[i] += alpha * s[i] */
+void orc_scaled_add(float* dst, const float* src, float alpha, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) dst[i] += alpha * src[i];
+}
+/* cppsrc/ops/embedding.cpp:16-34; returns -1 on an id outside [0, V) */
+int orc_embedding_fwd(const float* w, const int64_t* ids, float* out, int64_t n, int64_t V, int64_t D) {
+  for (int64_t i = 0; i < n; ++i) {
+    const int64_t idx = ids[i];
+    if (idx < 0 || idx >= V) return -1;
+    memcpy(out + i * D, w + idx * D, (size_t)D * sizeof(float));
+  }
+  return 0;
+}
+/* cppsrc/ops/embedding.cpp:36-50: rows accumulated in token order */
+void orc_embedding_bwd(const float* g, const int64_t* ids, float* dw, int64_t n, int64_t V, int64_t D) {
+  memset(dw, 0, (size_t)V * (size_t)D * sizeof(float));
+  for (int64_t i = 0; i < n; ++i) {
+    const float* grow = g + i * D;
+    float* drow = dw + ids[i] * D;
+    for (int64_t k = 0; k < D; ++k) drow[k] += grow[k];
+  }
+}
+/* cppsrc/ops/cross_entropy.cpp:20-49: per-row float lse, double total over
+ * active rows, float mean; returns -1 on a target outside [0, V). */
+int orc_cross_entropy_fwd(const float* L, const int64_t* T, float* loss, int64_t N, int64_t V,
+                          int64_t ignore_index) {
+  double total = 0.0;
+  int64_t active = 0;
+  for (int64_t i = 0; i < N; ++i) {
+    const int64_t t = T[i];
+    if (t == ignore_index) continue;
+    if (t < 0 || t >= V) return -1;
+    const float* row = L + i * V;
+    float m = row[0];
+    for (int64_t v = 1; v < V; ++v)
+      if (row[v] > m) m = row[v];
+    float s = 0.0f;
+    for (int64_t v = 0; v < V; ++v) s += expf(row[v] - m);
+    const float lse = m + logf(s);
+    total += (double)(lse - row[t]);
+    ++active;
+  }
+  *loss = active > 0 ? (float)(total / (double)active) : 0.0f;
+  return 0;
+}
+/* cppsrc/ops/cross_entropy.cpp:51-85 */
+void orc_cross_entropy_bwd(float go, const float* L, const int64_t* T, float* DL, int64_t N, int64_t V,
+                           int64_t ignore_index) {
+  memset(DL, 0, (size_t)N * (size_t)V * sizeof(float));
+  int64_t active = 0;
+  for (int64_t i = 0; i < N; ++i)
+    if (T[i] != ignore_index) ++active;
+  if (active == 0) return;
+  const float scale = go / (float)active;
+  for (int64_t i = 0; i < N; ++i) {
+    const int64_t t = T[i];
+    if (t == ignore_index) continue;
+    const float* row = L + i * V;
+    float* drow = DL + i * V;
+    float m = row[0];
+    for (int64_t v = 1; v < V; ++v)
+      if (row[v] > m) m = row[v];
+    float s = 0.0f;
+    for (int64_t v = 0; v < V; ++v) {
+      drow[v] = expf(row[v] - m);
+      s += drow[v];
+    }
+    const float inv_s = 1.0f / s;
+    for (int64_t v = 0; v < V; ++v) drow[v] = (drow[v] * inv_s) * scale;
+    drow[t] -= scale;
+  }
+}
+/* cppsrc/ops/adamw.cpp:27-45 */
+void orc_adamw(float* p, const float* g, float* mp, float* vp, int64_t n, float lr, float beta1, float beta2,
+               float eps, float weight_decay, float bc1, float bc2) {
+  const float one_minus_b1 = 1.0f - beta1;
+  const float one_minus_b2 = 1.0f - beta2;
+  const float wd_factor = 1.0f - lr * weight_decay;
+  for (int64_t i = 0; i < n; ++i) {
+    const float gi = g[i];
+    const float mi = beta1 * mp[i] + one_minus_b1 * gi;
+    const float vi = beta2 * vp[i] + one_minus_b2 * gi * gi;
+    mp[i] = mi;
+    vp[i] = vi;
+    const float m_hat = mi / bc1;
+    const float v_hat = vi / bc2;
+    p[i] = p[i] * wd_factor - lr * m_hat / (sqrtf(v_hat) + eps);
+  }
 }

@@ -13,6 +13,10 @@
 #include <vector>
 
 #include "core/tensor.hpp"
+#include "ops/adamw.hpp"
+#include "ops/cross_entropy.hpp"
+#include "ops/elementwise.hpp"
+#include "ops/embedding.hpp"
 #include "ops/flash_attention.hpp"
 #include "ops/layernorm.hpp"
 #include "ops/matmul.hpp"
@@ -107,6 +111,115 @@ int ref_attention(const float* q, const float* k, const float* v, const float* d
       out(*kt.grad(), dk);
       out(*vt.grad(), dv);
     }
+    return 0;
+  } catch (const std::exception&) {
+    return -1;
+  }
+}
+
+// Unary/binary elementwise ops, forward and (when g != NULL) the gradient of
+// sum(y * g) with respect to a, via autograd.
+// op: 0 sub(a,b), 1 mul(a,b), 2 scale(a,alpha), 3 relu(a), 4 gelu(a)
+int ref_elementwise(int op, const float* a, const float* b, float alpha, const float* g, float* y,
+                    float* da, int64_t n) {
+  try {
+    const bool grad = g != nullptr;
+    Tensor ta = make(a, {n}, grad);
+    Tensor tb = b ? make(b, {n}) : Tensor();
+    Tensor ty;
+    switch (op) {
+      case 0: ty = vlm::sub(ta, tb); break;
+      case 1: ty = vlm::mul(ta, tb); break;
+      case 2: ty = vlm::scale(ta, alpha); break;
+      case 3: ty = vlm::relu(ta); break;
+      default: ty = vlm::gelu(ta); break;
+    }
+    out(ty, y);
+    if (grad) {
+      ty.backward(make(g, {n}));
+      out(*ta.grad(), da);
+    }
+    return 0;
+  } catch (const std::exception&) {
+    return -1;
+  }
+}
+
+int ref_add_bias(const float* x, const float* bias, const float* g, float* y, float* dbias, int64_t rows,
+                 int64_t cols) {
+  try {
+    Tensor tx = make(x, {rows, cols});
+    Tensor tb = make(bias, {cols}, g != nullptr);
+    Tensor ty = vlm::add_bias(tx, tb);
+    out(ty, y);
+    if (g) {
+      ty.backward(make(g, {rows, cols}));
+      out(*tb.grad(), dbias);
+    }
+    return 0;
+  } catch (const std::exception&) {
+    return -1;
+  }
+}
+
+int ref_sum_all(const float* x, int64_t n, float* result) {
+  try {
+    Tensor s = vlm::sum_all(make(x, {n}));
+    *result = *static_cast<const float*>(s.data());
+    return 0;
+  } catch (const std::exception&) {
+    return -1;
+  }
+}
+
+int ref_embedding(const float* w, const int64_t* ids, const float* g, float* y, float* dw, int64_t n,
+                  int64_t vocab, int64_t dim) {
+  try {
+    Tensor tw = make(w, {vocab, dim}, g != nullptr);
+    Tensor ti = Tensor::empty({n}, DType::Int64);
+    std::memcpy(ti.data(), ids, n * sizeof(int64_t));
+    Tensor ty = vlm::embedding(tw, ti);
+    out(ty, y);
+    if (g) {
+      ty.backward(make(g, {n, dim}));
+      out(*tw.grad(), dw);
+    }
+    return 0;
+  } catch (const std::exception&) {
+    return -1;
+  }
+}
+
+// loss = cross_entropy(logits, targets); when dlogits != NULL also the
+// gradient for an upstream scalar grad `go`.
+int ref_cross_entropy(const float* logits, const int64_t* targets, int64_t n, int64_t vocab,
+                      int64_t ignore_index, float go, float* loss, float* dlogits) {
+  try {
+    Tensor tl = make(logits, {n, vocab}, dlogits != nullptr);
+    Tensor tt = Tensor::empty({n}, DType::Int64);
+    std::memcpy(tt.data(), targets, n * sizeof(int64_t));
+    Tensor l = vlm::cross_entropy(tl, tt, ignore_index);
+    *loss = *static_cast<const float*>(l.data());
+    if (dlogits) {
+      Tensor seed = Tensor::empty({}, DType::Fp32);
+      *static_cast<float*>(seed.data()) = go;
+      l.backward(seed);
+      out(*tl.grad(), dlogits);
+    }
+    return 0;
+  } catch (const std::exception&) {
+    return -1;
+  }
+}
+
+int ref_adamw(float* p, const float* g, float* m, float* v, int64_t n, float lr, float b1, float b2, float eps,
+              float wd, float bc1, float bc2) {
+  try {
+    Tensor tp = make(p, {n}), tg = make(g, {n}), tm = make(m, {n}), tv = make(v, {n});
+    vlm::adamw_step(tp, tg, tm, tv, lr, b1, b2, eps, wd, bc1, bc2);
+    out(tp, p);
+    out(tm, m);
+    out(tv, v);
     return 0;
   } catch (const std::exception&) {
     return -1;

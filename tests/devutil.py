@@ -11,7 +11,8 @@ LIB = Path(__file__).resolve().parent.parent / "aar-vlm_amd" / "aargrad" / "liba
 
 
 def dev(ag, arr, requires_grad=False):
-    t = ag.from_numpy(np.ascontiguousarray(arr, np.float32)).to(ag.Device.CUDA)
+    # np.array (not ascontiguousarray) keeps 0-d arrays 0-d
+    t = ag.from_numpy(np.array(arr, dtype=np.float32, order="C")).to(ag.Device.CUDA)
     if requires_grad:
         t.requires_grad = True
     return t

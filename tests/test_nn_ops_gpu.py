@@ -1,0 +1,153 @@
+"""GPU parity of the GPT-step ops against the oracle: elementwise family,
+bias add/grad, sum_all, SGD/AdamW updates, embedding (one-hot MFMA backward)
+and cross entropy, including ignore_index, deferred out-of-range errors and
+bit-reproducible reductions.  Tolerance 1e-4 (both metrics) except where the
+op is exact."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle as O
+from conftest import TOL, assert_close
+from devutil import dev, host
+
+pytestmark = pytest.mark.gpu
+f32 = np.float32
+
+
+def ids_dev(gpu, ids):
+    return gpu.from_numpy(np.ascontiguousarray(ids, np.int64)).to(gpu.Device.CUDA)
+
+
+@pytest.mark.parametrize("n", [1, 7, 4096, 1_000_003])
+def test_elementwise_family(gpu, n):
+    rng = np.random.default_rng(n)
+    a, b, g = (rng.standard_normal(n).astype(f32) for _ in range(3))
+    ta, tb = dev(gpu, a, True), dev(gpu, b, True)
+    np.testing.assert_array_equal(host(gpu, gpu.sub(ta, tb)), O.sub(a, b))
+    np.testing.assert_array_equal(host(gpu, gpu.mul(ta, tb)), O.mul(a, b))
+    np.testing.assert_array_equal(host(gpu, gpu.scale(ta, 0.37)), O.scale(a, 0.37))
+    np.testing.assert_array_equal(host(gpu, gpu.relu(ta)), O.relu(a))
+    assert_close(host(gpu, gpu.gelu(ta)), O.gelu(a), 1e-6, "gelu")
+    # backward legs through autograd
+    for name, fn, ref in (("relu", gpu.relu, O.relu_backward(g, a)), ("gelu", gpu.gelu, O.gelu_backward(g, a))):
+        x = dev(gpu, a, True)
+        fn(x).backward(dev(gpu, g))
+        assert_close(host(gpu, x.grad), ref, 1e-6, f"{name} backward")
+    x, y = dev(gpu, a, True), dev(gpu, b, True)
+    gpu.mul(x, y).backward(dev(gpu, g))
+    np.testing.assert_array_equal(host(gpu, x.grad), O.mul(g, b))
+    np.testing.assert_array_equal(host(gpu, y.grad), O.mul(g, a))
+    x, y = dev(gpu, a, True), dev(gpu, b, True)
+    gpu.sub(x, y).backward(dev(gpu, g))
+    np.testing.assert_array_equal(host(gpu, x.grad), g)
+    np.testing.assert_array_equal(host(gpu, y.grad), -g)
+
+
+@pytest.mark.parametrize("rows,cols", [(1, 1), (3, 5), (16384, 1536), (16384, 384), (1000, 65)])
+def test_bias_add_and_grad(gpu, rows, cols):
+    rng = np.random.default_rng(rows + cols)
+    x = rng.standard_normal((rows, cols)).astype(f32)
+    bias = rng.standard_normal(cols).astype(f32)
+    g = rng.standard_normal((rows, cols)).astype(f32)
+    tx, tb = dev(gpu, x, True), dev(gpu, bias, True)
+    y = gpu.add_bias(tx, tb)
+    y.backward(dev(gpu, g))
+    np.testing.assert_array_equal(host(gpu, y), O.add_bias(x, bias))
+    np.testing.assert_array_equal(host(gpu, tx.grad), g)
+    assert_close(host(gpu, tb.grad), O.bias_grad(g, cols), TOL, "bias grad")
+
+
+@pytest.mark.parametrize("n", [1, 10, 1000, 1 << 20, 3_000_001])
+def test_sum_all_and_backward(gpu, n):
+    rng = np.random.default_rng(n)
+    x = rng.standard_normal(n).astype(f32)
+    tx = dev(gpu, x, True)
+    s = gpu.sum_all(tx)
+    assert s.shape == []
+    got = host(gpu, s)
+    ref64 = x.astype(np.float64).sum()
+    assert abs(float(got) - ref64) <= TOL * max(np.abs(x).sum(), 1.0)
+    s.backward()
+    np.testing.assert_array_equal(host(gpu, tx.grad), np.ones(n, f32))
+    # reproducible
+    assert host(gpu, gpu.sum_all(dev(gpu, x))) == got
+
+
+def test_sum_all_reference_kat(gpu):
+    # tests/cpp/test_autograd_ops.cpp:45-85: CUDA sum/mul fan-out, add_grads on device
+    a = dev(gpu, np.array([1, 2, 3, 4], f32), True)
+    gpu.sum_all(gpu.mul(a, a)).backward()
+    np.testing.assert_array_equal(host(gpu, a.grad), [2, 4, 6, 8])
+
+
+def test_sgd_and_adamw(gpu):
+    rng = np.random.default_rng(3)
+    p, g = rng.standard_normal(10001).astype(f32), rng.standard_normal(10001).astype(f32)
+    tp = dev(gpu, p)
+    gpu.scaled_add_inplace(tp, dev(gpu, g), -1e-3)
+    # the device may fuse p + alpha*g into one fma: agreement to rounding
+    assert_close(host(gpu, tp), O.scaled_add(p, g, -1e-3), 1e-6, "sgd")
+    m, v = (0.1 * rng.standard_normal(10001)).astype(f32), np.abs(0.1 * rng.standard_normal(10001)).astype(f32)
+    tp, tm, tv = dev(gpu, p), dev(gpu, m), dev(gpu, v)
+    gpu.adamw_step(tp, dev(gpu, g), tm, tv, 1e-3, 0.9, 0.999, 1e-8, 0.01, 0.19, 0.002)
+    rp, rm, rv = O.adamw(p, g, m, v, 1e-3, 0.9, 0.999, 1e-8, 0.01, 0.19, 0.002)
+    assert_close(host(gpu, tm), rm, 1e-6, "m")
+    assert_close(host(gpu, tv), rv, 1e-6, "v")
+    assert_close(host(gpu, tp), rp, 1e-6, "p")
+
+
+@pytest.mark.parametrize("vocab,dim,shape", [(7, 4, (2, 3)), (65, 384, (64, 256)), (256, 384, (64, 256)),
+                                             (5, 3, (6,))])
+def test_embedding_fwd_bwd(gpu, vocab, dim, shape):
+    rng = np.random.default_rng(vocab + dim)
+    w = rng.standard_normal((vocab, dim)).astype(f32)
+    ids = rng.integers(0, vocab, shape)
+    g = rng.standard_normal(shape + (dim,)).astype(f32)
+    tw = dev(gpu, w, True)
+    y = gpu.embedding(tw, ids_dev(gpu, ids))
+    assert y.shape == list(shape) + [dim]
+    np.testing.assert_array_equal(host(gpu, y), O.embedding(w, ids))
+    y.backward(dev(gpu, g))
+    assert_close(host(gpu, tw.grad), O.embedding_backward(g, ids, vocab), TOL, "embedding dW")
+
+
+def test_embedding_out_of_range_is_reported(gpu):
+    w = dev(gpu, np.ones((5, 3), f32))
+    y = gpu.embedding(w, ids_dev(gpu, np.array([1, 5], np.int64)))  # 5 is out of range
+    with pytest.raises(IndexError):
+        host(gpu, y)
+    # the flag is cleared after reporting
+    np.testing.assert_array_equal(host(gpu, gpu.embedding(w, ids_dev(gpu, np.array([0], np.int64)))),
+                                  np.ones((1, 3), f32))
+
+
+@pytest.mark.parametrize("N,V", [(6, 5), (4, 6), (16384, 65), (1000, 300)])
+def test_cross_entropy_fwd_bwd(gpu, N, V):
+    rng = np.random.default_rng(N + V)
+    logits = (2 * rng.standard_normal((N, V))).astype(f32)
+    t = rng.integers(0, V, N)
+    t[::7] = -100
+    tl = dev(gpu, logits, True)
+    loss = gpu.cross_entropy(tl, ids_dev(gpu, t))
+    assert loss.shape == []
+    got = float(host(gpu, loss))
+    ref = float(O.cross_entropy(logits, t))
+    assert abs(got - ref) <= TOL * max(abs(ref), 1.0)
+    go = np.array(1.7, f32)
+    loss.backward(dev(gpu, go))
+    assert_close(host(gpu, tl.grad), O.cross_entropy_backward(1.7, logits, t), TOL, "dlogits")
+
+
+def test_cross_entropy_all_ignored_and_errors(gpu):
+    logits = dev(gpu, np.zeros((3, 4), f32), True)
+    loss = gpu.cross_entropy(logits, ids_dev(gpu, np.full(3, -100, np.int64)))
+    assert float(host(gpu, loss)) == 0.0
+    loss.backward()
+    np.testing.assert_array_equal(host(gpu, logits.grad), np.zeros((3, 4), f32))
+    bad = gpu.cross_entropy(dev(gpu, np.zeros((2, 4), f32)), ids_dev(gpu, np.array([0, 4], np.int64)))
+    with pytest.raises(IndexError):
+        host(gpu, bad)
+    with pytest.raises(ValueError, match="targets must be Int64"):
+        gpu.cross_entropy(logits, dev(gpu, np.zeros(3, f32)))
