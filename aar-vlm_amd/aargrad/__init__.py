@@ -56,6 +56,9 @@ from ._core import (  # noqa: E402
     cuda_synchronize,
 )
 
+from . import nn  # noqa: E402
+from . import optim  # noqa: E402
+
 __all__ = [
     "Tensor",
     "DType",
@@ -93,6 +96,8 @@ __all__ = [
     "adamw_step",
     "flash_attention",
     "cuda_synchronize",
+    "nn",
+    "optim",
 ]
 
 

@@ -247,6 +247,136 @@ def bench_copy(ev: Events, iters: int = 5, n: int = 1 << 26):
     return {"n": n, "read_bytes": 8 * n, "write_bytes": 4 * n, "ms": ms, "GB_s": 12 * n / (ms * 1e-3) / 1e9}
 
 
+# ----------------------------------------------------------------- GPT step
+# decoder-only char GPT, 6 layers, d_model 384, 6 heads,
+# context 256, batch 64, vocab 65, pre-LN, 4x ReLU MLP (biased), bias-free
+# attention, final LN, bias-free head, mean cross entropy, SGD lr 1e-3;
+# weights N(0, 0.02), LN gamma 1 / beta 0, biases 0; ids uniform in [0, 65).
+GPT5 = dict(vocab=65, ctx=256, layers=6, d_model=384, heads=6, batch=64)
+
+
+def gpt_param_shapes(vocab, ctx, layers, d_model, **_):
+    """Parameter shapes in Module.parameters() order (tok_emb, pos_emb, then per
+    block ln1 w/b, qkv W, out W, ln2 w/b, fc1 W/b, fc2 W/b; ln_f w/b; head W)."""
+    d, f = d_model, 4 * d_model
+    shapes = [("tok_emb", (vocab, d)), ("pos_emb", (ctx, d))]
+    for i in range(layers):
+        shapes += [(f"b{i}.ln1.w", (d,)), (f"b{i}.ln1.b", (d,)), (f"b{i}.qkv", (3 * d, d)),
+                   (f"b{i}.out", (d, d)), (f"b{i}.ln2.w", (d,)), (f"b{i}.ln2.b", (d,)),
+                   (f"b{i}.fc1.w", (f, d)), (f"b{i}.fc1.b", (f,)), (f"b{i}.fc2.w", (d, f)), (f"b{i}.fc2.b", (d,))]
+    shapes += [("ln_f.w", (d,)), ("ln_f.b", (d,)), ("head", (vocab, d))]
+    return shapes
+
+
+def gpt_init_params(cfg, seed=0):
+    rng = np.random.default_rng(seed)
+    out = []
+    for name, shape in gpt_param_shapes(**cfg):
+        if name.endswith((".ln1.w", ".ln2.w")) or name == "ln_f.w":
+            out.append(np.ones(shape, np.float32))
+        elif name.endswith((".ln1.b", ".ln2.b", ".fc1.b", ".fc2.b")) or name == "ln_f.b":
+            out.append(np.zeros(shape, np.float32))
+        else:
+            out.append((0.02 * rng.standard_normal(shape)).astype(np.float32))
+    return out
+
+
+def gpt_tokens(cfg, batch, seed=1):
+    ids = np.random.default_rng(seed).integers(0, cfg["vocab"], (batch, cfg["ctx"] + 1)).astype(np.int64)
+    return np.ascontiguousarray(ids[:, :-1]), np.ascontiguousarray(ids[:, 1:])
+
+
+class GPT:
+    """Config-5 GPT on aargrad (same composition as the reference's
+    python/shakespeare/scripts/model.py with ReLU and no dropout)."""
+
+    def __init__(self, ag, cfg, params):
+        self.ag, self.cfg = ag, cfg
+        self.p = []
+        for arr in params:
+            t = ag.from_numpy(arr).to(ag.Device.CUDA)
+            t.requires_grad = True
+            self.p.append(t)
+
+    def forward(self, ids, pos):
+        ag, c, p = self.ag, self.cfg, self.p
+        B, T = ids.shape
+        d, H = c["d_model"], c["heads"]
+        x = ag.add(ag.embedding(p[0], ids), ag.embedding(p[1], pos))
+        for i in range(c["layers"]):
+            (l1w, l1b, wqkv, wout, l2w, l2b, f1w, f1b, f2w, f2b) = p[2 + 10 * i: 12 + 10 * i]
+            h = ag.layernorm(x, l1w, l1b, 1e-5)
+            qkv = ag.reshape(ag.matmul_a_bt(h, wqkv), [B, T, 3, H, d // H])
+            q, k, v = (ag.transpose(ag.squeeze(ag.slice(qkv, 2, j, j + 1), 2), 1, 2) for j in range(3))
+            a = ag.reshape(ag.transpose(ag.flash_attention(q, k, v, True), 1, 2), [B, T, d])
+            x = ag.add(x, ag.matmul_a_bt(a, wout))
+            h = ag.layernorm(x, l2w, l2b, 1e-5)
+            h = ag.relu(ag.add_bias(ag.matmul_a_bt(h, f1w), f1b))
+            x = ag.add(x, ag.add_bias(ag.matmul_a_bt(h, f2w), f2b))
+        x = ag.layernorm(x, p[-3], p[-2], 1e-5)
+        return ag.matmul_a_bt(x, p[-1])
+
+    def step(self, ids, pos, targets, lr):
+        ag = self.ag
+        logits = self.forward(ids, pos)
+        B, T = ids.shape
+        loss = ag.cross_entropy(ag.reshape(logits, [B * T, self.cfg["vocab"]]), targets, -100)
+        for t in self.p:
+            t.zero_grad()
+        loss.backward()
+        for t in self.p:
+            ag.scaled_add_inplace(t, t.grad, -lr)
+        return loss
+
+
+def gpt_flops_per_step(cfg, batch):
+    d, L, T, V, H = cfg["d_model"], cfg["layers"], cfg["ctx"], cfg["vocab"], cfg["heads"]
+    linear_weights = L * (3 * d * d + d * d + 2 * 4 * d * d) + V * d
+    gemm = 6.0 * linear_weights * batch * T
+    attn = L * 7.0 * batch * H * T * T * (d // H)  # causal fwd (2) + bwd (5), halved by the mask
+    return gemm + attn
+
+
+def bench_gpt(ag, ev: Events, steps: int = 10, warmup: int = 3, cfg=GPT5):
+    B, T = cfg["batch"], cfg["ctx"]
+    params = gpt_init_params(cfg)
+    model = GPT(ag, cfg, params)
+    ids_np, tgt_np = gpt_tokens(cfg, B)
+    ids = ag.from_numpy(ids_np).to(ag.Device.CUDA)
+    tgt = ag.from_numpy(tgt_np.reshape(-1)).to(ag.Device.CUDA)
+    pos = ag.from_numpy(np.tile(np.arange(T, dtype=np.int64), (B, 1))).to(ag.Device.CUDA)
+    for _ in range(warmup):
+        model.step(ids, pos, tgt, 1e-3)
+    ag.cuda_synchronize()
+    ev.start()
+    for _ in range(steps):
+        loss = model.step(ids, pos, tgt, 1e-3)
+    ms = ev.stop_ms() / steps
+    ag.cuda_synchronize()
+    last = float(ag.to_numpy(loss.to(ag.Device.CPU)))
+    tokens = B * T
+    return {"tokens_per_s": round(tokens / (ms * 1e-3), 1), "ms_per_step": round(ms, 3),
+            "implied_tflops": round(gpt_flops_per_step(cfg, B) / (ms * 1e-3) / 1e12, 2),
+            "loss_after_steps": round(last, 5), "batch": B, "ctx": T,
+            "config": "6 layers, d_model 384, 6 heads, ctx 256, batch 64, vocab 65, ReLU MLP, SGD lr 1e-3"}
+
+
+def cpu_baseline_gpt(cfg=GPT5, batch: int = 2):
+    """The reference's own CPU GPT step (oracle/_ref, built from its sources)
+    on one core at a reduced batch: tokens/s = batch*ctx / t_step."""
+    import oracle
+
+    if not oracle.ref_available():
+        return None
+    params = gpt_init_params(cfg)
+    ids, tgt = gpt_tokens(cfg, batch)
+    t0 = time.perf_counter()
+    oracle.ref_gpt_step(cfg, params, ids, tgt, 1e-3)
+    t = time.perf_counter() - t0
+    return {"tokens_per_s": round(batch * cfg["ctx"] / t, 2), "s_per_step": round(t, 2), "batch": batch,
+            "cores": 1, "kind": "reference"}
+
+
 def cpu_baseline_matmul(ab, budget_s: float = 12.0):
     """The reference CPU path (oracle/_ref: the reference's own matmul built
     from its sources; else the C restatement) on one core, on a row band of
@@ -291,7 +421,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=60)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--flash-steps", type=int, default=6)
-    ap.add_argument("--only", choices=["all", "gemm", "flash", "rowwise", "copy"], default="all",
+    ap.add_argument("--only", choices=["all", "gemm", "flash", "rowwise", "copy", "gpt"], default="all",
                     help="run one part (profiling runs); the JSON line is printed for 'all'")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -314,6 +444,9 @@ def main() -> int:
     if args.only == "rowwise":
         log(json.dumps(bench_rowwise(ev)))
         return 0
+    if args.only == "gpt":
+        log(json.dumps(bench_gpt(ag, ev)))
+        return 0
     if args.only == "flash":
         fa_ms, fa_flops = bench_flash(ag, args.flash_steps, 3, ev)
         log(f"flash fwd+bwd {fa_ms:.3f} ms {fa_flops / (fa_ms * 1e-3) / 1e12:.2f} TFLOPS")
@@ -334,6 +467,14 @@ def main() -> int:
     rowwise = bench_rowwise(ev)
     for k, v in rowwise.items():
         log(f"{k}: {v['GB_s']} GB/s ({100 * v['frac_of_hbm_peak']:.1f}% of HBM peak)")
+
+    gpt = bench_gpt(ag, ev)
+    log(f"GPT step (config 5): {gpt['tokens_per_s']:.0f} tokens/s, {gpt['ms_per_step']} ms/step, "
+        f"{gpt['implied_tflops']} TFLOPS implied")
+    if not args.no_cpu_baseline:
+        gpt["cpu_baseline"] = cpu_baseline_gpt()
+        if gpt["cpu_baseline"]:
+            log(f"GPT step reference CPU (batch 2, 1 core): {gpt['cpu_baseline']['tokens_per_s']} tokens/s")
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -367,6 +508,7 @@ def main() -> int:
             "config": "causal, B8 H12 T4096 d64, fwd+bwd, flops = 3.5 * 4*B*H*T^2*d/2",
         },
         "rowwise_hbm": rowwise,
+        "gpt_train_step": gpt,
         "roofline": {
             "bound": "mfma",
             "achieved": round(tflops, 3),

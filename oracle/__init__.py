@@ -104,6 +104,9 @@ def ref():
         R.ref_cross_entropy.argtypes = [_f32p, _i64p, _i64, _i64, _i64, ctypes.c_float,
                                         ctypes.POINTER(ctypes.c_float), vp]
         R.ref_adamw.argtypes = [_f32p, _f32p, _f32p, _f32p, _i64] + [ctypes.c_float] * 7
+        R.ref_gpt_step.argtypes = [_i64] * 6 + [ctypes.POINTER(ctypes.c_void_p), _i64p, _i64p, ctypes.c_float,
+                                                 ctypes.POINTER(ctypes.c_float)]
+        R.ref_gpt_step.restype = ctypes.c_int
         for f in (R.ref_matmul, R.ref_softmax, R.ref_layernorm, R.ref_attention, R.ref_elementwise,
                   R.ref_add_bias, R.ref_sum_all, R.ref_embedding, R.ref_cross_entropy, R.ref_adamw):
             f.restype = ctypes.c_int
@@ -445,3 +448,18 @@ def ref_adamw(p, g, m, v, lr, b1, b2, eps, wd, bc1, bc2):
     if ref().ref_adamw(p, _c(g), m, v, p.size, lr, b1, b2, eps, wd, bc1, bc2) != 0:
         raise RuntimeError("reference adamw failed")
     return p, m, v
+
+
+def ref_gpt_step(cfg, params, ids, targets, lr):
+    """One SGD step of the config-5 GPT on the reference CPU path.  Returns
+    (loss before the update, updated parameter arrays)."""
+    ps = [np.ascontiguousarray(p, np.float32).copy() for p in params]
+    ptrs = (ctypes.c_void_p * len(ps))(*[p.ctypes.data for p in ps])
+    ids = np.ascontiguousarray(ids, np.int64)
+    targets = np.ascontiguousarray(targets, np.int64).reshape(-1)
+    loss = ctypes.c_float()
+    rc = ref().ref_gpt_step(cfg["vocab"], cfg["ctx"], cfg["layers"], cfg["d_model"], cfg["heads"], ids.shape[0],
+                            ptrs, ids.reshape(-1), targets, lr, ctypes.byref(loss))
+    if rc != 0:
+        raise RuntimeError("reference gpt step failed")
+    return float(loss.value), ps

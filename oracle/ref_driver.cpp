@@ -20,6 +20,7 @@
 #include "ops/flash_attention.hpp"
 #include "ops/layernorm.hpp"
 #include "ops/matmul.hpp"
+#include "ops/shape.hpp"
 #include "ops/softmax.hpp"
 
 using vlm::DType;
@@ -220,6 +221,65 @@ int ref_adamw(float* p, const float* g, float* m, float* v, int64_t n, float lr,
     out(tp, p);
     out(tm, m);
     out(tv, v);
+    return 0;
+  } catch (const std::exception&) {
+    return -1;
+  }
+}
+
+// One SGD training step of the decoder-only GPT of BASELINE config 5 on the
+// reference CPU path, composed from the reference's public ops exactly as
+// python/shakespeare/scripts/model.py composes them (with ReLU and no
+// dropout).  params: pointers in Module.parameters() order (tok_emb, pos_emb,
+// per block ln1 w/b, qkv, out, ln2 w/b, fc1 w/b, fc2 w/b, then ln_f w/b,
+// head), updated in place; *loss_out receives the loss before the update.
+int ref_gpt_step(int64_t vocab, int64_t ctx, int64_t layers, int64_t d, int64_t heads, int64_t batch,
+                 float* const* params, const int64_t* ids, const int64_t* targets, float lr, float* loss_out) {
+  try {
+    const int64_t B = batch, T = ctx, f = 4 * d;
+    std::vector<std::vector<int64_t>> shapes = {{vocab, d}, {ctx, d}};
+    for (int64_t i = 0; i < layers; ++i) {
+      for (auto s : std::vector<std::vector<int64_t>>{{d}, {d}, {3 * d, d}, {d, d}, {d}, {d}, {f, d}, {f}, {d, f}, {d}})
+        shapes.push_back(s);
+    }
+    shapes.push_back({d});
+    shapes.push_back({d});
+    shapes.push_back({vocab, d});
+    std::vector<Tensor> P;
+    for (size_t i = 0; i < shapes.size(); ++i) P.push_back(make(params[i], shapes[i], true));
+
+    Tensor tids = Tensor::empty({B, T}, DType::Int64);
+    std::memcpy(tids.data(), ids, B * T * sizeof(int64_t));
+    Tensor pos = Tensor::empty({B, T}, DType::Int64);
+    for (int64_t b = 0; b < B; ++b)
+      for (int64_t t = 0; t < T; ++t) static_cast<int64_t*>(pos.data())[b * T + t] = t;
+    Tensor tgt = Tensor::empty({B * T}, DType::Int64);
+    std::memcpy(tgt.data(), targets, B * T * sizeof(int64_t));
+
+    Tensor x = vlm::add(vlm::embedding(P[0], tids), vlm::embedding(P[1], pos));
+    for (int64_t i = 0; i < layers; ++i) {
+      const Tensor* w = &P[2 + 10 * i];
+      Tensor h = vlm::layernorm(x, w[0], w[1], 1e-5f);
+      Tensor qkv = vlm::reshape(vlm::matmul_a_bt(h, w[2]), {B, T, 3, heads, d / heads});
+      Tensor q = vlm::transpose(vlm::squeeze(vlm::slice(qkv, 2, 0, 1), 2), 1, 2);
+      Tensor k = vlm::transpose(vlm::squeeze(vlm::slice(qkv, 2, 1, 2), 2), 1, 2);
+      Tensor v = vlm::transpose(vlm::squeeze(vlm::slice(qkv, 2, 2, 3), 2), 1, 2);
+      Tensor a = vlm::reshape(vlm::transpose(vlm::flash_attention(q, k, v, true), 1, 2), {B, T, d});
+      x = vlm::add(x, vlm::matmul_a_bt(a, w[3]));
+      h = vlm::layernorm(x, w[4], w[5], 1e-5f);
+      h = vlm::relu(vlm::add_bias(vlm::matmul_a_bt(h, w[6]), w[7]));
+      x = vlm::add(x, vlm::add_bias(vlm::matmul_a_bt(h, w[8]), w[9]));
+    }
+    const size_t n = P.size();
+    x = vlm::layernorm(x, P[n - 3], P[n - 2], 1e-5f);
+    Tensor logits = vlm::matmul_a_bt(x, P[n - 1]);
+    Tensor loss = vlm::cross_entropy(vlm::reshape(logits, {B * T, vocab}), tgt, -100);
+    *loss_out = *static_cast<const float*>(loss.data());
+    loss.backward();
+    for (size_t i = 0; i < n; ++i) {
+      vlm::scaled_add_inplace(P[i], *P[i].grad(), -lr);
+      out(P[i], params[i]);
+    }
     return 0;
   } catch (const std::exception&) {
     return -1;
