@@ -49,6 +49,43 @@ strided_copy_kernel(const float* __restrict__ src, float* __restrict__ dst, Stri
   }
 }
 
+// Fast path: the innermost dim is contiguous in both views, so each row of
+// `inner` floats is copied with 128-bit accesses; the outer index is
+// decomposed once per row (32-bit math: outer extents < 2^31).
+struct RowDesc {
+  int ndim;  // outer dims (all but the last)
+  int shape[7];
+  int64_t src[7];
+  int64_t dst[7];
+};
+
+template <bool VEC>
+__global__ void __launch_bounds__(256)
+strided_rows_kernel(const float* __restrict__ src, float* __restrict__ dst, RowDesc desc, int64_t rows,
+                    int inner) {
+  const int per_row = VEC ? inner / 4 : inner;
+  const int64_t total = rows * per_row;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += stride) {
+    const int64_t row = e / per_row;
+    const int c = (int)(e - row * per_row);
+    int64_t so = 0, dof = 0;
+    uint32_t rem = (uint32_t)row;
+    for (int dim = desc.ndim - 1; dim >= 0; --dim) {
+      const uint32_t ext = (uint32_t)desc.shape[dim];
+      const uint32_t idx = rem % ext;
+      rem /= ext;
+      so += (int64_t)idx * desc.src[dim];
+      dof += (int64_t)idx * desc.dst[dim];
+    }
+    if (VEC) {
+      *reinterpret_cast<f32x4*>(dst + dof + 4 * c) = *reinterpret_cast<const f32x4*>(src + so + 4 * c);
+    } else {
+      dst[dof + c] = src[so + c];
+    }
+  }
+}
+
 unsigned grid_for(int64_t work) {
   const int64_t cap = (int64_t)device_cu_count() * 16;
   int64_t g = (work + 255) / 256;
@@ -101,6 +138,27 @@ extern "C" int aar_strided_copy_f32(const float* src, float* dst, int ndim, cons
   }
   if (n == 0) return AAR_OK;
   if (!src || !dst) return AAR_EINVAL;
-  strided_copy_kernel<<<dim3(grid_for(n)), dim3(256), 0, as_stream(stream)>>>(src, dst, desc, n);
+  hipStream_t st = as_stream(stream);
+  const int64_t inner = ndim > 0 ? shape[ndim - 1] : 1;
+  const int64_t rows = ndim > 0 ? n / inner : 1;
+  if (ndim >= 1 && src_strides[ndim - 1] == 1 && dst_strides[ndim - 1] == 1 && rows < INT32_MAX &&
+      inner < INT32_MAX) {
+    RowDesc rd;
+    rd.ndim = ndim - 1;
+    for (int i = 0; i < ndim - 1; ++i) {
+      rd.shape[i] = (int)shape[i];
+      rd.src[i] = src_strides[i];
+      rd.dst[i] = dst_strides[i];
+    }
+    bool vec = inner % 4 == 0 && aligned16(src) && aligned16(dst);
+    for (int i = 0; i < ndim - 1 && vec; ++i) vec = (src_strides[i] % 4 == 0) && (dst_strides[i] % 4 == 0);
+    if (vec) {
+      strided_rows_kernel<true><<<dim3(grid_for(n / 4)), dim3(256), 0, st>>>(src, dst, rd, rows, (int)inner);
+    } else {
+      strided_rows_kernel<false><<<dim3(grid_for(n)), dim3(256), 0, st>>>(src, dst, rd, rows, (int)inner);
+    }
+    return launch_status();
+  }
+  strided_copy_kernel<<<dim3(grid_for(n)), dim3(256), 0, st>>>(src, dst, desc, n);
   return launch_status();
 }
