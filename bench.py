@@ -247,6 +247,44 @@ def bench_copy(ev: Events, iters: int = 5, n: int = 1 << 26):
     return {"n": n, "read_bytes": 8 * n, "write_bytes": 4 * n, "ms": ms, "GB_s": 12 * n / (ms * 1e-3) / 1e9}
 
 
+def bench_gemm_sweep(ev: Events, iters: int = 20):
+    """BASELINE config 1 and 2 shapes in all three layouts through the C ABI
+    (kernel-level timing, workspace preallocated)."""
+    abi = Abi(ev.L)
+    L = ev.L
+    vp, i64, sz = ctypes.c_void_p, ctypes.c_int64, ctypes.c_size_t
+    L.aar_gemm_f32.argtypes = [ctypes.c_int, i64, i64, i64, vp, vp, vp, vp, sz, vp]
+    L.aar_gemm_f32_workspace_bytes.restype = sz
+    L.aar_gemm_f32_workspace_bytes.argtypes = [ctypes.c_int, i64, i64, i64]
+    shapes = [(1024, 1024, 1024), (2048, 2048, 2048), (4096, 4096, 4096), (8192, 8192, 8192),
+              (16384, 1536, 384), (16384, 384, 1536), (1536, 384, 16384), (384, 1536, 16384),
+              (16384, 1152, 384), (16384, 65, 384), (1152, 384, 16384)]
+    out = {}
+    rng = np.random.default_rng(0)
+    try:
+        for (M, N, K) in shapes:
+            big = max(M, N, K) * max(sorted((M, N, K))[1], 1)
+            a = rng.standard_normal(max(M * K, 1)).astype(np.float32)
+            b = rng.standard_normal(max(K * N, 1)).astype(np.float32)
+            pa, pb, pc = abi.put(a), abi.put(b), abi.alloc(4 * M * N)
+            for op, name in ((0, "nn"), (1, "nt"), (2, "tn")):
+                wsb = L.aar_gemm_f32_workspace_bytes(op, M, N, K)
+                ws = abi.alloc(wsb) if wsb else None
+                n_it = iters if 2.0 * M * N * K < 2e11 else max(3, iters // 4)
+                for _ in range(3):
+                    assert L.aar_gemm_f32(op, M, N, K, pa, pb, pc, ws, wsb, None) == 0
+                ev.start()
+                for _ in range(n_it):
+                    L.aar_gemm_f32(op, M, N, K, pa, pb, pc, ws, wsb, None)
+                ms = ev.stop_ms() / n_it
+                out[f"{name}_{M}x{N}x{K}"] = round(2.0 * M * N * K / (ms * 1e-3) / 1e12, 2)
+            del big
+            abi.free()
+    finally:
+        abi.free()
+    return out
+
+
 # ----------------------------------------------------------------- GPT step
 # BASELINE config 5: decoder-only char GPT, 6 layers, d_model 384, 6 heads,
 # context 256, batch 64, vocab 65, pre-LN, 4x ReLU MLP (biased), bias-free
@@ -421,7 +459,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=60)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--flash-steps", type=int, default=6)
-    ap.add_argument("--only", choices=["all", "gemm", "flash", "rowwise", "copy", "gpt"], default="all",
+    ap.add_argument("--only", choices=["all", "gemm", "flash", "rowwise", "copy", "gpt", "sweep"], default="all",
                     help="run one part (profiling runs); the JSON line is printed for 'all'")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -443,6 +481,9 @@ def main() -> int:
         return 0
     if args.only == "rowwise":
         log(json.dumps(bench_rowwise(ev)))
+        return 0
+    if args.only == "sweep":
+        log(json.dumps(bench_gemm_sweep(ev)))
         return 0
     if args.only == "gpt":
         log(json.dumps(bench_gpt(ag, ev)))
