@@ -96,6 +96,23 @@ int aar_gemm_f32(int op, int64_t M, int64_t N, int64_t K,
                  const float* A, const float* B, float* C,
                  void* workspace, size_t workspace_bytes, void* stream);
 
+/* Tuning and test access to the GEMM tile configurations (no counterpart in
+ * the reference, whose launchers pick a tile size internally,
+ * cppsrc/ops/matmul.cu:792-832).  Configurations are numbered 0..n-1;
+ * aar_gemm_f32_tile_config returns AAR_EINVAL past the last one.
+ * aar_gemm_f32_plan reports the configuration and split count aar_gemm_f32
+ * would use with `workspace_bytes` of scratch.  aar_gemm_f32_with_config runs
+ * a given configuration and split-K count (needs splits*M*N*4 bytes of
+ * workspace when splits > 1, else AAR_EWORKSPACE); results agree with
+ * aar_gemm_f32 up to summation order. */
+int aar_gemm_f32_tile_config(int config, int* tile_m, int* tile_n, int* tile_k);
+int aar_gemm_f32_plan(int op, int64_t M, int64_t N, int64_t K, size_t workspace_bytes,
+                      int* config, int* splits);
+int aar_gemm_f32_with_config(int op, int64_t M, int64_t N, int64_t K,
+                             const float* A, const float* B, float* C,
+                             void* workspace, size_t workspace_bytes,
+                             int config, int splits, void* stream);
+
 /* ------------------------------------------------------- row-wise kernels */
 
 /* y = softmax(x) over the last dim; x,y [rows, cols].

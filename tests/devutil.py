@@ -36,6 +36,11 @@ class Abi:
         L.aar_gemm_f32.argtypes = [ctypes.c_int, i64, i64, i64, vp, vp, vp, vp, sz, vp]
         L.aar_gemm_f32_workspace_bytes.restype = sz
         L.aar_gemm_f32_workspace_bytes.argtypes = [ctypes.c_int, i64, i64, i64]
+        ip = ctypes.POINTER(ctypes.c_int)
+        L.aar_gemm_f32_tile_config.argtypes = [ctypes.c_int, ip, ip, ip]
+        L.aar_gemm_f32_plan.argtypes = [ctypes.c_int, i64, i64, i64, sz, ip, ip]
+        L.aar_gemm_f32_with_config.argtypes = [ctypes.c_int, i64, i64, i64, vp, vp, vp, vp, sz, ctypes.c_int,
+                                               ctypes.c_int, vp]
         L.aar_softmax_fwd_f32.argtypes = [vp, vp, i64, i64, vp]
         L.aar_softmax_bwd_f32.argtypes = [vp, vp, vp, i64, i64, vp]
         L.aar_layernorm_fwd_f32.argtypes = [vp, vp, vp, vp, vp, vp, i64, i64, ctypes.c_float, vp]

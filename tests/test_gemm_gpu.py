@@ -5,6 +5,8 @@ closed forms on sampled rows plus full-size checksums at the BASELINE sweep.
 Tolerance: 1e-4*sqrt(K) for both error metrics (conftest.errs)."""
 from __future__ import annotations
 
+import ctypes
+
 import numpy as np
 import pytest
 
@@ -179,3 +181,56 @@ def test_linear_layer_grads_match_oracle(gpu):
     assert_close(host(gpu, y).reshape(-1, 48), O.matmul("nt", x2, w), gemm_tol(64), "y")
     assert_close(host(gpu, tx.grad).reshape(-1, 64), O.matmul("nn", g2, w), gemm_tol(48), "dx")
     assert_close(host(gpu, tw.grad), O.matmul("tn", g2, x2), gemm_tol(192), "dw")
+
+
+def gemm_configs(abi):
+    out, c = [], 0
+    m, n, k = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+    while abi.L.aar_gemm_f32_tile_config(c, ctypes.byref(m), ctypes.byref(n), ctypes.byref(k)) == 0:
+        out.append((c, m.value, n.value, k.value))
+        c += 1
+    return out
+
+
+@pytest.mark.parametrize("op", [0, 1, 2])
+def test_every_tile_config_vs_oracle(gpu, op):
+    """Each tile configuration, forced through aar_gemm_f32_with_config, on
+    ragged shapes: partial M/N tiles, a K tail shorter than the tile depth,
+    the 128-bit path (aligned, extents % 4 == 0) and the predicated path
+    (odd extents), with and without a forced split-K."""
+    name = ["nn", "nt", "tn"][op]
+    abi = Abi()
+    try:
+        cfgs = gemm_configs(abi)
+        assert len(cfgs) >= 3
+        for (M, N, K) in [(300, 260, 200), (77, 93, 45)]:
+            rng = np.random.default_rng(M + N + K + op)
+            a, b = operands(name, M, N, K, rng)
+            ref = O.matmul(name, a, b)
+            pa, pb = abi.put(a), abi.put(b)
+            ws = abi.alloc(4 * 4 * M * N)
+            for (cfg, bm, bn, bk) in cfgs:
+                for splits in (1, 3):
+                    pc = abi.empty(M * N)
+                    abi.check(abi.L.aar_gemm_f32_with_config(op, M, N, K, pa, pb, pc, ws, 16 * M * N, cfg,
+                                                             splits, None))
+                    assert_close(abi.get(pc, (M, N)), ref, gemm_tol(K), f"{name} cfg {cfg} ({bm}x{bn}x{bk}) "
+                                 f"splits {splits} shape {(M, N, K)}")
+    finally:
+        abi.free()
+
+
+def test_plan_and_config_errors(gpu):
+    abi = Abi()
+    try:
+        cfg, sp = ctypes.c_int(-1), ctypes.c_int(-1)
+        abi.check(abi.L.aar_gemm_f32_plan(0, 4096, 4096, 4096, 0, ctypes.byref(cfg), ctypes.byref(sp)))
+        assert cfg.value >= 0 and sp.value == 1
+        n = len(gemm_configs(abi))
+        p = abi.alloc(4096)
+        assert abi.L.aar_gemm_f32_with_config(0, 8, 8, 8, p, p, p, None, 0, n, 1, None) == -1  # EINVAL
+        assert abi.L.aar_gemm_f32_with_config(0, 8, 8, 8, p, p, p, None, 0, 0, 0, None) == -1
+        # a forced split needs workspace
+        assert abi.L.aar_gemm_f32_with_config(0, 64, 64, 4096, p, p, p, None, 0, 0, 4, None) == -2
+    finally:
+        abi.free()
