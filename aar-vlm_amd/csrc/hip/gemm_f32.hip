@@ -527,6 +527,8 @@ constexpr Cfg kCfgs[] = {
     {128, 256, 16, 64, 128, 2, 3, 0.83f},   // 2
     {128, 128, 16, 64, 64, 2, 3, 0.84f},    // 3
     {64, 64, 16, 32, 32, 4, 4, 0.77f},      // 4
+    {128, 64, 16, 64, 32, 3, 3, 0.78f},     // 5
+    {64, 128, 16, 32, 64, 3, 3, 0.80f},     // 6
 };
 constexpr int kNumCfgs = sizeof(kCfgs) / sizeof(kCfgs[0]);
 constexpr int kMaxSplits = 64;
@@ -606,12 +608,14 @@ int launch_op(int cfg, bool vec, const float* A, const float* B, float* C, int64
     AAR_GEMM_CFG(2)
     AAR_GEMM_CFG(3)
     AAR_GEMM_CFG(4)
+    AAR_GEMM_CFG(5)
+    AAR_GEMM_CFG(6)
     default:
       return AAR_EINVAL;
   }
 #undef AAR_GEMM_CFG
 }
-static_assert(kNumCfgs == 5, "launch_op lists every configuration");
+static_assert(kNumCfgs == 7, "launch_op lists every configuration");
 
 // 128-bit loads need 16-byte aligned operands whose contiguous extents are
 // multiples of 4, and the 32-bit per-thread offsets need BR*ld*4 < 2^32.
