@@ -40,6 +40,14 @@ CXX_FLAGS = ["-O2", "-std=c++20", "-fPIC", "-Wall", "-Wno-sign-compare", f"-I{IN
 
 LIB_NAME = "libaar_hip.so"
 
+# Per-file extra flags.  The flash-attention kernels rescale their MFMA
+# accumulators with VALU ops every tile, so their accumulators are kept in
+# arch VGPRs (no accvgpr copies in the loop); the GEMM keeps its 256-register
+# accumulator tiles in AGPRs.
+HIP_FILE_FLAGS = {
+    "flash_attn": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
+
 
 def _headers(d: Path, pattern: str) -> list[Path]:
     return sorted(d.glob(pattern))
@@ -68,7 +76,7 @@ def build_hip(force: bool = False, jobs: int = 8) -> Path:
         o = OBJ_DIR / (s.stem + ".hip.o")
         objs.append(o)
         if force or _stale(o, [s] + hdrs):
-            todo.append([HIPCC, *HIP_FLAGS, "-c", str(s), "-o", str(o)])
+            todo.append([HIPCC, *HIP_FLAGS, *HIP_FILE_FLAGS.get(s.stem, []), "-c", str(s), "-o", str(o)])
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
         list(ex.map(_run, todo))
     out = OUT_DIR / LIB_NAME

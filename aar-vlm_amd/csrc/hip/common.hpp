@@ -42,6 +42,27 @@ __device__ __forceinline__ float lane_xor32(float v) {
   return __shfl_xor(v, 32, 64);
 }
 
+// v (op) v[lane ^ 32] in one VALU op pair: v_permlane32_swap (gfx950) hands
+// every lane both halves' values, so no LDS round trip is needed.  Both
+// halves compute the same commutative op and end with identical bits.  The
+// builtin exists only for the device target; the host pass never runs this.
+__device__ __forceinline__ float half_swap_sum(float v) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+#else
+  return v;
+#endif
+}
+__device__ __forceinline__ float half_swap_max(float v) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+#else
+  return v;
+#endif
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
   v += dpp_quad_xor1(v);
   v += dpp_quad_xor2(v);

@@ -55,6 +55,17 @@ __device__ __forceinline__ f32x16 zero16() {
   return z;
 }
 
+// 2^x on the transcendental unit (v_exp_f32): inputs are scaled logits minus
+// a running max, so results below 2^-126 (flushed to zero) carry no weight.
+// The builtin exists only for the device target; the host pass never runs it.
+__device__ __forceinline__ float fast_exp2(float x) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  return __builtin_amdgcn_exp2f(x);
+#else
+  return x;
+#endif
+}
+
 // Row index (within a 32-row tile) of accumulator register r for lane half h.
 __device__ __forceinline__ int acc_row(int r, int h) { return 8 * (r >> 2) + 4 * h + (r & 3); }
 
@@ -117,10 +128,37 @@ struct TileCopy {
       }
     }
   }
+
+  // Transposed: element (row r, column c) to s[c * LDT + r], so that 4
+  // consecutive rows of one column are one 128-bit LDS read.
+  template <int LDT>
+  __device__ __forceinline__ void store_t(float* __restrict__ s, int tid) const {
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int u = tid + i * kFaThreads;
+      if (u < kUnits) {
+        const int r = u / (DP / 4);
+        const int c = (u % (DP / 4)) * 4;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) s[(c + e) * LDT + r] = reg[i][e];
+      }
+    }
+  }
 };
+
+// Row stride of a transposed [DP][32] tile: 36 keeps the 128-bit reads of 32
+// consecutive columns (one per lane) bank-conflict free.
+constexpr int kLdt = kTile + 4;
 
 // ------------------------------------------------------------------ forward
 
+// Software pipeline: K runs one tile ahead of V.  Iteration t holds K tile
+// t+1 and V tile t in LDS and issues S_{t+1} = K_{t+1} Q^T on the matrix
+// cores in the same basic block as the online softmax of S_t (VALU,
+// independent), so the exp/max/sum work executes in the shadow of the MFMAs;
+// then O += V_t P_t.  V is staged transposed so each 128-bit LDS read feeds
+// four PV steps.  Only tiles that cross the causal diagonal or the sequence
+// end are masked.  One barrier per tile.
 template <int DP, bool CAUSAL, bool VEC>
 __global__ void __launch_bounds__(kFaThreads)
 flash_fwd_kernel(const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
@@ -128,10 +166,9 @@ flash_fwd_kernel(const float* __restrict__ Q, const float* __restrict__ K, const
                  float scale_log2) {
   constexpr int NC = DP / 8;   // head-dim chunks
   constexpr int NB = DP / 32;  // head-dim output blocks
-  constexpr int KLD = DP + 4;
-  constexpr int VLD = DP + 4;
-  __shared__ __attribute__((aligned(16))) float ks[2][kTile * KLD];
-  __shared__ __attribute__((aligned(16))) float vs[2][kTile * VLD];
+  constexpr int LD = DP + 4;
+  __shared__ __attribute__((aligned(16))) float ks[2][kTile * LD];
+  __shared__ __attribute__((aligned(16))) float vts[2][DP * kLdt];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int lr = lane & 31, h = lane >> 5;
@@ -155,33 +192,24 @@ flash_fwd_kernel(const float* __restrict__ Q, const float* __restrict__ K, const
 
   const int kv_end = CAUSAL ? min(T, qb * kBlock + kBlock) : T;
   const int ntiles = (kv_end + kTile - 1) / kTile;
+  // Last key tile that holds a key this wave's queries may see.
+  const int wlast = CAUSAL ? min(ntiles - 1, (q0 + kTile - 1) / kTile) : ntiles - 1;
 
-  TileCopy<DP, VEC> kc, vc;
-  kc.load(K + off, 0, T, d, tid);
-  vc.load(V + off, 0, T, d, tid);
-  kc.template store<KLD>(ks[0], tid);
-  vc.template store<VLD>(vs[0], tid);
-  __syncthreads();
-
-  for (int t = 0; t < ntiles; ++t) {
-    const int cur = t & 1;
-    const int kv0 = t * kTile;
-    const bool has_next = t + 1 < ntiles;
-    if (has_next) {
-      kc.load(K + off, kv0 + kTile, T, d, tid);
-      vc.load(V + off, kv0 + kTile, T, d, tid);
+  // S^T tile from K rows in LDS: lane = query, register r = key acc_row(r, h).
+  auto qk = [&](const float* kt) {
+    f32x16 s = zero16();
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const f32x4 kf = *reinterpret_cast<const f32x4*>(kt + lr * LD + 8 * c + 4 * h);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) s = mfma32(kf[e], qr[c][e], s);
     }
-    if (!CAUSAL || kv0 <= q0 + kTile - 1) {
-      const float* kt = ks[cur];
-      const float* vt = vs[cur];
-      f32x16 s = zero16();
-#pragma unroll
-      for (int c = 0; c < NC; ++c) {
-        const f32x4 kf = *reinterpret_cast<const f32x4*>(kt + lr * KLD + 8 * c + 4 * h);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) s = mfma32(kf[e], qr[c][e], s);
-      }
-      float mx = -INFINITY;
+    return s;
+  };
+  // Online softmax of tile t (S in s) and O += V_t P_t.
+  auto soft_pv = [&](f32x16 s, const float* vt, int kv0) {
+    float mx = -INFINITY;
+    if ((CAUSAL && kv0 + kTile - 1 > q0) || kv0 + kTile > T) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int key = kv0 + acc_row(r, h);
@@ -190,39 +218,72 @@ flash_fwd_kernel(const float* __restrict__ Q, const float* __restrict__ K, const
         s[r] = v;
         mx = fmaxf(mx, v);
       }
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      const float m_new = fmaxf(m, mx);
-      const float m_use = m_new == -INFINITY ? 0.f : m_new;
-      const float alpha = exp2f(m - m_use);
-      float ps = 0.f;
+    } else {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const float p = exp2f(s[r] - m_use);
-        s[r] = p;
-        ps += p;
-      }
-      ps += __shfl_xor(ps, 32, 64);
-      l = l * alpha + ps;
-      m = m_new;
-#pragma unroll
-      for (int b = 0; b < NB; ++b) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) o[b][r] *= alpha;
-      }
-#pragma unroll
-      for (int b = 0; b < NB; ++b) {
-#pragma unroll
-        for (int st = 0; st < 16; ++st) {
-          const float vf = vt[acc_row(st, h) * VLD + b * 32 + lr];
-          o[b] = mfma32(vf, s[st], o[b]);
-        }
+        s[r] *= scale_log2;
+        mx = fmaxf(mx, s[r]);
       }
     }
-    if (has_next) {
-      kc.template store<KLD>(ks[cur ^ 1], tid);
-      vc.template store<VLD>(vs[cur ^ 1], tid);
+    mx = half_swap_max(mx);
+    const float m_new = fmaxf(m, mx);
+    const float m_use = m_new == -INFINITY ? 0.f : m_new;
+    const float alpha = fast_exp2(m - m_use);
+    float ps = 0.f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const float p = fast_exp2(s[r] - m_use);
+      s[r] = p;
+      ps += p;
     }
+    ps = half_swap_sum(ps);
+    l = l * alpha + ps;
+    m = m_new;
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[b][r] *= alpha;
+    }
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const f32x4 vf = *reinterpret_cast<const f32x4*>(vt + (b * 32 + lr) * kLdt + 8 * g + 4 * h);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[b] = mfma32(vf[e], s[4 * g + e], o[b]);
+      }
+    }
+  };
+
+  TileCopy<DP, VEC> kc, vc;
+  kc.load(K + off, 0, T, d, tid);
+  vc.load(V + off, 0, T, d, tid);
+  kc.template store<LD>(ks[0], tid);
+  vc.template store_t<kLdt>(vts[0], tid);
+  if (ntiles > 1) {
+    kc.load(K + off, kTile, T, d, tid);
+    kc.template store<LD>(ks[1], tid);
+  }
+  __syncthreads();
+  f32x16 s_cur = qk(ks[0]);
+  __syncthreads();  // K tile 0's buffer is refilled in iteration 0
+
+  for (int t = 0; t < ntiles; ++t) {
+    const bool load_k = t + 2 < ntiles;  // K_{t+2} -> ks[t & 1]
+    const bool load_v = t + 1 < ntiles;  // V_{t+1} -> vts[(t + 1) & 1]
+    if (load_k) kc.load(K + off, (t + 2) * kTile, T, d, tid);
+    if (load_v) vc.load(V + off, (t + 1) * kTile, T, d, tid);
+    f32x16 s_next = zero16();
+    if (t + 1 <= wlast) {
+      s_next = qk(ks[(t + 1) & 1]);
+      soft_pv(s_cur, vts[t & 1], t * kTile);
+    } else if (t <= wlast) {
+      soft_pv(s_cur, vts[t & 1], t * kTile);
+    }
+    if (load_k) kc.template store<LD>(ks[t & 1], tid);
+    if (load_v) vc.template store_t<kLdt>(vts[(t + 1) & 1], tid);
     __syncthreads();
+    s_cur = s_next;
   }
 
   if (qi < T) {
