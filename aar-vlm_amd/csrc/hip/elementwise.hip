@@ -86,10 +86,13 @@ strided_rows_kernel(const float* __restrict__ src, float* __restrict__ dst, RowD
   }
 }
 
+// One thread per work item over a grid that covers the data once (faster HBM
+// streaming on MI355X than a persistent grid-stride loop); past 2^20 blocks
+// the kernels' grid-stride loops take over.
 unsigned grid_for(int64_t work) {
-  const int64_t cap = (int64_t)device_cu_count() * 16;
+  constexpr int64_t kCap = int64_t(1) << 20;
   int64_t g = (work + 255) / 256;
-  if (g > cap) g = cap;
+  if (g > kCap) g = kCap;
   return (unsigned)(g > 0 ? g : 1);
 }
 

@@ -12,11 +12,12 @@
 //    so every slot is a contiguous 1 KB segment across the wave.
 //  * Reductions are wave64 DPP/ds_swizzle butterflies; with W = 4 the four
 //    wave partials meet in LDS and are summed in a fixed order.
-//  * Workgroups are persistent (a few per CU) and stride over rows, so gamma/
-//    beta stay in registers and layernorm's dgamma/dbeta accumulate per lane
-//    in registers; each workgroup writes one partial row to a workspace and a
-//    second kernel sums the partials in a fixed order.  No float atomics: the
-//    result is bit-reproducible on a given device.
+//  * Softmax and layernorm forward launch a grid that covers the rows once.
+//    Layernorm backward's workgroups are persistent (a few per CU) and stride
+//    over rows, so gamma stays in registers and dgamma/dbeta accumulate per
+//    lane in registers; each workgroup writes one partial row to a workspace
+//    and a fixed-order tree sums the partials.  No float atomics: the result
+//    is bit-reproducible on a given device.
 #include <hip/hip_runtime.h>
 #include <math.h>
 
@@ -86,12 +87,12 @@ struct RowSlots {
 // Row-group reduction: full wave reduction, then (W > 1) a fixed-order sum of
 // the W wave partials through LDS.  `slot` selects a private LDS cell set; all
 // waves of the workgroup must call this uniformly.
-template <int W, bool MAX>
+template <int W, bool MAX, int NW = kWaves>
 __device__ __forceinline__ float group_reduce(float v, float* red, int slot, int grp, int wr,
                                               int lane) {
   v = MAX ? wave_max(v) : wave_sum(v);
   if (W == 1) return v;
-  float* cell = red + (slot * kWaves + grp * W);
+  float* cell = red + (slot * NW + grp * W);
   if (lane == 0) cell[wr] = v;
   __syncthreads();
   float r = cell[0];
@@ -105,14 +106,20 @@ __device__ __forceinline__ float group_reduce(float v, float* red, int slot, int
 // small row leaves HBM latency exposed).
 template <int NV, int W>
 struct RowsPerIter {
-  static constexpr int value = W == 1 ? (NV <= 2 ? 4 : (NV == 4 ? 2 : 1)) : 1;
+  static_assert(W == 1 || NV <= 8, "row-group size");
+  static constexpr int value = W == 1 ? (NV <= 2 ? 2 : (NV == 4 ? 2 : 1)) : 1;
 };
 
-inline int rows_per_iter(int nv, int w) { return w == 1 ? (nv <= 2 ? 4 : (nv == 4 ? 2 : 1)) : 1; }
+inline int rows_per_iter(int nv, int w) { return w == 1 ? (nv <= 2 ? 2 : (nv == 4 ? 2 : 1)) : 1; }
 
-// Persistent grid: enough workgroups to cover the rows once, capped at
-// `per_cu` workgroups per CU.
-inline int rows_grid(int64_t rows, int nv, int W, int per_cu = 8) {
+// Workgroups to cover the rows once, capped at `per_cu` workgroups per CU.
+// Softmax and layernorm forward use a covering grid (one pass per
+// workgroup, no row loop), which streams HBM faster on MI355X than a
+// persistent grid: the dispatcher walks the workgroups in address order, so
+// the in-flight rows form one compact window.  Layernorm backward keeps a
+// persistent grid because each workgroup emits one dgamma/dbeta partial row.
+constexpr int kCoverPerCu = 1 << 12;
+inline int rows_grid(int64_t rows, int nv, int W, int per_cu) {
   const int64_t per_wg_iter = (int64_t)(kWaves / W) * rows_per_iter(nv, W);
   const int64_t need = ceil_div(rows, per_wg_iter);
   const int64_t cap = (int64_t)device_cu_count() * per_cu;
@@ -125,8 +132,11 @@ __device__ __forceinline__ int64_t group_row0(int64_t it, int per_iter, int grp,
   return ((it * gridDim.x + blockIdx.x) * per_iter + grp) * U;
 }
 
-// LDS cells used by group_reduce: 2 parities x U rows x 2 reductions x 4 waves.
-constexpr int kRedCells = 2 * 4 * 2 * kWaves;
+// LDS cells used by group_reduce: 2 parities x U rows (at most 8) x 2
+// reductions x 4 waves.  (W == 1 row groups reduce within the wave and use
+// no cells.)
+constexpr int kMaxRowsPerIter = 8;
+constexpr int kRedCells = 2 * kMaxRowsPerIter * 2 * kWaves;
 
 // ------------------------------------------------------------------ softmax
 
@@ -221,6 +231,7 @@ layernorm_fwd_kernel(const float* __restrict__ x, const float* __restrict__ w,
   constexpr int per_iter = kWaves / W;
   const int64_t iters = ceil_div(rows, (int64_t)gridDim.x * per_iter * U);
   using RS = RowSlots<NV, W, VEC>;
+  __shared__ float stat[2][2][per_iter * U];
   RS sw, sb;
   sw.template load<false>(w, cols, wr, lane);
   sb.template load<false>(b, cols, wr, lane);
@@ -256,12 +267,22 @@ layernorm_fwd_kernel(const float* __restrict__ x, const float* __restrict__ w,
       const float r = 1.0f / sqrtf(var + eps);
 #pragma unroll
       for (int k = 0; k < RS::kN; ++k) s[u].v[k] = (s[u].v[k] - mu) * r * sw.v[k] + sb.v[k];
-      if (row < rows) {
-        s[u].store(y + row * cols, cols, wr, lane);
-        if (STATS && wr == 0 && lane == 0) {
-          mean[row] = mu;
-          rstd[row] = r;
-        }
+      if (row < rows) s[u].store(y + row * cols, cols, wr, lane);
+      if (STATS && wr == 0 && lane == 0) {
+        stat[it & 1][0][grp * U + u] = mu;
+        stat[it & 1][1][grp * U + u] = r;
+      }
+    }
+    if (STATS) {
+      // The workgroup's rows of this iteration are consecutive: write their
+      // statistics as one contiguous run per array instead of scattered
+      // single floats.  (Parity-buffered, so one barrier per iteration.)
+      __syncthreads();
+      const int64_t base = group_row0(it, per_iter, 0, U);
+      const int t = threadIdx.x;
+      if (t < per_iter * U && base + t < rows) {
+        mean[base + t] = stat[it & 1][0][t];
+        rstd[base + t] = stat[it & 1][1][t];
       }
     }
   }
@@ -269,18 +290,19 @@ layernorm_fwd_kernel(const float* __restrict__ x, const float* __restrict__ w,
 
 // Stage 1 of layernorm backward: dx per row, plus per-workgroup partial
 // column sums of gy*xhat (dgamma) and gy (dbeta) written to
-// part[blockIdx.x][2][cols].
-template <int NV, int W, bool VEC>
-__global__ void __launch_bounds__(kThreads)
+// part[blockIdx.x][2][cols].  Workgroups of NW waves are persistent (16
+// waves per CU) and stride over the rows.
+template <int NV, int W, bool VEC, int NW>
+__global__ void __launch_bounds__(NW * 64)
 layernorm_bwd_kernel(const float* __restrict__ gy, const float* __restrict__ x,
                      const float* __restrict__ w, const float* __restrict__ mean,
                      const float* __restrict__ rstd, float* __restrict__ dx,
                      float* __restrict__ part, int64_t rows, int cols) {
   constexpr int U = RowsPerIter<NV, W>::value;
-  __shared__ float red[kRedCells];
+  constexpr int per_iter = NW / W;
+  __shared__ float red[2 * kMaxRowsPerIter * 2 * NW];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int grp = wave / W, wr = wave % W;
-  constexpr int per_iter = kWaves / W;
   const int64_t iters = ceil_div(rows, (int64_t)gridDim.x * per_iter * U);
   using RS = RowSlots<NV, W, VEC>;
   RS sw, dwacc, dbacc;
@@ -322,8 +344,8 @@ layernorm_bwd_kernel(const float* __restrict__ gy, const float* __restrict__ x,
         dbacc.v[k] += sg[u].v[k];
         sx[u].v[k] = n;  // keep xhat
       }
-      sum_g = group_reduce<W, false>(sum_g, red, (((int)(it & 1) * U + u) * 2 + 0), grp, wr, lane);
-      sum_gn = group_reduce<W, false>(sum_gn, red, (((int)(it & 1) * U + u) * 2 + 1), grp, wr, lane);
+      sum_g = group_reduce<W, false, NW>(sum_g, red, (((int)(it & 1) * U + u) * 2 + 0), grp, wr, lane);
+      sum_gn = group_reduce<W, false, NW>(sum_gn, red, (((int)(it & 1) * U + u) * 2 + 1), grp, wr, lane);
 #pragma unroll
       for (int k = 0; k < RS::kN; ++k) {
         const float gg = sg[u].v[k] * sw.v[k];
@@ -335,16 +357,15 @@ layernorm_bwd_kernel(const float* __restrict__ gy, const float* __restrict__ x,
   // Combine the row groups of this workgroup in a fixed order: group 0 seeds
   // the LDS accumulator, groups 1.. add in turn, then group 0's waves write
   // the workgroup's partial row.
-  constexpr int ngrp = kWaves / W;
-  if (ngrp == 1) {
+  if (per_iter == 1) {
     float* pw = part + (int64_t)blockIdx.x * 2 * cols;
     dwacc.store(pw, cols, wr, lane);
     dbacc.store(pw + cols, cols, wr, lane);
     return;
   }
   __shared__ float stage[2][RS::kN * kWave * W];
-#pragma unroll
-  for (int gi = 0; gi < ngrp; ++gi) {
+#pragma unroll 1
+  for (int gi = 0; gi < per_iter; ++gi) {
     if (grp == gi) {
 #pragma unroll
       for (int k = 0; k < RS::kN; ++k) {
@@ -367,6 +388,12 @@ layernorm_bwd_kernel(const float* __restrict__ gy, const float* __restrict__ x,
     dbacc.store(pw + cols, cols, wr, lane);
   }
 }
+
+// Waves per layernorm-backward workgroup: 8 for rows spread over 4 waves
+// with up to 4 slots per lane (measured faster on MI355X than four 4-wave
+// workgroups per CU), else 4; each wave keeps its rows in registers without
+// spilling.
+constexpr int ln_bwd_waves(int nv, int w) { return (w > 1 && nv <= 4) ? 8 : 4; }
 
 // Stage 2 of layernorm backward, a fixed-order two-level tree over the
 // partial rows part[p][0..2C) (dgamma in [0,C), dbeta in [C,2C)):
@@ -586,11 +613,27 @@ RowPlan plan_rows(int64_t cols, bool vec) {
     }                                                   \
   } while (0)
 
-// Number of dgamma/dbeta partial rows (= workgroups of the backward kernel).
-int ln_bwd_parts(int64_t rows) {
-  const int64_t cap = (int64_t)device_cu_count() * 4;
-  const int64_t p = rows < cap ? rows : cap;
-  return (int)(p > 0 ? p : 1);
+// Number of dgamma/dbeta partial rows = persistent workgroups of the
+// backward kernel: 16 waves per CU.
+int ln_bwd_parts_for(int64_t rows, const RowPlan& p) {
+  const int64_t cus = device_cu_count();
+  int64_t cap, pass;
+  if (p.nv == 0) {
+    cap = cus * 4;
+    pass = 1;
+  } else {
+    const int nw = ln_bwd_waves(p.nv, p.w);
+    cap = cus * (16 / nw);  // 16 waves per CU
+    pass = (int64_t)(nw / p.w) * rows_per_iter(p.nv, p.w);
+  }
+  const int64_t need = ceil_div(rows, pass);
+  return (int)(need < cap ? need : cap);
+}
+// Workspace sizing does not know the pointers' alignment: cover both plans.
+int ln_bwd_parts_max(int64_t rows, int64_t cols) {
+  const int a = ln_bwd_parts_for(rows, plan_rows(cols, true));
+  const int b = ln_bwd_parts_for(rows, plan_rows(cols, false));
+  return a > b ? a : b;
 }
 
 }  // namespace
@@ -608,7 +651,7 @@ extern "C" int aar_softmax_fwd_f32(const float* x, float* y, int64_t rows, int64
     softmax_fwd_wide_kernel<<<dim3((unsigned)rows), dim3(kThreads), 0, st>>>(x, y, cols);
     return launch_status();
   }
-  const int grid = rows_grid(rows, p.nv, p.w);
+  const int grid = rows_grid(rows, p.nv, p.w, kCoverPerCu);
 #define L(NV, W, V) softmax_fwd_kernel<NV, W, V><<<dim3(grid), dim3(kThreads), 0, st>>>(x, y, rows, (int)cols)
   AAR_ROW_DISPATCH(p, L);
 #undef L
@@ -626,7 +669,7 @@ extern "C" int aar_softmax_bwd_f32(const float* g, const float* y, float* dx, in
     softmax_bwd_wide_kernel<<<dim3((unsigned)rows), dim3(kThreads), 0, st>>>(g, y, dx, cols);
     return launch_status();
   }
-  const int grid = rows_grid(rows, p.nv, p.w);
+  const int grid = rows_grid(rows, p.nv, p.w, kCoverPerCu);
 #define L(NV, W, V) \
   softmax_bwd_kernel<NV, W, V><<<dim3(grid), dim3(kThreads), 0, st>>>(g, y, dx, rows, (int)cols)
   AAR_ROW_DISPATCH(p, L);
@@ -649,7 +692,7 @@ extern "C" int aar_layernorm_fwd_f32(const float* x, const float* w, const float
         x, w, b, y, stats ? mean : nullptr, stats ? rstd : nullptr, cols, eps);
     return launch_status();
   }
-  const int grid = rows_grid(rows, p.nv, p.w);
+  const int grid = rows_grid(rows, p.nv, p.w, kCoverPerCu);
   if (stats) {
 #define L(NV, W, V)                                                                              \
   layernorm_fwd_kernel<NV, W, V, true><<<dim3(grid), dim3(kThreads), 0, st>>>(x, w, b, y, mean, \
@@ -669,7 +712,7 @@ extern "C" int aar_layernorm_fwd_f32(const float* x, const float* w, const float
 
 extern "C" size_t aar_layernorm_bwd_workspace_bytes(int64_t rows, int64_t cols) {
   if (rows <= 0 || cols <= 0) return 0;
-  const int64_t parts = ln_bwd_parts(rows);
+  const int64_t parts = ln_bwd_parts_max(rows, cols);
   const int64_t groups = ceil_div(parts, kPartGroup);
   return (size_t)(parts + groups) * 2 * (size_t)cols * sizeof(float);
 }
@@ -687,15 +730,15 @@ extern "C" int aar_layernorm_bwd_f32(const float* gy, const float* x, const floa
     return rc;
   }
   if (!gy || !x || !w || !mean || !rstd || !dx) return AAR_EINVAL;
-  const int parts = ln_bwd_parts(rows);
+  const bool vec = cols % 4 == 0 && aligned16(gy) && aligned16(x) && aligned16(w) &&
+                   aligned16(dx) && aligned16(workspace);
+  const RowPlan p = plan_rows(cols, vec);
+  const int parts = ln_bwd_parts_for(rows, p);
   const int groups = (int)ceil_div(parts, kPartGroup);
   const size_t need = (size_t)(parts + groups) * 2 * (size_t)cols * sizeof(float);
   if (!workspace || workspace_bytes < need) return AAR_EWORKSPACE;
   float* part = static_cast<float*>(workspace);
   float* grp = part + (int64_t)parts * 2 * cols;
-  const bool vec = cols % 4 == 0 && aligned16(gy) && aligned16(x) && aligned16(w) &&
-                   aligned16(dx) && aligned16(workspace);
-  const RowPlan p = plan_rows(cols, vec);
   int rc;
   if (p.nv == 0) {
     layernorm_bwd_wide_kernel<<<dim3((unsigned)rows), dim3(kThreads), 0, st>>>(gy, x, w, mean, rstd,
@@ -705,10 +748,10 @@ extern "C" int aar_layernorm_bwd_f32(const float* gy, const float* x, const floa
     layernorm_bwd_wide_cols_kernel<<<dim3((unsigned)ceil_div(cols, kThreads), (unsigned)parts),
                                      dim3(kThreads), 0, st>>>(gy, x, mean, rstd, part, rows, cols);
   } else {
-#define L(NV, W, V)                                                                           \
-  layernorm_bwd_kernel<NV, W, V><<<dim3(parts), dim3(kThreads), 0, st>>>(gy, x, w, mean, rstd, \
-                                                                         dx, part, rows,      \
-                                                                         (int)cols)
+#define L(NV, W, V)                                                                          \
+  layernorm_bwd_kernel<NV, W, V, ln_bwd_waves(NV, W)>                                            \
+      <<<dim3(parts), dim3(ln_bwd_waves(NV, W) * kWave), 0, st>>>(gy, x, w, mean, rstd, dx, part, \
+                                                                 rows, (int)cols)
     AAR_ROW_DISPATCH(p, L);
 #undef L
   }
