@@ -170,8 +170,11 @@ def scaled_dot_product_attention(q, k, v, *, causal=False):
 
 
 class MultiHeadAttention(Module):
-    """qkv projection, per-head views, fused flash attention, output
-    projection (aargrad/nn.py:164-192)."""
+    """qkv projection, per-head views, flash attention, output projection
+    (aargrad/nn.py:164-192).  The views, the attention and the head merge run
+    as one op (_core._flash_attention_qkv) that reads q/k/v in place from the
+    packed projection and writes the merged heads directly; the math is the
+    reference composition's."""
 
     def __init__(self, d_model, n_heads, *, causal=False, bias=True, rng=None):
         super().__init__()
@@ -191,6 +194,11 @@ class MultiHeadAttention(Module):
         return _core.transpose(part, 1, 2)
 
     def forward(self, x):
+        return self.out_proj(_core._flash_attention_qkv(self.qkv_proj(x), self.n_heads, self.causal))
+
+    def forward_views(self, x):
+        """The reference's literal composition through per-head views and
+        flash_attention (same result as forward)."""
         B, T, _ = x.shape
         qkv = _core.reshape(self.qkv_proj(x), [B, T, 3, self.n_heads, self.d_head])
         q, k, v = (self._head_view(qkv, i) for i in range(3))

@@ -33,6 +33,8 @@
 #include <hip/hip_runtime.h>
 #include <math.h>
 
+#include <initializer_list>
+
 #include "common.hpp"
 
 namespace aar {
@@ -104,14 +106,15 @@ struct TileCopy {
   static constexpr int kPer = (kUnits + kFaThreads - 1) / kFaThreads;
   f32x4 reg[kPer];
 
-  __device__ __forceinline__ void load(const float* __restrict__ base, int row0, int T, int d, int tid) {
+  __device__ __forceinline__ void load(const float* __restrict__ base, int64_t st, int row0, int T, int d,
+                                       int tid) {
 #pragma unroll
     for (int i = 0; i < kPer; ++i) {
       const int u = tid + i * kFaThreads;
       const int r = u / (DP / 4);
       const int c = (u % (DP / 4)) * 4;
       f32x4 v = {0.f, 0.f, 0.f, 0.f};
-      if (u < kUnits && row0 + r < T) v = load4<VEC>(base + (int64_t)(row0 + r) * d + c, d - c);
+      if (u < kUnits && row0 + r < T) v = load4<VEC>(base + (int64_t)(row0 + r) * st + c, d - c);
       reg[i] = v;
     }
   }
@@ -146,6 +149,25 @@ struct TileCopy {
   }
 };
 
+// A [B, H, T, d] operand with element (b, h, t, c) at p[b*sb + h*sh + t*st + c]
+// (the head dim is contiguous).  Contiguous [B*H, T, d] tensors, the q/k/v
+// views of a packed [B, T, 3, H, d] projection and outputs in [B, T, H, d]
+// are all of this form.
+struct FaIn {
+  const float* p;
+  int64_t sb, sh, st;
+  __device__ __forceinline__ const float* head(int bh, int H) const {
+    return p + (int64_t)(bh / H) * sb + (int64_t)(bh % H) * sh;
+  }
+};
+struct FaOut {
+  float* p;
+  int64_t sb, sh, st;
+  __device__ __forceinline__ float* head(int bh, int H) const {
+    return p + (int64_t)(bh / H) * sb + (int64_t)(bh % H) * sh;
+  }
+};
+
 // Row stride of a transposed [DP][32] tile: 36 keeps the 128-bit reads of 32
 // consecutive columns (one per lane) bank-conflict free.
 constexpr int kLdt = kTile + 4;
@@ -161,9 +183,8 @@ constexpr int kLdt = kTile + 4;
 // end are masked.  One barrier per tile.
 template <int DP, bool CAUSAL, bool VEC>
 __global__ void __launch_bounds__(kFaThreads)
-flash_fwd_kernel(const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
-                 float* __restrict__ O, float* __restrict__ Lse, int T, int d, int nqb, int BH,
-                 float scale_log2) {
+flash_fwd_kernel(FaIn Qv, FaIn Kv, FaIn Vv, FaOut Ov, float* __restrict__ Lse, int T, int d, int H,
+                 int nqb, int BH, float scale_log2) {
   constexpr int NC = DP / 8;   // head-dim chunks
   constexpr int NB = DP / 32;  // head-dim output blocks
   constexpr int LD = DP + 4;
@@ -175,7 +196,9 @@ flash_fwd_kernel(const float* __restrict__ Q, const float* __restrict__ K, const
   // Longest work first: the last query blocks have the most key tiles.
   const int qb = CAUSAL ? nqb - 1 - (int)(blockIdx.x / BH) : (int)(blockIdx.x / BH);
   const int bh = blockIdx.x % BH;
-  const int64_t off = (int64_t)bh * T * d;
+  const float* __restrict__ Q = Qv.head(bh, H);
+  const float* __restrict__ K = Kv.head(bh, H);
+  const float* __restrict__ V = Vv.head(bh, H);
   const int q0 = qb * kBlock + wave * kTile;  // first query of this wave
   const int qi = q0 + lr;                     // this lane's query
 
@@ -183,7 +206,7 @@ flash_fwd_kernel(const float* __restrict__ Q, const float* __restrict__ K, const
 #pragma unroll
   for (int c = 0; c < NC; ++c) {
     const int dd = 8 * c + 4 * h;
-    qr[c] = qi < T ? load4<VEC>(Q + off + (int64_t)qi * d + dd, d - dd) : f32x4{0.f, 0.f, 0.f, 0.f};
+    qr[c] = qi < T ? load4<VEC>(Q + (int64_t)qi * Qv.st + dd, d - dd) : f32x4{0.f, 0.f, 0.f, 0.f};
   }
   f32x16 o[NB];
 #pragma unroll
@@ -256,12 +279,12 @@ flash_fwd_kernel(const float* __restrict__ Q, const float* __restrict__ K, const
   };
 
   TileCopy<DP, VEC> kc, vc;
-  kc.load(K + off, 0, T, d, tid);
-  vc.load(V + off, 0, T, d, tid);
+  kc.load(K, Kv.st, 0, T, d, tid);
+  vc.load(V, Vv.st, 0, T, d, tid);
   kc.template store<LD>(ks[0], tid);
   vc.template store_t<kLdt>(vts[0], tid);
   if (ntiles > 1) {
-    kc.load(K + off, kTile, T, d, tid);
+    kc.load(K, Kv.st, kTile, T, d, tid);
     kc.template store<LD>(ks[1], tid);
   }
   __syncthreads();
@@ -271,8 +294,8 @@ flash_fwd_kernel(const float* __restrict__ Q, const float* __restrict__ K, const
   for (int t = 0; t < ntiles; ++t) {
     const bool load_k = t + 2 < ntiles;  // K_{t+2} -> ks[t & 1]
     const bool load_v = t + 1 < ntiles;  // V_{t+1} -> vts[(t + 1) & 1]
-    if (load_k) kc.load(K + off, (t + 2) * kTile, T, d, tid);
-    if (load_v) vc.load(V + off, (t + 1) * kTile, T, d, tid);
+    if (load_k) kc.load(K, Kv.st, (t + 2) * kTile, T, d, tid);
+    if (load_v) vc.load(V, Vv.st, (t + 1) * kTile, T, d, tid);
     f32x16 s_next = zero16();
     if (t + 1 <= wlast) {
       s_next = qk(ks[(t + 1) & 1]);
@@ -288,7 +311,7 @@ flash_fwd_kernel(const float* __restrict__ Q, const float* __restrict__ K, const
 
   if (qi < T) {
     const float inv_l = 1.0f / l;
-    float* orow = O + off + (int64_t)qi * d;
+    float* orow = Ov.head(bh, H) + (int64_t)qi * Ov.st;
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
 #pragma unroll
@@ -305,16 +328,16 @@ flash_fwd_kernel(const float* __restrict__ Q, const float* __restrict__ K, const
 
 // ------------------------------------------------------------- backward 0
 
-// D[row] = sum_d dO[row][d] * O[row][d]; 16 lanes per row.
+// D[bh*T + t] = sum_c dO[bh][t][c] * O[bh][t][c]; 16 lanes per row.
 __global__ void __launch_bounds__(256)
-flash_bwd_dot_kernel(const float* __restrict__ dO, const float* __restrict__ O, float* __restrict__ D,
-                     int64_t rows, int d) {
+flash_bwd_dot_kernel(FaIn dOv, FaIn Ov, float* __restrict__ D, int64_t rows, int T, int H, int d) {
   const int64_t row = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 4;
   const int sub = threadIdx.x & 15;
   float acc = 0.f;
   if (row < rows) {
-    const float* a = dO + row * d;
-    const float* b = O + row * d;
+    const int bh = (int)(row / T), t = (int)(row % T);
+    const float* a = dOv.head(bh, H) + (int64_t)t * dOv.st;
+    const float* b = Ov.head(bh, H) + (int64_t)t * Ov.st;
     for (int c = sub; c < d; c += 16) acc += a[c] * b[c];
   }
   acc += dpp_quad_xor1(acc);
@@ -328,11 +351,9 @@ flash_bwd_dot_kernel(const float* __restrict__ dO, const float* __restrict__ O, 
 
 template <int DP, bool CAUSAL, bool VEC>
 __global__ void __launch_bounds__(kFaThreads)
-flash_bwd_dkdv_kernel(const float* __restrict__ Q, const float* __restrict__ K,
-                      const float* __restrict__ V, const float* __restrict__ dO,
-                      const float* __restrict__ Lse, const float* __restrict__ Dv,
-                      float* __restrict__ dK, float* __restrict__ dV, int T, int d, int nkb, int BH,
-                      float scale, float scale_log2) {
+flash_bwd_dkdv_kernel(FaIn Qv, FaIn Kv, FaIn Vv, FaIn dOv, const float* __restrict__ Lse,
+                      const float* __restrict__ Dv, FaOut dKv, FaOut dVv, int T, int d, int H, int nkb,
+                      int BH, float scale, float scale_log2) {
   constexpr int NC = DP / 8;
   constexpr int NB = DP / 32;
   constexpr int LD = DP + 4;
@@ -347,7 +368,10 @@ flash_bwd_dkdv_kernel(const float* __restrict__ Q, const float* __restrict__ K,
   // most query tiles.
   const int kb = (int)(blockIdx.x / BH);
   const int bh = blockIdx.x % BH;
-  const int64_t off = (int64_t)bh * T * d;
+  const float* __restrict__ Q = Qv.head(bh, H);
+  const float* __restrict__ K = Kv.head(bh, H);
+  const float* __restrict__ V = Vv.head(bh, H);
+  const float* __restrict__ dO = dOv.head(bh, H);
   const int k0 = kb * kBlock + wave * kTile;  // first key of this wave
   const int kj = k0 + lr;                     // this lane's key
 
@@ -356,8 +380,8 @@ flash_bwd_dkdv_kernel(const float* __restrict__ Q, const float* __restrict__ K,
   for (int c = 0; c < NC; ++c) {
     const int dd = 8 * c + 4 * h;
     const bool ok = kj < T;
-    kr[c] = ok ? load4<VEC>(K + off + (int64_t)kj * d + dd, d - dd) : f32x4{0.f, 0.f, 0.f, 0.f};
-    vr[c] = ok ? load4<VEC>(V + off + (int64_t)kj * d + dd, d - dd) : f32x4{0.f, 0.f, 0.f, 0.f};
+    kr[c] = ok ? load4<VEC>(K + (int64_t)kj * Kv.st + dd, d - dd) : f32x4{0.f, 0.f, 0.f, 0.f};
+    vr[c] = ok ? load4<VEC>(V + (int64_t)kj * Vv.st + dd, d - dd) : f32x4{0.f, 0.f, 0.f, 0.f};
   }
   f32x16 dk[NB], dv[NB];
 #pragma unroll
@@ -375,8 +399,8 @@ flash_bwd_dkdv_kernel(const float* __restrict__ Q, const float* __restrict__ K,
   TileCopy<DP, VEC> qc, dc;
   float lreg = 0.f, dreg = 0.f;
   auto load_tile = [&](int t) {
-    qc.load(Q + off, t * kTile, T, d, tid);
-    dc.load(dO + off, t * kTile, T, d, tid);
+    qc.load(Q, Qv.st, t * kTile, T, d, tid);
+    dc.load(dO, dOv.st, t * kTile, T, d, tid);
     if (tid < kTile) {
       const int q = t * kTile + tid;
       // Past-the-end queries get lse = +inf so that their P is exactly 0.
@@ -446,8 +470,8 @@ flash_bwd_dkdv_kernel(const float* __restrict__ Q, const float* __restrict__ K,
   }
 
   if (kj < T) {
-    float* krow = dK + off + (int64_t)kj * d;
-    float* vrow = dV + off + (int64_t)kj * d;
+    float* krow = dKv.head(bh, H) + (int64_t)kj * dKv.st;
+    float* vrow = dVv.head(bh, H) + (int64_t)kj * dVv.st;
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
 #pragma unroll
@@ -468,11 +492,9 @@ flash_bwd_dkdv_kernel(const float* __restrict__ Q, const float* __restrict__ K,
 
 template <int DP, bool CAUSAL, bool VEC>
 __global__ void __launch_bounds__(kFaThreads)
-flash_bwd_dq_kernel(const float* __restrict__ Q, const float* __restrict__ K,
-                    const float* __restrict__ V, const float* __restrict__ dO,
-                    const float* __restrict__ Lse, const float* __restrict__ Dv,
-                    float* __restrict__ dQ, int T, int d, int nqb, int BH, float scale,
-                    float scale_log2) {
+flash_bwd_dq_kernel(FaIn Qv, FaIn Kv, FaIn Vv, FaIn dOv, const float* __restrict__ Lse,
+                    const float* __restrict__ Dv, FaOut dQv, int T, int d, int H, int nqb, int BH,
+                    float scale, float scale_log2) {
   constexpr int NC = DP / 8;
   constexpr int NB = DP / 32;
   constexpr int LD = DP + 4;
@@ -483,7 +505,10 @@ flash_bwd_dq_kernel(const float* __restrict__ Q, const float* __restrict__ K,
   const int lr = lane & 31, h = lane >> 5;
   const int qb = CAUSAL ? nqb - 1 - (int)(blockIdx.x / BH) : (int)(blockIdx.x / BH);
   const int bh = blockIdx.x % BH;
-  const int64_t off = (int64_t)bh * T * d;
+  const float* __restrict__ Q = Qv.head(bh, H);
+  const float* __restrict__ K = Kv.head(bh, H);
+  const float* __restrict__ V = Vv.head(bh, H);
+  const float* __restrict__ dO = dOv.head(bh, H);
   const int q0 = qb * kBlock + wave * kTile;
   const int qi = q0 + lr;
 
@@ -492,8 +517,8 @@ flash_bwd_dq_kernel(const float* __restrict__ Q, const float* __restrict__ K,
   for (int c = 0; c < NC; ++c) {
     const int dd = 8 * c + 4 * h;
     const bool ok = qi < T;
-    qr[c] = ok ? load4<VEC>(Q + off + (int64_t)qi * d + dd, d - dd) : f32x4{0.f, 0.f, 0.f, 0.f};
-    dor[c] = ok ? load4<VEC>(dO + off + (int64_t)qi * d + dd, d - dd) : f32x4{0.f, 0.f, 0.f, 0.f};
+    qr[c] = ok ? load4<VEC>(Q + (int64_t)qi * Qv.st + dd, d - dd) : f32x4{0.f, 0.f, 0.f, 0.f};
+    dor[c] = ok ? load4<VEC>(dO + (int64_t)qi * dOv.st + dd, d - dd) : f32x4{0.f, 0.f, 0.f, 0.f};
   }
   const float l2 = qi < T ? Lse[(int64_t)bh * T + qi] * kLog2e : INFINITY;
   const float dq_sum = qi < T ? Dv[(int64_t)bh * T + qi] : 0.f;
@@ -505,8 +530,8 @@ flash_bwd_dq_kernel(const float* __restrict__ Q, const float* __restrict__ K,
   const int ntiles = (kv_end + kTile - 1) / kTile;
 
   TileCopy<DP, VEC> kc, vc;
-  kc.load(K + off, 0, T, d, tid);
-  vc.load(V + off, 0, T, d, tid);
+  kc.load(K, Kv.st, 0, T, d, tid);
+  vc.load(V, Vv.st, 0, T, d, tid);
   kc.template store<LD>(ks[0], tid);
   vc.template store<LD>(vs[0], tid);
   __syncthreads();
@@ -516,8 +541,8 @@ flash_bwd_dq_kernel(const float* __restrict__ Q, const float* __restrict__ K,
     const int kv0 = t * kTile;
     const bool has_next = t + 1 < ntiles;
     if (has_next) {
-      kc.load(K + off, kv0 + kTile, T, d, tid);
-      vc.load(V + off, kv0 + kTile, T, d, tid);
+      kc.load(K, Kv.st, kv0 + kTile, T, d, tid);
+      vc.load(V, Vv.st, kv0 + kTile, T, d, tid);
     }
     if (!CAUSAL || kv0 <= q0 + kTile - 1) {
       const float* kt = ks[cur];
@@ -557,7 +582,7 @@ flash_bwd_dq_kernel(const float* __restrict__ Q, const float* __restrict__ K,
   }
 
   if (qi < T) {
-    float* qrow = dQ + off + (int64_t)qi * d;
+    float* qrow = dQv.head(bh, H) + (int64_t)qi * dQv.st;
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
 #pragma unroll
@@ -595,9 +620,10 @@ int dispatch_fa(int dp, bool causal, bool vec, Args... args) {
 }
 
 struct FwdArgs {
-  const float *q, *k, *v;
-  float *o, *lse;
-  int T, d, BH;
+  FaIn q, k, v;
+  FaOut o;
+  float* lse;
+  int T, d, H, BH;
   float scale;
   hipStream_t st;
 };
@@ -607,15 +633,16 @@ struct FwdLaunch {
   static int run(const FwdArgs& a) {
     const int nqb = (a.T + kBlock - 1) / kBlock;
     flash_fwd_kernel<DP, C, VEC><<<dim3((unsigned)(nqb * a.BH)), dim3(kFaThreads), 0, a.st>>>(
-        a.q, a.k, a.v, a.o, a.lse, a.T, a.d, nqb, a.BH, a.scale * kLog2e);
+        a.q, a.k, a.v, a.o, a.lse, a.T, a.d, a.H, nqb, a.BH, a.scale * kLog2e);
     return launch_status();
   }
 };
 
 struct BwdArgs {
-  const float *q, *k, *v, *dout, *lse, *D;
-  float *dq, *dk, *dv;
-  int T, d, BH;
+  FaIn q, k, v, dout;
+  const float *lse, *D;
+  FaOut dq, dk, dv;
+  int T, d, H, BH;
   float scale;
   hipStream_t st;
 };
@@ -625,14 +652,28 @@ struct BwdLaunch {
   static int run(const BwdArgs& a) {
     const int nb = (a.T + kBlock - 1) / kBlock;
     flash_bwd_dkdv_kernel<DP, C, VEC><<<dim3((unsigned)(nb * a.BH)), dim3(kFaThreads), 0, a.st>>>(
-        a.q, a.k, a.v, a.dout, a.lse, a.D, a.dk, a.dv, a.T, a.d, nb, a.BH, a.scale, a.scale * kLog2e);
+        a.q, a.k, a.v, a.dout, a.lse, a.D, a.dk, a.dv, a.T, a.d, a.H, nb, a.BH, a.scale, a.scale * kLog2e);
     int rc = launch_status();
     if (rc != AAR_OK) return rc;
     flash_bwd_dq_kernel<DP, C, VEC><<<dim3((unsigned)(nb * a.BH)), dim3(kFaThreads), 0, a.st>>>(
-        a.q, a.k, a.v, a.dout, a.lse, a.D, a.dq, a.T, a.d, nb, a.BH, a.scale, a.scale * kLog2e);
+        a.q, a.k, a.v, a.dout, a.lse, a.D, a.dq, a.T, a.d, a.H, nb, a.BH, a.scale, a.scale * kLog2e);
     return launch_status();
   }
 };
+
+// 128-bit accesses need 16-byte aligned head rows: aligned bases, d and all
+// strides multiples of 4.
+bool fa_vec_ok(int64_t d, std::initializer_list<const void*> ptrs, const int64_t* strides, int nstrides) {
+  if (d % 4 != 0) return false;
+  for (const void* p : ptrs)
+    if (!aligned16(p)) return false;
+  for (int i = 0; i < nstrides; ++i)
+    if (strides[i] % 4 != 0) return false;
+  return true;
+}
+
+FaIn fa_in(const float* p, const int64_t* s) { return FaIn{p, s[0], s[1], s[2]}; }
+FaOut fa_out(float* p, const int64_t* s) { return FaOut{p, s[0], s[1], s[2]}; }
 
 bool fa_shape_ok(int64_t bh, int64_t T, int64_t d) {
   return bh > 0 && T > 0 && d > 0 && d <= 128 && T <= (1 << 24) && bh <= (1 << 24) &&
@@ -644,17 +685,28 @@ bool fa_shape_ok(int64_t bh, int64_t T, int64_t d) {
 
 using namespace aar;
 
+extern "C" int aar_flash_fwd_strided_f32(const float* q, const float* k, const float* v, float* o, float* lse,
+                                         int64_t B, int64_t H, int64_t T, int64_t d, const int64_t* strides,
+                                         int causal, float scale, void* stream) {
+  if (B < 0 || H < 0 || T < 0 || d <= 0) return AAR_EINVAL;
+  if (d > 128) return AAR_EINVAL;
+  if (B == 0 || H == 0 || T == 0) return AAR_OK;
+  if (!q || !k || !v || !o || !lse || !strides) return AAR_EINVAL;
+  if (!fa_shape_ok(B * H, T, d) || H > INT32_MAX) return AAR_EUNSUPPORTED;
+  const bool vec = fa_vec_ok(d, {q, k, v, o}, strides, 12);
+  FwdArgs a{fa_in(q, strides),      fa_in(k, strides + 3), fa_in(v, strides + 6), fa_out(o, strides + 9),
+            lse,                    (int)T,                (int)d,                (int)H,
+            (int)(B * H),           scale,                 as_stream(stream)};
+  return dispatch_fa<FwdLaunch>(pad_dim(d), causal != 0, vec, a);
+}
+
 extern "C" int aar_flash_fwd_f32(const float* q, const float* k, const float* v, float* o, float* lse,
                                  int64_t bh, int64_t T, int64_t d, int causal, float scale,
                                  void* stream) {
   if (bh < 0 || T < 0 || d <= 0) return AAR_EINVAL;
-  if (d > 128) return AAR_EINVAL;
-  if (bh == 0 || T == 0) return AAR_OK;
-  if (!q || !k || !v || !o || !lse) return AAR_EINVAL;
-  if (!fa_shape_ok(bh, T, d)) return AAR_EUNSUPPORTED;
-  const bool vec = d % 4 == 0 && aligned16(q) && aligned16(k) && aligned16(v) && aligned16(o);
-  FwdArgs a{q, k, v, o, lse, (int)T, (int)d, (int)bh, scale, as_stream(stream)};
-  return dispatch_fa<FwdLaunch>(pad_dim(d), causal != 0, vec, a);
+  const int64_t c[3] = {bh * T * d, T * d, d};  // [1, bh, T, d] contiguous
+  const int64_t strides[12] = {c[0], c[1], c[2], c[0], c[1], c[2], c[0], c[1], c[2], c[0], c[1], c[2]};
+  return aar_flash_fwd_strided_f32(q, k, v, o, lse, 1, bh, T, d, strides, causal, scale, stream);
 }
 
 extern "C" size_t aar_flash_bwd_workspace_bytes(int64_t bh, int64_t T, int64_t d) {
@@ -663,25 +715,45 @@ extern "C" size_t aar_flash_bwd_workspace_bytes(int64_t bh, int64_t T, int64_t d
   return (size_t)bh * (size_t)T * sizeof(float);
 }
 
+extern "C" int aar_flash_bwd_strided_f32(const float* q, const float* k, const float* v, const float* o,
+                                         const float* lse, const float* dout, float* dq, float* dk, float* dv,
+                                         int64_t B, int64_t H, int64_t T, int64_t d, const int64_t* strides,
+                                         int causal, float scale, void* workspace, size_t workspace_bytes,
+                                         void* stream) {
+  if (B < 0 || H < 0 || T < 0 || d <= 0) return AAR_EINVAL;
+  if (d > 128) return AAR_EINVAL;
+  if (B == 0 || H == 0 || T == 0) return AAR_OK;
+  if (!q || !k || !v || !o || !lse || !dout || !dq || !dk || !dv || !strides) return AAR_EINVAL;
+  if (!fa_shape_ok(B * H, T, d) || H > INT32_MAX) return AAR_EUNSUPPORTED;
+  const int64_t bh = B * H;
+  if (!workspace || workspace_bytes < aar_flash_bwd_workspace_bytes(bh, T, d)) return AAR_EWORKSPACE;
+  hipStream_t st = as_stream(stream);
+  float* D = static_cast<float*>(workspace);
+  const int64_t rows = bh * T;
+  flash_bwd_dot_kernel<<<dim3((unsigned)ceil_div(rows * 16, (int64_t)256)), dim3(256), 0, st>>>(
+      fa_in(dout, strides + 12), fa_in(o, strides + 9), D, rows, (int)T, (int)H, (int)d);
+  int rc = launch_status();
+  if (rc != AAR_OK) return rc;
+  const bool vec = fa_vec_ok(d, {q, k, v, dout, dq, dk, dv}, strides, 24);
+  BwdArgs a{fa_in(q, strides),          fa_in(k, strides + 3),      fa_in(v, strides + 6),
+            fa_in(dout, strides + 12),  lse,                        D,
+            fa_out(dq, strides + 15),   fa_out(dk, strides + 18),   fa_out(dv, strides + 21),
+            (int)T,                     (int)d,                     (int)H,
+            (int)bh,                    scale,                      st};
+  return dispatch_fa<BwdLaunch>(pad_dim(d), causal != 0, vec, a);
+}
+
 extern "C" int aar_flash_bwd_f32(const float* q, const float* k, const float* v, const float* o,
                                  const float* lse, const float* dout, float* dq, float* dk, float* dv,
                                  int64_t bh, int64_t T, int64_t d, int causal, float scale,
                                  void* workspace, size_t workspace_bytes, void* stream) {
   if (bh < 0 || T < 0 || d <= 0) return AAR_EINVAL;
-  if (d > 128) return AAR_EINVAL;
-  if (bh == 0 || T == 0) return AAR_OK;
-  if (!q || !k || !v || !o || !lse || !dout || !dq || !dk || !dv) return AAR_EINVAL;
-  if (!fa_shape_ok(bh, T, d)) return AAR_EUNSUPPORTED;
-  if (!workspace || workspace_bytes < aar_flash_bwd_workspace_bytes(bh, T, d)) return AAR_EWORKSPACE;
-  hipStream_t st = as_stream(stream);
-  float* D = static_cast<float*>(workspace);
-  const int64_t rows = bh * T;
-  flash_bwd_dot_kernel<<<dim3((unsigned)ceil_div(rows * 16, 256)), dim3(256), 0, st>>>(dout, o, D, rows,
-                                                                                     (int)d);
-  int rc = launch_status();
-  if (rc != AAR_OK) return rc;
-  const bool vec = d % 4 == 0 && aligned16(q) && aligned16(k) && aligned16(v) && aligned16(dout) &&
-                   aligned16(dq) && aligned16(dk) && aligned16(dv);
-  BwdArgs a{q, k, v, dout, lse, D, dq, dk, dv, (int)T, (int)d, (int)bh, scale, st};
-  return dispatch_fa<BwdLaunch>(pad_dim(d), causal != 0, vec, a);
+  int64_t strides[24];
+  for (int i = 0; i < 8; ++i) {
+    strides[3 * i] = bh * T * d;
+    strides[3 * i + 1] = T * d;
+    strides[3 * i + 2] = d;
+  }
+  return aar_flash_bwd_strided_f32(q, k, v, o, lse, dout, dq, dk, dv, 1, bh, T, d, strides, causal, scale,
+                                   workspace, workspace_bytes, stream);
 }

@@ -171,6 +171,10 @@ PYBIND11_MODULE(_core, m) {
   m.def("_flash_attention_fwd", &flash_attention_fwd_lse, py::arg("q"), py::arg("k"), py::arg("v"),
         py::arg("causal"), gil_release(),
         "Forward flash attention returning (O, lse); lse = m + ln(l) per query row.");
+  m.def("_flash_attention_qkv", &flash_attention_qkv, py::arg("qkv"), py::arg("n_heads"), py::arg("causal"),
+        gil_release(),
+        "Attention over a packed projection [..., T, 3*D] -> [..., T, D]: the MultiHeadAttention "
+        "composition (per-head views of q, k, v, flash attention, heads merged back) in one op.");
   m.def("_device_count", &device_count);
   m.def("_empty_cache", &device_empty_cache, gil_release());
   m.def("_memory_in_use", &device_bytes_in_use);

@@ -344,23 +344,94 @@ class LayerNormFunction : public Function {
 
 // ------------------------------------------------------------- attention
 
+// A [B, H, T, d] view as the kernels take it: element (b, h, t, c) at
+// data[b*sb + h*sh + t*st + c].  Leading dims of a [..., T, d] tensor fold
+// into (B, H) = (prod(shape[:-3]), shape[-3]) when the folded dims are
+// uniformly strided; otherwise (or if d is not unit-stride) the tensor is
+// made contiguous first.
+struct FlashView {
+  Tensor t;  // the tensor the pointer refers to (keeps storage alive)
+  int64_t s[3];
+};
+
+bool fold_strides(const Tensor& t, int64_t out[3]) {
+  const size_t r = t.shape.size();
+  if (t.strides[r - 1] != 1) return false;
+  out[1] = t.strides[r - 3];
+  out[2] = t.strides[r - 2];
+  // Fold dims [0, r-3) into one batch dim: the non-trivial ones must nest
+  // (stride of dim i = stride of the next inner one x its extent).
+  int64_t sb = 0, span = 0;
+  bool have = false;
+  for (size_t i = r - 3; i-- > 0;) {
+    if (t.shape[i] == 1) continue;
+    if (!have) {
+      sb = t.strides[i];
+      span = t.shape[i];
+      have = true;
+      continue;
+    }
+    if (t.strides[i] != sb * span) return false;
+    span *= t.shape[i];
+  }
+  out[0] = sb;
+  return true;
+}
+
+FlashView flash_view(const Tensor& t) {
+  FlashView v{t, {0, 0, 0}};
+  if (!fold_strides(t, v.s)) {
+    v.t = contiguous(t);
+    fold_strides(v.t, v.s);
+  }
+  return v;
+}
+
+void flash_dims(const Tensor& t, int64_t& B, int64_t& H, int64_t& T, int64_t& d) {
+  const size_t r = t.shape.size();
+  d = t.shape[r - 1];
+  T = t.shape[r - 2];
+  H = t.shape[r - 3];
+  B = 1;
+  for (size_t i = 0; i + 3 < r; ++i) B *= t.shape[i];
+}
+
+void put3(int64_t* dst, const int64_t* s) {
+  dst[0] = s[0];
+  dst[1] = s[1];
+  dst[2] = s[2];
+}
+
 class FlashAttentionFunction : public Function {
  public:
-  Tensor saved_q, saved_k, saved_v, saved_o, saved_lse;
+  FlashView q, k, v;
+  Tensor saved_o, saved_lse;
   bool causal = false;
   float scale_factor = 1.0f;
   std::vector<Tensor> backward(const Tensor& grad_output) override {
-    Tensor go = as_contig(grad_output);
-    Tensor dq = Tensor::empty(saved_q.shape, saved_q.dtype, saved_q.device);
-    Tensor dk = Tensor::empty(saved_k.shape, saved_k.dtype, saved_k.device);
-    Tensor dv = Tensor::empty(saved_v.shape, saved_v.dtype, saved_v.device);
-    const int64_t d = saved_q.shape.back();
-    const int64_t T = saved_q.shape[saved_q.shape.size() - 2];
-    const int64_t bh = T * d ? static_cast<int64_t>(saved_q.numel()) / (T * d) : 0;
-    Workspace ws(aar_flash_bwd_workspace_bytes(bh, T, d));
-    check_status(aar_flash_bwd_f32(fp(saved_q), fp(saved_k), fp(saved_v), fp(saved_o), fp(saved_lse),
-                                   fp(go), fp(dq), fp(dk), fp(dv), bh, T, d, causal ? 1 : 0,
-                                   scale_factor, ws.data(), ws.bytes(), current_stream()),
+    FlashView go = flash_view(grad_output);
+    const Tensor& shp = q.t;
+    Tensor dq = Tensor::empty(shp.shape, shp.dtype, shp.device);
+    Tensor dk = Tensor::empty(shp.shape, shp.dtype, shp.device);
+    Tensor dv = Tensor::empty(shp.shape, shp.dtype, shp.device);
+    int64_t B, H, T, d;
+    flash_dims(shp, B, H, T, d);
+    int64_t st[24];
+    int64_t oc[3], dc[3];
+    fold_strides(saved_o, oc);
+    fold_strides(dq, dc);
+    put3(st, q.s);
+    put3(st + 3, k.s);
+    put3(st + 6, v.s);
+    put3(st + 9, oc);
+    put3(st + 12, go.s);
+    put3(st + 15, dc);
+    put3(st + 18, dc);
+    put3(st + 21, dc);
+    Workspace ws(aar_flash_bwd_workspace_bytes(B * H, T, d));
+    check_status(aar_flash_bwd_strided_f32(fp(q.t), fp(k.t), fp(v.t), fp(saved_o), fp(saved_lse), fp(go.t),
+                                           fp(dq), fp(dk), fp(dv), B, H, T, d, st, causal ? 1 : 0, scale_factor,
+                                           ws.data(), ws.bytes(), current_stream()),
                  "flash_attention backward");
     return {dq, dk, dv};
   }
@@ -382,21 +453,62 @@ void flash_check(const Tensor& q, const Tensor& k, const Tensor& v) {
   }
 }
 
-// Forward on contiguous inputs; returns (O, lse).
-std::tuple<Tensor, Tensor> flash_forward_device(const Tensor& qc, const Tensor& kc, const Tensor& vc,
+// Forward on (possibly strided) views; O and lse are contiguous.
+std::tuple<Tensor, Tensor> flash_forward_device(const FlashView& q, const FlashView& k, const FlashView& v,
                                                 bool causal, float s) {
-  const int64_t d = qc.shape.back();
+  int64_t B, H, T, d;
+  flash_dims(q.t, B, H, T, d);
   if (d > 128) throw std::invalid_argument("flash_attention: d_head exceeds D_MAX (128)");
-  const int64_t T = qc.shape[qc.shape.size() - 2];
-  std::vector<int64_t> lse_shape(qc.shape.begin(), qc.shape.end() - 1);
-  Tensor out = Tensor::empty(qc.shape, qc.dtype, qc.device);
-  Tensor lse = Tensor::empty(lse_shape, qc.dtype, qc.device);
-  const int64_t bh = T * d ? static_cast<int64_t>(qc.numel()) / (T * d) : 0;
-  check_status(aar_flash_fwd_f32(fp(qc), fp(kc), fp(vc), fp(out), fp(lse), bh, T, d, causal ? 1 : 0, s,
-                                 current_stream()),
+  std::vector<int64_t> lse_shape(q.t.shape.begin(), q.t.shape.end() - 1);
+  Tensor out = Tensor::empty(q.t.shape, q.t.dtype, q.t.device);
+  Tensor lse = Tensor::empty(lse_shape, q.t.dtype, q.t.device);
+  int64_t st[12], oc[3];
+  fold_strides(out, oc);
+  put3(st, q.s);
+  put3(st + 3, k.s);
+  put3(st + 6, v.s);
+  put3(st + 9, oc);
+  check_status(aar_flash_fwd_strided_f32(fp(q.t), fp(k.t), fp(v.t), fp(out), fp(lse), B, H, T, d, st,
+                                         causal ? 1 : 0, s, current_stream()),
                "flash_attention");
   return {out, lse};
 }
+
+// Fused attention over a packed projection qkv [..., T, 3*D] (q, k, v are
+// the column blocks [0, D), [D, 2D), [2D, 3D), each split into H heads of
+// d = D/H): O [..., T, D] with O[t][h*d + c] = attention of head h.  The same
+// math as flash_attention on the per-head views (nn.py's MultiHeadAttention
+// composition, aargrad/nn.py:177-192), without materialising the views: the
+// kernels read q/k/v in place, write O in [T, H, d] order and the backward
+// writes dq/dk/dv straight into one packed gradient.
+class FlashQKVFunction : public Function {
+ public:
+  Tensor saved_qkv, saved_o, saved_lse;
+  int64_t B = 0, H = 0, T = 0, d = 0;
+  bool causal = false;
+  float scale_factor = 1.0f;
+  std::vector<Tensor> backward(const Tensor& grad_output) override {
+    Tensor go = as_contig(grad_output);
+    Tensor dqkv = Tensor::empty(saved_qkv.shape, saved_qkv.dtype, saved_qkv.device);
+    const int64_t D = H * d;
+    const int64_t pk[3] = {T * 3 * D, d, 3 * D};  // packed q/k/v/dq/dk/dv
+    const int64_t po[3] = {T * D, d, D};          // O and dO
+    int64_t st[24];
+    for (int i : {0, 1, 2, 5, 6, 7}) put3(st + 3 * i, pk);
+    put3(st + 9, po);
+    put3(st + 12, po);
+    float* g = fp(dqkv);
+    const float* x = fp(saved_qkv);
+    Workspace ws(aar_flash_bwd_workspace_bytes(B * H, T, d));
+    check_status(aar_flash_bwd_strided_f32(x, x + D, x + 2 * D, fp(saved_o), fp(saved_lse), fp(go), g, g + D,
+                                           g + 2 * D, B, H, T, d, st, causal ? 1 : 0, scale_factor, ws.data(),
+                                           ws.bytes(), current_stream()),
+                 "flash_attention_qkv backward");
+    return {dqkv};
+  }
+  const char* name() const override { return "FlashQKVFunction"; }
+};
+
 
 // ------------------------------------------------------------------ add
 
@@ -649,18 +761,18 @@ Tensor layernorm(const Tensor& x, const Tensor& weight, const Tensor& bias, floa
 
 Tensor flash_attention(const Tensor& q, const Tensor& k, const Tensor& v, bool causal) {
   flash_check(q, k, v);
-  Tensor qc = as_contig(q), kc = as_contig(k), vc = as_contig(v);
-  if (qc.device == Device::CPU) throw_cpu_compute("flash_attention");
-  const float s = 1.0f / std::sqrt(static_cast<float>(qc.shape.back()));
-  auto [out, lse] = flash_forward_device(qc, kc, vc, causal, s);
-  if (!qc.requires_grad && !kc.requires_grad && !vc.requires_grad) return out;
+  if (q.device == Device::CPU) throw_cpu_compute("flash_attention");
+  FlashView qv = flash_view(q), kv = flash_view(k), vv = flash_view(v);
+  const float s = 1.0f / std::sqrt(static_cast<float>(q.shape.back()));
+  auto [out, lse] = flash_forward_device(qv, kv, vv, causal, s);
+  if (!q.requires_grad && !k.requires_grad && !v.requires_grad) return out;
   auto fn = std::make_shared<FlashAttentionFunction>();
-  fn->record_input(qc);
-  fn->record_input(kc);
-  fn->record_input(vc);
-  fn->saved_q = qc;
-  fn->saved_k = kc;
-  fn->saved_v = vc;
+  fn->record_input(q);
+  fn->record_input(k);
+  fn->record_input(v);
+  fn->q = qv;
+  fn->k = kv;
+  fn->v = vv;
   fn->saved_o = out;
   fn->saved_lse = lse;
   fn->causal = causal;
@@ -673,10 +785,55 @@ Tensor flash_attention(const Tensor& q, const Tensor& k, const Tensor& v, bool c
 std::tuple<Tensor, Tensor> flash_attention_fwd_lse(const Tensor& q, const Tensor& k, const Tensor& v,
                                                    bool causal) {
   flash_check(q, k, v);
-  Tensor qc = as_contig(q), kc = as_contig(k), vc = as_contig(v);
-  if (qc.device == Device::CPU) throw_cpu_compute("flash_attention");
-  const float s = 1.0f / std::sqrt(static_cast<float>(qc.shape.back()));
-  return flash_forward_device(qc, kc, vc, causal, s);
+  if (q.device == Device::CPU) throw_cpu_compute("flash_attention");
+  const float s = 1.0f / std::sqrt(static_cast<float>(q.shape.back()));
+  return flash_forward_device(flash_view(q), flash_view(k), flash_view(v), causal, s);
+}
+
+Tensor flash_attention_qkv(const Tensor& qkv, int64_t n_heads, bool causal) {
+  if (qkv.dtype != DType::Fp32) throw std::invalid_argument("flash_attention_qkv: only Fp32 supported");
+  if (qkv.shape.size() < 2) throw std::invalid_argument("flash_attention_qkv: need [..., T, 3*D]");
+  const int64_t D3 = qkv.shape.back();
+  if (n_heads <= 0 || D3 % (3 * n_heads) != 0) {
+    throw std::invalid_argument("flash_attention_qkv: last dim must be 3 * n_heads * d_head");
+  }
+  if (qkv.device == Device::CPU) throw_cpu_compute("flash_attention_qkv");
+  Tensor x = as_contig(qkv);
+  const int64_t D = D3 / 3, d = D / n_heads, T = x.shape[x.shape.size() - 2];
+  if (d > 128) throw std::invalid_argument("flash_attention: d_head exceeds D_MAX (128)");
+  int64_t B = 1;
+  for (size_t i = 0; i + 2 < x.shape.size(); ++i) B *= x.shape[i];
+  std::vector<int64_t> oshape(x.shape);
+  oshape.back() = D;
+  Tensor out = Tensor::empty(oshape, x.dtype, x.device);
+  Tensor lse = Tensor::empty({B * n_heads, T}, x.dtype, x.device);
+  const int64_t pk[3] = {T * 3 * D, d, 3 * D};
+  const int64_t po[3] = {T * D, d, D};
+  int64_t st[12];
+  put3(st, pk);
+  put3(st + 3, pk);
+  put3(st + 6, pk);
+  put3(st + 9, po);
+  const float s = 1.0f / std::sqrt(static_cast<float>(d));
+  const float* p = fp(x);
+  check_status(aar_flash_fwd_strided_f32(p, p + D, p + 2 * D, fp(out), fp(lse), B, n_heads, T, d, st,
+                                         causal ? 1 : 0, s, current_stream()),
+               "flash_attention_qkv");
+  if (!qkv.requires_grad) return out;
+  auto fn = std::make_shared<FlashQKVFunction>();
+  fn->record_input(qkv);
+  fn->saved_qkv = x;
+  fn->saved_o = out;
+  fn->saved_lse = lse;
+  fn->B = B;
+  fn->H = n_heads;
+  fn->T = T;
+  fn->d = d;
+  fn->causal = causal;
+  fn->scale_factor = s;
+  out.requires_grad = true;
+  out.grad_fn = fn;
+  return out;
 }
 
 Tensor add(const Tensor& a, const Tensor& b) {

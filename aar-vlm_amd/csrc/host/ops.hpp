@@ -27,6 +27,9 @@ Tensor layernorm(const Tensor& x, const Tensor& weight, const Tensor& bias, floa
 
 // Attention (cppsrc/ops/flash_attention.cpp:65-98).
 Tensor flash_attention(const Tensor& q, const Tensor& k, const Tensor& v, bool causal);
+// Attention over a packed projection [..., T, 3*D] -> [..., T, D] (the
+// MultiHeadAttention composition without materialised head views).
+Tensor flash_attention_qkv(const Tensor& qkv, int64_t n_heads, bool causal);
 // Forward returning (O, lse) for benchmarks and parity checks; no autograd node.
 std::tuple<Tensor, Tensor> flash_attention_fwd_lse(const Tensor& q, const Tensor& k, const Tensor& v,
                                                    bool causal);

@@ -342,9 +342,9 @@ class GPT:
         for i in range(c["layers"]):
             (l1w, l1b, wqkv, wout, l2w, l2b, f1w, f1b, f2w, f2b) = p[2 + 10 * i: 12 + 10 * i]
             h = ag.layernorm(x, l1w, l1b, 1e-5)
-            qkv = ag.reshape(ag.matmul_a_bt(h, wqkv), [B, T, 3, H, d // H])
-            q, k, v = (ag.transpose(ag.squeeze(ag.slice(qkv, 2, j, j + 1), 2), 1, 2) for j in range(3))
-            a = ag.reshape(ag.transpose(ag.flash_attention(q, k, v, True), 1, 2), [B, T, d])
+            # nn.MultiHeadAttention's composition (per-head views of the packed
+            # projection, causal flash attention, heads merged) as one fused op
+            a = ag._core._flash_attention_qkv(ag.matmul_a_bt(h, wqkv), H, True)
             x = ag.add(x, ag.matmul_a_bt(a, wout))
             h = ag.layernorm(x, l2w, l2b, 1e-5)
             h = ag.relu(ag.add_bias(ag.matmul_a_bt(h, f1w), f1b))

@@ -163,6 +163,28 @@ int aar_flash_bwd_f32(const float* q, const float* k, const float* v,
                       int64_t bh, int64_t T, int64_t d, int causal, float scale,
                       void* workspace, size_t workspace_bytes, void* stream);
 
+/* Strided forms of the two calls above, for q/k/v views of a packed
+ * [B, T, 3, H, d] projection and outputs in [B, T, H, d] order (the
+ * MultiHeadAttention views of aargrad/nn.py:177-189, which the reference
+ * copies to contiguous tensors first, cppsrc/ops/shape.cpp:244-274).  Every
+ * [B, H, T, d] operand X has element (b, h, t, c) at
+ *   X[b*sb + h*sh + t*st + c]      (element strides, head dim contiguous)
+ * and `strides` lists (sb, sh, st) per operand: 12 values for the forward
+ * (q, k, v, o), 24 for the backward (q, k, v, o, dout, dq, dk, dv).  lse and
+ * the workspace are contiguous [B*H, T].  128-bit paths need 16-byte aligned
+ * pointers and d and all strides multiples of 4; other layouts take the
+ * element-wise path.  The unstrided calls are these with contiguous strides. */
+int aar_flash_fwd_strided_f32(const float* q, const float* k, const float* v,
+                              float* o, float* lse, int64_t B, int64_t H,
+                              int64_t T, int64_t d, const int64_t* strides,
+                              int causal, float scale, void* stream);
+int aar_flash_bwd_strided_f32(const float* q, const float* k, const float* v,
+                              const float* o, const float* lse, const float* dout,
+                              float* dq, float* dk, float* dv,
+                              int64_t B, int64_t H, int64_t T, int64_t d,
+                              const int64_t* strides, int causal, float scale,
+                              void* workspace, size_t workspace_bytes, void* stream);
+
 /* Strided fp32 copy of an ndim <= 8 view: dst[idx] = src[idx] for every index
  * of `shape`, element offsets given by the two stride arrays (host arrays, read
  * during the call).  Replaces contiguous_cuda / copy_contiguous_into_strided_cuda

@@ -5,6 +5,7 @@ build, sampled heads of BASELINE config 4 and full-size checksum identities.
 Tolerance 1e-4 on both error metrics."""
 from __future__ import annotations
 
+import ctypes
 import math
 
 import numpy as np
@@ -147,7 +148,7 @@ def test_backward_is_reproducible(gpu):
 
 def test_strided_views_like_mha(gpu):
     """nn.MultiHeadAttention feeds slice/squeeze/transpose views of qkv
-    [B,T,3,H,d] (aargrad/nn.py:177-189); they are made contiguous first."""
+    [B,T,3,H,d] (aargrad/nn.py:177-189); the kernels read them in place."""
     B, T, H, d = 2, 48, 3, 16
     rng = np.random.default_rng(9)
     qkv = rng.standard_normal((B, T, 3, H, d)).astype(f32)
@@ -197,3 +198,111 @@ def test_head_dim_limit(gpu):
     x = dev(gpu, np.zeros((1, 4, 136), f32))
     with pytest.raises(ValueError, match="D_MAX"):
         gpu.flash_attention(x, x, x, True)
+
+
+def _packed_reference(qkv, H, causal, do):
+    """Per-head q/k/v of a packed [B,T,3D] projection, oracle O [B,T,D] and
+    the packed gradient for upstream dO [B,T,D]."""
+    B, T, D3 = qkv.shape
+    D = D3 // 3
+    d = D // H
+    heads = qkv.reshape(B, T, 3, H, d)
+    q, k, v = (np.ascontiguousarray(heads[:, :, i].transpose(0, 2, 1, 3)).reshape(B * H, T, d) for i in range(3))
+    o = O.attention(q, k, v, causal).reshape(B, H, T, d).transpose(0, 2, 1, 3).reshape(B, T, D)
+    dob = np.ascontiguousarray(do.reshape(B, T, H, d).transpose(0, 2, 1, 3)).reshape(B * H, T, d)
+    gq, gk, gv = O.attention_backward(q, k, v, dob, causal)
+    g = np.stack([x.reshape(B, H, T, d).transpose(0, 2, 1, 3) for x in (gq, gk, gv)], axis=2)
+    return o, g.reshape(B, T, 3 * D)
+
+
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("shape", [(2, 70, 3, 16), (1, 64, 2, 64), (2, 33, 2, 18)], ids=str)
+def test_packed_qkv_attention(gpu, shape, causal):
+    """_flash_attention_qkv (MultiHeadAttention's fused path) against the
+    oracle on the per-head views, forward and the packed gradient; d = 18
+    takes the element-wise (non-128-bit) path."""
+    B, T, H, d = shape
+    D = H * d
+    rng = np.random.default_rng(B * T + H * d + causal)
+    qkv = rng.standard_normal((B, T, 3 * D)).astype(f32)
+    do = rng.standard_normal((B, T, D)).astype(f32)
+    t = dev(gpu, qkv, True)
+    o = gpu._core._flash_attention_qkv(t, H, causal)
+    assert o.shape == [B, T, D] and o.is_contiguous()
+    o.backward(dev(gpu, do))
+    ro, rg = _packed_reference(qkv, H, causal, do)
+    assert_close(host(gpu, o), ro, TOL, "O")
+    assert_close(host(gpu, t.grad), rg, TOL, "dqkv")
+
+
+def test_mha_fused_equals_views(gpu):
+    """nn.MultiHeadAttention.forward (fused) and forward_views (the
+    reference's literal composition) give the same output and gradients."""
+    from aargrad import nn
+    rng = np.random.default_rng(12)
+    B, T, D, H = 2, 40, 48, 3
+    mha = nn.MultiHeadAttention(D, H, causal=True, bias=True, rng=rng).to(gpu.Device.CUDA)
+    x_np = rng.standard_normal((B, T, D)).astype(f32)
+    g_np = rng.standard_normal((B, T, D)).astype(f32)
+    outs, grads = [], []
+    for fwd in (mha.forward, mha.forward_views):
+        mha.zero_grad()
+        x = dev(gpu, x_np, True)
+        y = fwd(x)
+        y.backward(dev(gpu, g_np))
+        outs.append(host(gpu, y))
+        grads.append([host(gpu, x.grad)] + [host(gpu, p.tensor.grad) for p in mha.parameters()])
+    assert_close(outs[0], outs[1], TOL, "y")
+    for a, b in zip(grads[0], grads[1]):
+        assert_close(a, b, TOL, "grad")
+
+
+def test_rank5_and_unfoldable_batch_views(gpu):
+    """Leading dims fold into one batch stride when they nest; a view whose
+    batch dims do not nest (swapped) is copied first.  Both match the oracle."""
+    rng = np.random.default_rng(13)
+    q, k, v = (rng.standard_normal((2, 3, 2, 40, 16)).astype(f32) for _ in range(3))
+    o = host(gpu, gpu.flash_attention(dev(gpu, q), dev(gpu, k), dev(gpu, v), True))
+    ref = O.attention(q.reshape(12, 40, 16), k.reshape(12, 40, 16), v.reshape(12, 40, 16), True)
+    assert_close(o.reshape(12, 40, 16), ref, TOL, "rank5")
+    tq, tk, tv = (gpu.transpose(dev(gpu, x), 0, 1) for x in (q, k, v))  # [3, 2, 2, T, d] views
+    assert not tq.is_contiguous()
+    o2 = host(gpu, gpu.flash_attention(tq, tk, tv, True))
+    qs, ks, vs = (np.ascontiguousarray(x.transpose(1, 0, 2, 3, 4)).reshape(12, 40, 16) for x in (q, k, v))
+    assert_close(o2.reshape(12, 40, 16), O.attention(qs, ks, vs, True), TOL, "swapped batch")
+
+
+def test_abi_strided_output_layout(gpu):
+    """aar_flash_fwd/bwd_strided_f32 with q/k/v read from a packed
+    [B,T,3,H,d] buffer and O, dO, dq/dk/dv in [B,T,H,d] order."""
+    B, T, H, d = 2, 50, 3, 32
+    rng = np.random.default_rng(14)
+    qkv = rng.standard_normal((B, T, 3, H, d)).astype(f32)
+    do = rng.standard_normal((B, T, H, d)).astype(f32)
+    abi = Abi()
+    L = abi.L
+    i64p = ctypes.POINTER(ctypes.c_int64)
+    vp, i64 = ctypes.c_void_p, ctypes.c_int64
+    L.aar_flash_fwd_strided_f32.argtypes = [vp] * 5 + [i64] * 4 + [i64p, ctypes.c_int, ctypes.c_float, vp]
+    L.aar_flash_bwd_strided_f32.argtypes = [vp] * 9 + [i64] * 4 + [i64p, ctypes.c_int, ctypes.c_float, vp,
+                                                                  ctypes.c_size_t, vp]
+    try:
+        px = abi.put(qkv)
+        D = H * d
+        pk = [T * 3 * D, d, 3 * D]
+        po = [T * D, d, D]
+        st = (ctypes.c_int64 * 24)(*(pk * 3 + po + po + [T * 3 * D, d, 3 * D] * 3))
+        pq, pkk, pv = px, px + 4 * D, px + 8 * D
+        pout, plse = abi.empty(B * T * D), abi.empty(B * H * T)
+        s = 1.0 / math.sqrt(d)
+        abi.check(L.aar_flash_fwd_strided_f32(pq, pkk, pv, pout, plse, B, H, T, d, st, 1, s, None))
+        ro, rg = _packed_reference(qkv.reshape(B, T, 3 * D), H, True, do.reshape(B, T, D))
+        assert_close(abi.get(pout, (B, T, D)), ro, TOL, "O")
+        pdo = abi.put(do)
+        pg = abi.empty(B * T * 3 * D)
+        wsb = L.aar_flash_bwd_workspace_bytes(B * H, T, d)
+        abi.check(L.aar_flash_bwd_strided_f32(pq, pkk, pv, pout, plse, pdo, pg, pg + 4 * D, pg + 8 * D, B, H, T,
+                                              d, st, 1, s, abi.alloc(wsb), wsb, None))
+        assert_close(abi.get(pg, (B, T, 3 * D)), rg, TOL, "dqkv")
+    finally:
+        abi.free()
