@@ -161,8 +161,8 @@ class Sequential(Module):
 
 
 def scaled_dot_product_attention(q, k, v, *, causal=False):
-    """Unfused attention (aargrad/nn.py:154-161); needs bmm-style products on
-    the device, which this build routes through flash_attention instead."""
+    """Unfused attention over [T, d] operands (aargrad/nn.py:154-161): every
+    step (product, scale, causal mask, softmax, product) runs on the device."""
     scores = _core.scale(_core.matmul_a_bt(q, k), 1.0 / math.sqrt(q.shape[-1]))
     if causal:
         scores = _core.apply_causal_mask(scores)

@@ -142,7 +142,8 @@ template <int BM, int BN, int BK, int WM, int WN, int WPE, bool A_KC, bool B_KC>
 __global__ void __launch_bounds__((BM / WM) * (BN / WN) * 64, WPE)
 gemm_f32_kernel(const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C,
                 int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc,
-                int64_t k_per_split, int64_t split_stride, int tiles_m, int tiles_n) {
+                int64_t k_per_split, int64_t split_stride, int tiles_m, int tiles_n, int64_t sA, int64_t sB,
+                int64_t sC) {
   constexpr int NWM = BM / WM;
   constexpr int NT = NWM * (BN / WN) * 64;
   constexpr int TM = WM / 32;
@@ -171,6 +172,10 @@ gemm_f32_kernel(const float* __restrict__ A, const float* __restrict__ B, float*
   const int64_t kbeg = (int64_t)blockIdx.y * k_per_split;
   const int64_t kend = min(K, kbeg + k_per_split);
   C += (int64_t)blockIdx.y * split_stride;
+  // batched launches: one grid layer per matrix (blockIdx.z)
+  A += (int64_t)blockIdx.z * sA;
+  B += (int64_t)blockIdx.z * sB;
+  C += (int64_t)blockIdx.z * sC;
 
   f32x16 acc[TM][TN];
 #pragma unroll
@@ -374,7 +379,8 @@ template <int BM, int BN, int BK, int WM, int WN, int WPE, int S, bool A_KC, boo
 __global__ void __launch_bounds__((BM / WM) * (BN / WN) * 64, WPE)
 gemm_f32_dma_kernel(const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C,
                     int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc,
-                    int64_t k_per_split, int64_t split_stride, int tiles_m, int tiles_n) {
+                    int64_t k_per_split, int64_t split_stride, int tiles_m, int tiles_n, int64_t sA,
+                    int64_t sB, int64_t sC) {
   constexpr int NWM = BM / WM;
   constexpr int NW = NWM * (BN / WN);
   constexpr int TM = WM / 32;
@@ -407,6 +413,10 @@ gemm_f32_dma_kernel(const float* __restrict__ A, const float* __restrict__ B, fl
   const int ntiles = kend > kbeg ? (int)ceil_div(kend - kbeg, (int64_t)BK) : 0;
   const bool ragged = kend > kbeg && ((kend - kbeg) % BK) != 0;
   C += (int64_t)blockIdx.y * split_stride;
+  // batched launches: one grid layer per matrix (blockIdx.z)
+  A += (int64_t)blockIdx.z * sA;
+  B += (int64_t)blockIdx.z * sB;
+  C += (int64_t)blockIdx.z * sC;
 
   f32x16 acc[TM][TN];
 #pragma unroll
@@ -546,14 +556,14 @@ int64_t split_chunk(int64_t K, int splits, int bk) { return ceil_div(ceil_div(K,
 // of `eff` with one block); split-K adds the partial-sum traffic and the
 // reduction launch.  Fitted to measured throughput of every configuration on
 // the square, MLP and weight-gradient shapes of the GPT step.
-Plan plan_gemm(int64_t M, int64_t N, int64_t K, size_t ws_bytes, bool allow_split) {
+Plan plan_gemm(int64_t M, int64_t N, int64_t K, size_t ws_bytes, bool allow_split, int64_t batch = 1) {
   const int cus = device_cu_count();
   const double cu_flops = 157.3e12 / 256;  // fp32 MFMA FLOP/s per CU
   Plan best{kNumCfgs - 1, 1, K};
   double best_t = 1e300;
   for (int c = 0; c < kNumCfgs; ++c) {
     const Cfg& cf = kCfgs[c];
-    const int64_t tiles = ceil_div(M, (int64_t)cf.bm) * ceil_div(N, (int64_t)cf.bn);
+    const int64_t tiles = ceil_div(M, (int64_t)cf.bm) * ceil_div(N, (int64_t)cf.bn) * batch;
     for (int splits = 1; splits <= kMaxSplits; splits *= 2) {
       if (splits > 1) {
         if (!allow_split) break;
@@ -575,33 +585,40 @@ Plan plan_gemm(int64_t M, int64_t N, int64_t K, size_t ws_bytes, bool allow_spli
   return best;
 }
 
+// Batched launches: `count` matrices at element strides sA / sB / sC.
+struct Batch {
+  int64_t count, sA, sB, sC;
+};
+constexpr Batch kSingle{1, 0, 0, 0};
+
 template <int BM, int BN, int BK, int WM, int WN, int RES, int STAGES, bool A_KC, bool B_KC>
 int launch_cfg(bool vec, const float* A, const float* B, float* C, int64_t M, int64_t N, int64_t K,
                int64_t lda, int64_t ldb, int64_t ldc, int splits, int64_t kps, int64_t split_stride,
-               hipStream_t st) {
+               const Batch& bt, hipStream_t st) {
   constexpr int kWaves = (BM / WM) * (BN / WN);
   constexpr int kWpe = (RES * kWaves + 3) / 4;
   const int tiles_m = (int)ceil_div(M, (int64_t)BM);
   const int tiles_n = (int)ceil_div(N, (int64_t)BN);
-  dim3 grid((unsigned)(tiles_m * tiles_n), (unsigned)splits);
+  dim3 grid((unsigned)(tiles_m * tiles_n), (unsigned)splits, (unsigned)bt.count);
   dim3 block(kWaves * 64);
   if (vec)
     gemm_f32_dma_kernel<BM, BN, BK, WM, WN, kWpe, STAGES, A_KC, B_KC><<<grid, block, 0, st>>>(
-        A, B, C, M, N, K, lda, ldb, ldc, kps, split_stride, tiles_m, tiles_n);
+        A, B, C, M, N, K, lda, ldb, ldc, kps, split_stride, tiles_m, tiles_n, bt.sA, bt.sB, bt.sC);
   else
     gemm_f32_kernel<BM, BN, BK, WM, WN, kWpe, A_KC, B_KC><<<grid, block, 0, st>>>(
-        A, B, C, M, N, K, lda, ldb, ldc, kps, split_stride, tiles_m, tiles_n);
+        A, B, C, M, N, K, lda, ldb, ldc, kps, split_stride, tiles_m, tiles_n, bt.sA, bt.sB, bt.sC);
   return launch_status();
 }
 
 template <bool A_KC, bool B_KC>
 int launch_op(int cfg, bool vec, const float* A, const float* B, float* C, int64_t M, int64_t N,
               int64_t K, int64_t lda, int64_t ldb, int64_t ldc, int splits, int64_t kps,
-              int64_t split_stride, hipStream_t st) {
+              int64_t split_stride, const Batch& bt, hipStream_t st) {
 #define AAR_GEMM_CFG(I)                                                                                   \
   case I:                                                                                                 \
     return launch_cfg<kCfgs[I].bm, kCfgs[I].bn, kCfgs[I].bk, kCfgs[I].wm, kCfgs[I].wn, kCfgs[I].resident, \
-                      kCfgs[I].stages, A_KC, B_KC>(vec, A, B, C, M, N, K, lda, ldb, ldc, splits, kps, split_stride, st);
+                      kCfgs[I].stages, A_KC, B_KC>(vec, A, B, C, M, N, K, lda, ldb, ldc, splits, kps, split_stride, \
+                                                   bt, st);
   switch (cfg) {
     AAR_GEMM_CFG(0)
     AAR_GEMM_CFG(1)
@@ -617,44 +634,53 @@ int launch_op(int cfg, bool vec, const float* A, const float* B, float* C, int64
 }
 static_assert(kNumCfgs == 7, "launch_op lists every configuration");
 
-// 128-bit loads need 16-byte aligned operands whose contiguous extents are
-// multiples of 4, and the 32-bit per-thread offsets need BR*ld*4 < 2^32.
-bool gemm_vec_ok(int op, int64_t M, int64_t N, int64_t K, const float* A, const float* B) {
+// 128-bit loads need 16-byte aligned operands whose contiguous extents and
+// leading dimensions are multiples of 4, and the 32-bit per-thread offsets
+// need BR*ld*4 < 2^32.
+constexpr int64_t kMaxLd = (int64_t(1) << 32) / (4 * 256) - 1;
+bool gemm_vec_ok(int op, int64_t M, int64_t N, int64_t K, const float* A, const float* B, int64_t lda,
+                 int64_t ldb) {
   if (!aligned16(A) || !aligned16(B)) return false;
-  constexpr int64_t kMaxLd = (int64_t(1) << 32) / (4 * 256) - 1;
+  if (lda % 4 != 0 || ldb % 4 != 0 || lda > kMaxLd || ldb > kMaxLd) return false;
   switch (op) {
-    case AAR_GEMM_NN: return (K % 4 == 0) && (N % 4 == 0) && K <= kMaxLd && N <= kMaxLd;
-    case AAR_GEMM_NT: return (K % 4 == 0) && K <= kMaxLd;
-    default: return (M % 4 == 0) && (N % 4 == 0) && M <= kMaxLd && N <= kMaxLd;
+    case AAR_GEMM_NN: return (K % 4 == 0) && (N % 4 == 0);
+    case AAR_GEMM_NT: return (K % 4 == 0);
+    default: return (M % 4 == 0) && (N % 4 == 0);
   }
 }
 
-int run_gemm(int op, int64_t M, int64_t N, int64_t K, const float* A, const float* B, float* C,
-             void* workspace, const Plan& p, hipStream_t st) {
-  const bool vec = gemm_vec_ok(op, M, N, K, A, B);
-  int64_t lda, ldb;
+int default_ld(int op, int64_t M, int64_t N, int64_t K, int64_t& lda, int64_t& ldb) {
   switch (op) {
     case AAR_GEMM_NN: lda = K; ldb = N; break;
     case AAR_GEMM_NT: lda = K; ldb = K; break;
     default: lda = M; ldb = N; break;
   }
-  float* out = p.splits > 1 ? static_cast<float*>(workspace) : C;
-  const int64_t split_stride = p.splits > 1 ? M * N : 0;
-  int rc;
+  return AAR_OK;
+}
+
+int dispatch_op(int op, int cfg, bool vec, const float* A, const float* B, float* C, int64_t M, int64_t N,
+                int64_t K, int64_t lda, int64_t ldb, int64_t ldc, int splits, int64_t kps, int64_t split_stride,
+                const Batch& bt, hipStream_t st) {
   switch (op) {
     case AAR_GEMM_NN:
-      rc = launch_op<true, false>(p.cfg, vec, A, B, out, M, N, K, lda, ldb, N, p.splits, p.k_per_split,
-                                  split_stride, st);
-      break;
+      return launch_op<true, false>(cfg, vec, A, B, C, M, N, K, lda, ldb, ldc, splits, kps, split_stride, bt, st);
     case AAR_GEMM_NT:
-      rc = launch_op<true, true>(p.cfg, vec, A, B, out, M, N, K, lda, ldb, N, p.splits, p.k_per_split,
-                                 split_stride, st);
-      break;
+      return launch_op<true, true>(cfg, vec, A, B, C, M, N, K, lda, ldb, ldc, splits, kps, split_stride, bt, st);
     default:
-      rc = launch_op<false, false>(p.cfg, vec, A, B, out, M, N, K, lda, ldb, N, p.splits,
-                                   p.k_per_split, split_stride, st);
-      break;
+      return launch_op<false, false>(cfg, vec, A, B, C, M, N, K, lda, ldb, ldc, splits, kps, split_stride, bt,
+                                     st);
   }
+}
+
+int run_gemm(int op, int64_t M, int64_t N, int64_t K, const float* A, const float* B, float* C,
+             void* workspace, const Plan& p, hipStream_t st) {
+  int64_t lda, ldb;
+  default_ld(op, M, N, K, lda, ldb);
+  const bool vec = gemm_vec_ok(op, M, N, K, A, B, lda, ldb);
+  float* out = p.splits > 1 ? static_cast<float*>(workspace) : C;
+  const int64_t split_stride = p.splits > 1 ? M * N : 0;
+  int rc = dispatch_op(op, p.cfg, vec, A, B, out, M, N, K, lda, ldb, N, p.splits, p.k_per_split, split_stride,
+                       kSingle, st);
   if (rc != AAR_OK || p.splits <= 1) return rc;
   const int64_t n = M * N;
   if (n % 4 == 0 && aligned16(out) && aligned16(C)) {
@@ -731,4 +757,24 @@ extern "C" int aar_gemm_f32_with_config(int op, int64_t M, int64_t N, int64_t K,
   if (real_splits > 1 && (!workspace || workspace_bytes < (size_t)real_splits * M * N * sizeof(float)))
     return AAR_EWORKSPACE;
   return run_gemm(op, M, N, K, A, B, C, workspace, Plan{config, real_splits, kps}, as_stream(stream));
+}
+
+extern "C" int aar_gemm_f32_batched(int op, int64_t batch, int64_t M, int64_t N, int64_t K, const float* A,
+                                    int64_t lda, int64_t strideA, const float* B, int64_t ldb, int64_t strideB,
+                                    float* C, int64_t ldc, int64_t strideC, void* stream) {
+  if (op < 0 || op > 2 || batch < 0 || M < 0 || N < 0 || K < 0) return AAR_EINVAL;
+  if (batch == 0 || M == 0 || N == 0) return AAR_OK;
+  if (!C || ldc < N) return AAR_EINVAL;
+  if (K == 0) {
+    if (ldc != N || (batch > 1 && strideC != M * N)) return AAR_EUNSUPPORTED;
+    return aar_memset_zero(C, (size_t)(batch * M * N) * sizeof(float), stream);
+  }
+  if (!A || !B) return AAR_EINVAL;
+  const int64_t need_a = op == AAR_GEMM_TN ? M : K, need_b = op == AAR_GEMM_NT ? K : N;
+  if (lda < need_a || ldb < need_b) return AAR_EINVAL;
+  if (M > INT32_MAX / 2 || N > INT32_MAX / 2 || batch > 65535) return AAR_EUNSUPPORTED;
+  const bool vec = gemm_vec_ok(op, M, N, K, A, B, lda, ldb) && strideA % 4 == 0 && strideB % 4 == 0;
+  const Plan p = plan_gemm(M, N, K, 0, false, batch);
+  return dispatch_op(op, p.cfg, vec, A, B, C, M, N, K, lda, ldb, ldc, 1, p.k_per_split, 0,
+                     Batch{batch, strideA, strideB, strideC}, as_stream(stream));
 }

@@ -372,6 +372,72 @@ adamw_kernel(float* __restrict__ p, const float* __restrict__ g, float* __restri
   }
 }
 
+// ---------------------------------------------------------------- dropout
+
+// Philox-4x32-10 (Salmon, Moraes, Dror, Shaw, "Parallel Random Numbers: As
+// Easy as 1, 2, 3", SC'11): counter (idx lo, idx hi, 0, 0), key (seed lo,
+// seed hi), ten rounds with the Weyl key bump between rounds; the uniform is
+// word 0 scaled by 2^-32 in float arithmetic, which is the stream the
+// reference's dropout draws (cppsrc/core/rng.hpp:13-46).
+__device__ __forceinline__ float philox_uniform(uint64_t seed, uint64_t idx) {
+  uint32_t c0 = (uint32_t)idx, c1 = (uint32_t)(idx >> 32), c2 = 0u, c3 = 0u;
+  uint32_t k0 = (uint32_t)seed, k1 = (uint32_t)(seed >> 32);
+#pragma unroll
+  for (int r = 0; r < 10; ++r) {
+    const uint32_t lo0 = c0 * 0xD2511F53u, hi0 = __umulhi(c0, 0xD2511F53u);
+    const uint32_t lo1 = c2 * 0xCD9E8D57u, hi1 = __umulhi(c2, 0xCD9E8D57u);
+    const uint32_t n0 = hi1 ^ c1 ^ k0, n2 = hi0 ^ c3 ^ k1;
+    c0 = n0;
+    c1 = lo1;
+    c2 = n2;
+    c3 = lo0;
+    k0 += 0x9E3779B9u;
+    k1 += 0xBB67AE85u;
+  }
+  return (float)c0 * (1.0f / 4294967296.0f);
+}
+
+// out = x * m, m = (u >= p ? 1/(1-p) : 0) with u the Philox uniform of the
+// element's flat index (cppsrc/ops/dropout.cpp:30-42).
+__global__ void __launch_bounds__(256)
+dropout_kernel(const float* __restrict__ x, float* __restrict__ out, float* __restrict__ mask, int64_t n, float p,
+               float scale, uint64_t seed) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+    const float keep = philox_uniform(seed, (uint64_t)i) >= p ? scale : 0.0f;
+    mask[i] = keep;
+    out[i] = x[i] * keep;
+  }
+}
+
+// ---------------------------------------------------------------- causal mask
+
+// y[m][i][j] = j <= i ? x[m][i][j] : fill over [mats, T, T] (forward fill is
+// -inf, backward 0; cppsrc/ops/attention.cpp:24-73).  Four columns per
+// thread when T % 4 == 0 and the pointers are 16-byte aligned.
+__global__ void __launch_bounds__(256)
+causal_mask_vec_kernel(const f32x4* __restrict__ x, f32x4* __restrict__ y, int64_t n4, int64_t T, float fill) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t u = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; u < n4; u += stride) {
+    const int64_t e = u * 4;
+    const int64_t j = e % T, i = (e / T) % T;
+    f32x4 v = x[u];
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      if (j + k > i) v[k] = fill;
+    y[u] = v;
+  }
+}
+
+__global__ void __launch_bounds__(256)
+causal_mask_kernel(const float* __restrict__ x, float* __restrict__ y, int64_t n, int64_t T, float fill) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < n; e += stride) {
+    const int64_t j = e % T, i = (e / T) % T;
+    y[e] = j <= i ? x[e] : fill;
+  }
+}
+
 }  // namespace
 }  // namespace aar
 
@@ -554,6 +620,30 @@ int aar_adamw_f32(float* param, const float* grad, float* m, float* v, int64_t n
   if (!param || !grad || !m || !v) return AAR_EINVAL;
   adamw_kernel<<<dim3(stream_grid(n)), dim3(256), 0, as_stream(stream)>>>(
       param, grad, m, v, n, lr, beta1, beta2, eps, 1.0f - lr * weight_decay, bias_correction1, bias_correction2);
+  return launch_status();
+}
+
+int aar_dropout_f32(const float* x, float* out, float* mask, int64_t n, float p, uint64_t seed, void* stream) {
+  if (n < 0 || !(p >= 0.0f && p < 1.0f)) return AAR_EINVAL;
+  if (n == 0) return AAR_OK;
+  if (!x || !out || !mask) return AAR_EINVAL;
+  dropout_kernel<<<dim3(stream_grid(n)), dim3(256), 0, as_stream(stream)>>>(x, out, mask, n, p, 1.0f / (1.0f - p),
+                                                                             seed);
+  return launch_status();
+}
+
+int aar_causal_mask_f32(const float* x, float* y, int64_t mats, int64_t T, float fill, void* stream) {
+  if (mats < 0 || T < 0) return AAR_EINVAL;
+  if (mats == 0 || T == 0) return AAR_OK;
+  if (!x || !y) return AAR_EINVAL;
+  const int64_t n = mats * T * T;
+  hipStream_t st = as_stream(stream);
+  if (T % 4 == 0 && aligned16(x) && aligned16(y)) {
+    causal_mask_vec_kernel<<<dim3(stream_grid(n / 4)), dim3(256), 0, st>>>(
+        reinterpret_cast<const f32x4*>(x), reinterpret_cast<f32x4*>(y), n / 4, T, fill);
+  } else {
+    causal_mask_kernel<<<dim3(stream_grid(n)), dim3(256), 0, st>>>(x, y, n, T, fill);
+  }
   return launch_status();
 }
 

@@ -59,13 +59,6 @@ py::array to_numpy(const Tensor& t) {
   return out;
 }
 
-std::atomic<uint64_t> g_seed{0};
-
-[[noreturn]] void unavailable(const char* op, const Tensor& t) {
-  if (t.device == Device::CPU) throw_cpu_compute(op);
-  throw_not_on_device(op);
-}
-
 int device_count() {
   int n = 0;
   if (aar_device_count(&n) != AAR_OK) return 0;
@@ -157,15 +150,12 @@ PYBIND11_MODULE(_core, m) {
   m.def("adamw_step", &adamw_step, py::arg("param"), py::arg("grad"), py::arg("m"), py::arg("v"), py::arg("lr"),
         py::arg("beta1"), py::arg("beta2"), py::arg("eps"), py::arg("weight_decay"),
         py::arg("bias_correction1"), py::arg("bias_correction2"), gil_release());
-  m.def("manual_seed", [](uint64_t seed) { g_seed.store(seed); }, py::arg("seed"));
-
-  // Reference API entries this build does not run on the GPU yet.
-  m.def("apply_causal_mask", [](const Tensor& x) -> Tensor { unavailable("apply_causal_mask", x); });
-  m.def("bmm", [](const Tensor& a, const Tensor&) -> Tensor { unavailable("bmm", a); });
-  m.def("bmm_a_bt", [](const Tensor& a, const Tensor&) -> Tensor { unavailable("bmm_a_bt", a); });
-  m.def("bmm_at_b", [](const Tensor& a, const Tensor&) -> Tensor { unavailable("bmm_at_b", a); });
-  m.def("dropout", [](const Tensor& x, float) -> Tensor { unavailable("dropout", x); }, py::arg("x"),
-        py::arg("p"));
+  m.def("manual_seed", &manual_seed, py::arg("seed"));
+  m.def("apply_causal_mask", &apply_causal_mask, gil_release());
+  m.def("bmm", &bmm, gil_release());
+  m.def("bmm_a_bt", &bmm_a_bt, gil_release());
+  m.def("bmm_at_b", &bmm_at_b, gil_release());
+  m.def("dropout", &dropout, py::arg("x"), py::arg("p"), gil_release());
 
   // Extensions of this build (not in the reference API).
   m.def("_flash_attention_fwd", &flash_attention_fwd_lse, py::arg("q"), py::arg("k"), py::arg("v"),

@@ -54,4 +54,13 @@ Tensor cross_entropy(const Tensor& logits, const Tensor& targets, int64_t ignore
 void adamw_step(Tensor& param, const Tensor& grad, Tensor& m, Tensor& v, float lr, float beta1, float beta2,
                 float eps, float weight_decay, float bias_correction1, float bias_correction2);
 
+// Batched products, causal mask, dropout (cppsrc/ops/bmm.cpp:212-268,
+// attention.cpp:77-90, dropout.cpp:66-92).
+Tensor bmm(const Tensor& a, const Tensor& b);
+Tensor bmm_a_bt(const Tensor& a, const Tensor& b);
+Tensor bmm_at_b(const Tensor& a, const Tensor& b);
+Tensor apply_causal_mask(const Tensor& x);
+Tensor dropout(const Tensor& x, float p);
+void manual_seed(uint64_t seed);
+
 }  // namespace aar

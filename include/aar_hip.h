@@ -105,6 +105,17 @@ int aar_gemm_f32(int op, int64_t M, int64_t N, int64_t K,
  * a given configuration and split-K count (needs splits*M*N*4 bytes of
  * workspace when splits > 1, else AAR_EWORKSPACE); results agree with
  * aar_gemm_f32 up to summation order. */
+/* Batched GEMM with explicit leading dimensions: for b in [0, batch),
+ * C_b = op(A_b, B_b) with A_b = A + b*strideA (and so on), op as in
+ * aar_gemm_f32 but rows of A/B/C at lda/ldb/ldc elements (lda >= K for NN/NT,
+ * >= M for TN; ldb >= N for NN/TN, >= K for NT; ldc >= N).  No split-K, so no
+ * workspace.  K == 0 needs a contiguous C (ldc == N, strideC == M*N).
+ * Replaces bmm_cuda / bmm_a_bt_cuda / bmm_at_b_cuda (cppsrc/ops/bmm.cpp:9-11). */
+int aar_gemm_f32_batched(int op, int64_t batch, int64_t M, int64_t N, int64_t K,
+                         const float* A, int64_t lda, int64_t strideA,
+                         const float* B, int64_t ldb, int64_t strideB,
+                         float* C, int64_t ldc, int64_t strideC, void* stream);
+
 int aar_gemm_f32_tile_config(int config, int* tile_m, int* tile_n, int* tile_k);
 int aar_gemm_f32_plan(int op, int64_t M, int64_t N, int64_t K, size_t workspace_bytes,
                       int* config, int* splits);
@@ -261,6 +272,21 @@ int aar_cross_entropy_bwd_f32(const float* grad, const float* logits, const int6
 int aar_adamw_f32(float* param, const float* grad, float* m, float* v, int64_t n, float lr,
                   float beta1, float beta2, float eps, float weight_decay,
                   float bias_correction1, float bias_correction2, void* stream);
+
+/* Dropout over n floats with the reference's counter-based stream: element i
+ * keeps iff philox_uniform(seed, i) >= p (Philox-4x32-10, word 0 / 2^32);
+ * mask[i] = keep ? 1/(1-p) : 0, out[i] = x[i] * mask[i].  Bit-identical to the
+ * reference CPU path for the same seed.  0 <= p < 1.  Replaces dropout_cuda
+ * (cppsrc/ops/dropout.cpp:14-15, kernel dropout.cu:8-18). */
+int aar_dropout_f32(const float* x, float* out, float* mask, int64_t n, float p, uint64_t seed,
+                    void* stream);
+
+/* y[m][i][j] = (j <= i) ? x[m][i][j] : fill over `mats` contiguous [T, T]
+ * matrices; fill = -inf is apply_causal_mask, fill = 0 its backward.
+ * Replaces apply_causal_mask_cuda / causal_mask_backward_cuda
+ * (cppsrc/ops/attention.cpp:10-11). */
+int aar_causal_mask_f32(const float* x, float* y, int64_t mats, int64_t T, float fill,
+                        void* stream);
 
 #ifdef __cplusplus
 }  /* extern "C" */

@@ -79,6 +79,12 @@ def lib():
         L.orc_cross_entropy_fwd.restype = ctypes.c_int
         L.orc_cross_entropy_bwd.argtypes = [ctypes.c_float, _f32p, _i64p, _f32p, _i64, _i64, _i64]
         L.orc_adamw.argtypes = [_f32p, _f32p, _f32p, _f32p, _i64] + [ctypes.c_float] * 7
+        _u32p = np.ctypeslib.ndpointer(dtype=np.uint32, flags="C_CONTIGUOUS")
+        L.orc_philox4x32_10.argtypes = [_u32p, _u32p, _u32p]
+        L.orc_philox_uniform.argtypes = [ctypes.c_uint64, ctypes.c_uint64]
+        L.orc_philox_uniform.restype = ctypes.c_float
+        L.orc_dropout.argtypes = [_f32p, _f32p, _f32p, _i64, ctypes.c_float, ctypes.c_uint64]
+        L.orc_causal_mask.argtypes = [_f32p, _f32p, _i64, _i64, ctypes.c_float]
         _lib = L
     return _lib
 
@@ -107,6 +113,13 @@ def ref():
         R.ref_gpt_step.argtypes = [_i64] * 6 + [ctypes.POINTER(ctypes.c_void_p), _i64p, _i64p, ctypes.c_float,
                                                  ctypes.POINTER(ctypes.c_float)]
         R.ref_gpt_step.restype = ctypes.c_int
+        R.ref_philox_uniform.argtypes = [ctypes.c_uint64, ctypes.c_uint64]
+        R.ref_philox_uniform.restype = ctypes.c_float
+        R.ref_dropout.argtypes = [_f32p, _f32p, vp, _i64, ctypes.c_float, ctypes.c_uint64]
+        R.ref_causal_mask.argtypes = [_f32p, vp, _f32p, vp, _i64, _i64]
+        R.ref_bmm.argtypes = [ctypes.c_int, _f32p, _f32p, _f32p, _i64, _i64, _i64, _i64]
+        for f in (R.ref_dropout, R.ref_causal_mask, R.ref_bmm):
+            f.restype = ctypes.c_int
         for f in (R.ref_matmul, R.ref_softmax, R.ref_layernorm, R.ref_attention, R.ref_elementwise,
                   R.ref_add_bias, R.ref_sum_all, R.ref_embedding, R.ref_cross_entropy, R.ref_adamw):
             f.restype = ctypes.c_int
@@ -215,6 +228,52 @@ def add(a, b) -> np.ndarray:
     a, b = _c(a), _c(b)
     c = np.empty_like(a)
     lib().orc_add(a, b, c, a.size)
+    return c
+
+
+def philox4x32_10(counter, key) -> np.ndarray:
+    """One Philox-4x32-10 block: uint32[4] counter, uint32[2] key -> uint32[4]."""
+    c = np.ascontiguousarray(counter, np.uint32)
+    k = np.ascontiguousarray(key, np.uint32)
+    out = np.empty(4, np.uint32)
+    lib().orc_philox4x32_10(c, k, out)
+    return out
+
+
+def philox_uniform(seed: int, idx: int) -> float:
+    return float(np.float32(lib().orc_philox_uniform(seed, idx)))
+
+
+def dropout(x, p: float, seed: int):
+    """(out, mask) of dropout over the flattened x with stream `seed`."""
+    x = _c(x)
+    o, m = np.empty_like(x), np.empty_like(x)
+    lib().orc_dropout(x, o, m, x.size, p, seed)
+    return o, m
+
+
+def causal_mask(x, fill: float = float("-inf")) -> np.ndarray:
+    """x [..., T, T] with entries above the diagonal replaced by `fill`."""
+    x = _c(x)
+    T = x.shape[-1]
+    y = np.empty_like(x)
+    lib().orc_causal_mask(x, y, x.size // (T * T), T, fill)
+    return y
+
+
+BMM_OPS = ("bmm", "bmm_a_bt", "bmm_at_b")
+
+
+def bmm(op: str, a, b) -> np.ndarray:
+    """Batched product over the leading dimension: per batch, matmul with op
+    nn (bmm), nt (bmm_a_bt) or tn (bmm_at_b)."""
+    a, b = _c(a), _c(b)
+    g = {"bmm": "nn", "bmm_a_bt": "nt", "bmm_at_b": "tn"}[op]
+    M, N, _ = gemm_shapes(g, a[0] if a.shape[0] else np.empty(a.shape[1:], np.float32),
+                          b[0] if b.shape[0] else np.empty(b.shape[1:], np.float32))
+    c = np.empty((a.shape[0], M, N), np.float32)
+    for i in range(a.shape[0]):
+        c[i] = matmul(g, a[i], b[i])
     return c
 
 
@@ -463,3 +522,44 @@ def ref_gpt_step(cfg, params, ids, targets, lr):
     if rc != 0:
         raise RuntimeError("reference gpt step failed")
     return float(loss.value), ps
+
+
+def ref_philox_uniform(seed: int, idx: int) -> float:
+    return float(np.float32(ref().ref_philox_uniform(seed, idx)))
+
+
+def ref_dropout(x, p: float, seed: int, grad: bool = False):
+    """vlm::manual_seed(seed); vlm::dropout(x, p) on the reference CPU path.
+    With grad, also d(sum(out))/dx (the mask)."""
+    x = _c(x).reshape(-1)
+    y = np.empty_like(x)
+    dx = np.empty_like(x) if grad else None
+    if ref().ref_dropout(x, y, _ptr(dx), x.size, p, seed) != 0:
+        raise RuntimeError("reference dropout failed")
+    return (y, dx) if grad else y
+
+
+def ref_causal_mask(x, g=None):
+    x = _c(x)
+    T = x.shape[-1]
+    y = np.empty_like(x)
+    g = None if g is None else _c(g)
+    dx = np.empty_like(x) if g is not None else None
+    if ref().ref_causal_mask(x, _ptr(g), y, _ptr(dx), x.size // (T * T), T) != 0:
+        raise RuntimeError("reference apply_causal_mask failed")
+    return (y, dx) if g is not None else y
+
+
+def ref_bmm(op: str, a, b) -> np.ndarray:
+    a, b = _c(a), _c(b)
+    Bn = a.shape[0]
+    if op == "bmm":
+        M, K, N = a.shape[1], a.shape[2], b.shape[2]
+    elif op == "bmm_a_bt":
+        M, K, N = a.shape[1], a.shape[2], b.shape[1]
+    else:
+        K, M, N = a.shape[1], a.shape[2], b.shape[2]
+    c = np.empty((Bn, M, N), np.float32)
+    if ref().ref_bmm(BMM_OPS.index(op), a, b, c, Bn, M, N, K) != 0:
+        raise RuntimeError("reference bmm failed")
+    return c

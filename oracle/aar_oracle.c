@@ -38,6 +38,16 @@
  *                       KATs of tests/cpp/test_elementwise.cpp and
  *                       tests/python/test_{embedding,cross_entropy,adamw}.py,
  *                       float64 closed forms, bit-exact vs oracle/_ref.
+ *   orc_philox4x32_10   the published Philox-4x32-10 known-answer vectors
+ *                       (Random123 kat_vectors), bit-exact vs the reference's
+ *                       philox_uniform through oracle/_ref.
+ *   orc_dropout         the properties of tests/python/test_dropout.py
+ *                       (drop rate, rescaled survivors, reproducibility),
+ *                       bit-exact vs oracle/_ref.
+ *   orc_causal_mask     numpy triangle closed form, bit-exact vs oracle/_ref.
+ *   bmm                 per-batch orc_matmul_* (the reference's bmm_cpu loops
+ *                       accumulate exactly as matmul_cpu does), bit-exact vs
+ *                       oracle/_ref.
  */
 #include <math.h>
 #include <stdint.h>
@@ -484,4 +494,67 @@ void orc_adamw(float* p, const float* g, float* mp, float* vp, int64_t n, float 
     const float v_hat = vi / bc2;
     p[i] = p[i] * wd_factor - lr * m_hat / (sqrtf(v_hat) + eps);
   }
+}
+
+/* ------------------------------------------------------------- dropout */
+
+/* Philox-4x32-10 block function (Salmon et al., SC'11): counter ctr[4], key
+ * key[2] -> out[4].  Round: (c0,c1,c2,c3) <- (hi(c2*M1)^c1^k0, lo(c2*M1),
+ * hi(c0*M0)^c3^k1, lo(c0*M0)); key += (W0, W1) between rounds
+ * (cppsrc/core/rng.hpp:14-43). */
+void orc_philox4x32_10(const uint32_t ctr[4], const uint32_t key[2], uint32_t out[4]) {
+  uint32_t c[4] = {ctr[0], ctr[1], ctr[2], ctr[3]};
+  uint32_t k0 = key[0], k1 = key[1];
+  for (int r = 0; r < 10; ++r) {
+    const uint64_t p0 = (uint64_t)c[0] * 0xD2511F53u;
+    const uint64_t p1 = (uint64_t)c[2] * 0xCD9E8D57u;
+    const uint32_t n0 = (uint32_t)(p1 >> 32) ^ c[1] ^ k0;
+    const uint32_t n1 = (uint32_t)p1;
+    const uint32_t n2 = (uint32_t)(p0 >> 32) ^ c[3] ^ k1;
+    const uint32_t n3 = (uint32_t)p0;
+    c[0] = n0;
+    c[1] = n1;
+    c[2] = n2;
+    c[3] = n3;
+    if (r < 9) {
+      k0 += 0x9E3779B9u;
+      k1 += 0xBB67AE85u;
+    }
+  }
+  memcpy(out, c, sizeof(c));
+}
+
+/* Uniform in [0, 1) of element idx under seed: word 0 of the block for
+ * counter (idx lo, idx hi, 0, 0) and key (seed lo, seed hi), times 2^-32 in
+ * float (cppsrc/core/rng.hpp:14-46). */
+float orc_philox_uniform(uint64_t seed, uint64_t idx) {
+  const uint32_t ctr[4] = {(uint32_t)idx, (uint32_t)(idx >> 32), 0u, 0u};
+  const uint32_t key[2] = {(uint32_t)seed, (uint32_t)(seed >> 32)};
+  uint32_t out[4];
+  orc_philox4x32_10(ctr, key, out);
+  return (float)out[0] * (1.0f / 4294967296.0f);
+}
+
+/* dropout_cpu (cppsrc/ops/dropout.cpp:30-42). */
+void orc_dropout(const float* X, float* O, float* M, int64_t n, float p, uint64_t seed) {
+  const float scale = 1.0f / (1.0f - p);
+  for (int64_t i = 0; i < n; ++i) {
+    const float r = orc_philox_uniform(seed, (uint64_t)i);
+    const float keep = (r >= p) ? scale : 0.0f;
+    M[i] = keep;
+    O[i] = X[i] * keep;
+  }
+}
+
+/* --------------------------------------------------------- causal mask */
+
+/* apply_causal_mask_cpu / causal_mask_backward_cpu
+ * (cppsrc/ops/attention.cpp:24-56): fill = -inf forward, 0 backward. */
+void orc_causal_mask(const float* X, float* Y, int64_t mats, int64_t T, float fill) {
+  for (int64_t m = 0; m < mats; ++m)
+    for (int64_t i = 0; i < T; ++i)
+      for (int64_t j = 0; j < T; ++j) {
+        const int64_t idx = m * T * T + i * T + j;
+        Y[idx] = (j <= i) ? X[idx] : fill;
+      }
 }

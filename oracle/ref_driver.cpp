@@ -14,6 +14,10 @@
 
 #include "core/tensor.hpp"
 #include "ops/adamw.hpp"
+#include "ops/attention.hpp"
+#include "ops/bmm.hpp"
+#include "ops/dropout.hpp"
+#include "core/rng.hpp"
 #include "ops/cross_entropy.hpp"
 #include "ops/elementwise.hpp"
 #include "ops/embedding.hpp"
@@ -221,6 +225,56 @@ int ref_adamw(float* p, const float* g, float* m, float* v, int64_t n, float lr,
     out(tp, p);
     out(tm, m);
     out(tv, v);
+    return 0;
+  } catch (const std::exception&) {
+    return -1;
+  }
+}
+
+// philox_uniform of the reference (cppsrc/core/rng.hpp:14-46).
+float ref_philox_uniform(uint64_t seed, uint64_t idx) { return vlm::philox_uniform(seed, idx); }
+
+// dropout(x, p) after manual_seed(seed): the call draws exactly `seed`.
+int ref_dropout(const float* x, float* y, float* dx, int64_t n, float p, uint64_t seed) {
+  try {
+    Tensor tx = make(x, {n}, dx != nullptr);
+    vlm::manual_seed(seed);
+    Tensor ty = vlm::dropout(tx, p);
+    out(ty, y);
+    if (dx) {
+      vlm::sum_all(ty).backward();
+      out(*tx.grad(), dx);
+    }
+    return 0;
+  } catch (const std::exception&) {
+    return -1;
+  }
+}
+
+// apply_causal_mask on [mats, T, T]; with g also its backward.
+int ref_causal_mask(const float* x, const float* g, float* y, float* dx, int64_t mats, int64_t T) {
+  try {
+    Tensor tx = make(x, {mats, T, T}, g != nullptr);
+    Tensor ty = vlm::apply_causal_mask(tx);
+    out(ty, y);
+    if (g) {
+      ty.backward(make(g, {mats, T, T}));
+      out(*tx.grad(), dx);
+    }
+    return 0;
+  } catch (const std::exception&) {
+    return -1;
+  }
+}
+
+// op: 0 = bmm (A[b,M,K] B[b,K,N]), 1 = bmm_a_bt (B[b,N,K]), 2 = bmm_at_b (A[b,K,M]).
+int ref_bmm(int op, const float* A, const float* B, float* C, int64_t batch, int64_t M, int64_t N, int64_t K) {
+  try {
+    Tensor c;
+    if (op == 0) c = vlm::bmm(make(A, {batch, M, K}), make(B, {batch, K, N}));
+    else if (op == 1) c = vlm::bmm_a_bt(make(A, {batch, M, K}), make(B, {batch, N, K}));
+    else c = vlm::bmm_at_b(make(A, {batch, K, M}), make(B, {batch, K, N}));
+    out(c, C);
     return 0;
   } catch (const std::exception&) {
     return -1;
