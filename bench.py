@@ -229,6 +229,61 @@ def bench_rowwise(ev: Events, iters: int = 20, min_set_bytes: float = 1.2e9):
     return out
 
 
+def bench_extra(ev: Events, iters: int = 10):
+    """The non-flash attention ops and dropout through the C ABI.  dropout
+    over 2^26 floats (algorithmic 12 B/element: x in, out and mask out);
+    causal mask over [96, 1024, 1024] (8 B/element); bmm_a_bt scores
+    (96 x 1024x1024x64, the unfused attention of B8 H12 T1024 d64) and a
+    square batched NN product (8 x 2048^3), counted as 2*B*M*N*K flops."""
+    abi = Abi(ev.L)
+    L = ev.L
+    vp, i64 = ctypes.c_void_p, ctypes.c_int64
+    L.aar_dropout_f32.argtypes = [vp, vp, vp, i64, ctypes.c_float, ctypes.c_uint64, vp]
+    L.aar_causal_mask_f32.argtypes = [vp, vp, i64, i64, ctypes.c_float, vp]
+    L.aar_gemm_f32_batched.argtypes = [ctypes.c_int] + [i64] * 4 + [vp, i64, i64, vp, i64, i64, vp, i64, i64, vp]
+    out = {}
+    rng = np.random.default_rng(0)
+
+    def timed(fn):
+        for _ in range(2):
+            assert fn() == 0
+        ev.start()
+        for _ in range(iters):
+            assert fn() == 0
+        return ev.stop_ms() / iters
+
+    try:
+        n = 1 << 26
+        px, po, pm = abi.put(rng.standard_normal(n).astype(np.float32)), abi.alloc(4 * n), abi.alloc(4 * n)
+        ms = timed(lambda: L.aar_dropout_f32(px, po, pm, n, ctypes.c_float(0.1), 1234, None))
+        out["dropout_n2^26"] = {"ms": round(ms, 4), "GB_s": round(12 * n / (ms * 1e-3) / 1e9, 1),
+                                "frac_of_hbm_peak": round(12 * n / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
+        abi.free()
+        mats, T = 96, 1024
+        px, py = abi.put(rng.standard_normal(mats * T * T).astype(np.float32)), abi.alloc(4 * mats * T * T)
+        ms = timed(lambda: L.aar_causal_mask_f32(px, py, mats, T, ctypes.c_float(float("-inf")), None))
+        nb = 8 * mats * T * T
+        out["causal_mask_96x1024x1024"] = {"ms": round(ms, 4), "GB_s": round(nb / (ms * 1e-3) / 1e9, 1),
+                                           "frac_of_hbm_peak": round(nb / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
+        abi.free()
+        for name, (op, Bn, M, N, K) in {"bmm_a_bt_96x1024x1024x64": (1, 96, 1024, 1024, 64),
+                                        "bmm_8x2048x2048x2048": (0, 8, 2048, 2048, 2048)}.items():
+            pa = abi.put(rng.standard_normal(Bn * M * K).astype(np.float32))
+            pb = abi.put(rng.standard_normal(Bn * N * K).astype(np.float32))
+            pc = abi.alloc(4 * Bn * M * N)
+            ldb = K if op == 1 else N
+            ms = timed(lambda: L.aar_gemm_f32_batched(op, Bn, M, N, K, pa, K, M * K, pb, ldb, N * K, pc, N, M * N,
+                                                      None))
+            tf = 2.0 * Bn * M * N * K / (ms * 1e-3) / 1e12
+            out[name] = {"ms": round(ms, 4), "TFLOPS": round(tf, 2),
+                         "pct_of_fp32_mfma_peak": round(100 * tf / PEAK_FP32_MFMA_TFLOPS, 2),
+                         "min_hbm_GB_s": round(4 * Bn * (M * K + N * K + M * N) / (ms * 1e-3) / 1e9, 1)}
+            abi.free()
+    finally:
+        abi.free()
+    return out
+
+
 def bench_copy(ev: Events, iters: int = 5, n: int = 1 << 26):
     """Calibration kernel for the HBM byte counters: c = a + b over n floats
     (reads 8n bytes, writes 4n bytes per launch)."""
@@ -457,7 +512,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=60)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--flash-steps", type=int, default=6)
-    ap.add_argument("--only", choices=["all", "gemm", "flash", "rowwise", "copy", "gpt", "sweep"], default="all",
+    ap.add_argument("--only", choices=["all", "gemm", "flash", "rowwise", "extra", "copy", "gpt", "sweep"], default="all",
                     help="run one part (profiling runs); the JSON line is printed for 'all'")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -479,6 +534,9 @@ def main() -> int:
         return 0
     if args.only == "rowwise":
         log(json.dumps(bench_rowwise(ev)))
+        return 0
+    if args.only == "extra":
+        log(json.dumps(bench_extra(ev)))
         return 0
     if args.only == "sweep":
         log(json.dumps(bench_gemm_sweep(ev)))
@@ -506,6 +564,10 @@ def main() -> int:
     rowwise = bench_rowwise(ev)
     for k, v in rowwise.items():
         log(f"{k}: {v['GB_s']} GB/s ({100 * v['frac_of_hbm_peak']:.1f}% of HBM peak)")
+
+    extra = bench_extra(ev)
+    for k, v in extra.items():
+        log(f"{k}: " + ", ".join(f"{a} {b}" for a, b in v.items()))
 
     gpt = bench_gpt(ag, ev)
     log(f"GPT step (config 5): {gpt['tokens_per_s']:.0f} tokens/s, {gpt['ms_per_step']} ms/step, "
@@ -547,6 +609,7 @@ def main() -> int:
             "config": "causal, B8 H12 T4096 d64, fwd+bwd, flops = 3.5 * 4*B*H*T^2*d/2",
         },
         "rowwise_hbm": rowwise,
+        "attention_ops_and_dropout": extra,
         "gpt_train_step": gpt,
         "roofline": {
             "bound": "mfma",

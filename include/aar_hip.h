@@ -110,7 +110,7 @@ int aar_gemm_f32(int op, int64_t M, int64_t N, int64_t K,
  * aar_gemm_f32 but rows of A/B/C at lda/ldb/ldc elements (lda >= K for NN/NT,
  * >= M for TN; ldb >= N for NN/TN, >= K for NT; ldc >= N).  No split-K, so no
  * workspace.  K == 0 needs a contiguous C (ldc == N, strideC == M*N).
- * Replaces bmm_cuda / bmm_a_bt_cuda / bmm_at_b_cuda (cppsrc/ops/bmm.cpp:9-11). */
+ * Replaces bmm_cuda / bmm_a_bt_cuda / bmm_at_b_cuda (cppsrc/ops/bmm.cpp:10-12). */
 int aar_gemm_f32_batched(int op, int64_t batch, int64_t M, int64_t N, int64_t K,
                          const float* A, int64_t lda, int64_t strideA,
                          const float* B, int64_t ldb, int64_t strideB,

@@ -93,6 +93,12 @@ def test_dropout_module_and_strided_input(gpu):
     got = host(gpu, gpu.dropout(xt, 0.25))
     want = O.dropout(np.ascontiguousarray(x_np.T), 0.25, 5)[0].reshape(48, 64)
     np.testing.assert_array_equal(got, want)
+    # a slice at an odd offset is contiguous but not 16-byte aligned: the
+    # element-wise kernel takes it
+    flat = np.random.default_rng(1).standard_normal(10001).astype(f32)
+    sl = gpu.slice(dev(gpu, flat), 0, 1, 10001)
+    gpu.manual_seed(6)
+    np.testing.assert_array_equal(host(gpu, gpu.dropout(sl, 0.6)), O.dropout(flat[1:], 0.6, 6)[0])
 
 
 # ------------------------------------------------------------ causal mask
