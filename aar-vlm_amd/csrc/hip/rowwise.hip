@@ -21,6 +21,8 @@
 #include <hip/hip_runtime.h>
 #include <math.h>
 
+#include <algorithm>
+
 #include "common.hpp"
 
 namespace aar {
@@ -107,10 +109,10 @@ __device__ __forceinline__ float group_reduce(float v, float* red, int slot, int
 template <int NV, int W>
 struct RowsPerIter {
   static_assert(W == 1 || NV <= 8, "row-group size");
-  static constexpr int value = W == 1 ? (NV <= 2 ? 2 : (NV == 4 ? 2 : 1)) : 1;
+  static constexpr int value = W == 1 && NV <= 4 ? 2 : 1;
 };
 
-inline int rows_per_iter(int nv, int w) { return w == 1 ? (nv <= 2 ? 2 : (nv == 4 ? 2 : 1)) : 1; }
+inline int rows_per_iter(int nv, int w) { return w == 1 && nv <= 4 ? 2 : 1; }
 
 // Workgroups to cover the rows once, capped at `per_cu` workgroups per CU.
 // Softmax and layernorm forward use a covering grid (one pass per
@@ -288,17 +290,59 @@ layernorm_fwd_kernel(const float* __restrict__ x, const float* __restrict__ w,
   }
 }
 
+// Layernorm-backward shape per row plan (NV slots per lane, W waves per row):
+//  * waves per workgroup: 8 for rows spread over 4 waves with up to 4 slots
+//    per lane (measured faster on MI355X than four 4-wave workgroups per
+//    CU), else 4 (16-wave workgroups, which would cut the partial rows 4x,
+//    measured slower);
+//  * rows per row group and iteration (all loads issued before the first
+//    reduction);
+//  * minimum waves per SIMD the register allocation must allow;
+//  * next-rows prefetch (two row sets in flight per wave): measured slower
+//    than the occupancy it costs, so off;
+//  * resident waves per CU the persistent grid is sized for.
+constexpr int ln_bwd_waves(int nv, int w) { return (w > 1 && nv <= 4) ? 8 : 4; }
+constexpr int ln_bwd_rows(int nv, int w) { return w == 1 && nv <= 4 ? 2 : 1; }
+constexpr int ln_bwd_min_waves(int nv, int w) { return w == 1 && nv == 3 ? 4 : 1; }
+constexpr bool ln_bwd_prefetch(int, int) { return false; }
+constexpr int kLnBwdWavesPerCu = 16;
+
+// Rows U of row group `grp` starting at row0: gy and x slots, mean and rstd
+// (rows past the end read as zeros and are never stored).
+template <int U, typename RS>
+__device__ __forceinline__ void ln_bwd_load(RS (&sg)[U], RS (&sx)[U], float (&mu)[U], float (&r)[U],
+                                            const float* __restrict__ gy, const float* __restrict__ x,
+                                            const float* __restrict__ mean, const float* __restrict__ rstd,
+                                            int64_t row0, int64_t rows, int cols, int wr, int lane) {
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    if (row0 + u < rows) {
+      sg[u].load(gy + (row0 + u) * cols, cols, wr, lane);
+      sx[u].load(x + (row0 + u) * cols, cols, wr, lane);
+      mu[u] = mean[row0 + u];
+      r[u] = rstd[row0 + u];
+    } else {
+#pragma unroll
+      for (int k = 0; k < RS::kN; ++k) sg[u].v[k] = sx[u].v[k] = 0.f;
+      mu[u] = 0.f;
+      r[u] = 0.f;
+    }
+  }
+}
+
 // Stage 1 of layernorm backward: dx per row, plus per-workgroup partial
 // column sums of gy*xhat (dgamma) and gy (dbeta) written to
-// part[blockIdx.x][2][cols].  Workgroups of NW waves are persistent (16
-// waves per CU) and stride over the rows.
-template <int NV, int W, bool VEC, int NW>
-__global__ void __launch_bounds__(NW * 64)
+// part[blockIdx.x][2][cols].  Workgroups of NW waves are persistent (as many
+// as fit on the device at once, at most 16 waves per CU) and stride over the
+// rows.  PF: the next iteration's rows are loaded before the current ones
+// are reduced, so each wave keeps two row sets in flight.
+template <int NV, int W, bool VEC, int NW, bool PF>
+__global__ void __launch_bounds__(NW * 64, ln_bwd_min_waves(NV, W))
 layernorm_bwd_kernel(const float* __restrict__ gy, const float* __restrict__ x,
                      const float* __restrict__ w, const float* __restrict__ mean,
                      const float* __restrict__ rstd, float* __restrict__ dx,
                      float* __restrict__ part, int64_t rows, int cols) {
-  constexpr int U = RowsPerIter<NV, W>::value;
+  constexpr int U = ln_bwd_rows(NV, W);
   constexpr int per_iter = NW / W;
   __shared__ float red[2 * kMaxRowsPerIter * 2 * NW];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -313,23 +357,17 @@ layernorm_bwd_kernel(const float* __restrict__ gy, const float* __restrict__ x,
     dbacc.v[k] = 0.f;
   }
   const float inv_d = 1.0f / (float)cols;
+  RS sg[U], sx[U];
+  float mu[U], r[U];
+  if (PF) ln_bwd_load<U>(sg, sx, mu, r, gy, x, mean, rstd, group_row0(0, per_iter, grp, U), rows, cols, wr, lane);
   for (int64_t it = 0; it < iters; ++it) {
     const int64_t row0 = group_row0(it, per_iter, grp, U);
-    RS sg[U], sx[U];
-    float mu[U], r[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      if (row0 + u < rows) {
-        sg[u].load(gy + (row0 + u) * cols, cols, wr, lane);
-        sx[u].load(x + (row0 + u) * cols, cols, wr, lane);
-        mu[u] = mean[row0 + u];
-        r[u] = rstd[row0 + u];
-      } else {
-#pragma unroll
-        for (int k = 0; k < RS::kN; ++k) sg[u].v[k] = sx[u].v[k] = 0.f;
-        mu[u] = 0.f;
-        r[u] = 0.f;
-      }
+    if (!PF) ln_bwd_load<U>(sg, sx, mu, r, gy, x, mean, rstd, row0, rows, cols, wr, lane);
+    RS ng[U], nx[U];
+    float nmu[U], nr[U];
+    if (PF && it + 1 < iters) {
+      ln_bwd_load<U>(ng, nx, nmu, nr, gy, x, mean, rstd, group_row0(it + 1, per_iter, grp, U), rows, cols, wr,
+                     lane);
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -352,6 +390,15 @@ layernorm_bwd_kernel(const float* __restrict__ gy, const float* __restrict__ x,
         sg[u].v[k] = r[u] * (gg - sum_g * inv_d - sx[u].v[k] * sum_gn * inv_d);
       }
       if (row0 + u < rows) sg[u].store(dx + (row0 + u) * cols, cols, wr, lane);
+    }
+    if (PF) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        sg[u] = ng[u];
+        sx[u] = nx[u];
+        mu[u] = nmu[u];
+        r[u] = nr[u];
+      }
     }
   }
   // Combine the row groups of this workgroup in a fixed order: group 0 seeds
@@ -389,46 +436,45 @@ layernorm_bwd_kernel(const float* __restrict__ gy, const float* __restrict__ x,
   }
 }
 
-// Waves per layernorm-backward workgroup: 8 for rows spread over 4 waves
-// with up to 4 slots per lane (measured faster on MI355X than four 4-wave
-// workgroups per CU), else 4; each wave keeps its rows in registers without
-// spilling.
-constexpr int ln_bwd_waves(int nv, int w) { return (w > 1 && nv <= 4) ? 8 : 4; }
+// Stage 2 of layernorm backward: dw[c] and db[c] from the partial rows
+// part[p][0..2C) (dgamma in [0,C), dbeta in [C,2C)) in one launch.  A
+// workgroup owns kRedCols consecutive columns of the 2C and kRedSlices
+// slices of the parts; slice j sums its contiguous run of parts in order
+// (all loads issued together), then a fixed pairwise tree over the slices
+// in LDS finishes the column.  Deterministic.
+constexpr int kRedCols = 16;
+constexpr int kRedThreads = 1024;
+constexpr int kRedSlices = kRedThreads / kRedCols;
 
-// Stage 2 of layernorm backward, a fixed-order two-level tree over the
-// partial rows part[p][0..2C) (dgamma in [0,C), dbeta in [C,2C)):
-//   2a: grp[g][c] = sum of part[p][c] for p in [32g, 32g+32), in order
-//   2b: dw[c] = sum_g grp[g][c], db[c] = sum_g grp[g][C+c], in order
-// Deterministic, and every level runs with full column parallelism.
-constexpr int kPartGroup = 32;
-
-__global__ void __launch_bounds__(256)
-layernorm_bwd_reduce_a_kernel(const float* __restrict__ part, float* __restrict__ grp, int nparts,
-                              int64_t ncol2) {
-  const int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (c >= ncol2) return;
-  const int p0 = blockIdx.y * kPartGroup;
-  const int p1 = min(nparts, p0 + kPartGroup);
-  float s = 0.f;
-#pragma unroll 8
-  for (int p = p0; p < p1; ++p) s += part[(int64_t)p * ncol2 + c];
-  grp[(int64_t)blockIdx.y * ncol2 + c] = s;
-}
-
-__global__ void __launch_bounds__(256)
-layernorm_bwd_reduce_b_kernel(const float* __restrict__ grp, float* __restrict__ dw, float* __restrict__ db,
-                              int ngroups, int cols) {
-  const int c = blockIdx.x * 256 + threadIdx.x;
-  if (c >= cols) return;
+__global__ void __launch_bounds__(kRedThreads)
+layernorm_bwd_reduce_kernel(const float* __restrict__ part, float* __restrict__ dw, float* __restrict__ db,
+                            int nparts, int cols) {
+  __shared__ float acc[kRedSlices][kRedCols];
+  const int cl = threadIdx.x % kRedCols, slice = threadIdx.x / kRedCols;
   const int64_t ncol2 = 2 * (int64_t)cols;
-  float a = 0.f, b = 0.f;
-#pragma unroll 8
-  for (int g = 0; g < ngroups; ++g) {
-    a += grp[g * ncol2 + c];
-    b += grp[g * ncol2 + cols + c];
+  const int64_t c = (int64_t)blockIdx.x * kRedCols + cl;
+  const int per = (nparts + kRedSlices - 1) / kRedSlices;
+  const int p0 = slice * per;
+  const int p1 = min(nparts, p0 + per);
+  float s = 0.f;
+  if (c < ncol2) {
+#pragma unroll 16
+    for (int p = p0; p < p1; ++p) s += part[(int64_t)p * ncol2 + c];
   }
-  dw[c] = a;
-  db[c] = b;
+  acc[slice][cl] = s;
+  __syncthreads();
+#pragma unroll
+  for (int h = kRedSlices / 2; h >= 1; h /= 2) {
+    if (slice < h) acc[slice][cl] += acc[slice + h][cl];
+    __syncthreads();
+  }
+  if (slice == 0 && c < ncol2) {
+    if (c < cols) {
+      dw[c] = acc[0][cl];
+    } else {
+      db[c - cols] = acc[0][cl];
+    }
+  }
 }
 
 // ------------------------------------------------------- generic wide rows
@@ -557,7 +603,7 @@ layernorm_bwd_wide_cols_kernel(const float* __restrict__ gy, const float* __rest
 // ------------------------------------------------------------ dispatching
 
 struct RowPlan {
-  int nv;   // slots per lane: 1, 2, 4 or 8 (0 = use the wide kernels)
+  int nv;   // slots per lane: 1, 2, 3, 4 or 8 (0 = use the wide kernels)
   int w;    // waves per row: 1 or 4
   bool vec;
 };
@@ -566,9 +612,9 @@ RowPlan plan_rows(int64_t cols, bool vec) {
   const int64_t units = vec ? cols / 4 : cols;  // slots needed per row
   RowPlan p{0, 1, vec};
   for (int w : {1, 4}) {
-    for (int nv : {1, 2, 4, 8}) {
+    for (int nv : {1, 2, 3, 4, 8}) {
       if (units <= (int64_t)nv * kWave * w) {
-        if (w == 4 && nv < 2) continue;
+        if (w == 4 && (nv < 2 || nv == 3)) continue;
         p.nv = nv;
         p.w = w;
         return p;
@@ -585,6 +631,7 @@ RowPlan plan_rows(int64_t cols, bool vec) {
         switch ((PLAN).nv) {                            \
           case 1: LAUNCH(1, 1, true); break;            \
           case 2: LAUNCH(2, 1, true); break;            \
+          case 3: LAUNCH(3, 1, true); break;            \
           case 4: LAUNCH(4, 1, true); break;            \
           default: LAUNCH(8, 1, true); break;           \
         }                                               \
@@ -600,6 +647,7 @@ RowPlan plan_rows(int64_t cols, bool vec) {
         switch ((PLAN).nv) {                            \
           case 1: LAUNCH(1, 1, false); break;           \
           case 2: LAUNCH(2, 1, false); break;           \
+          case 3: LAUNCH(3, 1, false); break;           \
           case 4: LAUNCH(4, 1, false); break;           \
           default: LAUNCH(8, 1, false); break;          \
         }                                               \
@@ -613,8 +661,25 @@ RowPlan plan_rows(int64_t cols, bool vec) {
     }                                                   \
   } while (0)
 
+// Workgroups of a layernorm-backward instance resident on one CU at once
+// (register- and LDS-limited), from the runtime's occupancy calculator.
+template <int NV, int W, bool V>
+int ln_bwd_resident() {
+  static const int n = [] {
+    int b = 0;
+    constexpr int nw = ln_bwd_waves(NV, W);
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &b, layernorm_bwd_kernel<NV, W, V, nw, ln_bwd_prefetch(NV, W)>, nw * kWave, 0) != hipSuccess) {
+      b = 1;
+    }
+    return b > 0 ? b : 1;
+  }();
+  return n;
+}
+
 // Number of dgamma/dbeta partial rows = persistent workgroups of the
-// backward kernel: 16 waves per CU.
+// backward kernel: as many as are resident at once, at most
+// kLnBwdWavesPerCu waves per CU, so no workgroup waits for a second round.
 int ln_bwd_parts_for(int64_t rows, const RowPlan& p) {
   const int64_t cus = device_cu_count();
   int64_t cap, pass;
@@ -623,8 +688,12 @@ int ln_bwd_parts_for(int64_t rows, const RowPlan& p) {
     pass = 1;
   } else {
     const int nw = ln_bwd_waves(p.nv, p.w);
-    cap = cus * (16 / nw);  // 16 waves per CU
-    pass = (int64_t)(nw / p.w) * rows_per_iter(p.nv, p.w);
+    int resident = 1;
+#define R(NV, W, V) resident = ln_bwd_resident<NV, W, V>()
+    AAR_ROW_DISPATCH(p, R);
+#undef R
+    cap = cus * std::min(resident, kLnBwdWavesPerCu / nw);
+    pass = (int64_t)(nw / p.w) * ln_bwd_rows(p.nv, p.w);
   }
   const int64_t need = ceil_div(rows, pass);
   return (int)(need < cap ? need : cap);
@@ -713,8 +782,7 @@ extern "C" int aar_layernorm_fwd_f32(const float* x, const float* w, const float
 extern "C" size_t aar_layernorm_bwd_workspace_bytes(int64_t rows, int64_t cols) {
   if (rows <= 0 || cols <= 0) return 0;
   const int64_t parts = ln_bwd_parts_max(rows, cols);
-  const int64_t groups = ceil_div(parts, kPartGroup);
-  return (size_t)(parts + groups) * 2 * (size_t)cols * sizeof(float);
+  return (size_t)parts * 2 * (size_t)cols * sizeof(float);
 }
 
 extern "C" int aar_layernorm_bwd_f32(const float* gy, const float* x, const float* w,
@@ -734,11 +802,9 @@ extern "C" int aar_layernorm_bwd_f32(const float* gy, const float* x, const floa
                    aligned16(dx) && aligned16(workspace);
   const RowPlan p = plan_rows(cols, vec);
   const int parts = ln_bwd_parts_for(rows, p);
-  const int groups = (int)ceil_div(parts, kPartGroup);
-  const size_t need = (size_t)(parts + groups) * 2 * (size_t)cols * sizeof(float);
+  const size_t need = (size_t)parts * 2 * (size_t)cols * sizeof(float);
   if (!workspace || workspace_bytes < need) return AAR_EWORKSPACE;
   float* part = static_cast<float*>(workspace);
-  float* grp = part + (int64_t)parts * 2 * cols;
   int rc;
   if (p.nv == 0) {
     layernorm_bwd_wide_kernel<<<dim3((unsigned)rows), dim3(kThreads), 0, st>>>(gy, x, w, mean, rstd,
@@ -749,7 +815,7 @@ extern "C" int aar_layernorm_bwd_f32(const float* gy, const float* x, const floa
                                      dim3(kThreads), 0, st>>>(gy, x, mean, rstd, part, rows, cols);
   } else {
 #define L(NV, W, V)                                                                          \
-  layernorm_bwd_kernel<NV, W, V, ln_bwd_waves(NV, W)>                                            \
+  layernorm_bwd_kernel<NV, W, V, ln_bwd_waves(NV, W), ln_bwd_prefetch(NV, W)>                    \
       <<<dim3(parts), dim3(ln_bwd_waves(NV, W) * kWave), 0, st>>>(gy, x, w, mean, rstd, dx, part, \
                                                                  rows, (int)cols)
     AAR_ROW_DISPATCH(p, L);
@@ -757,12 +823,7 @@ extern "C" int aar_layernorm_bwd_f32(const float* gy, const float* x, const floa
   }
   rc = launch_status();
   if (rc != AAR_OK) return rc;
-  const int64_t ncol2 = 2 * cols;
-  layernorm_bwd_reduce_a_kernel<<<dim3((unsigned)ceil_div(ncol2, 256), (unsigned)groups), dim3(256), 0, st>>>(
-      part, grp, parts, ncol2);
-  rc = launch_status();
-  if (rc != AAR_OK) return rc;
-  layernorm_bwd_reduce_b_kernel<<<dim3((unsigned)ceil_div(cols, 256)), dim3(256), 0, st>>>(grp, dw, db, groups,
-                                                                                          (int)cols);
+  layernorm_bwd_reduce_kernel<<<dim3((unsigned)ceil_div(2 * cols, kRedCols)), dim3(kRedThreads), 0, st>>>(
+      part, dw, db, parts, (int)cols);
   return launch_status();
 }
