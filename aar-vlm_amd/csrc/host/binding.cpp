@@ -165,6 +165,10 @@ PYBIND11_MODULE(_core, m) {
         gil_release(),
         "Attention over a packed projection [..., T, 3*D] -> [..., T, D]: the MultiHeadAttention "
         "composition (per-head views of q, k, v, flash attention, heads merged back) in one op.");
+  m.def("_token_windows", &token_windows, py::arg("tokens"), py::arg("starts"), py::arg("seq_len"),
+        gil_release(),
+        "(x, y) int64 [len(starts), seq_len] with x[b] = tokens[s:s+T], y[b] = tokens[s+1:s+T+1], "
+        "s = starts[b], gathered on the device from a token stream resident there.");
   m.def("_device_count", &device_count);
   m.def("_empty_cache", &device_empty_cache, gil_release());
   m.def("_memory_in_use", &device_bytes_in_use);

@@ -210,12 +210,13 @@ void check_device_errors() {
     words = g_err_words;
   }
   if (!words) return;
-  int host[kErrSlots] = {0, 0};
+  int host[kErrSlots] = {};
   check_status(aar_memcpy(host, words, sizeof(host), 2, current_stream()), "device error word");
-  if (host[0] || host[1]) {
+  if (host[kErrEmbeddingId] || host[kErrCrossEntropyTarget] || host[kErrTokenWindow]) {
     check_status(aar_memset_zero(words, sizeof(host), current_stream()), "device error word");
-    if (host[0]) throw std::out_of_range("embedding: id out of range [0, vocab_size)");
-    throw std::out_of_range("cross_entropy: target out of range [0, V)");
+    if (host[kErrEmbeddingId]) throw std::out_of_range("embedding: id out of range [0, vocab_size)");
+    if (host[kErrCrossEntropyTarget]) throw std::out_of_range("cross_entropy: target out of range [0, V)");
+    throw std::out_of_range("token_windows: window start out of range");
   }
 }
 

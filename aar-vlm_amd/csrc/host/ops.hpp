@@ -63,4 +63,8 @@ Tensor apply_causal_mask(const Tensor& x);
 Tensor dropout(const Tensor& x, float p);
 void manual_seed(uint64_t seed);
 
+// Token-window batch (x, y) of shape [starts, seq_len] gathered on the device
+// from an int64 token stream (python/shakespeare/scripts/data.py:38-53).
+std::tuple<Tensor, Tensor> token_windows(const Tensor& tokens, const Tensor& starts, int64_t seq_len);
+
 }  // namespace aar

@@ -128,11 +128,11 @@ void* current_stream();
 
 void copy_bytes(void* dst, Device dst_device, const void* src, Device src_device, size_t nbytes);
 
-// Deferred device-side errors.  Kernels that cannot throw (an embedding id or
-// a cross-entropy target out of range) set a word here; the host raises
+// Deferred device-side errors.  Kernels that cannot throw (an embedding id,
+// a cross-entropy target or a token window out of range) set a word here; the host raises
 // std::out_of_range at its next synchronisation point (a device-to-host copy
 // or cuda_synchronize), the way the reference raises on its CPU path.
-enum DeviceErrorSlot { kErrEmbeddingId = 0, kErrCrossEntropyTarget = 1, kErrSlots = 2 };
+enum DeviceErrorSlot { kErrEmbeddingId = 0, kErrCrossEntropyTarget = 1, kErrTokenWindow = 2, kErrSlots = 3 };
 int* device_error_word(DeviceErrorSlot slot);
 void check_device_errors();
 void zero_bytes(void* p, Device device, size_t nbytes);

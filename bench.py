@@ -230,7 +230,8 @@ def bench_rowwise(ev: Events, iters: int = 20, min_set_bytes: float = 1.2e9):
 
 
 def bench_extra(ev: Events, iters: int = 10):
-    """The non-flash attention ops and dropout through the C ABI.  dropout
+    """The non-flash attention ops, dropout and the token-window gather
+    through the C ABI.  dropout
     over 2^26 floats (algorithmic 12 B/element: x in, out and mask out);
     causal mask over [96, 1024, 1024] (8 B/element); bmm_a_bt scores
     (96 x 1024x1024x64, the unfused attention of B8 H12 T1024 d64) and a
@@ -265,6 +266,19 @@ def bench_extra(ev: Events, iters: int = 10):
         nb = 8 * mats * T * T
         out["causal_mask_96x1024x1024"] = {"ms": round(ms, 4), "GB_s": round(nb / (ms * 1e-3) / 1e9, 1),
                                            "frac_of_hbm_peak": round(nb / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
+        abi.free()
+        # token-window batch gather from an HBM-resident stream: batch 512 x
+        # 1024 windows of int64 (algorithmic 16 B per token position written,
+        # 8 B read: x and y reads overlap)
+        L.aar_token_windows_i64.argtypes = [vp, i64, vp, i64, i64, vp, vp, vp, vp]
+        n_tok, bsz, T = 1 << 24, 512, 1024
+        ptok = abi.put(rng.integers(0, 65, n_tok))
+        pst = abi.put(rng.integers(0, n_tok - T - 1, bsz))
+        px, py = abi.alloc(8 * bsz * T), abi.alloc(8 * bsz * T)
+        ms = timed(lambda: L.aar_token_windows_i64(ptok, n_tok, pst, bsz, T, px, py, None, None))
+        nb = 24 * bsz * T
+        out["token_windows_512x1024"] = {"ms": round(ms, 4), "GB_s": round(nb / (ms * 1e-3) / 1e9, 1),
+                                         "frac_of_hbm_peak": round(nb / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
         abi.free()
         for name, (op, Bn, M, N, K) in {"bmm_a_bt_96x1024x1024x64": (1, 96, 1024, 1024, 64),
                                         "bmm_8x2048x2048x2048": (0, 8, 2048, 2048, 2048)}.items():

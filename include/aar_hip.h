@@ -253,6 +253,16 @@ size_t aar_embedding_bwd_workspace_bytes(int64_t n, int64_t vocab, int64_t dim);
 int aar_embedding_bwd_f32(const float* g, const int64_t* ids, float* dw, int64_t n, int64_t vocab,
                           int64_t dim, void* workspace, size_t workspace_bytes, void* stream);
 
+/* Token-window batch from an int64 token stream on the device:
+ * x[b][t] = tokens[starts[b] + t], y[b][t] = tokens[starts[b] + t + 1] for
+ * b < batch, t < seq_len.  A start outside [0, n_tokens - seq_len - 1] yields
+ * zero rows and sets *err = 1 (err may be NULL).  Replaces the host-side
+ * window gather, collate and batch copy of TokenWindowDataset.__getitem__ /
+ * default_collate / to_device_batch (python/shakespeare/scripts/data.py:38-53,
+ * train.py:99-102). */
+int aar_token_windows_i64(const int64_t* tokens, int64_t n_tokens, const int64_t* starts, int64_t batch,
+                          int64_t seq_len, int64_t* x, int64_t* y, int* err, void* stream);
+
 /* Mean cross entropy over rows whose target != ignore_index; logits [n, vocab],
  * targets int64 [n], loss a device scalar.  A target outside [0, vocab) (and not
  * ignore_index) sets *err = 1 and the row is skipped.  Replaces
