@@ -30,6 +30,10 @@
 //   pass 2  workgroup per 128 queries (wave per 32 queries, Q and dO in regs),
 //           loop over key tiles: S^T, dP^T (lane = query), dS^T,
 //           dQ^T += K^T dS^T.
+// With a large enough workspace (HBM is plentiful on MI355X: 3.2 GB for
+// causal B8 H12 T4096), pass 1 also stores every dS tile it computes, in the
+// order pass 2's MFMA operands consume it, and pass 2 becomes dQ^T += K^T
+// dS^T over the stored tiles: 5 GEMM-equivalents per tile pair instead of 7.
 #include <hip/hip_runtime.h>
 #include <math.h>
 
@@ -171,6 +175,21 @@ struct FaOut {
 // Row stride of a transposed [DP][32] tile: 36 keeps the 128-bit reads of 32
 // consecutive columns (one per lane) bank-conflict free.
 constexpr int kLdt = kTile + 4;
+
+// Stored dS: one 32x32 tile per (query tile, key tile) pair with work, 1024
+// floats each, pairs of a head numbered row by row (the lower triangle only
+// when causal).  Inside a tile, dS[q][k] sits at
+//   (k / 8) * 256 + ((k / 4) % 2) * 128 + q * 4 + k % 4,
+// so the dQ pass (lane = query q + 32 * ((k / 4) % 2)) reads its operands of
+// key chunk k / 8 as one coalesced 128-bit load per lane.
+constexpr int kDsTile = kTile * kTile;
+
+__host__ __device__ __forceinline__ int64_t ds_pairs(int64_t nt, bool causal) {
+  return causal ? nt * (nt + 1) / 2 : nt * nt;
+}
+__device__ __forceinline__ int64_t ds_pair(int qt, int kt, int nt, bool causal) {
+  return causal ? (int64_t)qt * (qt + 1) / 2 + kt : (int64_t)qt * nt + kt;
+}
 
 // ------------------------------------------------------------------ forward
 
@@ -349,11 +368,11 @@ flash_bwd_dot_kernel(FaIn dOv, FaIn Ov, float* __restrict__ D, int64_t rows, int
 
 // ------------------------------------------------------------- backward 1
 
-template <int DP, bool CAUSAL, bool VEC>
-__global__ void __launch_bounds__(kFaThreads)
+template <int DP, bool CAUSAL, bool VEC, bool STORE_DS>
+__global__ void __launch_bounds__(kFaThreads, DP <= 64 && (CAUSAL || !STORE_DS) ? 2 : 1)
 flash_bwd_dkdv_kernel(FaIn Qv, FaIn Kv, FaIn Vv, FaIn dOv, const float* __restrict__ Lse,
-                      const float* __restrict__ Dv, FaOut dKv, FaOut dVv, int T, int d, int H, int nkb,
-                      int BH, float scale, float scale_log2) {
+                      const float* __restrict__ Dv, FaOut dKv, FaOut dVv, float* __restrict__ dS, int T, int d,
+                      int H, int nkb, int BH, float scale, float scale_log2) {
   constexpr int NC = DP / 8;
   constexpr int NB = DP / 32;
   constexpr int LD = DP + 4;
@@ -374,6 +393,7 @@ flash_bwd_dkdv_kernel(FaIn Qv, FaIn Kv, FaIn Vv, FaIn dOv, const float* __restri
   const float* __restrict__ dO = dOv.head(bh, H);
   const int k0 = kb * kBlock + wave * kTile;  // first key of this wave
   const int kj = k0 + lr;                     // this lane's key
+  const bool key_ok = kj < T;
 
   f32x4 kr[NC], vr[NC];
 #pragma unroll
@@ -393,6 +413,12 @@ flash_bwd_dkdv_kernel(FaIn Qv, FaIn Kv, FaIn Vv, FaIn dOv, const float* __restri
   const int q_begin = CAUSAL ? kb * kBlock : 0;  // first query tile with work
   const int t0 = q_begin / kTile;
   const int ntiles = (T + kTile - 1) / kTile;
+  // This lane's slot in a stored dS tile (key k = lr of the wave's key tile).
+  float* dS_head = STORE_DS ? dS + (int64_t)bh * ds_pairs(ntiles, CAUSAL) * kDsTile : nullptr;
+  // acc_row(r, h) * 4 = 32 * (r / 4) + 16 * h + 4 * (r % 4): the lane half
+  // goes into the base, so the 16 stores take immediate offsets.
+  const int ds_lane = (lr >> 3) * 256 + ((lr >> 2) & 1) * 128 + (lr & 3) + 16 * h;
+  const int ktile = k0 / kTile;
   const float* Lb = Lse + (int64_t)bh * T;
   const float* Db = Dv + (int64_t)bh * T;
 
@@ -450,7 +476,9 @@ flash_bwd_dkdv_kernel(FaIn Qv, FaIn Kv, FaIn Vv, FaIn dOv, const float* __restri
         for (int e = 0; e < 4; ++e) {
           const int r = 4 * g + e;
           float p = exp2f(s[r] * scale_log2 - l4[e]);
-          if (CAUSAL && kj > qt0 + acc_row(r, h)) p = 0.f;
+          // Keys past the end (zero-filled K) get P = 0, so a stored dS
+          // tile is exactly zero there whatever the query's lse.
+          if ((CAUSAL && kj > qt0 + acc_row(r, h)) || !key_ok) p = 0.f;
           s[r] = p;
           dp[r] = p * (dp[r] - d4[e]);
         }
@@ -463,6 +491,11 @@ flash_bwd_dkdv_kernel(FaIn Qv, FaIn Kv, FaIn Vv, FaIn dOv, const float* __restri
           dv[b] = mfma32(dot[q * LD + b * 32 + lr], s[st], dv[b]);
           dk[b] = mfma32(qt[q * LD + b * 32 + lr], dp[st], dk[b]);
         }
+      }
+      if (STORE_DS && k0 < T) {  // waves past the last key tile own no stored tile
+        float* tile = dS_head + ds_pair(t, ktile, ntiles, CAUSAL) * kDsTile + ds_lane;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) tile[32 * (r >> 2) + 4 * (r & 3)] = dp[r];
       }
     }
     if (has_next) store_tile(cur ^ 1);
@@ -597,6 +630,91 @@ flash_bwd_dq_kernel(FaIn Qv, FaIn Kv, FaIn Vv, FaIn dOv, const float* __restrict
   }
 }
 
+// ------------------------------------------------ backward 2, stored dS
+
+// dQ^T += K^T dS^T over the dS tiles pass 1 stored (lane = query): per key
+// tile, K through LDS (double-buffered) and the wave's dS tile as four
+// coalesced 128-bit loads per lane, fetched one tile ahead.
+template <int DP, bool CAUSAL, bool VEC>
+__global__ void __launch_bounds__(kFaThreads)
+flash_bwd_dq_ds_kernel(FaIn Kv, const float* __restrict__ dS, FaOut dQv, int T, int d, int H, int nqb, int BH,
+                       float scale) {
+  constexpr int NB = DP / 32;
+  constexpr int LD = DP + 4;
+  __shared__ __attribute__((aligned(16))) float ks[2][kTile * LD];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int lr = lane & 31, h = lane >> 5;
+  const int qb = CAUSAL ? nqb - 1 - (int)(blockIdx.x / BH) : (int)(blockIdx.x / BH);
+  const int bh = blockIdx.x % BH;
+  const float* __restrict__ K = Kv.head(bh, H);
+  const int q0 = qb * kBlock + wave * kTile;
+  const int qi = q0 + lr;
+  const int qtile = q0 / kTile;
+  const int nt = (T + kTile - 1) / kTile;
+  const bool active = q0 < T;  // tiles past the end were never stored
+  const float* __restrict__ dS_head = dS + (int64_t)bh * ds_pairs(nt, CAUSAL) * kDsTile + lane * 4;
+
+  f32x16 dq[NB];
+#pragma unroll
+  for (int b = 0; b < NB; ++b) dq[b] = zero16();
+
+  const int kv_end = CAUSAL ? min(T, qb * kBlock + kBlock) : T;
+  const int ntiles = (kv_end + kTile - 1) / kTile;
+  auto has_work = [&](int t) { return active && (!CAUSAL || t <= qtile); };
+  auto load_ds = [&](int t, f32x4 (&r)[4]) {
+    const float* tile = dS_head + ds_pair(qtile, t, nt, CAUSAL) * kDsTile;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) r[c] = *reinterpret_cast<const f32x4*>(tile + c * 256);
+  };
+
+  TileCopy<DP, VEC> kc;
+  kc.load(K, Kv.st, 0, T, d, tid);
+  kc.template store<LD>(ks[0], tid);
+  f32x4 dsr[4];
+  if (has_work(0)) load_ds(0, dsr);
+  __syncthreads();
+
+  for (int t = 0; t < ntiles; ++t) {
+    const int cur = t & 1;
+    const bool has_next = t + 1 < ntiles;
+    if (has_next) kc.load(K, Kv.st, (t + 1) * kTile, T, d, tid);
+    f32x4 nxt[4];
+    if (has_next && has_work(t + 1)) load_ds(t + 1, nxt);
+    if (has_work(t)) {
+      const float* kt = ks[cur];
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+#pragma unroll
+        for (int st = 0; st < 16; ++st) {
+          dq[b] = mfma32(kt[acc_row(st, h) * LD + b * 32 + lr], dsr[st >> 2][st & 3], dq[b]);
+        }
+      }
+    }
+    if (has_next) {
+      kc.template store<LD>(ks[cur ^ 1], tid);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) dsr[c] = nxt[c];
+    }
+    __syncthreads();
+  }
+
+  if (qi < T) {
+    float* qrow = dQv.head(bh, H) + (int64_t)qi * dQv.st;
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int dd = b * 32 + 8 * g + 4 * h;
+        if (dd >= d) continue;
+        f32x4 v = {dq[b][4 * g] * scale, dq[b][4 * g + 1] * scale, dq[b][4 * g + 2] * scale,
+                   dq[b][4 * g + 3] * scale};
+        store4<VEC>(qrow + dd, v, d - dd);
+      }
+    }
+  }
+}
+
 // ------------------------------------------------------------ dispatching
 
 int pad_dim(int64_t d) { return d <= 32 ? 32 : (d <= 64 ? 64 : 128); }
@@ -642,6 +760,7 @@ struct BwdArgs {
   FaIn q, k, v, dout;
   const float *lse, *D;
   FaOut dq, dk, dv;
+  float* dS;  // stored-dS path when non-null
   int T, d, H, BH;
   float scale;
   hipStream_t st;
@@ -651,12 +770,24 @@ template <int DP, bool C, bool VEC>
 struct BwdLaunch {
   static int run(const BwdArgs& a) {
     const int nb = (a.T + kBlock - 1) / kBlock;
-    flash_bwd_dkdv_kernel<DP, C, VEC><<<dim3((unsigned)(nb * a.BH)), dim3(kFaThreads), 0, a.st>>>(
-        a.q, a.k, a.v, a.dout, a.lse, a.D, a.dk, a.dv, a.T, a.d, a.H, nb, a.BH, a.scale, a.scale * kLog2e);
+    if (a.dS) {
+      flash_bwd_dkdv_kernel<DP, C, VEC, true><<<dim3((unsigned)(nb * a.BH)), dim3(kFaThreads), 0, a.st>>>(
+          a.q, a.k, a.v, a.dout, a.lse, a.D, a.dk, a.dv, a.dS, a.T, a.d, a.H, nb, a.BH, a.scale,
+          a.scale * kLog2e);
+    } else {
+      flash_bwd_dkdv_kernel<DP, C, VEC, false><<<dim3((unsigned)(nb * a.BH)), dim3(kFaThreads), 0, a.st>>>(
+          a.q, a.k, a.v, a.dout, a.lse, a.D, a.dk, a.dv, nullptr, a.T, a.d, a.H, nb, a.BH, a.scale,
+          a.scale * kLog2e);
+    }
     int rc = launch_status();
     if (rc != AAR_OK) return rc;
-    flash_bwd_dq_kernel<DP, C, VEC><<<dim3((unsigned)(nb * a.BH)), dim3(kFaThreads), 0, a.st>>>(
-        a.q, a.k, a.v, a.dout, a.lse, a.D, a.dq, a.T, a.d, a.H, nb, a.BH, a.scale, a.scale * kLog2e);
+    if (a.dS) {
+      flash_bwd_dq_ds_kernel<DP, C, VEC><<<dim3((unsigned)(nb * a.BH)), dim3(kFaThreads), 0, a.st>>>(
+          a.k, a.dS, a.dq, a.T, a.d, a.H, nb, a.BH, a.scale);
+    } else {
+      flash_bwd_dq_kernel<DP, C, VEC><<<dim3((unsigned)(nb * a.BH)), dim3(kFaThreads), 0, a.st>>>(
+          a.q, a.k, a.v, a.dout, a.lse, a.D, a.dq, a.T, a.d, a.H, nb, a.BH, a.scale, a.scale * kLog2e);
+    }
     return launch_status();
   }
 };
@@ -715,6 +846,18 @@ extern "C" size_t aar_flash_bwd_workspace_bytes(int64_t bh, int64_t T, int64_t d
   return (size_t)bh * (size_t)T * sizeof(float);
 }
 
+// D rows, padded to 256 bytes, then the dS tiles.
+static size_t fa_d_bytes(int64_t bh, int64_t T) {
+  return ((size_t)bh * (size_t)T * sizeof(float) + 255) / 256 * 256;
+}
+
+extern "C" size_t aar_flash_bwd_fast_workspace_bytes(int64_t bh, int64_t T, int64_t d, int causal) {
+  (void)d;
+  if (bh <= 0 || T <= 0) return 0;
+  const int64_t nt = (T + kTile - 1) / kTile;
+  return fa_d_bytes(bh, T) + (size_t)bh * (size_t)ds_pairs(nt, causal != 0) * kDsTile * sizeof(float);
+}
+
 extern "C" int aar_flash_bwd_strided_f32(const float* q, const float* k, const float* v, const float* o,
                                          const float* lse, const float* dout, float* dq, float* dk, float* dv,
                                          int64_t B, int64_t H, int64_t T, int64_t d, const int64_t* strides,
@@ -735,11 +878,15 @@ extern "C" int aar_flash_bwd_strided_f32(const float* q, const float* k, const f
   int rc = launch_status();
   if (rc != AAR_OK) return rc;
   const bool vec = fa_vec_ok(d, {q, k, v, dout, dq, dk, dv}, strides, 24);
+  float* dS = workspace_bytes >= aar_flash_bwd_fast_workspace_bytes(bh, T, d, causal) && aligned16(workspace)
+                  ? reinterpret_cast<float*>(static_cast<char*>(workspace) + fa_d_bytes(bh, T))
+                  : nullptr;
   BwdArgs a{fa_in(q, strides),          fa_in(k, strides + 3),      fa_in(v, strides + 6),
             fa_in(dout, strides + 12),  lse,                        D,
             fa_out(dq, strides + 15),   fa_out(dk, strides + 18),   fa_out(dv, strides + 21),
-            (int)T,                     (int)d,                     (int)H,
-            (int)bh,                    scale,                      st};
+            dS,                         (int)T,                     (int)d,
+            (int)H,                     (int)bh,                    scale,
+            st};
   return dispatch_fa<BwdLaunch>(pad_dim(d), causal != 0, vec, a);
 }
 

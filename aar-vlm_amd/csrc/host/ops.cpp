@@ -17,11 +17,29 @@
 #include <cmath>
 #include <cstring>
 
+#include <new>
+
 #include "aar_hip.h"
 
 namespace aar {
 
 namespace {
+
+// Flash backward workspace.  The stored-dS size (the dQ pass then reads the
+// dS tiles the dK/dV pass wrote instead of recomputing them) when it stays
+// under kFlashDsCap and the allocator can serve it; otherwise the minimum,
+// which selects the recompute path.
+constexpr size_t kFlashDsCap = size_t(16) << 30;
+Workspace flash_bwd_workspace(int64_t bh, int64_t T, int64_t d, bool causal) {
+  const size_t fast = aar_flash_bwd_fast_workspace_bytes(bh, T, d, causal ? 1 : 0);
+  if (fast <= kFlashDsCap) {
+    try {
+      return Workspace(fast);
+    } catch (const std::bad_alloc&) {
+    }
+  }
+  return Workspace(aar_flash_bwd_workspace_bytes(bh, T, d));
+}
 
 const float* fp(const Tensor& t) { return static_cast<const float*>(t.data()); }
 float* fp(Tensor& t) { return static_cast<float*>(t.data()); }
@@ -428,7 +446,7 @@ class FlashAttentionFunction : public Function {
     put3(st + 15, dc);
     put3(st + 18, dc);
     put3(st + 21, dc);
-    Workspace ws(aar_flash_bwd_workspace_bytes(B * H, T, d));
+    Workspace ws = flash_bwd_workspace(B * H, T, d, causal);
     check_status(aar_flash_bwd_strided_f32(fp(q.t), fp(k.t), fp(v.t), fp(saved_o), fp(saved_lse), fp(go.t),
                                            fp(dq), fp(dk), fp(dv), B, H, T, d, st, causal ? 1 : 0, scale_factor,
                                            ws.data(), ws.bytes(), current_stream()),
@@ -499,7 +517,7 @@ class FlashQKVFunction : public Function {
     put3(st + 12, po);
     float* g = fp(dqkv);
     const float* x = fp(saved_qkv);
-    Workspace ws(aar_flash_bwd_workspace_bytes(B * H, T, d));
+    Workspace ws = flash_bwd_workspace(B * H, T, d, causal);
     check_status(aar_flash_bwd_strided_f32(x, x + D, x + 2 * D, fp(saved_o), fp(saved_lse), fp(go), g, g + D,
                                            g + 2 * D, B, H, T, d, st, causal ? 1 : 0, scale_factor, ws.data(),
                                            ws.bytes(), current_stream()),

@@ -165,6 +165,14 @@ int aar_flash_fwd_f32(const float* q, const float* k, const float* v,
                       int causal, float scale, void* stream);
 
 size_t aar_flash_bwd_workspace_bytes(int64_t bh, int64_t T, int64_t d);
+/* Workspace that also holds every dS tile of the dK/dV pass (a 32x32 float
+ * tile per query/key tile pair with work: bh * n(n+1)/2 tiles causal, bh * n^2
+ * otherwise, n = ceil(T/32); 3.2 GB for causal bh=96, T=4096).  Given at
+ * least this much, aar_flash_bwd_f32 / _strided_f32 compute dQ from the stored
+ * tiles instead of recomputing P and dP; with less (but at least
+ * aar_flash_bwd_workspace_bytes) they recompute.  No counterpart in the
+ * reference, whose backward keeps no workspace. */
+size_t aar_flash_bwd_fast_workspace_bytes(int64_t bh, int64_t T, int64_t d, int causal);
 
 /* dq, dk, dv [bh, T, d] (fully overwritten; no float atomics).  Replaces
  * flash_attention_backward_cuda (cppsrc/ops/flash_attention.cpp:18-22). */

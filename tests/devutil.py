@@ -51,6 +51,8 @@ class Abi:
         L.aar_flash_bwd_workspace_bytes.restype = sz
         L.aar_flash_bwd_workspace_bytes.argtypes = [i64, i64, i64]
         L.aar_flash_bwd_f32.argtypes = [vp] * 9 + [i64, i64, i64, ctypes.c_int, ctypes.c_float, vp, sz, vp]
+        L.aar_flash_bwd_fast_workspace_bytes.restype = sz
+        L.aar_flash_bwd_fast_workspace_bytes.argtypes = [i64, i64, i64, ctypes.c_int]
         L.aar_add_f32.argtypes = [vp, vp, vp, i64, vp]
         L.aar_strided_copy_f32.argtypes = [vp, vp, ctypes.c_int, ctypes.POINTER(i64), ctypes.POINTER(i64),
                                            ctypes.POINTER(i64), vp]

@@ -194,6 +194,66 @@ def test_abi_misaligned(gpu):
         abi.free()
 
 
+def _abi_bwd_both_paths(q, k, v, do, causal):
+    """(O, grads through the recompute path, grads through the stored-dS
+    path) via the C ABI: the workspace size selects the path."""
+    bh, T, d = q.shape
+    abi = Abi()
+    try:
+        pq, pk, pv, pdo = (abi.put(t) for t in (q, k, v, do))
+        po, pl = abi.empty(bh * T * d), abi.empty(bh * T)
+        s = 1.0 / math.sqrt(d)
+        abi.check(abi.L.aar_flash_fwd_f32(pq, pk, pv, po, pl, bh, T, d, int(causal), s, None))
+        out = [abi.get(po, (bh, T, d))]
+        small = abi.L.aar_flash_bwd_workspace_bytes(bh, T, d)
+        big = abi.L.aar_flash_bwd_fast_workspace_bytes(bh, T, d, int(causal))
+        assert big > small
+        for wsb in (small, big):
+            pdq, pdk, pdv = (abi.empty(bh * T * d) for _ in range(3))
+            abi.check(abi.L.aar_flash_bwd_f32(pq, pk, pv, po, pl, pdo, pdq, pdk, pdv, bh, T, d, int(causal), s,
+                                              abi.alloc(wsb), wsb, None))
+            out.append([abi.get(p, (bh, T, d)) for p in (pdq, pdk, pdv)])
+        return out
+    finally:
+        abi.free()
+
+
+@pytest.mark.parametrize("bh,T,d,causal", [(3, 77, 64, True), (2, 45, 64, False), (2, 130, 100, True),
+                                           (1, 33, 32, False), (2, 257, 128, True), (4, 64, 64, True),
+                                           (2, 96, 128, False)])
+def test_abi_stored_ds_path(gpu, bh, T, d, causal):
+    """Both backward paths against the oracle; they evaluate the same products
+    in the same order, so they also agree bit for bit."""
+    rng = np.random.default_rng(bh * 1000 + T + d)
+    q, k, v, do = (rng.standard_normal((bh, T, d)).astype(f32) for _ in range(4))
+    o, slow, fast = _abi_bwd_both_paths(q, k, v, do, causal)
+    assert_close(o, O.attention(q, k, v, causal), TOL, "O")
+    ref = O.attention_backward(q, k, v, do, causal)
+    for g, r, n in zip(fast, ref, ("dq", "dk", "dv")):
+        assert_close(g, r, TOL, n + " (stored dS)")
+    for a, b in zip(fast, slow):
+        np.testing.assert_array_equal(a, b)
+
+
+def test_stored_ds_padded_keys_with_extreme_lse(gpu):
+    """Logits near -128 put lse below -88, where exp(-lse) overflows: the
+    padded keys of the last tile (T = 45) must store dS = 0, not inf * 0."""
+    bh, T, d = 2, 45, 64
+    rng = np.random.default_rng(5)
+    q = (4 + 0.1 * rng.standard_normal((bh, T, d))).astype(f32)
+    k = (-4 + 0.1 * rng.standard_normal((bh, T, d))).astype(f32)
+    v, do = (rng.standard_normal((bh, T, d)).astype(f32) for _ in range(2))
+    assert O.attention_lse(q, k, False).max() < -88
+    o, slow, fast = _abi_bwd_both_paths(q, k, v, do, False)
+    for a, b in zip(fast, slow):
+        assert np.isfinite(a).all()
+        np.testing.assert_array_equal(a, b)
+    # logits of magnitude 128 carry absolute rounding ~1e-5 into exp
+    ref = O.attention_backward(q, k, v, do, False)
+    for g, r, n in zip(fast, ref, ("dq", "dk", "dv")):
+        assert_close(g, r, 1e-3, n)
+
+
 def test_head_dim_limit(gpu):
     x = dev(gpu, np.zeros((1, 4, 136), f32))
     with pytest.raises(ValueError, match="D_MAX"):
