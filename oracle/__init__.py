@@ -113,6 +113,10 @@ def ref():
         R.ref_gpt_step.argtypes = [_i64] * 6 + [ctypes.POINTER(ctypes.c_void_p), _i64p, _i64p, ctypes.c_float,
                                                  ctypes.POINTER(ctypes.c_float)]
         R.ref_gpt_step.restype = ctypes.c_int
+        pp = ctypes.POINTER(ctypes.c_void_p)
+        R.ref_lm_step.argtypes = [_i64] * 6 + [ctypes.c_float, _i64, pp, pp, pp, _i64p, _i64p] + \
+            [ctypes.c_float] * 7 + [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p]
+        R.ref_lm_step.restype = ctypes.c_int
         R.ref_philox_uniform.argtypes = [ctypes.c_uint64, ctypes.c_uint64]
         R.ref_philox_uniform.restype = ctypes.c_float
         R.ref_dropout.argtypes = [_f32p, _f32p, vp, _i64, ctypes.c_float, ctypes.c_uint64]
@@ -563,3 +567,26 @@ def ref_bmm(op: str, a, b) -> np.ndarray:
     if ref().ref_bmm(BMM_OPS.index(op), a, b, c, Bn, M, N, K) != 0:
         raise RuntimeError("reference bmm failed")
     return c
+
+
+def ref_lm_step(cfg, params, m, v, ids, targets, *, dropout, seed, lr, betas, eps, wd, t, grads=False):
+    """One AdamW training step of the reference Shakespeare GPT on the
+    reference CPU path.  params, m and v are updated in place; returns the
+    loss before the update (and the gradients when grads is set).  seed >= 0
+    reseeds the dropout stream, a negative seed continues it."""
+    def ptrs(arrs):
+        return (ctypes.c_void_p * len(arrs))(*[a.ctypes.data for a in arrs])
+    for a in list(params) + list(m) + list(v):
+        assert a.dtype == np.float32 and a.flags.c_contiguous
+    g = [np.empty_like(p) for p in params] if grads else None
+    ids = np.ascontiguousarray(ids, np.int64)
+    targets = np.ascontiguousarray(targets, np.int64).reshape(-1)
+    b1, b2 = betas
+    bc1, bc2 = 1.0 - b1 ** t, 1.0 - b2 ** t  # AdamW.step, in double as the Python optimizer
+    loss = ctypes.c_float()
+    rc = ref().ref_lm_step(cfg["vocab"], cfg["ctx"], cfg["layers"], cfg["d_model"], cfg["heads"], ids.shape[0],
+                           dropout, seed, ptrs(params), ptrs(m), ptrs(v), ids.reshape(-1), targets, lr, b1, b2, eps,
+                           wd, bc1, bc2, ctypes.byref(loss), ptrs(g) if grads else None)
+    if rc != 0:
+        raise RuntimeError("reference lm step failed")
+    return (float(loss.value), g) if grads else float(loss.value)

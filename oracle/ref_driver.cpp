@@ -340,4 +340,76 @@ int ref_gpt_step(int64_t vocab, int64_t ctx, int64_t layers, int64_t d, int64_t 
   }
 }
 
+// One training step of the reference Shakespeare GPT
+// (python/shakespeare/scripts/model.py:8-57: pre-LN, GELU MLP with biases,
+// bias-free attention, dropout after the embeddings and on both residual
+// branches) with AdamW (aargrad/optim.py AdamW.step): forward, backward,
+// update.  seed >= 0 calls manual_seed(seed) first; otherwise the dropout
+// seed counter carries on from the previous call.  grads_out (may be null)
+// receives the gradients before the update; params, m and v are updated in
+// place.  bc1/bc2 are AdamW's bias corrections for this step, computed by
+// the caller as the Python optimizer does.
+int ref_lm_step(int64_t vocab, int64_t ctx, int64_t layers, int64_t d, int64_t heads, int64_t batch,
+                float dropout, int64_t seed, float* const* params, float* const* m_state, float* const* v_state,
+                const int64_t* ids, const int64_t* targets, float lr, float b1, float b2, float eps, float wd,
+                float bc1, float bc2, float* loss_out, float* const* grads_out) {
+  try {
+    const int64_t B = batch, T = ctx, f = 4 * d;
+    std::vector<std::vector<int64_t>> shapes = {{vocab, d}, {ctx, d}};
+    for (int64_t i = 0; i < layers; ++i) {
+      for (auto s : std::vector<std::vector<int64_t>>{{d}, {d}, {3 * d, d}, {d, d}, {d}, {d}, {f, d}, {f}, {d, f}, {d}})
+        shapes.push_back(s);
+    }
+    shapes.push_back({d});
+    shapes.push_back({d});
+    shapes.push_back({vocab, d});
+    std::vector<Tensor> P, M, V;
+    for (size_t i = 0; i < shapes.size(); ++i) {
+      P.push_back(make(params[i], shapes[i], true));
+      M.push_back(make(m_state[i], shapes[i]));
+      V.push_back(make(v_state[i], shapes[i]));
+    }
+    Tensor tids = Tensor::empty({B, T}, DType::Int64);
+    std::memcpy(tids.data(), ids, B * T * sizeof(int64_t));
+    Tensor pos = Tensor::empty({B, T}, DType::Int64);
+    for (int64_t b = 0; b < B; ++b)
+      for (int64_t t = 0; t < T; ++t) static_cast<int64_t*>(pos.data())[b * T + t] = t;
+    Tensor tgt = Tensor::empty({B * T}, DType::Int64);
+    std::memcpy(tgt.data(), targets, B * T * sizeof(int64_t));
+    if (seed >= 0) vlm::manual_seed((uint64_t)seed);
+    auto drop = [&](const Tensor& x) { return dropout > 0.0f ? vlm::dropout(x, dropout) : x; };
+
+    Tensor x = drop(vlm::add(vlm::embedding(P[0], tids), vlm::embedding(P[1], pos)));
+    for (int64_t i = 0; i < layers; ++i) {
+      const Tensor* w = &P[2 + 10 * i];
+      Tensor h = vlm::layernorm(x, w[0], w[1], 1e-5f);
+      Tensor qkv = vlm::reshape(vlm::matmul_a_bt(h, w[2]), {B, T, 3, heads, d / heads});
+      Tensor q = vlm::transpose(vlm::squeeze(vlm::slice(qkv, 2, 0, 1), 2), 1, 2);
+      Tensor k = vlm::transpose(vlm::squeeze(vlm::slice(qkv, 2, 1, 2), 2), 1, 2);
+      Tensor v = vlm::transpose(vlm::squeeze(vlm::slice(qkv, 2, 2, 3), 2), 1, 2);
+      Tensor a = vlm::reshape(vlm::transpose(vlm::flash_attention(q, k, v, true), 1, 2), {B, T, d});
+      x = vlm::add(x, drop(vlm::matmul_a_bt(a, w[3])));
+      h = vlm::layernorm(x, w[4], w[5], 1e-5f);
+      h = vlm::gelu(vlm::add_bias(vlm::matmul_a_bt(h, w[6]), w[7]));
+      x = vlm::add(x, drop(vlm::add_bias(vlm::matmul_a_bt(h, w[8]), w[9])));
+    }
+    const size_t n = P.size();
+    x = vlm::layernorm(x, P[n - 3], P[n - 2], 1e-5f);
+    Tensor logits = vlm::matmul_a_bt(x, P[n - 1]);
+    Tensor loss = vlm::cross_entropy(vlm::reshape(logits, {B * T, vocab}), tgt, -100);
+    *loss_out = *static_cast<const float*>(loss.data());
+    loss.backward();
+    for (size_t i = 0; i < n; ++i) {
+      if (grads_out) out(*P[i].grad(), grads_out[i]);
+      vlm::adamw_step(P[i], *P[i].grad(), M[i], V[i], lr, b1, b2, eps, wd, bc1, bc2);
+      out(P[i], params[i]);
+      out(M[i], m_state[i]);
+      out(V[i], v_state[i]);
+    }
+    return 0;
+  } catch (const std::exception&) {
+    return -1;
+  }
+}
+
 }  // extern "C"

@@ -154,3 +154,29 @@ def test_ref_bitexact_nn_ops():
     for x1, x2 in zip(O.ref_adamw(a, g, m, v, 1e-3, 0.9, 0.999, 1e-8, 0.01, 0.19, 0.002),
                       O.adamw(a, g, m, v, 1e-3, 0.9, 0.999, 1e-8, 0.01, 0.19, 0.002)):
         np.testing.assert_array_equal(x1, x2)
+
+
+@needs_ref
+def test_ref_lm_step_matches_oracle_forward():
+    """The reference Shakespeare-model step (oracle/_ref, dropout off) has the
+    loss of the oracle's forward of the same model, and AdamW lowers it."""
+    import lmutil
+
+    cfg = {"vocab": 65, "ctx": 16, "layers": 2, "d_model": 32, "heads": 4}
+    rng = np.random.default_rng(3)
+    shapes = [(65, 32), (16, 32)] + [(32,), (32,), (96, 32), (32, 32), (32,), (32,), (128, 32), (128,),
+                                     (32, 128), (32,)] * 2 + [(32,), (32,), (65, 32)]
+    params = [(1.0 + 0.1 * rng.standard_normal(s)) if len(s) == 1 and i > 1 else 0.2 * rng.standard_normal(s)
+              for i, s in enumerate(shapes)]
+    params = [np.ascontiguousarray(p, np.float32) for p in params]
+    m = [np.zeros_like(p) for p in params]
+    v = [np.zeros_like(p) for p in params]
+    ids = rng.integers(0, 65, (3, 16))
+    tgt = rng.integers(0, 65, (3, 16))
+    lcfg = {"vocab_size": 65, "max_seq_len": 16, "n_layer": 2, "n_head": 4, "d_model": 32}
+    want = float(O.cross_entropy(lmutil.oracle_forward(params, lcfg, ids).reshape(-1, 65), tgt.reshape(-1)))
+    kw = dict(dropout=0.0, seed=0, lr=1e-2, betas=(0.9, 0.95), eps=1e-8, wd=0.01)
+    loss0 = O.ref_lm_step(cfg, params, m, v, ids, tgt, t=1, **kw)
+    assert abs(loss0 - want) <= 1e-5 * max(abs(want), 1)
+    losses = [O.ref_lm_step(cfg, params, m, v, ids, tgt, t=t, **kw) for t in range(2, 6)]
+    assert losses[-1] < loss0
