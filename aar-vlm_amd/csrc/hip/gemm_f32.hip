@@ -532,7 +532,7 @@ struct Cfg {
   float eff;
 };
 constexpr Cfg kCfgs[] = {
-    {256, 256, 16, 128, 64, 1, 3, 0.895f},  // 0: 8 waves, 2 waves/SIMD
+    {256, 256, 32, 64, 128, 1, 2, 0.895f},  // 0: 8 waves, 2 waves/SIMD; BK 32 halves the barriers
     {256, 128, 16, 128, 64, 2, 3, 0.83f},   // 1
     {128, 256, 16, 64, 128, 2, 3, 0.83f},   // 2
     {128, 128, 16, 64, 64, 2, 3, 0.84f},    // 3
