@@ -178,10 +178,10 @@ constexpr int kLdt = kTile + 4;
 
 // Stored dS: one 32x32 tile per (query tile, key tile) pair with work, 1024
 // floats each, pairs of a head numbered row by row (the lower triangle only
-// when causal).  Inside a tile, dS[q][k] sits at
-//   (k / 8) * 256 + ((k / 4) % 2) * 128 + q * 4 + k % 4,
-// so the dQ pass (lane = query q + 32 * ((k / 4) % 2)) reads its operands of
-// key chunk k / 8 as one coalesced 128-bit load per lane.
+// when causal).  Inside a tile dS[q][k] sits at k * 32 + q: the dK/dV pass
+// (lane = key, accumulator registers 4g..4g+3 = four consecutive queries)
+// writes 128-bit runs, and each 32-bit load of the dQ pass (lane = query)
+// reads 128 contiguous bytes per half-wave.
 constexpr int kDsTile = kTile * kTile;
 
 __host__ __device__ __forceinline__ int64_t ds_pairs(int64_t nt, bool causal) {
@@ -415,9 +415,8 @@ flash_bwd_dkdv_kernel(FaIn Qv, FaIn Kv, FaIn Vv, FaIn dOv, const float* __restri
   const int ntiles = (T + kTile - 1) / kTile;
   // This lane's slot in a stored dS tile (key k = lr of the wave's key tile).
   float* dS_head = STORE_DS ? dS + (int64_t)bh * ds_pairs(ntiles, CAUSAL) * kDsTile : nullptr;
-  // acc_row(r, h) * 4 = 32 * (r / 4) + 16 * h + 4 * (r % 4): the lane half
-  // goes into the base, so the 16 stores take immediate offsets.
-  const int ds_lane = (lr >> 3) * 256 + ((lr >> 2) & 1) * 128 + (lr & 3) + 16 * h;
+  // dS[acc_row(4g + e, h)][lr] = dS[8g + 4h + e][lr] sits at lr * 32 + 4h + 8g + e.
+  const int ds_lane = lr * kTile + 4 * h;
   const int ktile = k0 / kTile;
   const float* Lb = Lse + (int64_t)bh * T;
   const float* Db = Dv + (int64_t)bh * T;
@@ -495,7 +494,10 @@ flash_bwd_dkdv_kernel(FaIn Qv, FaIn Kv, FaIn Vv, FaIn dOv, const float* __restri
       if (STORE_DS && k0 < T) {  // waves past the last key tile own no stored tile
         float* tile = dS_head + ds_pair(t, ktile, ntiles, CAUSAL) * kDsTile + ds_lane;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) tile[32 * (r >> 2) + 4 * (r & 3)] = dp[r];
+        for (int g = 0; g < 4; ++g) {
+          const f32x4 v = {dp[4 * g], dp[4 * g + 1], dp[4 * g + 2], dp[4 * g + 3]};
+          *reinterpret_cast<f32x4*>(tile + 8 * g) = v;
+        }
       }
     }
     if (has_next) store_tile(cur ^ 1);
@@ -633,8 +635,8 @@ flash_bwd_dq_kernel(FaIn Qv, FaIn Kv, FaIn Vv, FaIn dOv, const float* __restrict
 // ------------------------------------------------ backward 2, stored dS
 
 // dQ^T += K^T dS^T over the dS tiles pass 1 stored (lane = query): per key
-// tile, K through LDS (double-buffered) and the wave's dS tile as four
-// coalesced 128-bit loads per lane, fetched one tile ahead.
+// tile, K through LDS (double-buffered) and the wave's dS tile as sixteen
+// coalesced 32-bit loads per lane, fetched one tile ahead.
 template <int DP, bool CAUSAL, bool VEC>
 __global__ void __launch_bounds__(kFaThreads)
 flash_bwd_dq_ds_kernel(FaIn Kv, const float* __restrict__ dS, FaOut dQv, int T, int d, int H, int nqb, int BH,
@@ -653,7 +655,8 @@ flash_bwd_dq_ds_kernel(FaIn Kv, const float* __restrict__ dS, FaOut dQv, int T, 
   const int qtile = q0 / kTile;
   const int nt = (T + kTile - 1) / kTile;
   const bool active = q0 < T;  // tiles past the end were never stored
-  const float* __restrict__ dS_head = dS + (int64_t)bh * ds_pairs(nt, CAUSAL) * kDsTile + lane * 4;
+  // step st reads dS[lr][acc_row(st, h)] at (8 * (st / 4) + 4h + st % 4) * 32 + lr
+  const float* __restrict__ dS_head = dS + (int64_t)bh * ds_pairs(nt, CAUSAL) * kDsTile + 4 * h * kTile + lr;
 
   f32x16 dq[NB];
 #pragma unroll
@@ -662,16 +665,16 @@ flash_bwd_dq_ds_kernel(FaIn Kv, const float* __restrict__ dS, FaOut dQv, int T, 
   const int kv_end = CAUSAL ? min(T, qb * kBlock + kBlock) : T;
   const int ntiles = (kv_end + kTile - 1) / kTile;
   auto has_work = [&](int t) { return active && (!CAUSAL || t <= qtile); };
-  auto load_ds = [&](int t, f32x4 (&r)[4]) {
+  auto load_ds = [&](int t, float (&r)[16]) {
     const float* tile = dS_head + ds_pair(qtile, t, nt, CAUSAL) * kDsTile;
 #pragma unroll
-    for (int c = 0; c < 4; ++c) r[c] = *reinterpret_cast<const f32x4*>(tile + c * 256);
+    for (int st = 0; st < 16; ++st) r[st] = tile[(8 * (st >> 2) + (st & 3)) * kTile];
   };
 
   TileCopy<DP, VEC> kc;
   kc.load(K, Kv.st, 0, T, d, tid);
   kc.template store<LD>(ks[0], tid);
-  f32x4 dsr[4];
+  float dsr[16];
   if (has_work(0)) load_ds(0, dsr);
   __syncthreads();
 
@@ -679,7 +682,7 @@ flash_bwd_dq_ds_kernel(FaIn Kv, const float* __restrict__ dS, FaOut dQv, int T, 
     const int cur = t & 1;
     const bool has_next = t + 1 < ntiles;
     if (has_next) kc.load(K, Kv.st, (t + 1) * kTile, T, d, tid);
-    f32x4 nxt[4];
+    float nxt[16];
     if (has_next && has_work(t + 1)) load_ds(t + 1, nxt);
     if (has_work(t)) {
       const float* kt = ks[cur];
@@ -687,14 +690,14 @@ flash_bwd_dq_ds_kernel(FaIn Kv, const float* __restrict__ dS, FaOut dQv, int T, 
       for (int b = 0; b < NB; ++b) {
 #pragma unroll
         for (int st = 0; st < 16; ++st) {
-          dq[b] = mfma32(kt[acc_row(st, h) * LD + b * 32 + lr], dsr[st >> 2][st & 3], dq[b]);
+          dq[b] = mfma32(kt[acc_row(st, h) * LD + b * 32 + lr], dsr[st], dq[b]);
         }
       }
     }
     if (has_next) {
       kc.template store<LD>(ks[cur ^ 1], tid);
 #pragma unroll
-      for (int c = 0; c < 4; ++c) dsr[c] = nxt[c];
+      for (int st = 0; st < 16; ++st) dsr[st] = nxt[st];
     }
     __syncthreads();
   }
