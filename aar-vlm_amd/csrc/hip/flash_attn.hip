@@ -38,6 +38,7 @@
 #include <math.h>
 
 #include <initializer_list>
+#include <stdint.h>
 
 #include "common.hpp"
 
@@ -873,6 +874,9 @@ extern "C" size_t aar_flash_bwd_fast_workspace_bytes(int64_t bh, int64_t T, int6
   (void)d;
   if (bh <= 0 || T <= 0) return 0;
   const int64_t nt = (T + kTile - 1) / kTile;
+  // Sizes past 2^62 bytes cannot be allocated: saturate instead of wrapping.
+  const double bytes = (double)bh * (double)ds_pairs(nt, causal != 0) * kDsTile * sizeof(float);
+  if (bytes > 4.0e18) return SIZE_MAX;
   return fa_d_bytes(bh, T) + (size_t)bh * (size_t)ds_pairs(nt, causal != 0) * kDsTile * sizeof(float);
 }
 

@@ -61,6 +61,23 @@ def test_abi_validates_before_touching_the_device():
     lib.aar_flash_bwd_workspace_bytes.restype = ctypes.c_size_t
     lib.aar_flash_bwd_workspace_bytes.argtypes = [i64, i64, i64]
     assert lib.aar_flash_bwd_workspace_bytes(96, 4096, 64) == 96 * 4096 * 4
+    # stored-dS workspace: D rows (256-byte padded) + one 32x32 tile per pair with work
+    lib.aar_flash_bwd_fast_workspace_bytes.restype = ctypes.c_size_t
+    lib.aar_flash_bwd_fast_workspace_bytes.argtypes = [i64, i64, i64, ctypes.c_int]
+    d_rows = (96 * 4096 * 4 + 255) // 256 * 256
+    assert lib.aar_flash_bwd_fast_workspace_bytes(96, 4096, 64, 1) == d_rows + 96 * (128 * 129 // 2) * 4096
+    assert lib.aar_flash_bwd_fast_workspace_bytes(96, 4096, 64, 0) == d_rows + 96 * 128 * 128 * 4096
+    assert lib.aar_flash_bwd_fast_workspace_bytes(3, 45, 64, 1) == 768 + 3 * 3 * 4096  # ragged T: 540 B of D rows
+    assert lib.aar_flash_bwd_fast_workspace_bytes(1 << 24, 1 << 24, 64, 0) == 2 ** 64 - 1  # saturates
+    # token windows, dropout, causal mask: argument checks before any launch
+    lib.aar_token_windows_i64.argtypes = [vp, i64, vp, i64, i64, vp, vp, vp, vp]
+    assert lib.aar_token_windows_i64(None, 10, None, 2, 0, None, None, None, None) == -1  # seq_len 0
+    assert lib.aar_token_windows_i64(None, 10, None, 0, 4, None, None, None, None) == 0  # empty batch
+    lib.aar_dropout_f32.argtypes = [vp, vp, vp, i64, ctypes.c_float, ctypes.c_uint64, vp]
+    assert lib.aar_dropout_f32(None, None, None, 4, 1.0, 0, None) == -1  # p outside [0, 1)
+    assert lib.aar_dropout_f32(None, None, None, 0, 0.5, 0, None) == 0
+    lib.aar_causal_mask_f32.argtypes = [vp, vp, i64, i64, ctypes.c_float, vp]
+    assert lib.aar_causal_mask_f32(None, None, -1, 4, 0.0, None) == -1
 
 
 def test_core_exports_reference_api(ag):
