@@ -490,7 +490,7 @@ flash_bwd_dkdv_kernel(FaIn Qv, FaIn Kv, FaIn Vv, FaIn dOv, const float* __restri
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int r = 4 * g + e;
-          float p = exp2f(s[r] * scale_log2 - l4[e]);
+          float p = fast_exp2(s[r] * scale_log2 - l4[e]);
           // Keys past the end (zero-filled K) get P = 0, so a stored dS
           // tile is exactly zero there whatever the query's lse.
           if ((CAUSAL && kj > qt0 + acc_row(r, h)) || !key_ok) p = 0.f;
@@ -613,7 +613,7 @@ flash_bwd_dq_kernel(FaIn Qv, FaIn Kv, FaIn Vv, FaIn dOv, const float* __restrict
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int key = kv0 + acc_row(r, h);
-        float p = exp2f(s[r] * scale_log2 - l2);
+        float p = fast_exp2(s[r] * scale_log2 - l2);
         if (key >= T || (CAUSAL && key > qi)) p = 0.f;
         dp[r] = p * (dp[r] - dq_sum);
       }
