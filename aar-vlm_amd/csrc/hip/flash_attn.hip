@@ -651,15 +651,15 @@ flash_bwd_dq_kernel(FaIn Qv, FaIn Kv, FaIn Vv, FaIn dOv, const float* __restrict
 // ------------------------------------------------ backward 2, stored dS
 
 // dQ^T += K^T dS^T over the dS tiles pass 1 stored (lane = query): per key
-// tile, K through LDS (double-buffered) and the wave's dS tile as sixteen
-// coalesced 32-bit loads per lane, fetched one tile ahead.
+// tile, K staged transposed in LDS (double-buffered; one 128-bit read feeds 4
+// MFMA steps) and the wave's dS tile as sixteen coalesced 32-bit loads per
+// lane, fetched one tile ahead.
 template <int DP, bool CAUSAL, bool VEC>
 __global__ void __launch_bounds__(kFaThreads)
 flash_bwd_dq_ds_kernel(FaIn Kv, const float* __restrict__ dS, FaOut dQv, int T, int d, int H, int nqb, int BH,
                        float scale) {
   constexpr int NB = DP / 32;
-  constexpr int LD = DP + 4;
-  __shared__ __attribute__((aligned(16))) float ks[2][kTile * LD];
+  __shared__ __attribute__((aligned(16))) float kts[2][DP * kLdt];  // K tiles, transposed
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int lr = lane & 31, h = lane >> 5;
@@ -689,7 +689,7 @@ flash_bwd_dq_ds_kernel(FaIn Kv, const float* __restrict__ dS, FaOut dQv, int T, 
 
   TileCopy<DP, VEC> kc;
   kc.load(K, Kv.st, 0, T, d, tid);
-  kc.template store<LD>(ks[0], tid);
+  kc.template store_t<kLdt, false>(kts[0], tid);
   float dsr[16];
   if (has_work(0)) load_ds(0, dsr);
   __syncthreads();
@@ -701,17 +701,20 @@ flash_bwd_dq_ds_kernel(FaIn Kv, const float* __restrict__ dS, FaOut dQv, int T, 
     float nxt[16];
     if (has_next && has_work(t + 1)) load_ds(t + 1, nxt);
     if (has_work(t)) {
-      const float* kt = ks[cur];
+      const float* kt = kts[cur];
 #pragma unroll
       for (int b = 0; b < NB; ++b) {
 #pragma unroll
-        for (int st = 0; st < 16; ++st) {
-          dq[b] = mfma32(kt[acc_row(st, h) * LD + b * 32 + lr], dsr[st], dq[b]);
+        for (int g = 0; g < 4; ++g) {
+          // K^T[b*32 + lr][keys 8g + 4h .. +3]: one 128-bit read feeds 4 steps
+          const f32x4 kf = *reinterpret_cast<const f32x4*>(kt + (b * 32 + lr) * kLdt + 8 * g + 4 * h);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) dq[b] = mfma32(kf[e], dsr[4 * g + e], dq[b]);
         }
       }
     }
     if (has_next) {
-      kc.template store<LD>(ks[cur ^ 1], tid);
+      kc.template store_t<kLdt, false>(kts[cur ^ 1], tid);
 #pragma unroll
       for (int st = 0; st < 16; ++st) dsr[st] = nxt[st];
     }
