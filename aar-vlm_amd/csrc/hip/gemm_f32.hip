@@ -539,6 +539,7 @@ constexpr Cfg kCfgs[] = {
     {64, 64, 16, 32, 32, 4, 4, 0.77f},      // 4
     {128, 64, 16, 64, 32, 3, 3, 0.78f},     // 5
     {64, 128, 16, 32, 64, 3, 3, 0.80f},     // 6
+    {192, 192, 16, 96, 96, 1, 3, 0.80f},    // 7: 4 waves; split-K weight gradients (N or M = 384, 1536)
 };
 constexpr int kNumCfgs = sizeof(kCfgs) / sizeof(kCfgs[0]);
 constexpr int kMaxSplits = 64;
@@ -627,12 +628,13 @@ int launch_op(int cfg, bool vec, const float* A, const float* B, float* C, int64
     AAR_GEMM_CFG(4)
     AAR_GEMM_CFG(5)
     AAR_GEMM_CFG(6)
+    AAR_GEMM_CFG(7)
     default:
       return AAR_EINVAL;
   }
 #undef AAR_GEMM_CFG
 }
-static_assert(kNumCfgs == 7, "launch_op lists every configuration");
+static_assert(kNumCfgs == 8, "launch_op lists every configuration");
 
 // 128-bit loads need 16-byte aligned operands whose contiguous extents and
 // leading dimensions are multiples of 4, and the 32-bit per-thread offsets
