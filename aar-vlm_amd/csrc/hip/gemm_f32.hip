@@ -523,23 +523,33 @@ splitk_reduce_kernel(const float* __restrict__ W, float* __restrict__ C, int64_t
 }
 
 // Tile configurations.  `resident` is the number of workgroups one CU holds
-// (LDS and register budget), `stages` the LDS ring depth of the DMA path,
-// `eff` the fraction of the MFMA peak the configuration sustains on a fully
-// occupied GPU (measured on MI355X at 4096^3, DMA path; the
-// 256x128 shapes are rated below 128x128 because they lose to it at short K).
+// (LDS and register budget; it sets the kernel's launch bounds), `stages` the
+// LDS ring depth of the DMA path, `eff` the fraction of the MFMA peak the
+// configuration sustains on a fully occupied GPU (measured on MI355X at
+// 4096^3, DMA path; the 256x128 shapes are rated below 128x128 because they
+// lose to it at short K), `slots` the workgroups per CU below which the cost
+// model charges an occupancy penalty, and `ops` the layouts the planner may
+// pick it for.
+constexpr int kAllOps = (1 << AAR_GEMM_NN) | (1 << AAR_GEMM_NT) | (1 << AAR_GEMM_TN);
 struct Cfg {
   int bm, bn, bk, wm, wn, resident, stages;
   float eff;
+  int slots, ops;
 };
 constexpr Cfg kCfgs[] = {
-    {256, 256, 32, 64, 128, 1, 2, 0.895f},  // 0: 8 waves, 2 waves/SIMD; BK 32 halves the barriers
-    {256, 128, 16, 128, 64, 2, 3, 0.83f},   // 1
-    {128, 256, 16, 64, 128, 2, 3, 0.83f},   // 2
-    {128, 128, 16, 64, 64, 2, 3, 0.84f},    // 3
-    {64, 64, 16, 32, 32, 4, 4, 0.77f},      // 4
-    {128, 64, 16, 64, 32, 3, 3, 0.78f},     // 5
-    {64, 128, 16, 32, 64, 3, 3, 0.80f},     // 6
-    {192, 192, 16, 96, 96, 1, 3, 0.80f},    // 7: 4 waves; split-K weight gradients (N or M = 384, 1536)
+    {256, 256, 32, 64, 128, 1, 2, 0.895f, 1, kAllOps},  // 0: 8 waves, 2 waves/SIMD; BK 32 halves the barriers
+    {256, 128, 16, 128, 64, 2, 3, 0.83f, 2, kAllOps},   // 1
+    {128, 256, 16, 64, 128, 2, 3, 0.83f, 2, kAllOps},   // 2
+    {128, 128, 16, 64, 64, 2, 3, 0.84f, 2, kAllOps},    // 3
+    {64, 64, 16, 32, 32, 4, 4, 0.77f, 4, kAllOps},      // 4
+    {128, 64, 16, 64, 32, 3, 3, 0.78f, 3, kAllOps},     // 5
+    {64, 128, 16, 32, 64, 3, 3, 0.80f, 3, kAllOps},     // 6
+    {192, 192, 16, 96, 96, 1, 3, 0.80f, 1, kAllOps},    // 7: 4 waves; split-K weight gradients (N or M = 384, 1536)
+    // 8: 4 waves of 64x96; for NN with N a multiple of 192 (the dX products
+    // of the GPT step: +4-5 % over the 64x128 tile).  It keeps full speed
+    // with one workgroup per CU, hence one model slot; as NT it loses at
+    // N = 1152, so it is not planned there.
+    {128, 192, 32, 64, 96, 2, 2, 0.87f, 1, 1 << AAR_GEMM_NN},
 };
 constexpr int kNumCfgs = sizeof(kCfgs) / sizeof(kCfgs[0]);
 constexpr int kMaxSplits = 64;
@@ -557,13 +567,14 @@ int64_t split_chunk(int64_t K, int splits, int bk) { return ceil_div(ceil_div(K,
 // of `eff` with one block); split-K adds the partial-sum traffic and the
 // reduction launch.  Fitted to measured throughput of every configuration on
 // the square, MLP and weight-gradient shapes of the GPT step.
-Plan plan_gemm(int64_t M, int64_t N, int64_t K, size_t ws_bytes, bool allow_split, int64_t batch = 1) {
+Plan plan_gemm(int op, int64_t M, int64_t N, int64_t K, size_t ws_bytes, bool allow_split, int64_t batch = 1) {
   const int cus = device_cu_count();
   const double cu_flops = 157.3e12 / 256;  // fp32 MFMA FLOP/s per CU
-  Plan best{kNumCfgs - 1, 1, K};
+  Plan best{3, 1, K};
   double best_t = 1e300;
   for (int c = 0; c < kNumCfgs; ++c) {
     const Cfg& cf = kCfgs[c];
+    if (!(cf.ops & (1 << op))) continue;
     const int64_t tiles = ceil_div(M, (int64_t)cf.bm) * ceil_div(N, (int64_t)cf.bn) * batch;
     for (int splits = 1; splits <= kMaxSplits; splits *= 2) {
       if (splits > 1) {
@@ -574,7 +585,7 @@ Plan plan_gemm(int64_t M, int64_t N, int64_t K, size_t ws_bytes, bool allow_spli
       const int64_t kps = split_chunk(K, splits, cf.bk);
       const int64_t real_splits = ceil_div(K, kps);
       const int64_t per_cu = ceil_div(tiles * real_splits, (int64_t)cus);
-      const double occ = std::min(1.0, 0.6 + 0.4 * (double)per_cu / cf.resident);
+      const double occ = std::min(1.0, 0.6 + 0.4 * (double)per_cu / cf.slots);
       double t = (double)per_cu * 2.0 * cf.bm * cf.bn * (double)kps / (cf.eff * occ * cu_flops);
       if (real_splits > 1) t += 6e-6 + (double)(real_splits + 1) * M * N * 4.0 / 3e12;
       if (t < best_t) {
@@ -629,12 +640,13 @@ int launch_op(int cfg, bool vec, const float* A, const float* B, float* C, int64
     AAR_GEMM_CFG(5)
     AAR_GEMM_CFG(6)
     AAR_GEMM_CFG(7)
+    AAR_GEMM_CFG(8)
     default:
       return AAR_EINVAL;
   }
 #undef AAR_GEMM_CFG
 }
-static_assert(kNumCfgs == 8, "launch_op lists every configuration");
+static_assert(kNumCfgs == 9, "launch_op lists every configuration");
 
 // 128-bit loads need 16-byte aligned operands whose contiguous extents and
 // leading dimensions are multiples of 4, and the 32-bit per-thread offsets
@@ -718,7 +730,7 @@ using namespace aar;
 
 extern "C" size_t aar_gemm_f32_workspace_bytes(int op, int64_t M, int64_t N, int64_t K) {
   if (op < 0 || op > 2 || M <= 0 || N <= 0 || K <= 0) return 0;
-  const Plan p = plan_gemm(M, N, K, (size_t)-1, true);
+  const Plan p = plan_gemm(op, M, N, K, (size_t)-1, true);
   if (p.splits <= 1) return 0;
   return (size_t)p.splits * (size_t)M * (size_t)N * sizeof(float);
 }
@@ -727,7 +739,7 @@ extern "C" int aar_gemm_f32(int op, int64_t M, int64_t N, int64_t K, const float
                             float* C, void* workspace, size_t workspace_bytes, void* stream) {
   const int chk = check_gemm_args(op, M, N, K, A, B, C, stream);
   if (chk != AAR_OK) return chk == 1 ? AAR_OK : chk;
-  const Plan p = plan_gemm(M, N, K, workspace ? workspace_bytes : 0, workspace != nullptr);
+  const Plan p = plan_gemm(op, M, N, K, workspace ? workspace_bytes : 0, workspace != nullptr);
   return run_gemm(op, M, N, K, A, B, C, workspace, p, as_stream(stream));
 }
 
@@ -742,7 +754,7 @@ extern "C" int aar_gemm_f32_tile_config(int config, int* tile_m, int* tile_n, in
 extern "C" int aar_gemm_f32_plan(int op, int64_t M, int64_t N, int64_t K, size_t workspace_bytes,
                                  int* config, int* splits) {
   if (op < 0 || op > 2 || M <= 0 || N <= 0 || K <= 0) return AAR_EINVAL;
-  const Plan p = plan_gemm(M, N, K, workspace_bytes, workspace_bytes > 0);
+  const Plan p = plan_gemm(op, M, N, K, workspace_bytes, workspace_bytes > 0);
   if (config) *config = p.cfg;
   if (splits) *splits = p.splits;
   return AAR_OK;
@@ -776,7 +788,7 @@ extern "C" int aar_gemm_f32_batched(int op, int64_t batch, int64_t M, int64_t N,
   if (lda < need_a || ldb < need_b) return AAR_EINVAL;
   if (M > INT32_MAX / 2 || N > INT32_MAX / 2 || batch > 65535) return AAR_EUNSUPPORTED;
   const bool vec = gemm_vec_ok(op, M, N, K, A, B, lda, ldb) && strideA % 4 == 0 && strideB % 4 == 0;
-  const Plan p = plan_gemm(M, N, K, 0, false, batch);
+  const Plan p = plan_gemm(op, M, N, K, 0, false, batch);
   return dispatch_op(op, p.cfg, vec, A, B, C, M, N, K, lda, ldb, ldc, 1, p.k_per_split, 0,
                      Batch{batch, strideA, strideB, strideC}, as_stream(stream));
 }
