@@ -99,7 +99,9 @@ class CrossEntropyLoss(Module):
 
 class Linear(Module):
     """y = x W^T (+ b) with W [out, in]; the forward is matmul_a_bt, so its
-    backward runs matmul (dX) and matmul_at_b (dW)."""
+    backward runs matmul (dX) and matmul_at_b (dW).  With a bias the product
+    and the bias addition are one GEMM (bias in the epilogue), bit-identical
+    to matmul_a_bt followed by add_bias (reference aargrad/nn.py:101-105)."""
 
     def __init__(self, in_features, out_features, *, bias=False, rng=None):
         super().__init__()
@@ -110,8 +112,9 @@ class Linear(Module):
         self.bias = Parameter(_core.from_numpy(np.zeros((out_features,), np.float32))) if bias else None
 
     def forward(self, x):
-        y = _core.matmul_a_bt(x, self.weight.tensor)
-        return _core.add_bias(y, self.bias.tensor) if self.bias is not None else y
+        if self.bias is not None:
+            return _core._linear(x, self.weight.tensor, self.bias.tensor)
+        return _core.matmul_a_bt(x, self.weight.tensor)
 
 
 class ReLU(Module):

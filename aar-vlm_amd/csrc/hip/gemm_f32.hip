@@ -55,6 +55,33 @@ __device__ __forceinline__ void map_tile(int tiles_m, int tiles_n, int& tm, int&
   tn = in_group / rows;
 }
 
+// Epilogue: a wave's (32*TM) x (32*TN) accumulators to C, plus bias[col]
+// with BIAS (the fused epilogue of a linear layer: the same single fp32
+// addition as adding the bias to the stored product).  BIAS is a template
+// flag because the addition needs the accumulators in VGPRs: the kernels
+// without it store straight from the accumulators and keep their occupancy.
+// Accumulator layout of a 32x32 block: lane (lr, h), register r holds row
+// 8*(r/4) + 4*h + (r%4), column lr.
+template <int TM, int TN, bool BIAS>
+__device__ __forceinline__ void store_tile(const f32x16 (&acc)[TM][TN], float* __restrict__ C,
+                                           const float* __restrict__ bias, int64_t M, int64_t N, int64_t ldc,
+                                           int64_t r0, int64_t c0, int lr, int h) {
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int64_t col = c0 + 32 * j + lr;
+      float b = 0.f;
+      if constexpr (BIAS) b = col < N ? bias[col] : 0.f;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t row = r0 + 32 * i + 8 * (r / 4) + 4 * h + (r % 4);
+        if (row < M && col < N) C[row * ldc + col] = BIAS ? acc[i][j][r] + b : acc[i][j][r];
+      }
+    }
+  }
+}
+
 // ------------------------------------------------------- register path
 // Operands that are not 16-byte aligned or whose contiguous extent is not a
 // multiple of 4: predicated element loads into registers, stored to a padded,
@@ -138,12 +165,12 @@ struct TileLoader {
 
 // WPE: waves per SIMD the register allocation must allow (resident
 // workgroups per CU x waves per workgroup / 4).
-template <int BM, int BN, int BK, int WM, int WN, int WPE, bool A_KC, bool B_KC>
+template <int BM, int BN, int BK, int WM, int WN, int WPE, bool A_KC, bool B_KC, bool BIAS>
 __global__ void __launch_bounds__((BM / WM) * (BN / WN) * 64, WPE)
 gemm_f32_kernel(const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C,
                 int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc,
                 int64_t k_per_split, int64_t split_stride, int tiles_m, int tiles_n, int64_t sA, int64_t sB,
-                int64_t sC) {
+                int64_t sC, const float* __restrict__ bias) {
   constexpr int NWM = BM / WM;
   constexpr int NT = NWM * (BN / WN) * 64;
   constexpr int TM = WM / 32;
@@ -230,18 +257,7 @@ gemm_f32_kernel(const float* __restrict__ A, const float* __restrict__ B, float*
 
   // Accumulator layout of a 32x32 block: lane (lr, h), register r holds
   // row 8*(r/4) + 4*h + (r%4), column lr.
-#pragma unroll
-  for (int i = 0; i < TM; ++i) {
-#pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      const int64_t col = n0 + wn0 + 32 * j + lr;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int64_t row = m0 + wm0 + 32 * i + 8 * (r / 4) + 4 * h + (r % 4);
-        if (row < M && col < N) C[row * ldc + col] = acc[i][j][r];
-      }
-    }
-  }
+  store_tile<TM, TN, BIAS>(acc, C, bias, M, N, ldc, m0 + wm0, n0 + wn0, lr, h);
 }
 
 // ------------------------------------------------------------------ DMA path
@@ -375,12 +391,12 @@ __device__ __forceinline__ void ring_barrier() {
   asm volatile("" ::: "memory");
 }
 
-template <int BM, int BN, int BK, int WM, int WN, int WPE, int S, bool A_KC, bool B_KC>
+template <int BM, int BN, int BK, int WM, int WN, int WPE, int S, bool A_KC, bool B_KC, bool BIAS>
 __global__ void __launch_bounds__((BM / WM) * (BN / WN) * 64, WPE)
 gemm_f32_dma_kernel(const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C,
                     int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc,
                     int64_t k_per_split, int64_t split_stride, int tiles_m, int tiles_n, int64_t sA,
-                    int64_t sB, int64_t sC) {
+                    int64_t sB, int64_t sC, const float* __restrict__ bias) {
   constexpr int NWM = BM / WM;
   constexpr int NW = NWM * (BN / WN);
   constexpr int TM = WM / 32;
@@ -483,42 +499,35 @@ gemm_f32_dma_kernel(const float* __restrict__ A, const float* __restrict__ B, fl
     }
   }
 
-#pragma unroll
-  for (int i = 0; i < TM; ++i) {
-#pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      const int64_t col = n0 + wn0 + 32 * j + lr;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int64_t row = m0 + wm0 + 32 * i + 8 * (r / 4) + 4 * h + (r % 4);
-        if (row < M && col < N) C[row * ldc + col] = acc[i][j][r];
-      }
-    }
-  }
+  store_tile<TM, TN, BIAS>(acc, C, bias, M, N, ldc, m0 + wm0, n0 + wn0, lr, h);
 }
 
 // C[i] = sum_s W[s*stride + i], s in order 0..splits-1 (deterministic), four
 // consecutive outputs per thread with 128-bit loads (stride % 4 == 0 and
 // 16-byte aligned W/C); the split loop is unrolled so its loads overlap.
+// A bias (row-broadcast over the N columns; the vector kernel needs N % 4 == 0)
+// is added to the finished sum.
 __global__ void __launch_bounds__(256)
 splitk_reduce_vec_kernel(const f32x4* __restrict__ W, f32x4* __restrict__ C, int64_t n4, int64_t stride4,
-                         int splits) {
+                         int splits, const f32x4* __restrict__ bias, int64_t n_cols4) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n4) return;
   f32x4 s = W[i];
 #pragma unroll 8
   for (int p = 1; p < splits; ++p) s += W[p * stride4 + i];
+  if (bias) s += bias[i % n_cols4];
   C[i] = s;
 }
 
 __global__ void __launch_bounds__(256)
 splitk_reduce_kernel(const float* __restrict__ W, float* __restrict__ C, int64_t n, int64_t stride,
-                     int splits) {
+                     int splits, const float* __restrict__ bias, int64_t n_cols) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
   float s = W[i];
 #pragma unroll 8
   for (int p = 1; p < splits; ++p) s += W[p * stride + i];
+  if (bias) s += bias[i % n_cols];
   C[i] = s;
 }
 
@@ -606,31 +615,37 @@ constexpr Batch kSingle{1, 0, 0, 0};
 template <int BM, int BN, int BK, int WM, int WN, int RES, int STAGES, bool A_KC, bool B_KC>
 int launch_cfg(bool vec, const float* A, const float* B, float* C, int64_t M, int64_t N, int64_t K,
                int64_t lda, int64_t ldb, int64_t ldc, int splits, int64_t kps, int64_t split_stride,
-               const Batch& bt, hipStream_t st) {
+               const Batch& bt, const float* bias, hipStream_t st) {
   constexpr int kWaves = (BM / WM) * (BN / WN);
   constexpr int kWpe = (RES * kWaves + 3) / 4;
   const int tiles_m = (int)ceil_div(M, (int64_t)BM);
   const int tiles_n = (int)ceil_div(N, (int64_t)BN);
   dim3 grid((unsigned)(tiles_m * tiles_n), (unsigned)splits, (unsigned)bt.count);
   dim3 block(kWaves * 64);
-  if (vec)
-    gemm_f32_dma_kernel<BM, BN, BK, WM, WN, kWpe, STAGES, A_KC, B_KC><<<grid, block, 0, st>>>(
-        A, B, C, M, N, K, lda, ldb, ldc, kps, split_stride, tiles_m, tiles_n, bt.sA, bt.sB, bt.sC);
+  if (vec && bias)
+    gemm_f32_dma_kernel<BM, BN, BK, WM, WN, kWpe, STAGES, A_KC, B_KC, true><<<grid, block, 0, st>>>(
+        A, B, C, M, N, K, lda, ldb, ldc, kps, split_stride, tiles_m, tiles_n, bt.sA, bt.sB, bt.sC, bias);
+  else if (vec)
+    gemm_f32_dma_kernel<BM, BN, BK, WM, WN, kWpe, STAGES, A_KC, B_KC, false><<<grid, block, 0, st>>>(
+        A, B, C, M, N, K, lda, ldb, ldc, kps, split_stride, tiles_m, tiles_n, bt.sA, bt.sB, bt.sC, nullptr);
+  else if (bias)
+    gemm_f32_kernel<BM, BN, BK, WM, WN, kWpe, A_KC, B_KC, true><<<grid, block, 0, st>>>(
+        A, B, C, M, N, K, lda, ldb, ldc, kps, split_stride, tiles_m, tiles_n, bt.sA, bt.sB, bt.sC, bias);
   else
-    gemm_f32_kernel<BM, BN, BK, WM, WN, kWpe, A_KC, B_KC><<<grid, block, 0, st>>>(
-        A, B, C, M, N, K, lda, ldb, ldc, kps, split_stride, tiles_m, tiles_n, bt.sA, bt.sB, bt.sC);
+    gemm_f32_kernel<BM, BN, BK, WM, WN, kWpe, A_KC, B_KC, false><<<grid, block, 0, st>>>(
+        A, B, C, M, N, K, lda, ldb, ldc, kps, split_stride, tiles_m, tiles_n, bt.sA, bt.sB, bt.sC, nullptr);
   return launch_status();
 }
 
 template <bool A_KC, bool B_KC>
 int launch_op(int cfg, bool vec, const float* A, const float* B, float* C, int64_t M, int64_t N,
               int64_t K, int64_t lda, int64_t ldb, int64_t ldc, int splits, int64_t kps,
-              int64_t split_stride, const Batch& bt, hipStream_t st) {
+              int64_t split_stride, const Batch& bt, const float* bias, hipStream_t st) {
 #define AAR_GEMM_CFG(I)                                                                                   \
   case I:                                                                                                 \
     return launch_cfg<kCfgs[I].bm, kCfgs[I].bn, kCfgs[I].bk, kCfgs[I].wm, kCfgs[I].wn, kCfgs[I].resident, \
                       kCfgs[I].stages, A_KC, B_KC>(vec, A, B, C, M, N, K, lda, ldb, ldc, splits, kps, split_stride, \
-                                                   bt, st);
+                                                   bt, bias, st);
   switch (cfg) {
     AAR_GEMM_CFG(0)
     AAR_GEMM_CFG(1)
@@ -674,35 +689,40 @@ int default_ld(int op, int64_t M, int64_t N, int64_t K, int64_t& lda, int64_t& l
 
 int dispatch_op(int op, int cfg, bool vec, const float* A, const float* B, float* C, int64_t M, int64_t N,
                 int64_t K, int64_t lda, int64_t ldb, int64_t ldc, int splits, int64_t kps, int64_t split_stride,
-                const Batch& bt, hipStream_t st) {
+                const Batch& bt, hipStream_t st, const float* bias = nullptr) {
   switch (op) {
     case AAR_GEMM_NN:
-      return launch_op<true, false>(cfg, vec, A, B, C, M, N, K, lda, ldb, ldc, splits, kps, split_stride, bt, st);
+      return launch_op<true, false>(cfg, vec, A, B, C, M, N, K, lda, ldb, ldc, splits, kps, split_stride, bt, bias,
+                                    st);
     case AAR_GEMM_NT:
-      return launch_op<true, true>(cfg, vec, A, B, C, M, N, K, lda, ldb, ldc, splits, kps, split_stride, bt, st);
+      return launch_op<true, true>(cfg, vec, A, B, C, M, N, K, lda, ldb, ldc, splits, kps, split_stride, bt, bias,
+                                   st);
     default:
       return launch_op<false, false>(cfg, vec, A, B, C, M, N, K, lda, ldb, ldc, splits, kps, split_stride, bt,
-                                     st);
+                                     bias, st);
   }
 }
 
+// bias (may be null): added to every row of C, in the epilogue of an
+// unsplit launch or after the split-K reduction.
 int run_gemm(int op, int64_t M, int64_t N, int64_t K, const float* A, const float* B, float* C,
-             void* workspace, const Plan& p, hipStream_t st) {
+             void* workspace, const Plan& p, hipStream_t st, const float* bias = nullptr) {
   int64_t lda, ldb;
   default_ld(op, M, N, K, lda, ldb);
   const bool vec = gemm_vec_ok(op, M, N, K, A, B, lda, ldb);
   float* out = p.splits > 1 ? static_cast<float*>(workspace) : C;
   const int64_t split_stride = p.splits > 1 ? M * N : 0;
   int rc = dispatch_op(op, p.cfg, vec, A, B, out, M, N, K, lda, ldb, N, p.splits, p.k_per_split, split_stride,
-                       kSingle, st);
+                       kSingle, st, p.splits > 1 ? nullptr : bias);
   if (rc != AAR_OK || p.splits <= 1) return rc;
   const int64_t n = M * N;
-  if (n % 4 == 0 && aligned16(out) && aligned16(C)) {
+  if (n % 4 == 0 && aligned16(out) && aligned16(C) && (!bias || (N % 4 == 0 && aligned16(bias)))) {
     splitk_reduce_vec_kernel<<<dim3((unsigned)ceil_div(n / 4, (int64_t)256)), dim3(256), 0, st>>>(
-        reinterpret_cast<const f32x4*>(out), reinterpret_cast<f32x4*>(C), n / 4, split_stride / 4, p.splits);
+        reinterpret_cast<const f32x4*>(out), reinterpret_cast<f32x4*>(C), n / 4, split_stride / 4, p.splits,
+        reinterpret_cast<const f32x4*>(bias), N / 4);
   } else {
     splitk_reduce_kernel<<<dim3((unsigned)ceil_div(n, (int64_t)256)), dim3(256), 0, st>>>(out, C, n, split_stride,
-                                                                                         p.splits);
+                                                                                         p.splits, bias, N);
   }
   return launch_status();
 }
@@ -741,6 +761,19 @@ extern "C" int aar_gemm_f32(int op, int64_t M, int64_t N, int64_t K, const float
   if (chk != AAR_OK) return chk == 1 ? AAR_OK : chk;
   const Plan p = plan_gemm(op, M, N, K, workspace ? workspace_bytes : 0, workspace != nullptr);
   return run_gemm(op, M, N, K, A, B, C, workspace, p, as_stream(stream));
+}
+
+extern "C" int aar_gemm_f32_bias(int op, int64_t M, int64_t N, int64_t K, const float* A, const float* B,
+                                 const float* bias, float* C, void* workspace, size_t workspace_bytes,
+                                 void* stream) {
+  if (op < 0 || op > 2 || M < 0 || N < 0 || K < 0) return AAR_EINVAL;
+  if (M == 0 || N == 0) return AAR_OK;
+  if (!bias) return AAR_EINVAL;
+  if (K == 0) return AAR_EUNSUPPORTED;  // C = bias rows: not a product, left to the caller
+  const int chk = check_gemm_args(op, M, N, K, A, B, C, stream);
+  if (chk != AAR_OK) return chk;
+  const Plan p = plan_gemm(op, M, N, K, workspace ? workspace_bytes : 0, workspace != nullptr);
+  return run_gemm(op, M, N, K, A, B, C, workspace, p, as_stream(stream), bias);
 }
 
 extern "C" int aar_gemm_f32_tile_config(int config, int* tile_m, int* tile_n, int* tile_k) {

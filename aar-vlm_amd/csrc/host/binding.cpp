@@ -165,6 +165,9 @@ PYBIND11_MODULE(_core, m) {
         gil_release(),
         "Attention over a packed projection [..., T, 3*D] -> [..., T, D]: the MultiHeadAttention "
         "composition (per-head views of q, k, v, flash attention, heads merged back) in one op.");
+  m.def("_linear", &linear, py::arg("x"), py::arg("weight"), py::arg("bias"), gil_release(),
+        "x W^T + b as one GEMM with the bias added in its epilogue: the values and gradients of "
+        "add_bias(matmul_a_bt(x, W), b).");
   m.def("_token_windows", &token_windows, py::arg("tokens"), py::arg("starts"), py::arg("seq_len"),
         gil_release(),
         "(x, y) int64 [len(starts), seq_len] with x[b] = tokens[s:s+T], y[b] = tokens[s+1:s+T+1], "

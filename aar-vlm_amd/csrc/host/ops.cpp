@@ -308,6 +308,45 @@ Tensor with_matmul_grad(const Tensor& ac, const Tensor& bc, NoGrad no_grad) {
   return out;
 }
 
+// Linear layer y = x W^T + b as one GEMM whose epilogue adds b (the reference
+// runs matmul_a_bt and then add_bias: aargrad/nn.py:101-105).  The epilogue
+// performs the same single fp32 addition per element as add_bias, so the
+// result is bit-identical to the two-op composition.  K > 0 here.
+Tensor linear_no_grad(const Tensor& x, const Tensor& w, const Tensor& b) {
+  if (x.device == Device::CPU) throw_cpu_compute("linear");
+  const int64_t K = x.shape.back();
+  const int64_t N = w.shape[0];
+  const int64_t M = static_cast<int64_t>(x.numel()) / K;
+  Tensor out = Tensor::empty({M, N}, DType::Fp32, Device::CUDA);
+  if (out.numel() != 0) {
+    Workspace ws(aar_gemm_f32_workspace_bytes(AAR_GEMM_NT, M, N, K));
+    check_status(aar_gemm_f32_bias(AAR_GEMM_NT, M, N, K, fp(x), fp(w), fp(b), fp(out), ws.data(), ws.bytes(),
+                                   current_stream()),
+                 "linear");
+  }
+  if (x.shape.size() == 2) return out;
+  std::vector<int64_t> out_shape(x.shape.begin(), x.shape.end() - 1);
+  out_shape.push_back(N);
+  return as_view(out, std::move(out_shape));
+}
+
+// dx = g W, dW = g^T x (MatmulABTFunction) and db = column sums of g
+// (AddBiasFunction), the same kernels as the two-op composition.
+class LinearFunction : public Function {
+ public:
+  Tensor saved_x, saved_w;
+  std::vector<Tensor> backward(const Tensor& g) override {
+    Tensor gc = as_contig(g);
+    const int64_t N = saved_w.shape[0];
+    const int64_t rows = static_cast<int64_t>(gc.numel()) / N;
+    Tensor db = Tensor::empty({N}, DType::Fp32, Device::CUDA);
+    Workspace ws(aar_colsum_workspace_bytes(rows, N));
+    check_status(aar_colsum_f32(fp(gc), fp(db), rows, N, ws.data(), ws.bytes(), current_stream()), "linear backward");
+    return {matmul_no_grad(gc, saved_w), matmul_at_b_no_grad(gc, saved_x), db};
+  }
+  const char* name() const override { return "LinearFunction"; }
+};
+
 // -------------------------------------------------------------- softmax
 
 Tensor softmax_no_grad(const Tensor& x) {
@@ -701,6 +740,36 @@ Tensor matmul_a_bt(const Tensor& a, const Tensor& b) {
   if (a.dtype != DType::Fp32) throw std::invalid_argument("matmul_a_bt: only Fp32 supported");
   if (a.shape.back() != b.shape[1]) throw std::invalid_argument("matmul_a_bt: contraction dim mismatch");
   return with_matmul_grad<MatmulABTFunction>(as_contig(a), as_contig(b), matmul_a_bt_no_grad);
+}
+
+Tensor linear(const Tensor& x, const Tensor& w, const Tensor& b) {
+  // The checks (and messages) of matmul_a_bt followed by those of add_bias.
+  if (x.shape.size() < 2 || w.shape.size() != 2) {
+    throw std::invalid_argument("matmul_a_bt: LHS rank must be >= 2 and RHS must be 2D");
+  }
+  if (x.dtype != w.dtype || x.device != w.device) {
+    throw std::invalid_argument("matmul_a_bt: dtype/device mismatch");
+  }
+  if (x.dtype != DType::Fp32) throw std::invalid_argument("matmul_a_bt: only Fp32 supported");
+  if (x.shape.back() != w.shape[1]) throw std::invalid_argument("matmul_a_bt: contraction dim mismatch");
+  if (b.shape.size() != 1) throw std::invalid_argument("add_bias: bias must be 1-D");
+  if (w.shape[0] != b.shape[0]) throw std::invalid_argument("add_bias: bias size must match x's last dim");
+  if (b.dtype != DType::Fp32) throw std::invalid_argument("add_bias: only Fp32 supported");
+  if (x.device != b.device) throw std::invalid_argument("add_bias: device mismatch");
+  // An empty contraction is the bias broadcast, not a product: the two-op path.
+  if (x.shape.back() == 0) return add_bias(matmul_a_bt(x, w), b);
+  Tensor xc = as_contig(x), wc = as_contig(w), bc = as_contig(b);
+  if (!xc.requires_grad && !wc.requires_grad && !bc.requires_grad) return linear_no_grad(xc, wc, bc);
+  auto fn = std::make_shared<LinearFunction>();
+  fn->record_input(xc);
+  fn->record_input(wc);
+  fn->record_input(bc);
+  fn->saved_x = xc;
+  fn->saved_w = wc;
+  Tensor out = linear_no_grad(xc, wc, bc);
+  out.requires_grad = true;
+  out.grad_fn = fn;
+  return out;
 }
 
 Tensor matmul_at_b(const Tensor& a, const Tensor& b) {

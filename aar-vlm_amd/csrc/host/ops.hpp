@@ -20,6 +20,9 @@ Tensor unsqueeze(const Tensor& x, int64_t dim);
 Tensor matmul(const Tensor& a, const Tensor& b);
 Tensor matmul_a_bt(const Tensor& a, const Tensor& b);
 Tensor matmul_at_b(const Tensor& a, const Tensor& b);
+// nn.Linear with a bias (aargrad/nn.py:101-105: matmul_a_bt then add_bias)
+// as one GEMM with the bias added in its epilogue; same values and gradients.
+Tensor linear(const Tensor& x, const Tensor& w, const Tensor& b);
 
 // Row-wise (cppsrc/ops/softmax.cpp:75-96, cppsrc/ops/layernorm.cpp:174-227).
 Tensor softmax(const Tensor& x);

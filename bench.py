@@ -418,8 +418,9 @@ class GPT:
             a = ag._core._flash_attention_qkv(ag.matmul_a_bt(h, wqkv), H, True)
             x = ag.add(x, ag.matmul_a_bt(a, wout))
             h = ag.layernorm(x, l2w, l2b, 1e-5)
-            h = ag.relu(ag.add_bias(ag.matmul_a_bt(h, f1w), f1b))
-            x = ag.add(x, ag.add_bias(ag.matmul_a_bt(h, f2w), f2b))
+            # nn.Linear with bias: product and bias in one GEMM (bias in the epilogue)
+            h = ag.relu(ag._core._linear(h, f1w, f1b))
+            x = ag.add(x, ag._core._linear(h, f2w, f2b))
         x = ag.layernorm(x, p[-3], p[-2], 1e-5)
         return ag.matmul_a_bt(x, p[-1])
 

@@ -96,6 +96,15 @@ int aar_gemm_f32(int op, int64_t M, int64_t N, int64_t K,
                  const float* A, const float* B, float* C,
                  void* workspace, size_t workspace_bytes, void* stream);
 
+/* C[M,N] = op(A, B) + bias, bias[N] added to every row: the GEMM with the bias
+ * in its epilogue (or after the split-K reduction).  Bit-identical to
+ * aar_gemm_f32 followed by aar_add_bias_f32 (one fp32 addition per element).
+ * K == 0 returns AAR_EUNSUPPORTED.  Replaces the matmul_a_bt_cuda + add_bias_cuda
+ * pair of nn.Linear with bias (aargrad/nn.py:101-105, cppsrc/ops/matmul.cpp:11,
+ * elementwise.cpp:24). */
+int aar_gemm_f32_bias(int op, int64_t M, int64_t N, int64_t K, const float* A, const float* B,
+                      const float* bias, float* C, void* workspace, size_t workspace_bytes, void* stream);
+
 /* Tuning and test access to the GEMM tile configurations (no counterpart in
  * the reference, whose launchers pick a tile size internally,
  * cppsrc/ops/matmul.cu:792-832).  Configurations are numbered 0..n-1;

@@ -54,6 +54,11 @@ def test_abi_validates_before_touching_the_device():
     assert lib.aar_gemm_f32(7, 2, 2, 2, None, None, None, None, 0, None) == -1  # bad op
     assert lib.aar_gemm_f32(0, -1, 2, 2, None, None, None, None, 0, None) == -1
     assert lib.aar_gemm_f32(0, 0, 2, 2, None, None, None, None, 0, None) == 0  # empty is a no-op
+    lib.aar_gemm_f32_bias.argtypes = [ctypes.c_int, i64, i64, i64, vp, vp, vp, vp, vp, ctypes.c_size_t, vp]
+    assert lib.aar_gemm_f32_bias(3, 2, 2, 2, None, None, None, None, None, 0, None) == -1  # bad op
+    assert lib.aar_gemm_f32_bias(1, 2, 2, 2, None, None, None, None, None, 0, None) == -1  # no bias
+    assert lib.aar_gemm_f32_bias(1, 2, 0, 2, None, None, None, None, None, 0, None) == 0  # empty output
+    assert lib.aar_gemm_f32_bias(1, 2, 2, 0, None, None, 16, None, None, 0, None) == -3  # K = 0: not a product
     lib.aar_softmax_fwd_f32.argtypes = [vp, vp, i64, i64, vp]
     assert lib.aar_softmax_fwd_f32(None, None, 4, 0, None) == -1
     lib.aar_flash_fwd_f32.argtypes = [vp] * 5 + [i64, i64, i64, ctypes.c_int, ctypes.c_float, vp]
@@ -147,6 +152,13 @@ def test_validation_errors_match_reference(ag):
         ag.flash_attention(f(1, 2, 4, 8), f(1, 2, 4, 8), f(1, 2, 5, 8), True)
     with pytest.raises(ValueError, match="at least 3 dims"):
         ag.flash_attention(f(4, 8), f(4, 8), f(4, 8), True)
+    # the fused linear keeps the messages of matmul_a_bt and add_bias
+    with pytest.raises(ValueError, match="contraction dim mismatch"):
+        ag._core._linear(f(2, 3), f(4, 2), f(4))
+    with pytest.raises(ValueError, match="bias must be 1-D"):
+        ag._core._linear(f(2, 3), f(4, 3), f(1, 4))
+    with pytest.raises(ValueError, match="bias size must match"):
+        ag._core._linear(f(2, 3), f(4, 3), f(5))
 
 
 def test_host_compute_fails_loudly(ag):
@@ -156,7 +168,8 @@ def test_host_compute_fails_loudly(ag):
                  lambda: ag.layernorm(f(2, 3), f(3), f(3)),
                  lambda: ag.flash_attention(f(1, 4, 8), f(1, 4, 8), f(1, 4, 8), True),
                  lambda: ag.add(f(3), f(3)),
-                 lambda: ag.sum_all(f(3))):
+                 lambda: ag.sum_all(f(3)),
+                 lambda: ag._core._linear(f(2, 3), f(4, 3), f(4))):
         with pytest.raises(RuntimeError, match="GPU only"):
             call()
 
