@@ -10,7 +10,9 @@ A, B ~ N(0,1)/sqrt(K), synthetic, resident in HBM), issued through the product
 path: aargrad.matmul -> aargrad._core -> aar_gemm_f32 (C ABI) -> the gfx950
 MFMA kernel, all ordered on the null stream.  W untimed steps, then exactly K
 timed steps bracketed by device synchronisation; HIP events recorded on that
-same stream time the region.  One GPU only: --gpus N > 1 exits with a message.
+same stream time the region, one per step boundary, so the median and p99
+step times are reported beside the mean.  One GPU only: --gpus N > 1 exits
+with a message.
 
 Prints ONE JSON line on stdout; a human-readable summary goes to stderr.
 """
@@ -65,6 +67,41 @@ class Events:
         return float(ms.value)
 
 
+class StepTimer:
+    """One HIP event per step boundary on the null stream, for per-step
+    times (median and p99, the reference bench's protocol) beside the
+    whole-run mean.  Recording an event enqueues a marker only: no sync."""
+
+    def __init__(self, ev: Events, steps: int):
+        self.L = ev.L
+        self.evs = []
+        for _ in range(steps + 1):
+            e = ctypes.c_void_p()
+            assert self.L.aar_event_create(ctypes.byref(e)) == 0
+            self.evs.append(e)
+        self.i = 0
+
+    def mark(self):
+        self.L.aar_event_record(self.evs[self.i], None)
+        self.i += 1
+
+    def _ms(self, a, b):
+        ms = ctypes.c_float()
+        assert self.L.aar_event_elapsed_ms(ctypes.byref(ms), a, b) == 0
+        return float(ms.value)
+
+    def result(self):
+        """(total ms, {median, p99} per step in ms); call after a synchronize."""
+        assert self.i == len(self.evs), "one mark per step boundary"
+        per = np.array([self._ms(self.evs[k], self.evs[k + 1]) for k in range(len(self.evs) - 1)])
+        total = self._ms(self.evs[0], self.evs[-1])
+        for e in self.evs:
+            self.L.aar_event_destroy(e)
+        self.evs = []
+        return total, {"median_ms": round(float(np.median(per)), 5),
+                       "p99_ms": round(float(np.percentile(per, 99)), 5)}
+
+
 def cpu_model() -> str:
     try:
         for line in open("/proc/cpuinfo"):
@@ -98,13 +135,15 @@ def bench_matmul(ag, steps: int, warmup: int, ev: Events):
     for _ in range(warmup):
         ag.matmul(ta, tb)
     ag.cuda_synchronize()
+    st = StepTimer(ev, steps)
     t0 = time.perf_counter()
-    ev.start()
+    st.mark()
     for _ in range(steps):
         c = ag.matmul(ta, tb)
-    ms = ev.stop_ms()
+        st.mark()
     ag.cuda_synchronize()
     wall = time.perf_counter() - t0
+    ms, dist = st.result()
     # spot-check the timed output (rows sampled, float64 closed form)
     ch = ag.to_numpy(c.to(ag.Device.CPU))
     rows = rng.choice(n, 8, replace=False)
@@ -112,7 +151,7 @@ def bench_matmul(ag, steps: int, warmup: int, ev: Events):
     err = float(np.abs(ch[rows] - ref).max() / max(np.abs(ref).max(), 1.0))
     if not err <= 1e-4 * np.sqrt(n):
         raise SystemExit(f"bench: matmul result check failed (err {err:.3e})")
-    return ms / steps, wall, err, (a, b)
+    return ms / steps, wall, err, (a, b), dist
 
 
 def bench_flash(ag, steps: int, warmup: int, ev: Events, T: int = 4096):
@@ -134,13 +173,15 @@ def bench_flash(ag, steps: int, warmup: int, ev: Events, T: int = 4096):
     for _ in range(warmup):
         step()
     ag.cuda_synchronize()
-    ev.start()
+    st = StepTimer(ev, steps)
+    st.mark()
     for _ in range(steps):
         step()
-    ms = ev.stop_ms() / steps
+        st.mark()
     ag.cuda_synchronize()
+    ms, dist = st.result()
     fwd_flops = 4.0 * B * H * T * T * d / 2.0
-    return ms, 3.5 * fwd_flops
+    return ms / steps, 3.5 * fwd_flops, dist
 
 
 class Abi:
@@ -445,7 +486,7 @@ def gpt_flops_per_step(cfg, batch):
     return gemm + attn
 
 
-def bench_gpt(ag, ev: Events, steps: int = 10, warmup: int = 3, cfg=GPT5):
+def bench_gpt(ag, ev: Events, steps: int = 50, warmup: int = 10, cfg=GPT5):
     B, T = cfg["batch"], cfg["ctx"]
     params = gpt_init_params(cfg)
     model = GPT(ag, cfg, params)
@@ -456,14 +497,18 @@ def bench_gpt(ag, ev: Events, steps: int = 10, warmup: int = 3, cfg=GPT5):
     for _ in range(warmup):
         model.step(ids, pos, tgt, 1e-3)
     ag.cuda_synchronize()
-    ev.start()
+    st = StepTimer(ev, steps)
+    st.mark()
     for _ in range(steps):
         loss = model.step(ids, pos, tgt, 1e-3)
-    ms = ev.stop_ms() / steps
+        st.mark()
     ag.cuda_synchronize()
+    ms, dist = st.result()
+    ms /= steps
     last = float(ag.to_numpy(loss.to(ag.Device.CPU)))
     tokens = B * T
-    return {"tokens_per_s": round(tokens / (ms * 1e-3), 1), "ms_per_step": round(ms, 3),
+    return {"tokens_per_s": round(tokens / (ms * 1e-3), 1), "ms_per_step": round(ms, 3), "steps": steps,
+            "step_ms_median": dist["median_ms"], "step_ms_p99": dist["p99_ms"],
             "implied_tflops": round(gpt_flops_per_step(cfg, B) / (ms * 1e-3) / 1e12, 2),
             "loss_after_steps": round(last, 5), "batch": B, "ctx": T,
             "config": "6 layers, d_model 384, 6 heads, ctx 256, batch 64, vocab 65, ReLU MLP, SGD lr 1e-3"}
@@ -528,7 +573,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=60)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--flash-steps", type=int, default=6)
+    ap.add_argument("--flash-steps", type=int, default=50)
     ap.add_argument("--only", choices=["all", "gemm", "flash", "rowwise", "extra", "copy", "gpt", "sweep"], default="all",
                     help="run one part (profiling runs); the JSON line is printed for 'all'")
     args = ap.parse_args()
@@ -562,18 +607,18 @@ def main() -> int:
         log(json.dumps(bench_gpt(ag, ev)))
         return 0
     if args.only == "flash":
-        fa_ms, fa_flops = bench_flash(ag, args.flash_steps, 3, ev)
-        log(f"flash fwd+bwd {fa_ms:.3f} ms {fa_flops / (fa_ms * 1e-3) / 1e12:.2f} TFLOPS")
+        fa_ms, fa_flops, fa_dist = bench_flash(ag, args.flash_steps, 10, ev)
+        log(f"flash fwd+bwd {fa_ms:.3f} ms {fa_flops / (fa_ms * 1e-3) / 1e12:.2f} TFLOPS {fa_dist}")
         return 0
 
-    step_ms, wall, err, ab = bench_matmul(ag, args.steps, args.warmup, ev)
+    step_ms, wall, err, ab, mm_dist = bench_matmul(ag, args.steps, args.warmup, ev)
     tflops = flops / (step_ms * 1e-3) / 1e12
     log(f"matmul 4096^3: {step_ms:.4f} ms/step, {tflops:.2f} TFLOPS "
         f"({100 * tflops / PEAK_FP32_MFMA_TFLOPS:.1f}% of fp32 MFMA peak), check err {err:.2e}")
     if args.only == "gemm":
         return 0
 
-    fa_ms, fa_flops = bench_flash(ag, args.flash_steps, 3, ev)
+    fa_ms, fa_flops, fa_dist = bench_flash(ag, args.flash_steps, 10, ev)
     fa_tflops = fa_flops / (fa_ms * 1e-3) / 1e12
     log(f"flash causal B8 H12 T4096 d64 fwd+bwd: {fa_ms:.3f} ms, {fa_tflops:.2f} TFLOPS "
         f"({100 * fa_tflops / PEAK_FP32_MFMA_TFLOPS:.1f}%)")
@@ -607,6 +652,8 @@ def main() -> int:
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(step_ms, 5),
+        "ms_per_step_median": mm_dist["median_ms"],
+        "ms_per_step_p99": mm_dist["p99_ms"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": round(tflops / REF_PUBLISHED_TFLOPS, 3),
@@ -626,6 +673,9 @@ def main() -> int:
             "tflops": round(fa_tflops, 3),
             "pct_of_fp32_mfma_peak": round(100 * fa_tflops / PEAK_FP32_MFMA_TFLOPS, 2),
             "ms_per_step": round(fa_ms, 4),
+            "steps": args.flash_steps,
+            "ms_per_step_median": fa_dist["median_ms"],
+            "ms_per_step_p99": fa_dist["p99_ms"],
             "config": "causal, B8 H12 T4096 d64, fwd+bwd, flops = 3.5 * 4*B*H*T^2*d/2",
         },
         "rowwise_hbm": rowwise,
