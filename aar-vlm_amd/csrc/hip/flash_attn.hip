@@ -830,7 +830,7 @@ FaOut fa_out(float* p, const int64_t* s) { return FaOut{p, s[0], s[1], s[2]}; }
 
 bool fa_shape_ok(int64_t bh, int64_t T, int64_t d) {
   return bh > 0 && T > 0 && d > 0 && d <= 128 && T <= (1 << 24) && bh <= (1 << 24) &&
-         bh * ((T + kBlock - 1) / kBlock) < (int64_t)INT32_MAX;
+         bh * ((T + kBlock - 1) / kBlock) * kFaThreads <= (int64_t)UINT32_MAX;  // 32-bit grid work-items
 }
 
 }  // namespace

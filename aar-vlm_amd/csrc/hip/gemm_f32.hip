@@ -620,6 +620,8 @@ int launch_cfg(bool vec, const float* A, const float* B, float* C, int64_t M, in
   constexpr int kWpe = (RES * kWaves + 3) / 4;
   const int tiles_m = (int)ceil_div(M, (int64_t)BM);
   const int tiles_n = (int)ceil_div(N, (int64_t)BN);
+  // A dispatch holds each grid extent as a 32-bit work-item count.
+  if ((int64_t)tiles_m * tiles_n * kWaves * 64 > (int64_t)UINT32_MAX) return AAR_EUNSUPPORTED;
   dim3 grid((unsigned)(tiles_m * tiles_n), (unsigned)splits, (unsigned)bt.count);
   dim3 block(kWaves * 64);
   if (vec && bias)
@@ -819,9 +821,18 @@ extern "C" int aar_gemm_f32_batched(int op, int64_t batch, int64_t M, int64_t N,
   if (!A || !B) return AAR_EINVAL;
   const int64_t need_a = op == AAR_GEMM_TN ? M : K, need_b = op == AAR_GEMM_NT ? K : N;
   if (lda < need_a || ldb < need_b) return AAR_EINVAL;
-  if (M > INT32_MAX / 2 || N > INT32_MAX / 2 || batch > 65535) return AAR_EUNSUPPORTED;
+  if (M > INT32_MAX / 2 || N > INT32_MAX / 2) return AAR_EUNSUPPORTED;
   const bool vec = gemm_vec_ok(op, M, N, K, A, B, lda, ldb) && strideA % 4 == 0 && strideB % 4 == 0;
   const Plan p = plan_gemm(op, M, N, K, 0, false, batch);
-  return dispatch_op(op, p.cfg, vec, A, B, C, M, N, K, lda, ldb, ldc, 1, p.k_per_split, 0,
-                     Batch{batch, strideA, strideB, strideC}, as_stream(stream));
+  // Batches ride blockIdx.z (at most 65535 per launch): larger counts go in
+  // consecutive launches (offsets keep the 16-byte alignment, strides % 4 == 0).
+  constexpr int64_t kMaxGridZ = 65535;
+  for (int64_t b0 = 0; b0 < batch; b0 += kMaxGridZ) {
+    const int64_t nb = std::min(kMaxGridZ, batch - b0);
+    const int rc = dispatch_op(op, p.cfg, vec, A + b0 * strideA, B + b0 * strideB, C + b0 * strideC, M, N, K, lda,
+                               ldb, ldc, 1, p.k_per_split, 0, Batch{nb, strideA, strideB, strideC},
+                               as_stream(stream));
+    if (rc != AAR_OK) return rc;
+  }
+  return AAR_OK;
 }

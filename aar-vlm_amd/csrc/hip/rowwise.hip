@@ -134,6 +134,10 @@ __device__ __forceinline__ int64_t group_row0(int64_t it, int per_iter, int grp,
   return ((it * gridDim.x + blockIdx.x) * per_iter + grp) * U;
 }
 
+// Rows wider than the register plans take one workgroup each; a dispatch
+// holds each grid extent as a 32-bit work-item count.
+inline bool wide_grid_ok(int64_t rows) { return rows * kThreads <= (int64_t)UINT32_MAX; }
+
 // LDS cells used by group_reduce: 2 parities x U rows (at most 8) x 2
 // reductions x 4 waves.  (W == 1 row groups reduce within the wave and use
 // no cells.)
@@ -717,6 +721,7 @@ extern "C" int aar_softmax_fwd_f32(const float* x, float* y, int64_t rows, int64
   hipStream_t st = as_stream(stream);
   const RowPlan p = plan_rows(cols, cols % 4 == 0 && aligned16(x) && aligned16(y));
   if (p.nv == 0) {
+    if (!wide_grid_ok(rows)) return AAR_EUNSUPPORTED;
     softmax_fwd_wide_kernel<<<dim3((unsigned)rows), dim3(kThreads), 0, st>>>(x, y, cols);
     return launch_status();
   }
@@ -735,6 +740,7 @@ extern "C" int aar_softmax_bwd_f32(const float* g, const float* y, float* dx, in
   hipStream_t st = as_stream(stream);
   const RowPlan p = plan_rows(cols, cols % 4 == 0 && aligned16(g) && aligned16(y) && aligned16(dx));
   if (p.nv == 0) {
+    if (!wide_grid_ok(rows)) return AAR_EUNSUPPORTED;
     softmax_bwd_wide_kernel<<<dim3((unsigned)rows), dim3(kThreads), 0, st>>>(g, y, dx, cols);
     return launch_status();
   }
@@ -757,6 +763,7 @@ extern "C" int aar_layernorm_fwd_f32(const float* x, const float* w, const float
   const bool vec = cols % 4 == 0 && aligned16(x) && aligned16(y) && aligned16(w) && aligned16(b);
   const RowPlan p = plan_rows(cols, vec);
   if (p.nv == 0) {
+    if (!wide_grid_ok(rows)) return AAR_EUNSUPPORTED;
     layernorm_fwd_wide_kernel<<<dim3((unsigned)rows), dim3(kThreads), 0, st>>>(
         x, w, b, y, stats ? mean : nullptr, stats ? rstd : nullptr, cols, eps);
     return launch_status();
@@ -807,6 +814,7 @@ extern "C" int aar_layernorm_bwd_f32(const float* gy, const float* x, const floa
   float* part = static_cast<float*>(workspace);
   int rc;
   if (p.nv == 0) {
+    if (!wide_grid_ok(rows)) return AAR_EUNSUPPORTED;
     layernorm_bwd_wide_kernel<<<dim3((unsigned)rows), dim3(kThreads), 0, st>>>(gy, x, w, mean, rstd,
                                                                                 dx, cols);
     rc = launch_status();

@@ -222,6 +222,27 @@ def test_bmm_strided_operands(gpu):
     assert_close(got, want, gemm_tol(24), "rank-4 batch views")
 
 
+@pytest.mark.parametrize("op", O.BMM_OPS)
+def test_bmm_more_batches_than_one_launch(gpu, op):
+    # 70001 batches: a launch carries at most 65535 on blockIdx.z, so the
+    # second launch's operand offsets are exercised (forward and both grads)
+    rng = np.random.default_rng(70001)
+    a, b = _bmm_case(op, (70001,), 3, 5, 4, rng)
+    ta, tb = dev(gpu, a, True), dev(gpu, b, True)
+    c = getattr(gpu, op)(ta, tb)
+    assert_close(host(gpu, c), _bmm_oracle(op, a, b), gemm_tol(4), f"{op} fwd")
+    g = rng.standard_normal((70001, 3, 5)).astype(f32)
+    c.backward(dev(gpu, g))
+    if op == "bmm":
+        da, db = _bmm_oracle("bmm_a_bt", g, b), _bmm_oracle("bmm_at_b", a, g)
+    elif op == "bmm_a_bt":
+        da, db = _bmm_oracle("bmm", g, b), _bmm_oracle("bmm_at_b", g, a)
+    else:
+        da, db = _bmm_oracle("bmm_a_bt", b, g), _bmm_oracle("bmm", a, g)
+    assert_close(host(gpu, ta.grad), da, gemm_tol(5), f"{op} dA")
+    assert_close(host(gpu, tb.grad), db, gemm_tol(3), f"{op} dB")
+
+
 def test_bmm_errors(gpu):
     z = lambda *s: dev(gpu, np.zeros(s, f32))  # noqa: E731
     with pytest.raises(ValueError):
