@@ -1,7 +1,9 @@
 """Optimizers over aargrad._core, API-compatible with the reference's
 aargrad/optim.py (AARONKANG04/aar-vlm, aargrad/optim.py:4-54).  Both update
-parameters in place on the device: SGD with one scaled_add per parameter,
-AdamW with the fused adamw_step kernel."""
+parameters in place on the device.  The reference calls scaled_add_inplace /
+adamw_step once per parameter; here one multi-tensor call covers them all (up
+to 48 parameters per kernel launch), with the same per-element arithmetic,
+so the updates are bit-identical."""
 from __future__ import annotations
 
 from . import _core
@@ -17,10 +19,14 @@ class SGD:
             p.tensor.zero_grad()
 
     def step(self):
+        dsts, srcs = [], []
         for p in self.params:
             g = p.tensor.grad
             if g is not None:
-                _core.scaled_add_inplace(p.tensor, g, -self.lr)
+                dsts.append(p.tensor)
+                srcs.append(g)
+        if dsts:
+            _core._scaled_add_inplace_multi(dsts, srcs, -self.lr)
 
 
 class AdamW:
@@ -41,6 +47,7 @@ class AdamW:
         self.t += 1
         bc1 = 1.0 - self.beta1 ** self.t
         bc2 = 1.0 - self.beta2 ** self.t
+        ps, gs, ms, vs = [], [], [], []
         for p in self.params:
             g = p.tensor.grad
             if g is None:
@@ -50,6 +57,10 @@ class AdamW:
                 t = p.tensor
                 state = (_core.Tensor.zeros(t.shape, t.dtype, t.device), _core.Tensor.zeros(t.shape, t.dtype, t.device))
                 self._state[id(p)] = state
-            m, v = state
-            _core.adamw_step(p.tensor, g, m, v, self.lr, self.beta1, self.beta2, self.eps, self.weight_decay,
-                             bc1, bc2)
+            ps.append(p.tensor)
+            gs.append(g)
+            ms.append(state[0])
+            vs.append(state[1])
+        if ps:
+            _core._adamw_step_multi(ps, gs, ms, vs, self.lr, self.beta1, self.beta2, self.eps, self.weight_decay,
+                                    bc1, bc2)

@@ -159,15 +159,35 @@ colsum_stage1_kernel(const float* __restrict__ g, float* __restrict__ part, int6
   part[(int64_t)blockIdx.y * cols + c] = s;
 }
 
-// Stage 2: out[c] = sum_p part[p][c] in order.
-__global__ void __launch_bounds__(256)
+// Stage 2: out[c] = sum over p of part[p][c].  A workgroup owns kCsCols
+// columns and kCsSlices slices of the parts: slice j sums its contiguous run
+// of parts in order, then a fixed pairwise tree over the slices in LDS
+// finishes each column.  Deterministic; one thread per column and part run
+// instead of one per column keeps the few-column case off the latency floor.
+constexpr int kCsCols = 16;
+constexpr int kCsThreads = 1024;
+constexpr int kCsSlices = kCsThreads / kCsCols;
+
+__global__ void __launch_bounds__(kCsThreads)
 colsum_stage2_kernel(const float* __restrict__ part, float* __restrict__ out, int nparts, int64_t cols) {
-  const int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (c >= cols) return;
+  __shared__ float acc[kCsSlices][kCsCols];
+  const int cl = threadIdx.x % kCsCols, slice = threadIdx.x / kCsCols;
+  const int64_t c = (int64_t)blockIdx.x * kCsCols + cl;
+  const int per = (nparts + kCsSlices - 1) / kCsSlices;
+  const int p0 = slice * per;
+  const int p1 = min(nparts, p0 + per);
   float s = 0.f;
-#pragma unroll 8
-  for (int p = 0; p < nparts; ++p) s += part[(int64_t)p * cols + c];
-  out[c] = s;
+  if (c < cols) {
+    for (int p = p0; p < p1; ++p) s += part[(int64_t)p * cols + c];
+  }
+  acc[slice][cl] = s;
+  __syncthreads();
+#pragma unroll
+  for (int h = kCsSlices / 2; h >= 1; h /= 2) {
+    if (slice < h) acc[slice][cl] += acc[slice + h][cl];
+    __syncthreads();
+  }
+  if (slice == 0 && c < cols) out[c] = acc[0][cl];
 }
 
 int colsum_parts(int64_t rows) {
@@ -355,21 +375,108 @@ ce_bwd_kernel(const float* __restrict__ L, const int64_t* __restrict__ T, const 
 // ------------------------------------------------------------------- AdamW
 
 // Same per-element arithmetic as adamw_step_cpu (cppsrc/ops/adamw.cpp:22-44).
+// One AdamW element update (adamw.cu:11-50 arithmetic): m, v moments, bias
+// corrections as divisors, decoupled weight decay as a factor on p.
+__device__ __forceinline__ void adamw_elem(float& p, float g, float& m, float& v, float lr, float beta1, float beta2,
+                                           float eps, float wd_factor, float bc1, float bc2) {
+  const float mi = beta1 * m + (1.0f - beta1) * g;
+  const float vi = beta2 * v + (1.0f - beta2) * g * g;
+  m = mi;
+  v = vi;
+  const float m_hat = mi / bc1;
+  const float v_hat = vi / bc2;
+  p = p * wd_factor - lr * m_hat / (sqrtf(v_hat) + eps);
+}
+
 __global__ void __launch_bounds__(256)
 adamw_kernel(float* __restrict__ p, const float* __restrict__ g, float* __restrict__ m, float* __restrict__ v,
              int64_t n, float lr, float beta1, float beta2, float eps, float wd_factor, float bc1, float bc2) {
-  const float omb1 = 1.0f - beta1, omb2 = 1.0f - beta2;
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
-    const float gi = g[i];
-    const float mi = beta1 * m[i] + omb1 * gi;
-    const float vi = beta2 * v[i] + omb2 * gi * gi;
-    m[i] = mi;
-    v[i] = vi;
-    const float m_hat = mi / bc1;
-    const float v_hat = vi / bc2;
-    p[i] = p[i] * wd_factor - lr * m_hat / (sqrtf(v_hat) + eps);
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+    adamw_elem(p[i], g[i], m[i], v[i], lr, beta1, beta2, eps, wd_factor, bc1, bc2);
+}
+
+// ------------------------------------------------------ multi-tensor update
+
+// One launch updates up to kMultiMax tensors (an optimizer step over a
+// model's parameters is otherwise one small launch per parameter).  Pointers
+// and sizes travel by value in the kernel arguments; workgroup b works on
+// tensor t with start[t] <= b < start[t + 1], elements
+// [(b - start[t]) * kMultiChunk, +kMultiChunk).  The per-element arithmetic is
+// that of the single-tensor kernels, so results are bit-identical to them.
+constexpr int kMultiMax = 48;
+constexpr int kMultiChunk = 4096;
+struct MultiArgs {
+  float* a[kMultiMax];        // dst / param
+  const float* b[kMultiMax];  // src / grad
+  float* m[kMultiMax];
+  float* v[kMultiMax];
+  int64_t n[kMultiMax];
+  int start[kMultiMax + 1];
+  int count;
+};
+static_assert(sizeof(MultiArgs) < 4096, "kernel arguments");
+
+__device__ __forceinline__ int multi_tensor_of(const MultiArgs& A, int blk) {
+  int t = 0;
+  while (t + 1 < A.count && A.start[t + 1] <= blk) ++t;
+  return t;
+}
+
+template <bool ADAMW>
+__global__ void __launch_bounds__(256)
+multi_update_kernel(MultiArgs A, float alpha, float lr, float beta1, float beta2, float eps, float wd_factor,
+                    float bc1, float bc2) {
+  const int t = multi_tensor_of(A, blockIdx.x);
+  const int64_t i0 = (int64_t)(blockIdx.x - A.start[t]) * kMultiChunk;
+  const int64_t i1 = min(A.n[t], i0 + kMultiChunk);
+  float* a = A.a[t];  // may alias b (dst += alpha * dst)
+  const float* b = A.b[t];
+  for (int64_t i = i0 + threadIdx.x; i < i1; i += 256) {
+    if (ADAMW)
+      adamw_elem(a[i], b[i], A.m[t][i], A.v[t][i], lr, beta1, beta2, eps, wd_factor, bc1, bc2);
+    else
+      a[i] = ew<Ew::ScaledAdd>(a[i], b[i], alpha);
   }
+}
+
+// Launch groups of up to kMultiMax non-empty tensors.
+int launch_multi(bool adamw, int count, float* const* a, const float* const* b, float* const* m, float* const* v,
+                 const int64_t* n, float alpha, float lr, float beta1, float beta2, float eps, float wd_factor,
+                 float bc1, float bc2, hipStream_t st) {
+  MultiArgs A{};
+  int64_t blocks = 0;
+  auto flush = [&]() -> int {
+    if (A.count == 0) return AAR_OK;
+    A.start[A.count] = (int)blocks;
+    if (adamw)
+      multi_update_kernel<true><<<dim3((unsigned)blocks), dim3(256), 0, st>>>(A, alpha, lr, beta1, beta2, eps,
+                                                                              wd_factor, bc1, bc2);
+    else
+      multi_update_kernel<false><<<dim3((unsigned)blocks), dim3(256), 0, st>>>(A, alpha, lr, beta1, beta2, eps,
+                                                                               wd_factor, bc1, bc2);
+    const int rc = launch_status();
+    A = MultiArgs{};
+    blocks = 0;
+    return rc;
+  };
+  for (int i = 0; i < count; ++i) {
+    if (n[i] == 0) continue;
+    const int64_t nb = ceil_div(n[i], (int64_t)kMultiChunk);
+    if (A.count == kMultiMax || blocks + nb > INT32_MAX / 2) {
+      const int rc = flush();
+      if (rc != AAR_OK) return rc;
+    }
+    const int k = A.count++;
+    A.a[k] = a[i];
+    A.b[k] = b[i];
+    A.m[k] = adamw ? m[i] : nullptr;
+    A.v[k] = adamw ? v[i] : nullptr;
+    A.n[k] = n[i];
+    A.start[k] = (int)blocks;
+    blocks += nb;
+  }
+  return flush();
 }
 
 // ---------------------------------------------------------------- dropout
@@ -527,7 +634,8 @@ int aar_colsum_f32(const float* g, float* out, int64_t rows, int64_t cols, void*
                                                                                                   cols, chunk);
   int rc = launch_status();
   if (rc != AAR_OK) return rc;
-  colsum_stage2_kernel<<<dim3((unsigned)ceil_div(cols, 256)), dim3(256), 0, st>>>(part, out, parts, cols);
+  colsum_stage2_kernel<<<dim3((unsigned)ceil_div(cols, (int64_t)kCsCols)), dim3(kCsThreads), 0, st>>>(part, out, parts,
+                                                                                                   cols);
   return launch_status();
 }
 
@@ -638,6 +746,29 @@ int aar_adamw_f32(float* param, const float* grad, float* m, float* v, int64_t n
   adamw_kernel<<<dim3(stream_grid(n)), dim3(256), 0, as_stream(stream)>>>(
       param, grad, m, v, n, lr, beta1, beta2, eps, 1.0f - lr * weight_decay, bias_correction1, bias_correction2);
   return launch_status();
+}
+
+int aar_scaled_add_multi_f32(int count, float* const* dst, const float* const* src, const int64_t* n, float alpha,
+                             void* stream) {
+  if (count < 0) return AAR_EINVAL;
+  if (count == 0) return AAR_OK;
+  if (!dst || !src || !n) return AAR_EINVAL;
+  for (int i = 0; i < count; ++i)
+    if (n[i] < 0 || (n[i] > 0 && (!dst[i] || !src[i]))) return AAR_EINVAL;
+  return launch_multi(false, count, dst, src, nullptr, nullptr, n, alpha, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f,
+                      as_stream(stream));
+}
+
+int aar_adamw_multi_f32(int count, float* const* param, const float* const* grad, float* const* m, float* const* v,
+                        const int64_t* n, float lr, float beta1, float beta2, float eps, float weight_decay,
+                        float bias_correction1, float bias_correction2, void* stream) {
+  if (count < 0) return AAR_EINVAL;
+  if (count == 0) return AAR_OK;
+  if (!param || !grad || !m || !v || !n) return AAR_EINVAL;
+  for (int i = 0; i < count; ++i)
+    if (n[i] < 0 || (n[i] > 0 && (!param[i] || !grad[i] || !m[i] || !v[i]))) return AAR_EINVAL;
+  return launch_multi(true, count, param, grad, m, v, n, 0.f, lr, beta1, beta2, eps, 1.0f - lr * weight_decay,
+                      bias_correction1, bias_correction2, as_stream(stream));
 }
 
 int aar_dropout_f32(const float* x, float* out, float* mask, int64_t n, float p, uint64_t seed, void* stream) {

@@ -165,6 +165,12 @@ PYBIND11_MODULE(_core, m) {
         gil_release(),
         "Attention over a packed projection [..., T, 3*D] -> [..., T, D]: the MultiHeadAttention "
         "composition (per-head views of q, k, v, flash attention, heads merged back) in one op.");
+  m.def("_scaled_add_inplace_multi", &scaled_add_inplace_multi, py::arg("dsts"), py::arg("srcs"), py::arg("alpha"),
+        gil_release(), "scaled_add_inplace over lists of tensors, up to 48 per launch (bit-identical).");
+  m.def("_adamw_step_multi", &adamw_step_multi, py::arg("params"), py::arg("grads"), py::arg("m"), py::arg("v"),
+        py::arg("lr"), py::arg("beta1"), py::arg("beta2"), py::arg("eps"), py::arg("weight_decay"),
+        py::arg("bias_correction1"), py::arg("bias_correction2"), gil_release(),
+        "adamw_step over lists of tensors, up to 48 per launch (bit-identical).");
   m.def("_linear", &linear, py::arg("x"), py::arg("weight"), py::arg("bias"), gil_release(),
         "x W^T + b as one GEMM with the bias added in its epilogue: the values and gradients of "
         "add_bias(matmul_a_bt(x, W), b).");

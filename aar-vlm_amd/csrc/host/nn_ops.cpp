@@ -304,7 +304,8 @@ Tensor add_bias(const Tensor& x, const Tensor& bias) {
   return attach(fn, add_bias_dev(xc, bc));
 }
 
-void scaled_add_inplace(Tensor& dst, const Tensor& src, float alpha) {
+namespace {
+void check_scaled_add(const Tensor& dst, const Tensor& src) {
   if (dst.shape != src.shape) throw std::invalid_argument("scaled_add_inplace: shape mismatch");
   if (dst.dtype != src.dtype || dst.dtype != DType::Fp32) {
     throw std::invalid_argument("scaled_add_inplace: only Fp32 supported");
@@ -312,8 +313,32 @@ void scaled_add_inplace(Tensor& dst, const Tensor& src, float alpha) {
   if (dst.device != src.device) throw std::invalid_argument("scaled_add_inplace: device mismatch");
   if (!dst.is_contiguous()) throw std::invalid_argument("scaled_add_inplace: dst must be contiguous");
   if (dst.device == Device::CPU) throw_cpu_compute("scaled_add_inplace");
+}
+}  // namespace
+
+void scaled_add_inplace(Tensor& dst, const Tensor& src, float alpha) {
+  check_scaled_add(dst, src);
   Tensor sc = as_contig(src);
   check_status(aar_scaled_add_f32(fp(dst), fp(sc), alpha, n_of(dst), current_stream()), "scaled_add_inplace");
+}
+
+void scaled_add_inplace_multi(std::vector<Tensor>& dsts, const std::vector<Tensor>& srcs, float alpha) {
+  if (dsts.size() != srcs.size()) throw std::invalid_argument("scaled_add_inplace: list length mismatch");
+  std::vector<Tensor> sc;
+  sc.reserve(srcs.size());
+  std::vector<float*> d;
+  std::vector<const float*> s;
+  std::vector<int64_t> n;
+  for (size_t i = 0; i < dsts.size(); ++i) {
+    check_scaled_add(dsts[i], srcs[i]);
+    sc.push_back(as_contig(srcs[i]));
+    d.push_back(fp(dsts[i]));
+    s.push_back(fp(sc.back()));
+    n.push_back(n_of(dsts[i]));
+  }
+  check_status(aar_scaled_add_multi_f32(static_cast<int>(d.size()), d.data(), s.data(), n.data(), alpha,
+                                        current_stream()),
+               "scaled_add_inplace");
 }
 
 Tensor embedding(const Tensor& weight, const Tensor& ids) {
@@ -366,8 +391,8 @@ Tensor cross_entropy(const Tensor& logits, const Tensor& targets, int64_t ignore
   return attach(fn, out);
 }
 
-void adamw_step(Tensor& param, const Tensor& grad, Tensor& m, Tensor& v, float lr, float beta1, float beta2,
-                float eps, float weight_decay, float bias_correction1, float bias_correction2) {
+namespace {
+void check_adamw(const Tensor& param, const Tensor& grad, const Tensor& m, const Tensor& v) {
   if (param.dtype != DType::Fp32) throw std::invalid_argument("adamw_step: only Fp32 supported");
   auto check_match = [&](const Tensor& b, const char* what) {
     if (param.shape != b.shape) throw std::invalid_argument(std::string("adamw_step: ") + what + " shape mismatch");
@@ -383,8 +408,37 @@ void adamw_step(Tensor& param, const Tensor& grad, Tensor& m, Tensor& v, float l
     throw std::invalid_argument("adamw_step: all tensors must be contiguous");
   }
   if (param.device == Device::CPU) throw_cpu_compute("adamw_step");
+}
+}  // namespace
+
+void adamw_step(Tensor& param, const Tensor& grad, Tensor& m, Tensor& v, float lr, float beta1, float beta2,
+                float eps, float weight_decay, float bias_correction1, float bias_correction2) {
+  check_adamw(param, grad, m, v);
   check_status(aar_adamw_f32(fp(param), fp(grad), fp(m), fp(v), n_of(param), lr, beta1, beta2, eps, weight_decay,
                              bias_correction1, bias_correction2, current_stream()),
+               "adamw_step");
+}
+
+void adamw_step_multi(std::vector<Tensor>& params, const std::vector<Tensor>& grads, std::vector<Tensor>& ms,
+                      std::vector<Tensor>& vs, float lr, float beta1,
+                      float beta2, float eps, float weight_decay, float bias_correction1, float bias_correction2) {
+  if (grads.size() != params.size() || ms.size() != params.size() || vs.size() != params.size()) {
+    throw std::invalid_argument("adamw_step: list length mismatch");
+  }
+  std::vector<float*> p, m, v;
+  std::vector<const float*> g;
+  std::vector<int64_t> n;
+  for (size_t i = 0; i < params.size(); ++i) {
+    check_adamw(params[i], grads[i], ms[i], vs[i]);
+    p.push_back(fp(params[i]));
+    g.push_back(fp(grads[i]));
+    m.push_back(fp(ms[i]));
+    v.push_back(fp(vs[i]));
+    n.push_back(n_of(params[i]));
+  }
+  check_status(aar_adamw_multi_f32(static_cast<int>(p.size()), p.data(), g.data(), m.data(), v.data(), n.data(), lr,
+                                   beta1, beta2, eps, weight_decay, bias_correction1, bias_correction2,
+                                   current_stream()),
                "adamw_step");
 }
 

@@ -56,6 +56,13 @@ Tensor embedding(const Tensor& weight, const Tensor& ids);
 Tensor cross_entropy(const Tensor& logits, const Tensor& targets, int64_t ignore_index);
 void adamw_step(Tensor& param, const Tensor& grad, Tensor& m, Tensor& v, float lr, float beta1, float beta2,
                 float eps, float weight_decay, float bias_correction1, float bias_correction2);
+// One launch per up to 48 parameters instead of one per parameter (the
+// reference optimizers' loops, aargrad/optim.py:13-18, :36-54); same
+// validation and messages, bit-identical results.
+void scaled_add_inplace_multi(std::vector<Tensor>& dsts, const std::vector<Tensor>& srcs, float alpha);
+void adamw_step_multi(std::vector<Tensor>& params, const std::vector<Tensor>& grads, std::vector<Tensor>& ms,
+                      std::vector<Tensor>& vs, float lr, float beta1, float beta2, float eps, float weight_decay,
+                      float bias_correction1, float bias_correction2);
 
 // Batched products, causal mask, dropout (cppsrc/ops/bmm.cpp:212-268,
 // attention.cpp:77-90, dropout.cpp:66-92).

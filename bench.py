@@ -476,8 +476,8 @@ class GPT:
         for t in self.p:
             t.zero_grad()
         loss.backward()
-        for t in self.p:
-            ag.scaled_add_inplace(t, t.grad, -lr)
+        # SGD step as aargrad.optim.SGD takes it: one multi-tensor update
+        ag._core._scaled_add_inplace_multi(self.p, [t.grad for t in self.p], -lr)
         return loss
 
 

@@ -300,6 +300,20 @@ int aar_adamw_f32(float* param, const float* grad, float* m, float* v, int64_t n
                   float beta1, float beta2, float eps, float weight_decay,
                   float bias_correction1, float bias_correction2, void* stream);
 
+/* Multi-tensor optimizer updates: tensor i has n[i] floats at dst[i]/src[i]
+ * (param[i], grad[i], m[i], v[i]); up to 48 tensors go in one launch, their
+ * pointers passed by value in the kernel arguments.  Element for element the
+ * same arithmetic as aar_scaled_add_f32 / aar_adamw_f32, so results are
+ * bit-identical to calling those per tensor.  They replace the per-parameter
+ * loops of the reference optimizers: SGD.step calling scaled_add_inplace
+ * (aargrad/optim.py:13-18) and AdamW.step calling adamw_step
+ * (aargrad/optim.py:36-54), one launch per parameter there. */
+int aar_scaled_add_multi_f32(int count, float* const* dst, const float* const* src, const int64_t* n,
+                             float alpha, void* stream);
+int aar_adamw_multi_f32(int count, float* const* param, const float* const* grad, float* const* m,
+                        float* const* v, const int64_t* n, float lr, float beta1, float beta2, float eps,
+                        float weight_decay, float bias_correction1, float bias_correction2, void* stream);
+
 /* Dropout over n floats with the reference's counter-based stream: element i
  * keeps iff philox_uniform(seed, i) >= p (Philox-4x32-10, word 0 / 2^32);
  * mask[i] = keep ? 1/(1-p) : 0, out[i] = x[i] * mask[i].  Bit-identical to the

@@ -83,6 +83,21 @@ def test_abi_validates_before_touching_the_device():
     assert lib.aar_dropout_f32(None, None, None, 0, 0.5, 0, None) == 0
     lib.aar_causal_mask_f32.argtypes = [vp, vp, i64, i64, ctypes.c_float, vp]
     assert lib.aar_causal_mask_f32(None, None, -1, 4, 0.0, None) == -1
+    # multi-tensor optimizer updates: list and size checks before any launch
+    pp = ctypes.POINTER(vp)
+    lib.aar_scaled_add_multi_f32.argtypes = [ctypes.c_int, pp, pp, ctypes.POINTER(i64), ctypes.c_float, vp]
+    assert lib.aar_scaled_add_multi_f32(-1, None, None, None, 1.0, None) == -1
+    assert lib.aar_scaled_add_multi_f32(0, None, None, None, 1.0, None) == 0
+    assert lib.aar_scaled_add_multi_f32(2, None, None, None, 1.0, None) == -1
+    ptrs = (vp * 1)(None)
+    sizes = (i64 * 1)(-3)
+    assert lib.aar_scaled_add_multi_f32(1, ptrs, ptrs, sizes, 1.0, None) == -1  # negative size
+    sizes[0] = 8
+    assert lib.aar_scaled_add_multi_f32(1, ptrs, ptrs, sizes, 1.0, None) == -1  # null pointer with n > 0
+    lib.aar_adamw_multi_f32.argtypes = [ctypes.c_int, pp, pp, pp, pp, ctypes.POINTER(i64)] + [ctypes.c_float] * 7 + [vp]
+    assert lib.aar_adamw_multi_f32(1, ptrs, ptrs, ptrs, ptrs, sizes, *([0.1] * 7), None) == -1
+    sizes[0] = 0
+    assert lib.aar_adamw_multi_f32(1, ptrs, ptrs, ptrs, ptrs, sizes, *([0.1] * 7), None) == 0  # all empty: no launch
 
 
 def test_core_exports_reference_api(ag):

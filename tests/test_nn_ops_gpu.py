@@ -98,6 +98,69 @@ def test_sgd_and_adamw(gpu):
     assert_close(host(gpu, tp), rp, 1e-6, "p")
 
 
+def test_multi_tensor_updates_bit_identical(gpu):
+    # 100 tensors (three launches of at most 48), ragged sizes including empty
+    # ones and chunk edges: the multi-tensor SGD / AdamW updates equal the
+    # per-tensor ops bit for bit
+    rng = np.random.default_rng(17)
+    sizes = [int(s) for s in rng.choice([0, 1, 3, 4095, 4096, 4097, 12289, 70001], 100)]
+    ps = [rng.standard_normal(n).astype(f32) for n in sizes]
+    gs = [rng.standard_normal(n).astype(f32) for n in sizes]
+    ms = [(0.1 * rng.standard_normal(n)).astype(f32) for n in sizes]
+    vs = [np.abs(0.1 * rng.standard_normal(n)).astype(f32) for n in sizes]
+    one = [dev(gpu, p) for p in ps]
+    many = [dev(gpu, p) for p in ps]
+    for t, g in zip(one, gs):
+        gpu.scaled_add_inplace(t, dev(gpu, g), -3e-3)
+    gpu._core._scaled_add_inplace_multi(many, [dev(gpu, g) for g in gs], -3e-3)
+    for a, b in zip(one, many):
+        np.testing.assert_array_equal(host(gpu, a), host(gpu, b))
+    args = (1e-3, 0.9, 0.999, 1e-8, 0.01, 0.271, 0.00299)
+    st1 = [(dev(gpu, p), dev(gpu, m), dev(gpu, v)) for p, m, v in zip(ps, ms, vs)]
+    st2 = [(dev(gpu, p), dev(gpu, m), dev(gpu, v)) for p, m, v in zip(ps, ms, vs)]
+    for (p, m, v), g in zip(st1, gs):
+        gpu.adamw_step(p, dev(gpu, g), m, v, *args)
+    gpu._core._adamw_step_multi([s[0] for s in st2], [dev(gpu, g) for g in gs], [s[1] for s in st2],
+                                [s[2] for s in st2], *args)
+    for a, b in zip(st1, st2):
+        for x, y in zip(a, b):
+            np.testing.assert_array_equal(host(gpu, x), host(gpu, y))
+    # dst aliasing src: p += alpha * p
+    t = dev(gpu, ps[0] if sizes[0] else np.ones(5, f32))
+    ref = host(gpu, t)
+    gpu._core._scaled_add_inplace_multi([t], [t], 0.5)
+    np.testing.assert_array_equal(host(gpu, t), (ref + np.float32(0.5) * ref).astype(f32))
+    with pytest.raises(ValueError, match="shape mismatch"):
+        gpu._core._scaled_add_inplace_multi([dev(gpu, np.zeros(3, f32))], [dev(gpu, np.zeros(4, f32))], 1.0)
+
+
+def test_optimizers_take_one_multi_tensor_step(gpu, ag):
+    # optim.SGD / optim.AdamW (now one multi-tensor call per step) against the
+    # reference optimizers' per-parameter loops (aargrad/optim.py:13-18, :36-54)
+    rng = np.random.default_rng(5)
+    shapes = [(8, 3), (3,), (0,), (5, 7)]
+    for name in ("sgd", "adamw"):
+        init = [rng.standard_normal(s).astype(f32) for s in shapes]
+        grads = [rng.standard_normal(s).astype(f32) for s in shapes]
+        params = [ag.nn.Parameter(dev(gpu, a)) for a in init]
+        for p, g in zip(params, grads):
+            gpu.sum_all(gpu.mul(p.tensor, dev(gpu, g))).backward()  # grad = g
+        opt = ag.optim.SGD(params, lr=0.1) if name == "sgd" else ag.optim.AdamW(params, lr=1e-2)
+        opt.step()
+        opt.step()
+        ref = [dev(gpu, a) for a in init]
+        ms = [dev(gpu, np.zeros(s, f32)) for s in shapes]
+        vs = [dev(gpu, np.zeros(s, f32)) for s in shapes]
+        for t in (1, 2):
+            for r, g, m, v in zip(ref, grads, ms, vs):
+                if name == "sgd":
+                    gpu.scaled_add_inplace(r, dev(gpu, g), -0.1)
+                else:
+                    gpu.adamw_step(r, dev(gpu, g), m, v, 1e-2, 0.9, 0.999, 1e-8, 0.01, 1 - 0.9 ** t, 1 - 0.999 ** t)
+        for p, r in zip(params, ref):
+            np.testing.assert_array_equal(host(gpu, p.tensor), host(gpu, r))
+
+
 @pytest.mark.parametrize("vocab,dim,shape", [(7, 4, (2, 3)), (65, 384, (64, 256)), (256, 384, (64, 256)),
                                              (5, 3, (6,))])
 def test_embedding_fwd_bwd(gpu, vocab, dim, shape):
