@@ -1,6 +1,6 @@
 """In-tree build of the MI355X backend.
 
-Produces, next to the Python package (so gpurun snapshots carry them):
+Produces, next to the Python package (so a copy of the repository tree carries them):
   aargrad/libaar_hip.so   all HIP kernels + the C ABI (include/aar_hip.h), gfx950
   aargrad/_core<ext>.so   the pybind11 module aargrad._core (host C++), linked to
                           libaar_hip.so through an $ORIGIN rpath

@@ -582,7 +582,7 @@ def main() -> int:
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build targets one GPU; --gpus {args.gpus} is not supported "
-              "(the hot path is single-GPU; sharding is described in DESIGN.md)", file=sys.stderr)
+              "(every kernel here runs on one GPU's share; no collectives are built)", file=sys.stderr)
         return 2
 
     import aargrad as ag
