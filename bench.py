@@ -577,6 +577,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=60)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--flash-steps", type=int, default=50)
+    ap.add_argument("--flash-t", type=int, default=4096, choices=[1024, 4096],
+                    help="sequence length of the --only flash run (BASELINE config 4 has both)")
     ap.add_argument("--only", choices=["all", "gemm", "flash", "rowwise", "extra", "copy", "gpt", "sweep"], default="all",
                     help="run one part (profiling runs); the JSON line is printed for 'all'")
     args = ap.parse_args()
@@ -610,8 +612,8 @@ def main() -> int:
         log(json.dumps(bench_gpt(ag, ev)))
         return 0
     if args.only == "flash":
-        fa_ms, fa_flops, fa_dist = bench_flash(ag, args.flash_steps, 10, ev)
-        log(f"flash fwd+bwd {fa_ms:.3f} ms {fa_flops / (fa_ms * 1e-3) / 1e12:.2f} TFLOPS {fa_dist}")
+        fa_ms, fa_flops, fa_dist = bench_flash(ag, args.flash_steps, 10, ev, T=args.flash_t)
+        log(f"flash T={args.flash_t} fwd+bwd {fa_ms:.3f} ms {fa_flops / (fa_ms * 1e-3) / 1e12:.2f} TFLOPS {fa_dist}")
         return 0
 
     step_ms, wall, err, ab, mm_dist = bench_matmul(ag, args.steps, args.warmup, ev)
