@@ -105,6 +105,18 @@ int aar_gemm_f32(int op, int64_t M, int64_t N, int64_t K,
 int aar_gemm_f32_bias(int op, int64_t M, int64_t N, int64_t K, const float* A, const float* B,
                       const float* bias, float* C, void* workspace, size_t workspace_bytes, void* stream);
 
+/* Batched GEMM with explicit leading dimensions: for b in [0, batch),
+ * C_b = op(A_b, B_b) with A_b = A + b*strideA (and so on), op as in
+ * aar_gemm_f32 but rows of A/B/C at lda/ldb/ldc elements (lda >= K for NN/NT,
+ * >= M for TN; ldb >= N for NN/TN, >= K for NT; ldc >= N).  No split-K, so no
+ * workspace.  Any batch count: batches go in launches of at most 65535.
+ * K == 0 needs a contiguous C (ldc == N, strideC == M*N).
+ * Replaces bmm_cuda / bmm_a_bt_cuda / bmm_at_b_cuda (cppsrc/ops/bmm.cpp:10-12). */
+int aar_gemm_f32_batched(int op, int64_t batch, int64_t M, int64_t N, int64_t K,
+                         const float* A, int64_t lda, int64_t strideA,
+                         const float* B, int64_t ldb, int64_t strideB,
+                         float* C, int64_t ldc, int64_t strideC, void* stream);
+
 /* Tuning and test access to the GEMM tile configurations (no counterpart in
  * the reference, whose launchers pick a tile size internally,
  * cppsrc/ops/matmul.cu:792-832).  Configurations are numbered 0..n-1;
@@ -114,17 +126,6 @@ int aar_gemm_f32_bias(int op, int64_t M, int64_t N, int64_t K, const float* A, c
  * a given configuration and split-K count (needs splits*M*N*4 bytes of
  * workspace when splits > 1, else AAR_EWORKSPACE); results agree with
  * aar_gemm_f32 up to summation order. */
-/* Batched GEMM with explicit leading dimensions: for b in [0, batch),
- * C_b = op(A_b, B_b) with A_b = A + b*strideA (and so on), op as in
- * aar_gemm_f32 but rows of A/B/C at lda/ldb/ldc elements (lda >= K for NN/NT,
- * >= M for TN; ldb >= N for NN/TN, >= K for NT; ldc >= N).  No split-K, so no
- * workspace.  K == 0 needs a contiguous C (ldc == N, strideC == M*N).
- * Replaces bmm_cuda / bmm_a_bt_cuda / bmm_at_b_cuda (cppsrc/ops/bmm.cpp:10-12). */
-int aar_gemm_f32_batched(int op, int64_t batch, int64_t M, int64_t N, int64_t K,
-                         const float* A, int64_t lda, int64_t strideA,
-                         const float* B, int64_t ldb, int64_t strideB,
-                         float* C, int64_t ldc, int64_t strideC, void* stream);
-
 int aar_gemm_f32_tile_config(int config, int* tile_m, int* tile_n, int* tile_k);
 int aar_gemm_f32_plan(int op, int64_t M, int64_t N, int64_t K, size_t workspace_bytes,
                       int* config, int* splits);
@@ -152,6 +153,8 @@ int aar_layernorm_fwd_f32(const float* x, const float* w, const float* b,
                           float* y, float* mean, float* rstd,
                           int64_t rows, int64_t cols, float eps, void* stream);
 
+/* Workspace for aar_layernorm_bwd_f32: the dgamma/dbeta partial rows of its
+ * persistent workgroups (parts x 2 x cols floats; covers both load paths). */
 size_t aar_layernorm_bwd_workspace_bytes(int64_t rows, int64_t cols);
 
 /* dx [rows,cols], dw and db [cols] (fully overwritten; deterministic two-stage
@@ -173,6 +176,8 @@ int aar_flash_fwd_f32(const float* q, const float* k, const float* v,
                       float* o, float* lse, int64_t bh, int64_t T, int64_t d,
                       int causal, float scale, void* stream);
 
+/* Minimum workspace for aar_flash_bwd_f32 / _strided_f32: the D = rowsum(dO*O)
+ * rows, bh x T floats (the recompute path). */
 size_t aar_flash_bwd_workspace_bytes(int64_t bh, int64_t T, int64_t d);
 /* Workspace that also holds every dS tile of the dK/dV pass (a 32x32 float
  * tile per query/key tile pair with work: bh * n(n+1)/2 tiles causal, bh * n^2
