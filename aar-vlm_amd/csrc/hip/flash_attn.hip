@@ -37,6 +37,7 @@
 #include <hip/hip_runtime.h>
 #include <math.h>
 
+#include <algorithm>
 #include <initializer_list>
 #include <stdint.h>
 
@@ -210,6 +211,31 @@ __device__ __forceinline__ int64_t ds_pair(int qt, int kt, int nt, bool causal) 
   return causal ? (int64_t)qt * (qt + 1) / 2 + kt : (int64_t)qt * nt + kt;
 }
 
+// Causal forward split.  The query blocks of a head differ in work (block qb
+// sees 4(qb+1) key tiles), and when the grid holds at most one workgroup per
+// resident slot each CU ends on its longest block with the matrix cores
+// mostly idle.  Then (fa_fwd_split_blocks says when) the longest S = nqb/2
+// blocks have their key range cut in two halves, each half a workgroup of its
+// own that writes its normalised partial O and log2-sum-exp to the workspace,
+// and a combine pass merges the two halves of every split row.  item[] lists a head's work items longest
+// first (qb << 2 | part; part 0 whole block, 1 first half, 2 second half);
+// workgroup j*BH + bh runs item j of head bh.  Both halves of a split block
+// see every key they hold (the first half ends before the block's first
+// query, the second holds the diagonal), so every partial row has l > 0.
+constexpr int kFaMaxItems = 96;
+constexpr int64_t kFaSplitMaxGrid = 2048;  // largest grid (workgroups) that may split
+struct FaSplit {
+  int S;                           // blocks split in two; 0: no split, item[] unused
+  uint16_t item[kFaMaxItems];      // per-head work items, longest first
+  float* part_o;                   // [BH][S][2][kBlock][DP] normalised partial O
+  float* part_l;                   // [BH][S][2][kBlock] m + log2(l) of each partial row
+};
+
+// Partial-row index of (head bh, split slot s, half p, row r of the block).
+__host__ __device__ __forceinline__ int64_t fa_part_row(int bh, int S, int s, int p, int r) {
+  return (((int64_t)bh * S + s) * 2 + p) * kBlock + r;
+}
+
 // ------------------------------------------------------------------ forward
 
 // Software pipeline: K runs one tile ahead of V.  Iteration t holds K tile
@@ -219,10 +245,10 @@ __device__ __forceinline__ int64_t ds_pair(int qt, int kt, int nt, bool causal) 
 // then O += V_t P_t.  V is staged transposed so each 128-bit LDS read feeds
 // four PV steps.  Only tiles that cross the causal diagonal or the sequence
 // end are masked.  One barrier per tile.
-template <int DP, bool CAUSAL, bool VEC>
+template <int DP, bool CAUSAL, bool VEC, bool SPLIT>
 __global__ void __launch_bounds__(kFaThreads)
 flash_fwd_kernel(FaIn Qv, FaIn Kv, FaIn Vv, FaOut Ov, float* __restrict__ Lse, int T, int d, int H,
-                 int nqb, int BH, float scale_log2) {
+                 int nqb, int BH, float scale_log2, FaSplit sp) {
   constexpr int NC = DP / 8;   // head-dim chunks
   constexpr int NB = DP / 32;  // head-dim output blocks
   constexpr int LD = DP + 4;
@@ -233,7 +259,9 @@ flash_fwd_kernel(FaIn Qv, FaIn Kv, FaIn Vv, FaOut Ov, float* __restrict__ Lse, i
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int lr = lane & 31, h = lane >> 5;
   // Longest work first: the last query blocks have the most key tiles.
-  const int qb = CAUSAL ? nqb - 1 - (int)(blockIdx.x / BH) : (int)(blockIdx.x / BH);
+  const int item = (int)(blockIdx.x / BH);
+  const int qb = SPLIT ? sp.item[item] >> 2 : (CAUSAL ? nqb - 1 - item : item);
+  const int part = SPLIT ? sp.item[item] & 3 : 0;
   const int bh = blockIdx.x % BH;
   const float* __restrict__ Q = Qv.head(bh, H);
   const float* __restrict__ K = Kv.head(bh, H);
@@ -253,9 +281,13 @@ flash_fwd_kernel(FaIn Qv, FaIn Kv, FaIn Vv, FaOut Ov, float* __restrict__ Lse, i
   float m = -INFINITY, l = 0.f;
 
   const int kv_end = CAUSAL ? min(T, qb * kBlock + kBlock) : T;
-  const int ntiles = (kv_end + kTile - 1) / kTile;
+  // Key tiles [tb, te) of this work item.
+  const int nt_block = (kv_end + kTile - 1) / kTile;
+  const int tb = SPLIT && part == 2 ? nt_block / 2 : 0;
+  const int te = SPLIT && part == 1 ? nt_block / 2 : nt_block;
+  const int ntiles = te - tb;
   // Last key tile that holds a key this wave's queries may see.
-  const int wlast = CAUSAL ? min(ntiles - 1, (q0 + kTile - 1) / kTile) : ntiles - 1;
+  const int wlast = CAUSAL ? min(te - 1, (q0 + kTile - 1) / kTile) : te - 1;
 
   // S^T tile from K rows in LDS: lane = query, register r = key acc_row(r, h).
   auto qk = [&](const float* kt) {
@@ -318,30 +350,32 @@ flash_fwd_kernel(FaIn Qv, FaIn Kv, FaIn Vv, FaOut Ov, float* __restrict__ Lse, i
     }
   };
 
+  // Iteration t works on key tile tb + t (buffers indexed by t).
   TileCopy<DP, VEC> kc, vc;
-  kc.load(K, Kv.st, 0, T, d, tid);
-  vc.load(V, Vv.st, 0, T, d, tid);
+  kc.load(K, Kv.st, tb * kTile, T, d, tid);
+  vc.load(V, Vv.st, tb * kTile, T, d, tid);
   kc.template store<LD>(ks[0], tid);
   vc.template store_t<kLdt, kSwz>(vts[0], tid);
   if (ntiles > 1) {
-    kc.load(K, Kv.st, kTile, T, d, tid);
+    kc.load(K, Kv.st, (tb + 1) * kTile, T, d, tid);
     kc.template store<LD>(ks[1], tid);
   }
   __syncthreads();
   f32x16 s_cur = qk(ks[0]);
   __syncthreads();  // K tile 0's buffer is refilled in iteration 0
 
+  const int wl = wlast - tb;
   for (int t = 0; t < ntiles; ++t) {
     const bool load_k = t + 2 < ntiles;  // K_{t+2} -> ks[t & 1]
     const bool load_v = t + 1 < ntiles;  // V_{t+1} -> vts[(t + 1) & 1]
-    if (load_k) kc.load(K, Kv.st, (t + 2) * kTile, T, d, tid);
-    if (load_v) vc.load(V, Vv.st, (t + 1) * kTile, T, d, tid);
+    if (load_k) kc.load(K, Kv.st, (tb + t + 2) * kTile, T, d, tid);
+    if (load_v) vc.load(V, Vv.st, (tb + t + 1) * kTile, T, d, tid);
     f32x16 s_next = zero16();
-    if (t + 1 <= wlast) {
+    if (t + 1 <= wl) {
       s_next = qk(ks[(t + 1) & 1]);
-      soft_pv(s_cur, vts[t & 1], t * kTile);
-    } else if (t <= wlast) {
-      soft_pv(s_cur, vts[t & 1], t * kTile);
+      soft_pv(s_cur, vts[t & 1], (tb + t) * kTile);
+    } else if (t <= wl) {
+      soft_pv(s_cur, vts[t & 1], (tb + t) * kTile);
     }
     if (load_k) kc.template store<LD>(ks[t & 1], tid);
     if (load_v) vc.template store_t<kLdt, kSwz>(vts[(t + 1) & 1], tid);
@@ -349,6 +383,25 @@ flash_fwd_kernel(FaIn Qv, FaIn Kv, FaIn Vv, FaOut Ov, float* __restrict__ Lse, i
     s_cur = s_next;
   }
 
+  if (SPLIT && part != 0) {
+    // Half of a split block: normalised partial row and its m + log2(l).
+    if (qi < T) {
+      const float inv_l = 1.0f / l;
+      const int64_t prow = fa_part_row(bh, sp.S, qb - (nqb - sp.S), part - 1, qi - qb * kBlock);
+      float* po = sp.part_o + prow * DP;
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int dd = b * 32 + 8 * g + 4 * h;
+          *reinterpret_cast<f32x4*>(po + dd) = f32x4{o[b][4 * g] * inv_l, o[b][4 * g + 1] * inv_l,
+                                                     o[b][4 * g + 2] * inv_l, o[b][4 * g + 3] * inv_l};
+        }
+      }
+      if (h == 0) sp.part_l[prow] = m + log2f(l);
+    }
+    return;
+  }
   if (qi < T) {
     const float inv_l = 1.0f / l;
     float* orow = Ov.head(bh, H) + (int64_t)qi * Ov.st;
@@ -364,6 +417,37 @@ flash_fwd_kernel(FaIn Qv, FaIn Kv, FaIn Vv, FaOut Ov, float* __restrict__ Lse, i
     }
     if (h == 0) Lse[(int64_t)bh * T + qi] = (m + log2f(l)) * kLn2;
   }
+}
+
+// Merge of the two halves of every split row: with L_p = m_p + log2(l_p) and
+// M = max(L_0, L_1), w_p = 2^(L_p - M),
+//   O = (w_0 O_0 + w_1 O_1) / (w_0 + w_1),   lse = (M + log2(w_0 + w_1)) ln 2,
+// the softmax over the union of the two key ranges.  DP/4 lanes per row.
+template <int DP, bool VEC>
+__global__ void __launch_bounds__(256)
+flash_fwd_combine_kernel(FaSplit sp, FaOut Ov, float* __restrict__ Lse, int T, int d, int H, int nqb,
+                         int BH) {
+  constexpr int kLanes = DP / 4;
+  const int64_t u = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t row = u / kLanes;  // over BH x S x kBlock
+  if (row >= (int64_t)BH * sp.S * kBlock) return;
+  const int c = (int)(u % kLanes) * 4;
+  const int r = (int)(row % kBlock);
+  const int s = (int)((row / kBlock) % sp.S);
+  const int bh = (int)(row / ((int64_t)kBlock * sp.S));
+  const int qi = (nqb - sp.S + s) * kBlock + r;
+  if (qi >= T) return;
+  const int64_t p0 = fa_part_row(bh, sp.S, s, 0, r), p1 = fa_part_row(bh, sp.S, s, 1, r);
+  const float l0 = sp.part_l[p0], l1 = sp.part_l[p1];
+  const float mx = fmaxf(l0, l1);
+  const float w0 = fast_exp2(l0 - mx), w1 = fast_exp2(l1 - mx);
+  const float inv = 1.0f / (w0 + w1);
+  const f32x4 a = *reinterpret_cast<const f32x4*>(sp.part_o + p0 * DP + c);
+  const f32x4 b = *reinterpret_cast<const f32x4*>(sp.part_o + p1 * DP + c);
+  const f32x4 v = {(w0 * a[0] + w1 * b[0]) * inv, (w0 * a[1] + w1 * b[1]) * inv, (w0 * a[2] + w1 * b[2]) * inv,
+                   (w0 * a[3] + w1 * b[3]) * inv};
+  if (c < d) store4<VEC>(Ov.head(bh, H) + (int64_t)qi * Ov.st + c, v, d - c);
+  if (c == 0) Lse[(int64_t)bh * T + qi] = (mx + log2f(w0 + w1)) * kLn2;
 }
 
 // ------------------------------------------------------------- backward 0
@@ -772,15 +856,103 @@ struct FwdArgs {
   float* lse;
   int T, d, H, BH;
   float scale;
+  void* ws;  // split partials when non-null and large enough
+  size_t ws_bytes;
   hipStream_t st;
 };
+
+// Blocks the causal forward splits: nqb/2 (the longest) when the grid fills at
+// most half of the resident workgroup slots (`slots` = CUs x workgroups per
+// CU), or one full round with at least 8 query blocks.  Measured on MI355X,
+// d = 64, forward + combine against the unsplit forward: grids of 32-384
+// workgroups 0.53-0.87x the time, 768 workgroups 0.94x at T = 1024 and 0.86x
+// at T = 4096 but 1.06x at T = 512 (4 blocks of 4-16 key tiles, where the
+// combine pass costs more than the balance gains).  With more than one round
+// the dispatcher already balances the blocks.
+int fa_fwd_split_blocks(int64_t bh, int64_t nqb, int64_t slots) {
+  const int64_t grid = bh * nqb;
+  if (nqb < 2 || nqb + nqb / 2 > kFaMaxItems || grid > std::min(slots, kFaSplitMaxGrid)) return 0;
+  if (2 * grid > slots && nqb < 8) return 0;
+  return (int)(nqb / 2);
+}
+
+// Workspace of a split with S = nqb/2: partial rows (256-byte aligned), then
+// their log2-sum-exps.  Depends on the shape only, so it can be sized without
+// a device; grids above kFaSplitMaxGrid workgroups (more than any MI355X
+// holds at once) never split and need none.
+size_t fa_fwd_part_o_bytes(int64_t bh, int64_t T, int64_t d) {
+  const int64_t nqb = (T + kBlock - 1) / kBlock;
+  if (nqb < 2 || nqb + nqb / 2 > kFaMaxItems || bh * nqb > kFaSplitMaxGrid) return 0;
+  const int64_t rows = bh * (nqb / 2) * 2 * kBlock;
+  return ((size_t)rows * pad_dim(d) * sizeof(float) + 255) / 256 * 256;
+}
+size_t fa_fwd_split_bytes(int64_t bh, int64_t T, int64_t d) {
+  const size_t ob = fa_fwd_part_o_bytes(bh, T, d);
+  if (ob == 0) return 0;
+  const int64_t nqb = (T + kBlock - 1) / kBlock;
+  return ob + (size_t)(bh * (nqb / 2) * 2 * kBlock) * sizeof(float);
+}
+
+// Work items of one head, longest first (see FaSplit).
+void fa_fwd_items(FaSplit& sp, int T, int nqb) {
+  int len[kFaMaxItems], n = 0;
+  for (int qb = nqb - 1; qb >= 0; --qb) {
+    const int nt = (std::min(T, qb * kBlock + kBlock) + kTile - 1) / kTile;
+    if (qb >= nqb - sp.S) {
+      sp.item[n] = (uint16_t)(qb << 2 | 1), len[n++] = nt / 2;
+      sp.item[n] = (uint16_t)(qb << 2 | 2), len[n++] = nt - nt / 2;
+    } else {
+      sp.item[n] = (uint16_t)(qb << 2), len[n++] = nt;
+    }
+  }
+  for (int i = 1; i < n; ++i)  // stable insertion sort, descending length
+    for (int j = i; j > 0 && len[j] > len[j - 1]; --j) {
+      std::swap(len[j], len[j - 1]);
+      std::swap(sp.item[j], sp.item[j - 1]);
+    }
+}
+
+// Workgroups of the causal forward resident on one CU (register-limited).
+template <int DP, bool VEC>
+int fa_fwd_resident() {
+  static const int n = [] {
+    int b = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, flash_fwd_kernel<DP, true, VEC, true>, kFaThreads, 0) !=
+        hipSuccess) {
+      b = 1;
+    }
+    return b > 0 ? b : 1;
+  }();
+  return n;
+}
 
 template <int DP, bool C, bool VEC>
 struct FwdLaunch {
   static int run(const FwdArgs& a) {
     const int nqb = (a.T + kBlock - 1) / kBlock;
-    flash_fwd_kernel<DP, C, VEC><<<dim3((unsigned)(nqb * a.BH)), dim3(kFaThreads), 0, a.st>>>(
-        a.q, a.k, a.v, a.o, a.lse, a.T, a.d, a.H, nqb, a.BH, a.scale * kLog2e);
+    FaSplit sp{};
+    if (C && a.ws && aligned16(a.ws) && a.ws_bytes >= fa_fwd_split_bytes(a.BH, a.T, a.d)) {
+      sp.S = fa_fwd_split_blocks(a.BH, nqb, (int64_t)device_cu_count() * fa_fwd_resident<DP, VEC>());
+    }
+    if (sp.S > 0) {
+      fa_fwd_items(sp, a.T, nqb);
+      sp.part_o = static_cast<float*>(a.ws);
+      sp.part_l = reinterpret_cast<float*>(static_cast<char*>(a.ws) + fa_fwd_part_o_bytes(a.BH, a.T, a.d));
+    }
+    // The unsplit instance keeps the key loop free of the split's tile offsets
+    // (with them the T = 4096 causal forward ran 4 % slower).
+    if (sp.S > 0) {
+      flash_fwd_kernel<DP, C, VEC, true><<<dim3((unsigned)((nqb + sp.S) * a.BH)), dim3(kFaThreads), 0, a.st>>>(
+          a.q, a.k, a.v, a.o, a.lse, a.T, a.d, a.H, nqb, a.BH, a.scale * kLog2e, sp);
+    } else {
+      flash_fwd_kernel<DP, C, VEC, false><<<dim3((unsigned)(nqb * a.BH)), dim3(kFaThreads), 0, a.st>>>(
+          a.q, a.k, a.v, a.o, a.lse, a.T, a.d, a.H, nqb, a.BH, a.scale * kLog2e, sp);
+    }
+    int rc = launch_status();
+    if (rc != AAR_OK || sp.S == 0) return rc;
+    const int64_t lanes = (int64_t)a.BH * sp.S * kBlock * (DP / 4);
+    flash_fwd_combine_kernel<DP, VEC><<<dim3((unsigned)ceil_div(lanes, (int64_t)256)), dim3(256), 0, a.st>>>(
+        sp, a.o, a.lse, a.T, a.d, a.H, nqb, a.BH);
     return launch_status();
   }
 };
@@ -845,9 +1017,15 @@ bool fa_shape_ok(int64_t bh, int64_t T, int64_t d) {
 
 using namespace aar;
 
+extern "C" size_t aar_flash_fwd_workspace_bytes(int64_t bh, int64_t T, int64_t d, int causal) {
+  if (!causal || bh <= 0 || T <= 0 || d <= 0 || d > 128 || bh > (1 << 24) || T > (1 << 24)) return 0;
+  return fa_fwd_split_bytes(bh, T, d);
+}
+
 extern "C" int aar_flash_fwd_strided_f32(const float* q, const float* k, const float* v, float* o, float* lse,
                                          int64_t B, int64_t H, int64_t T, int64_t d, const int64_t* strides,
-                                         int causal, float scale, void* stream) {
+                                         int causal, float scale, void* workspace, size_t workspace_bytes,
+                                         void* stream) {
   if (B < 0 || H < 0 || T < 0 || d <= 0) return AAR_EINVAL;
   if (d > 128) return AAR_EINVAL;
   if (B == 0 || H == 0 || T == 0) return AAR_OK;
@@ -856,7 +1034,8 @@ extern "C" int aar_flash_fwd_strided_f32(const float* q, const float* k, const f
   const bool vec = fa_vec_ok(d, {q, k, v, o}, strides, 12);
   FwdArgs a{fa_in(q, strides),      fa_in(k, strides + 3), fa_in(v, strides + 6), fa_out(o, strides + 9),
             lse,                    (int)T,                (int)d,                (int)H,
-            (int)(B * H),           scale,                 as_stream(stream)};
+            (int)(B * H),           scale,                 workspace,             workspace_bytes,
+            as_stream(stream)};
   return dispatch_fa<FwdLaunch>(pad_dim(d), causal != 0, vec, a);
 }
 
@@ -866,7 +1045,7 @@ extern "C" int aar_flash_fwd_f32(const float* q, const float* k, const float* v,
   if (bh < 0 || T < 0 || d <= 0) return AAR_EINVAL;
   const int64_t c[3] = {bh * T * d, T * d, d};  // [1, bh, T, d] contiguous
   const int64_t strides[12] = {c[0], c[1], c[2], c[0], c[1], c[2], c[0], c[1], c[2], c[0], c[1], c[2]};
-  return aar_flash_fwd_strided_f32(q, k, v, o, lse, 1, bh, T, d, strides, causal, scale, stream);
+  return aar_flash_fwd_strided_f32(q, k, v, o, lse, 1, bh, T, d, strides, causal, scale, nullptr, 0, stream);
 }
 
 extern "C" size_t aar_flash_bwd_workspace_bytes(int64_t bh, int64_t T, int64_t d) {

@@ -41,6 +41,12 @@ Workspace flash_bwd_workspace(int64_t bh, int64_t T, int64_t d, bool causal) {
   return Workspace(aar_flash_bwd_workspace_bytes(bh, T, d));
 }
 
+// Flash forward workspace: the partials of the causal key-range split when
+// the shape may split (none otherwise).
+Workspace flash_fwd_workspace(int64_t bh, int64_t T, int64_t d, bool causal) {
+  return Workspace(aar_flash_fwd_workspace_bytes(bh, T, d, causal ? 1 : 0));
+}
+
 const float* fp(const Tensor& t) { return static_cast<const float*>(t.data()); }
 float* fp(Tensor& t) { return static_cast<float*>(t.data()); }
 
@@ -525,8 +531,9 @@ std::tuple<Tensor, Tensor> flash_forward_device(const FlashView& q, const FlashV
   put3(st + 3, k.s);
   put3(st + 6, v.s);
   put3(st + 9, oc);
+  Workspace ws = flash_fwd_workspace(B * H, T, d, causal);
   check_status(aar_flash_fwd_strided_f32(fp(q.t), fp(k.t), fp(v.t), fp(out), fp(lse), B, H, T, d, st,
-                                         causal ? 1 : 0, s, current_stream()),
+                                         causal ? 1 : 0, s, ws.data(), ws.bytes(), current_stream()),
                "flash_attention");
   return {out, lse};
 }
@@ -903,8 +910,9 @@ Tensor flash_attention_qkv(const Tensor& qkv, int64_t n_heads, bool causal) {
   put3(st + 9, po);
   const float s = 1.0f / std::sqrt(static_cast<float>(d));
   const float* p = fp(x);
+  Workspace ws = flash_fwd_workspace(B * n_heads, T, d, causal);
   check_status(aar_flash_fwd_strided_f32(p, p + D, p + 2 * D, fp(out), fp(lse), B, n_heads, T, d, st,
-                                         causal ? 1 : 0, s, current_stream()),
+                                         causal ? 1 : 0, s, ws.data(), ws.bytes(), current_stream()),
                "flash_attention_qkv");
   if (!qkv.requires_grad) return out;
   auto fn = std::make_shared<FlashQKVFunction>();

@@ -206,11 +206,21 @@ int aar_flash_bwd_f32(const float* q, const float* k, const float* v,
  * (q, k, v, o), 24 for the backward (q, k, v, o, dout, dq, dk, dv).  lse and
  * the workspace are contiguous [B*H, T].  128-bit paths need 16-byte aligned
  * pointers and d and all strides multiples of 4; other layouts take the
- * element-wise path.  The unstrided calls are these with contiguous strides. */
+ * element-wise path.  The unstrided calls are these with contiguous strides
+ * (the forward with no workspace). */
 int aar_flash_fwd_strided_f32(const float* q, const float* k, const float* v,
                               float* o, float* lse, int64_t B, int64_t H,
                               int64_t T, int64_t d, const int64_t* strides,
-                              int causal, float scale, void* stream);
+                              int causal, float scale,
+                              void* workspace, size_t workspace_bytes, void* stream);
+/* Workspace for the causal strided forward's key-range split (0 when the shape
+ * never splits; shape-only, no device needed).  With at least this much
+ * (16-byte aligned) and a grid of at most one round of resident workgroups,
+ * the longest half of the query blocks each run as two workgroups over the two
+ * halves of their key range, merged by a combine pass; with less, or a null
+ * workspace, every block is one workgroup.  Same results up to rounding.  No
+ * counterpart in the reference, whose forward keeps no workspace. */
+size_t aar_flash_fwd_workspace_bytes(int64_t bh, int64_t T, int64_t d, int causal);
 int aar_flash_bwd_strided_f32(const float* q, const float* k, const float* v,
                               const float* o, const float* lse, const float* dout,
                               float* dq, float* dk, float* dv,

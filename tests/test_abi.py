@@ -73,6 +73,17 @@ def test_abi_validates_before_touching_the_device():
     assert lib.aar_flash_bwd_fast_workspace_bytes(96, 4096, 64, 1) == d_rows + 96 * (128 * 129 // 2) * 4096
     assert lib.aar_flash_bwd_fast_workspace_bytes(96, 4096, 64, 0) == d_rows + 96 * 128 * 128 * 4096
     assert lib.aar_flash_bwd_fast_workspace_bytes(3, 45, 64, 1) == 768 + 3 * 3 * 4096  # ragged T: 540 B of D rows
+    # forward split partials: S = nqb/2 blocks x 2 halves x 128 rows, O rows of
+    # the padded head dim (256-byte aligned) then one log2-sum-exp per row
+    lib.aar_flash_fwd_workspace_bytes.restype = ctypes.c_size_t
+    lib.aar_flash_fwd_workspace_bytes.argtypes = [i64, i64, i64, ctypes.c_int]
+    rows = 96 * 4 * 2 * 128
+    assert lib.aar_flash_fwd_workspace_bytes(96, 1024, 64, 1) == rows * 64 * 4 + rows * 4
+    assert lib.aar_flash_fwd_workspace_bytes(2, 300, 30, 1) == 2 * 1 * 2 * 128 * (32 + 1) * 4
+    assert lib.aar_flash_fwd_workspace_bytes(96, 1024, 64, 0) == 0  # only the causal forward splits
+    assert lib.aar_flash_fwd_workspace_bytes(96, 4096, 64, 1) == 0  # 3072 workgroups: several rounds, no split
+    assert lib.aar_flash_fwd_workspace_bytes(3, 128, 64, 1) == 0  # one query block
+    assert lib.aar_flash_fwd_workspace_bytes(3, 100, 200, 1) == 0  # d > 128
     assert lib.aar_flash_bwd_fast_workspace_bytes(1 << 24, 1 << 24, 64, 0) == 2 ** 64 - 1  # saturates
     # token windows, dropout, causal mask: argument checks before any launch
     lib.aar_token_windows_i64.argtypes = [vp, i64, vp, i64, i64, vp, vp, vp, vp]

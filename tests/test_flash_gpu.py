@@ -343,7 +343,8 @@ def test_abi_strided_output_layout(gpu):
     L = abi.L
     i64p = ctypes.POINTER(ctypes.c_int64)
     vp, i64 = ctypes.c_void_p, ctypes.c_int64
-    L.aar_flash_fwd_strided_f32.argtypes = [vp] * 5 + [i64] * 4 + [i64p, ctypes.c_int, ctypes.c_float, vp]
+    L.aar_flash_fwd_strided_f32.argtypes = [vp] * 5 + [i64] * 4 + [i64p, ctypes.c_int, ctypes.c_float, vp,
+                                                                  ctypes.c_size_t, vp]
     L.aar_flash_bwd_strided_f32.argtypes = [vp] * 9 + [i64] * 4 + [i64p, ctypes.c_int, ctypes.c_float, vp,
                                                                   ctypes.c_size_t, vp]
     try:
@@ -355,7 +356,7 @@ def test_abi_strided_output_layout(gpu):
         pq, pkk, pv = px, px + 4 * D, px + 8 * D
         pout, plse = abi.empty(B * T * D), abi.empty(B * H * T)
         s = 1.0 / math.sqrt(d)
-        abi.check(L.aar_flash_fwd_strided_f32(pq, pkk, pv, pout, plse, B, H, T, d, st, 1, s, None))
+        abi.check(L.aar_flash_fwd_strided_f32(pq, pkk, pv, pout, plse, B, H, T, d, st, 1, s, None, 0, None))
         ro, rg = _packed_reference(qkv.reshape(B, T, 3 * D), H, True, do.reshape(B, T, D))
         assert_close(abi.get(pout, (B, T, D)), ro, TOL, "O")
         pdo = abi.put(do)
@@ -366,3 +367,49 @@ def test_abi_strided_output_layout(gpu):
         assert_close(abi.get(pg, (B, T, 3 * D)), rg, TOL, "dqkv")
     finally:
         abi.free()
+
+
+def _abi_forward(q, k, v, causal, split, offset=0):
+    """(O, lse) of the strided forward with contiguous strides, with the split
+    workspace (split=True) or none (every query block one workgroup)."""
+    bh, T, d = q.shape
+    abi = Abi()
+    L = abi.L
+    i64p = ctypes.POINTER(ctypes.c_int64)
+    vp, i64 = ctypes.c_void_p, ctypes.c_int64
+    L.aar_flash_fwd_strided_f32.argtypes = [vp] * 5 + [i64] * 4 + [i64p, ctypes.c_int, ctypes.c_float, vp,
+                                                                  ctypes.c_size_t, vp]
+    L.aar_flash_fwd_workspace_bytes.restype = ctypes.c_size_t
+    L.aar_flash_fwd_workspace_bytes.argtypes = [i64] * 3 + [ctypes.c_int]
+    try:
+        pq, pk, pv = (abi.put(t, offset) for t in (q, k, v))
+        po, pl = abi.empty(bh * T * d, offset), abi.empty(bh * T)
+        st = (ctypes.c_int64 * 12)(*([bh * T * d, T * d, d] * 4))
+        wsb = L.aar_flash_fwd_workspace_bytes(bh, T, d, int(causal)) if split else 0
+        if split:
+            assert wsb > 0
+        ws = abi.alloc(wsb) if wsb else None
+        abi.check(L.aar_flash_fwd_strided_f32(pq, pk, pv, po, pl, 1, bh, T, d, st, int(causal),
+                                              1.0 / math.sqrt(d), ws, wsb, None))
+        return abi.get(po, (bh, T, d)), abi.get(pl, (bh, T))
+    finally:
+        abi.free()
+
+
+@pytest.mark.parametrize("bh,T,d,offset", [(2, 300, 64, 0), (3, 1000, 64, 0), (1, 257, 128, 0), (2, 256, 32, 0),
+                                           (2, 300, 30, 0), (2, 390, 64, 1), (1, 2048, 64, 0)])
+def test_abi_forward_key_range_split(gpu, bh, T, d, offset):
+    """Causal forward with the key-range split (the longest half of the query
+    blocks as two workgroups each, merged by the combine pass) against the
+    oracle and against the unsplit launch.  offset=1 misaligns the operands,
+    which takes the element-wise load path."""
+    rng = np.random.default_rng(bh * 7919 + T + d)
+    q, k, v = (rng.standard_normal((bh, T, d)).astype(f32) for _ in range(3))
+    o_split, l_split = _abi_forward(q, k, v, True, True, offset)
+    o_whole, l_whole = _abi_forward(q, k, v, True, False, offset)
+    assert_close(o_split, O.attention(q, k, v, True), TOL, "O split")
+    assert_close(l_split, O.attention_lse(q, k, True), TOL, "lse split")
+    # same softmax over the same keys, merged from two halves: agreement far
+    # below the tolerance
+    assert_close(o_split, o_whole, 1e-5, "O split vs whole")
+    assert_close(l_split, l_whole, 1e-5, "lse split vs whole")
