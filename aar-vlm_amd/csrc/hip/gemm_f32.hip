@@ -35,6 +35,8 @@
 
 #include <algorithm>
 
+#include <type_traits>
+
 #include "common.hpp"
 
 namespace aar {
@@ -55,28 +57,45 @@ __device__ __forceinline__ void map_tile(int tiles_m, int tiles_n, int& tm, int&
   tn = in_group / rows;
 }
 
-// Epilogue: a wave's (32*TM) x (32*TN) accumulators to C, plus bias[col]
-// with BIAS (the fused epilogue of a linear layer: the same single fp32
-// addition as adding the bias to the stored product).  BIAS is a template
-// flag because the addition needs the accumulators in VGPRs: the kernels
-// without it store straight from the accumulators and keep their occupancy.
-// Accumulator layout of a 32x32 block: lane (lr, h), register r holds row
+// Epilogues (a template argument, because every one but the plain store
+// needs the accumulators in VGPRs: the kernels without one store straight
+// from the accumulators and keep their occupancy).  Each is the same fp32
+// operation as the separate op applied to the stored product:
+//   kEpiBias      C = acc + bias[col]            (linear layer: add_bias)
+//   kEpiBiasRelu  C = max(0, acc + bias[col])    (linear layer, then relu)
+//   kEpiMask      C = aux[row][col] > 0 ? acc : 0  (relu backward, aux = the
+//                 relu's output, which is positive exactly where its input is;
+//                 aux has C's layout)
+enum : int { kEpiNone = 0, kEpiBias = 1, kEpiBiasRelu = 2, kEpiMask = 3 };
+struct GemmEpi {
+  const float* bias;
+  const float* aux;
+};
+
+// Epilogue: a wave's (32*TM) x (32*TN) accumulators to C.  Accumulator
+// layout of a 32x32 block: lane (lr, h), register r holds row
 // 8*(r/4) + 4*h + (r%4), column lr.
-template <int TM, int TN, bool BIAS>
-__device__ __forceinline__ void store_tile(const f32x16 (&acc)[TM][TN], float* __restrict__ C,
-                                           const float* __restrict__ bias, int64_t M, int64_t N, int64_t ldc,
-                                           int64_t r0, int64_t c0, int lr, int h) {
+template <int TM, int TN, int EPI>
+__device__ __forceinline__ void store_tile(const f32x16 (&acc)[TM][TN], float* __restrict__ C, const GemmEpi& ep,
+                                           int64_t M, int64_t N, int64_t ldc, int64_t r0, int64_t c0, int lr,
+                                           int h) {
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
       const int64_t col = c0 + 32 * j + lr;
       float b = 0.f;
-      if constexpr (BIAS) b = col < N ? bias[col] : 0.f;
+      if constexpr (EPI == kEpiBias || EPI == kEpiBiasRelu) b = col < N ? ep.bias[col] : 0.f;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int64_t row = r0 + 32 * i + 8 * (r / 4) + 4 * h + (r % 4);
-        if (row < M && col < N) C[row * ldc + col] = BIAS ? acc[i][j][r] + b : acc[i][j][r];
+        if (row < M && col < N) {
+          float v = acc[i][j][r];
+          if constexpr (EPI == kEpiBias) v = v + b;
+          if constexpr (EPI == kEpiBiasRelu) v = fmaxf(0.0f, v + b);
+          if constexpr (EPI == kEpiMask) v = ep.aux[row * ldc + col] > 0.0f ? v : 0.0f;
+          C[row * ldc + col] = v;
+        }
       }
     }
   }
@@ -165,12 +184,12 @@ struct TileLoader {
 
 // WPE: waves per SIMD the register allocation must allow (resident
 // workgroups per CU x waves per workgroup / 4).
-template <int BM, int BN, int BK, int WM, int WN, int WPE, bool A_KC, bool B_KC, bool BIAS>
+template <int BM, int BN, int BK, int WM, int WN, int WPE, bool A_KC, bool B_KC, int EPI>
 __global__ void __launch_bounds__((BM / WM) * (BN / WN) * 64, WPE)
 gemm_f32_kernel(const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C,
                 int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc,
                 int64_t k_per_split, int64_t split_stride, int tiles_m, int tiles_n, int64_t sA, int64_t sB,
-                int64_t sC, const float* __restrict__ bias) {
+                int64_t sC, GemmEpi ep) {
   constexpr int NWM = BM / WM;
   constexpr int NT = NWM * (BN / WN) * 64;
   constexpr int TM = WM / 32;
@@ -257,7 +276,7 @@ gemm_f32_kernel(const float* __restrict__ A, const float* __restrict__ B, float*
 
   // Accumulator layout of a 32x32 block: lane (lr, h), register r holds
   // row 8*(r/4) + 4*h + (r%4), column lr.
-  store_tile<TM, TN, BIAS>(acc, C, bias, M, N, ldc, m0 + wm0, n0 + wn0, lr, h);
+  store_tile<TM, TN, EPI>(acc, C, ep, M, N, ldc, m0 + wm0, n0 + wn0, lr, h);
 }
 
 // ------------------------------------------------------------------ DMA path
@@ -391,12 +410,12 @@ __device__ __forceinline__ void ring_barrier() {
   asm volatile("" ::: "memory");
 }
 
-template <int BM, int BN, int BK, int WM, int WN, int WPE, int S, bool A_KC, bool B_KC, bool BIAS>
+template <int BM, int BN, int BK, int WM, int WN, int WPE, int S, bool A_KC, bool B_KC, int EPI>
 __global__ void __launch_bounds__((BM / WM) * (BN / WN) * 64, WPE)
 gemm_f32_dma_kernel(const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C,
                     int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc,
                     int64_t k_per_split, int64_t split_stride, int tiles_m, int tiles_n, int64_t sA,
-                    int64_t sB, int64_t sC, const float* __restrict__ bias) {
+                    int64_t sB, int64_t sC, GemmEpi ep) {
   constexpr int NWM = BM / WM;
   constexpr int NW = NWM * (BN / WN);
   constexpr int TM = WM / 32;
@@ -499,35 +518,48 @@ gemm_f32_dma_kernel(const float* __restrict__ A, const float* __restrict__ B, fl
     }
   }
 
-  store_tile<TM, TN, BIAS>(acc, C, bias, M, N, ldc, m0 + wm0, n0 + wn0, lr, h);
+  store_tile<TM, TN, EPI>(acc, C, ep, M, N, ldc, m0 + wm0, n0 + wn0, lr, h);
 }
 
 // C[i] = sum_s W[s*stride + i], s in order 0..splits-1 (deterministic), four
 // consecutive outputs per thread with 128-bit loads (stride % 4 == 0 and
 // 16-byte aligned W/C); the split loop is unrolled so its loads overlap.
-// A bias (row-broadcast over the N columns; the vector kernel needs N % 4 == 0)
-// is added to the finished sum.
+// The epilogue (kEpi*; bias row-broadcast over the N columns, aux with C's
+// layout; the vector kernel needs N % 4 == 0) is applied to the finished sum.
 __global__ void __launch_bounds__(256)
 splitk_reduce_vec_kernel(const f32x4* __restrict__ W, f32x4* __restrict__ C, int64_t n4, int64_t stride4,
-                         int splits, const f32x4* __restrict__ bias, int64_t n_cols4) {
+                         int splits, int epi, const f32x4* __restrict__ bias, const f32x4* __restrict__ aux,
+                         int64_t n_cols4) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n4) return;
   f32x4 s = W[i];
 #pragma unroll 8
   for (int p = 1; p < splits; ++p) s += W[p * stride4 + i];
-  if (bias) s += bias[i % n_cols4];
+  if (epi == kEpiBias || epi == kEpiBiasRelu) s += bias[i % n_cols4];
+  if (epi == kEpiBiasRelu) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) s[e] = fmaxf(0.0f, s[e]);
+  }
+  if (epi == kEpiMask) {
+    const f32x4 a = aux[i];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) s[e] = a[e] > 0.0f ? s[e] : 0.0f;
+  }
   C[i] = s;
 }
 
 __global__ void __launch_bounds__(256)
 splitk_reduce_kernel(const float* __restrict__ W, float* __restrict__ C, int64_t n, int64_t stride,
-                     int splits, const float* __restrict__ bias, int64_t n_cols) {
+                     int splits, int epi, const float* __restrict__ bias, const float* __restrict__ aux,
+                     int64_t n_cols) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
   float s = W[i];
 #pragma unroll 8
   for (int p = 1; p < splits; ++p) s += W[p * stride + i];
-  if (bias) s += bias[i % n_cols];
+  if (epi == kEpiBias || epi == kEpiBiasRelu) s += bias[i % n_cols];
+  if (epi == kEpiBiasRelu) s = fmaxf(0.0f, s);
+  if (epi == kEpiMask) s = aux[i] > 0.0f ? s : 0.0f;
   C[i] = s;
 }
 
@@ -615,7 +647,7 @@ constexpr Batch kSingle{1, 0, 0, 0};
 template <int BM, int BN, int BK, int WM, int WN, int RES, int STAGES, bool A_KC, bool B_KC>
 int launch_cfg(bool vec, const float* A, const float* B, float* C, int64_t M, int64_t N, int64_t K,
                int64_t lda, int64_t ldb, int64_t ldc, int splits, int64_t kps, int64_t split_stride,
-               const Batch& bt, const float* bias, hipStream_t st) {
+               const Batch& bt, int epi, const GemmEpi& ep, hipStream_t st) {
   constexpr int kWaves = (BM / WM) * (BN / WN);
   constexpr int kWpe = (RES * kWaves + 3) / 4;
   const int tiles_m = (int)ceil_div(M, (int64_t)BM);
@@ -624,30 +656,40 @@ int launch_cfg(bool vec, const float* A, const float* B, float* C, int64_t M, in
   if ((int64_t)tiles_m * tiles_n * kWaves * 64 > (int64_t)UINT32_MAX) return AAR_EUNSUPPORTED;
   dim3 grid((unsigned)(tiles_m * tiles_n), (unsigned)splits, (unsigned)bt.count);
   dim3 block(kWaves * 64);
-  if (vec && bias)
-    gemm_f32_dma_kernel<BM, BN, BK, WM, WN, kWpe, STAGES, A_KC, B_KC, true><<<grid, block, 0, st>>>(
-        A, B, C, M, N, K, lda, ldb, ldc, kps, split_stride, tiles_m, tiles_n, bt.sA, bt.sB, bt.sC, bias);
-  else if (vec)
-    gemm_f32_dma_kernel<BM, BN, BK, WM, WN, kWpe, STAGES, A_KC, B_KC, false><<<grid, block, 0, st>>>(
-        A, B, C, M, N, K, lda, ldb, ldc, kps, split_stride, tiles_m, tiles_n, bt.sA, bt.sB, bt.sC, nullptr);
-  else if (bias)
-    gemm_f32_kernel<BM, BN, BK, WM, WN, kWpe, A_KC, B_KC, true><<<grid, block, 0, st>>>(
-        A, B, C, M, N, K, lda, ldb, ldc, kps, split_stride, tiles_m, tiles_n, bt.sA, bt.sB, bt.sC, bias);
-  else
-    gemm_f32_kernel<BM, BN, BK, WM, WN, kWpe, A_KC, B_KC, false><<<grid, block, 0, st>>>(
-        A, B, C, M, N, K, lda, ldb, ldc, kps, split_stride, tiles_m, tiles_n, bt.sA, bt.sB, bt.sC, nullptr);
-  return launch_status();
+  auto go = [&](auto epi_tag) {
+    constexpr int E = decltype(epi_tag)::value;
+    if (vec)
+      gemm_f32_dma_kernel<BM, BN, BK, WM, WN, kWpe, STAGES, A_KC, B_KC, E><<<grid, block, 0, st>>>(
+          A, B, C, M, N, K, lda, ldb, ldc, kps, split_stride, tiles_m, tiles_n, bt.sA, bt.sB, bt.sC, ep);
+    else
+      gemm_f32_kernel<BM, BN, BK, WM, WN, kWpe, A_KC, B_KC, E><<<grid, block, 0, st>>>(
+          A, B, C, M, N, K, lda, ldb, ldc, kps, split_stride, tiles_m, tiles_n, bt.sA, bt.sB, bt.sC, ep);
+    return launch_status();
+  };
+  // bias + relu is instantiated for the linear layer's x W^T (NT) only, the
+  // relu mask for its input gradient dY W (NN) only.
+  switch (epi) {
+    case kEpiNone: return go(std::integral_constant<int, kEpiNone>{});
+    case kEpiBias: return go(std::integral_constant<int, kEpiBias>{});
+    case kEpiBiasRelu:
+      if constexpr (A_KC && B_KC) return go(std::integral_constant<int, kEpiBiasRelu>{});
+      return AAR_EUNSUPPORTED;
+    case kEpiMask:
+      if constexpr (A_KC && !B_KC) return go(std::integral_constant<int, kEpiMask>{});
+      return AAR_EUNSUPPORTED;
+    default: return AAR_EINVAL;
+  }
 }
 
 template <bool A_KC, bool B_KC>
 int launch_op(int cfg, bool vec, const float* A, const float* B, float* C, int64_t M, int64_t N,
               int64_t K, int64_t lda, int64_t ldb, int64_t ldc, int splits, int64_t kps,
-              int64_t split_stride, const Batch& bt, const float* bias, hipStream_t st) {
+              int64_t split_stride, const Batch& bt, int epi, const GemmEpi& ep, hipStream_t st) {
 #define AAR_GEMM_CFG(I)                                                                                   \
   case I:                                                                                                 \
     return launch_cfg<kCfgs[I].bm, kCfgs[I].bn, kCfgs[I].bk, kCfgs[I].wm, kCfgs[I].wn, kCfgs[I].resident, \
                       kCfgs[I].stages, A_KC, B_KC>(vec, A, B, C, M, N, K, lda, ldb, ldc, splits, kps, split_stride, \
-                                                   bt, bias, st);
+                                                   bt, epi, ep, st);
   switch (cfg) {
     AAR_GEMM_CFG(0)
     AAR_GEMM_CFG(1)
@@ -691,40 +733,41 @@ int default_ld(int op, int64_t M, int64_t N, int64_t K, int64_t& lda, int64_t& l
 
 int dispatch_op(int op, int cfg, bool vec, const float* A, const float* B, float* C, int64_t M, int64_t N,
                 int64_t K, int64_t lda, int64_t ldb, int64_t ldc, int splits, int64_t kps, int64_t split_stride,
-                const Batch& bt, hipStream_t st, const float* bias = nullptr) {
+                const Batch& bt, hipStream_t st, int epi = kEpiNone, const GemmEpi& ep = GemmEpi{}) {
   switch (op) {
     case AAR_GEMM_NN:
-      return launch_op<true, false>(cfg, vec, A, B, C, M, N, K, lda, ldb, ldc, splits, kps, split_stride, bt, bias,
-                                    st);
+      return launch_op<true, false>(cfg, vec, A, B, C, M, N, K, lda, ldb, ldc, splits, kps, split_stride, bt, epi,
+                                    ep, st);
     case AAR_GEMM_NT:
-      return launch_op<true, true>(cfg, vec, A, B, C, M, N, K, lda, ldb, ldc, splits, kps, split_stride, bt, bias,
-                                   st);
+      return launch_op<true, true>(cfg, vec, A, B, C, M, N, K, lda, ldb, ldc, splits, kps, split_stride, bt, epi,
+                                   ep, st);
     default:
       return launch_op<false, false>(cfg, vec, A, B, C, M, N, K, lda, ldb, ldc, splits, kps, split_stride, bt,
-                                     bias, st);
+                                     epi, ep, st);
   }
 }
 
-// bias (may be null): added to every row of C, in the epilogue of an
-// unsplit launch or after the split-K reduction.
+// epi / ep: the epilogue (kEpi*), applied in an unsplit launch or after the
+// split-K reduction.  C is contiguous (ldc = N), and so is ep.aux.
 int run_gemm(int op, int64_t M, int64_t N, int64_t K, const float* A, const float* B, float* C,
-             void* workspace, const Plan& p, hipStream_t st, const float* bias = nullptr) {
+             void* workspace, const Plan& p, hipStream_t st, int epi = kEpiNone, const GemmEpi& ep = GemmEpi{}) {
   int64_t lda, ldb;
   default_ld(op, M, N, K, lda, ldb);
   const bool vec = gemm_vec_ok(op, M, N, K, A, B, lda, ldb);
   float* out = p.splits > 1 ? static_cast<float*>(workspace) : C;
   const int64_t split_stride = p.splits > 1 ? M * N : 0;
   int rc = dispatch_op(op, p.cfg, vec, A, B, out, M, N, K, lda, ldb, N, p.splits, p.k_per_split, split_stride,
-                       kSingle, st, p.splits > 1 ? nullptr : bias);
+                       kSingle, st, p.splits > 1 ? kEpiNone : epi, ep);
   if (rc != AAR_OK || p.splits <= 1) return rc;
   const int64_t n = M * N;
-  if (n % 4 == 0 && aligned16(out) && aligned16(C) && (!bias || (N % 4 == 0 && aligned16(bias)))) {
+  if (n % 4 == 0 && aligned16(out) && aligned16(C) && (!ep.bias || (N % 4 == 0 && aligned16(ep.bias))) &&
+      (!ep.aux || aligned16(ep.aux))) {
     splitk_reduce_vec_kernel<<<dim3((unsigned)ceil_div(n / 4, (int64_t)256)), dim3(256), 0, st>>>(
-        reinterpret_cast<const f32x4*>(out), reinterpret_cast<f32x4*>(C), n / 4, split_stride / 4, p.splits,
-        reinterpret_cast<const f32x4*>(bias), N / 4);
+        reinterpret_cast<const f32x4*>(out), reinterpret_cast<f32x4*>(C), n / 4, split_stride / 4, p.splits, epi,
+        reinterpret_cast<const f32x4*>(ep.bias), reinterpret_cast<const f32x4*>(ep.aux), N / 4);
   } else {
-    splitk_reduce_kernel<<<dim3((unsigned)ceil_div(n, (int64_t)256)), dim3(256), 0, st>>>(out, C, n, split_stride,
-                                                                                         p.splits, bias, N);
+    splitk_reduce_kernel<<<dim3((unsigned)ceil_div(n, (int64_t)256)), dim3(256), 0, st>>>(
+        out, C, n, split_stride, p.splits, epi, ep.bias, ep.aux, N);
   }
   return launch_status();
 }
@@ -775,7 +818,33 @@ extern "C" int aar_gemm_f32_bias(int op, int64_t M, int64_t N, int64_t K, const 
   const int chk = check_gemm_args(op, M, N, K, A, B, C, stream);
   if (chk != AAR_OK) return chk;
   const Plan p = plan_gemm(op, M, N, K, workspace ? workspace_bytes : 0, workspace != nullptr);
-  return run_gemm(op, M, N, K, A, B, C, workspace, p, as_stream(stream), bias);
+  return run_gemm(op, M, N, K, A, B, C, workspace, p, as_stream(stream), kEpiBias, GemmEpi{bias, nullptr});
+}
+
+extern "C" int aar_gemm_f32_bias_relu(int op, int64_t M, int64_t N, int64_t K, const float* A, const float* B,
+                                      const float* bias, float* C, void* workspace, size_t workspace_bytes,
+                                      void* stream) {
+  if (op < 0 || op > 2 || M < 0 || N < 0 || K < 0) return AAR_EINVAL;
+  if (M == 0 || N == 0) return AAR_OK;
+  if (!bias) return AAR_EINVAL;
+  if (op != AAR_GEMM_NT || K == 0) return AAR_EUNSUPPORTED;
+  const int chk = check_gemm_args(op, M, N, K, A, B, C, stream);
+  if (chk != AAR_OK) return chk;
+  const Plan p = plan_gemm(op, M, N, K, workspace ? workspace_bytes : 0, workspace != nullptr);
+  return run_gemm(op, M, N, K, A, B, C, workspace, p, as_stream(stream), kEpiBiasRelu, GemmEpi{bias, nullptr});
+}
+
+extern "C" int aar_gemm_f32_relu_mask(int op, int64_t M, int64_t N, int64_t K, const float* A, const float* B,
+                                      const float* mask, float* C, void* workspace, size_t workspace_bytes,
+                                      void* stream) {
+  if (op < 0 || op > 2 || M < 0 || N < 0 || K < 0) return AAR_EINVAL;
+  if (M == 0 || N == 0) return AAR_OK;
+  if (!mask) return AAR_EINVAL;
+  if (op != AAR_GEMM_NN) return AAR_EUNSUPPORTED;
+  const int chk = check_gemm_args(op, M, N, K, A, B, C, stream);
+  if (chk != AAR_OK) return chk == 1 ? AAR_OK : chk;  // K == 0: C = 0, which the mask keeps
+  const Plan p = plan_gemm(op, M, N, K, workspace ? workspace_bytes : 0, workspace != nullptr);
+  return run_gemm(op, M, N, K, A, B, C, workspace, p, as_stream(stream), kEpiMask, GemmEpi{nullptr, mask});
 }
 
 extern "C" int aar_gemm_f32_tile_config(int config, int* tile_m, int* tile_n, int* tile_k) {

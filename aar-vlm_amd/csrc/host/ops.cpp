@@ -779,6 +779,89 @@ Tensor linear(const Tensor& x, const Tensor& w, const Tensor& b) {
   return out;
 }
 
+// The feed-forward composition linear(relu(linear(x, W1, b1)), W2, b2) of the
+// GPT block (add_bias(matmul_a_bt(.)) with a relu between, aargrad/nn.py:101-122)
+// in three GEMM launches: bias + relu in the first layer's epilogue, and in
+// the backward the relu's mask (h > 0, h = its output) in the epilogue of
+// dh = g W2.  The other gradients are LinearFunction's: same values and
+// gradients as the composition, bit for bit.
+class MlpReluFunction : public Function {
+ public:
+  Tensor saved_x, saved_w1, saved_w2, saved_h;  // x and h as [rows, features]
+  std::vector<int64_t> x_shape;
+  std::vector<Tensor> backward(const Tensor& g) override {
+    const int64_t N2 = saved_w2.shape[0], H = saved_w1.shape[0];
+    const int64_t rows = saved_h.shape[0];
+    Tensor gc = as_view(as_contig(g), {rows, N2});
+    Tensor db2 = Tensor::empty({N2}, DType::Fp32, Device::CUDA);
+    Tensor db1 = Tensor::empty({H}, DType::Fp32, Device::CUDA);
+    {
+      Workspace ws(aar_colsum_workspace_bytes(rows, N2));
+      check_status(aar_colsum_f32(fp(gc), fp(db2), rows, N2, ws.data(), ws.bytes(), current_stream()),
+                   "mlp backward");
+    }
+    Tensor dw2 = matmul_at_b_no_grad(gc, saved_h);
+    Tensor dh = Tensor::empty({rows, H}, DType::Fp32, Device::CUDA);
+    if (dh.numel() != 0) {
+      Workspace ws(aar_gemm_f32_workspace_bytes(AAR_GEMM_NN, rows, H, N2));
+      check_status(aar_gemm_f32_relu_mask(AAR_GEMM_NN, rows, H, N2, fp(gc), fp(saved_w2), fp(saved_h), fp(dh),
+                                          ws.data(), ws.bytes(), current_stream()),
+                   "mlp backward");
+    }
+    {
+      Workspace ws(aar_colsum_workspace_bytes(rows, H));
+      check_status(aar_colsum_f32(fp(dh), fp(db1), rows, H, ws.data(), ws.bytes(), current_stream()),
+                   "mlp backward");
+    }
+    Tensor dx = as_view(matmul_no_grad(dh, saved_w1), x_shape);
+    return {dx, matmul_at_b_no_grad(dh, saved_x), db1, dw2, db2};
+  }
+  const char* name() const override { return "MlpReluFunction"; }
+};
+
+Tensor mlp_relu(const Tensor& x, const Tensor& w1, const Tensor& b1, const Tensor& w2, const Tensor& b2) {
+  if (w1.shape.size() != 2 || w2.shape.size() != 2 || x.shape.empty() || w1.shape[0] == 0 ||
+      x.shape.back() == 0) {
+    return linear(relu(linear(x, w1, b1)), w2, b2);  // the composition's checks and edge cases
+  }
+  // The checks (and messages) of both layers' matmul_a_bt and add_bias.
+  if (x.shape.size() < 2 || x.dtype != DType::Fp32 || w1.dtype != DType::Fp32 || w2.dtype != DType::Fp32 ||
+      b1.dtype != DType::Fp32 || b2.dtype != DType::Fp32 || x.device != w1.device || x.device != w2.device ||
+      x.device != b1.device || x.device != b2.device || x.shape.back() != w1.shape[1] ||
+      w2.shape[1] != w1.shape[0] || b1.shape.size() != 1 || b2.shape.size() != 1 || b1.shape[0] != w1.shape[0] ||
+      b2.shape[0] != w2.shape[0]) {
+    return linear(relu(linear(x, w1, b1)), w2, b2);  // raises as the composition does
+  }
+  if (x.device == Device::CPU) throw_cpu_compute("linear");
+  Tensor xc = as_contig(x), w1c = as_contig(w1), b1c = as_contig(b1), w2c = as_contig(w2), b2c = as_contig(b2);
+  const int64_t d = x.shape.back(), H = w1.shape[0], N2 = w2.shape[0];
+  const int64_t rows = static_cast<int64_t>(x.numel()) / d;
+  Tensor x2 = as_view(xc, {rows, d});
+  Tensor h = Tensor::empty({rows, H}, DType::Fp32, Device::CUDA);
+  if (h.numel() != 0) {
+    Workspace ws(aar_gemm_f32_workspace_bytes(AAR_GEMM_NT, rows, H, d));
+    check_status(aar_gemm_f32_bias_relu(AAR_GEMM_NT, rows, H, d, fp(x2), fp(w1c), fp(b1c), fp(h), ws.data(),
+                                        ws.bytes(), current_stream()),
+                 "linear");
+  }
+  std::vector<int64_t> out_shape(x.shape.begin(), x.shape.end() - 1);
+  out_shape.push_back(N2);
+  Tensor out = as_view(linear_no_grad(h, w2c, b2c), out_shape);
+  if (!xc.requires_grad && !w1c.requires_grad && !b1c.requires_grad && !w2c.requires_grad && !b2c.requires_grad) {
+    return out;
+  }
+  auto fn = std::make_shared<MlpReluFunction>();
+  for (const Tensor* t : {&xc, &w1c, &b1c, &w2c, &b2c}) fn->record_input(*t);
+  fn->saved_x = x2;
+  fn->saved_w1 = w1c;
+  fn->saved_w2 = w2c;
+  fn->saved_h = h;
+  fn->x_shape = x.shape;
+  out.requires_grad = true;
+  out.grad_fn = fn;
+  return out;
+}
+
 Tensor matmul_at_b(const Tensor& a, const Tensor& b) {
   if (a.shape.size() != 2 || b.shape.size() != 2) {
     throw std::invalid_argument("matmul_at_b: inputs must be 2D");

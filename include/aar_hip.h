@@ -105,6 +105,23 @@ int aar_gemm_f32(int op, int64_t M, int64_t N, int64_t K,
 int aar_gemm_f32_bias(int op, int64_t M, int64_t N, int64_t K, const float* A, const float* B,
                       const float* bias, float* C, void* workspace, size_t workspace_bytes, void* stream);
 
+/* C = max(0, A W^T + bias[col]): the linear layer followed by relu, with both
+ * in the GEMM epilogue; bit-identical to aar_gemm_f32_bias then relu.  op must
+ * be AAR_GEMM_NT (else AAR_EUNSUPPORTED, as is K == 0).  Replaces
+ * matmul_a_bt_cuda + add_bias_cuda + relu_cuda of the MLP's first layer
+ * (cppsrc/ops/matmul.cpp:11, elementwise.cpp:24 and :15). */
+int aar_gemm_f32_bias_relu(int op, int64_t M, int64_t N, int64_t K, const float* A, const float* B,
+                           const float* bias, float* C, void* workspace, size_t workspace_bytes,
+                           void* stream);
+/* C = mask > 0 ? A B : 0 elementwise (mask [M, N] contiguous, the relu's
+ * output): the relu backward applied in the GEMM epilogue of the next layer's
+ * input gradient dY W; bit-identical to aar_gemm_f32 then relu_backward.  op
+ * must be AAR_GEMM_NN (else AAR_EUNSUPPORTED).  Replaces matmul_cuda +
+ * relu_backward_cuda (cppsrc/ops/matmul.cpp:10, elementwise.cpp:17). */
+int aar_gemm_f32_relu_mask(int op, int64_t M, int64_t N, int64_t K, const float* A, const float* B,
+                           const float* mask, float* C, void* workspace, size_t workspace_bytes,
+                           void* stream);
+
 /* Batched GEMM with explicit leading dimensions: for b in [0, batch),
  * C_b = op(A_b, B_b) with A_b = A + b*strideA (and so on), op as in
  * aar_gemm_f32 but rows of A/B/C at lda/ldb/ldc elements (lda >= K for NN/NT,

@@ -58,6 +58,17 @@ def test_abi_validates_before_touching_the_device():
     assert lib.aar_gemm_f32_bias(3, 2, 2, 2, None, None, None, None, None, 0, None) == -1  # bad op
     assert lib.aar_gemm_f32_bias(1, 2, 2, 2, None, None, None, None, None, 0, None) == -1  # no bias
     assert lib.aar_gemm_f32_bias(1, 2, 0, 2, None, None, None, None, None, 0, None) == 0  # empty output
+    # fused relu epilogues: bias + relu on the NT product only, the relu mask on the NN product only
+    for f in (lib.aar_gemm_f32_bias_relu, lib.aar_gemm_f32_relu_mask):
+        f.argtypes = lib.aar_gemm_f32_bias.argtypes
+    x = ctypes.c_void_p(16)  # never dereferenced: every call below returns before any device work
+    assert lib.aar_gemm_f32_bias_relu(1, 2, 2, 2, None, None, None, None, None, 0, None) == -1  # no bias
+    assert lib.aar_gemm_f32_bias_relu(0, 2, 2, 2, None, None, x, None, None, 0, None) == -3  # NN
+    assert lib.aar_gemm_f32_bias_relu(1, 2, 2, 0, None, None, x, None, None, 0, None) == -3  # K == 0
+    assert lib.aar_gemm_f32_bias_relu(1, 0, 2, 2, None, None, None, None, None, 0, None) == 0  # empty output
+    assert lib.aar_gemm_f32_relu_mask(0, 2, 2, 2, None, None, None, None, None, 0, None) == -1  # no mask
+    assert lib.aar_gemm_f32_relu_mask(1, 2, 2, 2, None, None, x, None, None, 0, None) == -3  # NT
+    assert lib.aar_gemm_f32_relu_mask(3, 2, 2, 2, None, None, x, None, None, 0, None) == -1  # bad op
     assert lib.aar_gemm_f32_bias(1, 2, 2, 0, None, None, 16, None, None, 0, None) == -3  # K = 0: not a product
     lib.aar_softmax_fwd_f32.argtypes = [vp, vp, i64, i64, vp]
     assert lib.aar_softmax_fwd_f32(None, None, 4, 0, None) == -1
