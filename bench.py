@@ -710,7 +710,7 @@ def main() -> int:
             "unit": "TFLOP/s",
             "frac": round(tflops / PEAK_FP32_MFMA_TFLOPS, 4),
             "traffic": load_traffic("gemm_f32_nn_4096"),
-            "kernel": "gemm_f32_dma_kernel<256, 256, 32, 64, 128, 2, 2, true, false, false> (NN, no bias; one launch per step)",
+            "kernel": "gemm_f32_dma_kernel<256, 256, 32, 64, 128, 2, 2, true, false, 0> (NN, plain epilogue; one launch per step)",
             "algorithmic_flops_per_launch": flops,
         },
         "cpu_baseline": cpu,
