@@ -196,6 +196,11 @@ def test_validation_errors_match_reference(ag):
         ag._core._linear(f(2, 3), f(4, 3), f(1, 4))
     with pytest.raises(ValueError, match="bias size must match"):
         ag._core._linear(f(2, 3), f(4, 3), f(5))
+    # the fused MLP raises what the composition linear -> relu -> linear raises
+    with pytest.raises(ValueError, match="contraction dim mismatch"):
+        ag._core._mlp_relu(f(2, 3), f(4, 2), f(4), f(5, 4), f(5))
+    with pytest.raises(ValueError, match="bias size must match"):
+        ag._core._mlp_relu(f(2, 3), f(4, 3), f(3), f(5, 4), f(5))
 
 
 def test_host_compute_fails_loudly(ag):
@@ -206,7 +211,8 @@ def test_host_compute_fails_loudly(ag):
                  lambda: ag.flash_attention(f(1, 4, 8), f(1, 4, 8), f(1, 4, 8), True),
                  lambda: ag.add(f(3), f(3)),
                  lambda: ag.sum_all(f(3)),
-                 lambda: ag._core._linear(f(2, 3), f(4, 3), f(4))):
+                 lambda: ag._core._linear(f(2, 3), f(4, 3), f(4)),
+                 lambda: ag._core._mlp_relu(f(2, 3), f(4, 3), f(4), f(5, 4), f(5))):
         with pytest.raises(RuntimeError, match="GPU only"):
             call()
 
