@@ -176,8 +176,8 @@ PYBIND11_MODULE(_core, m) {
         "add_bias(matmul_a_bt(x, W), b).");
   m.def("_mlp_relu", &mlp_relu, py::arg("x"), py::arg("w1"), py::arg("b1"), py::arg("w2"), py::arg("b2"),
         gil_release(),
-        "linear(relu(linear(x, w1, b1)), w2, b2) in three GEMMs with the bias, the relu and its backward "
-        "mask in their epilogues: the values and gradients of the composition.");
+        "linear(relu(linear(x, w1, b1)), w2, b2) with bias + relu in the first GEMM's epilogue: the "
+        "values and gradients of the composition.");
   m.def("_token_windows", &token_windows, py::arg("tokens"), py::arg("starts"), py::arg("seq_len"),
         gil_release(),
         "(x, y) int64 [len(starts), seq_len] with x[b] = tokens[s:s+T], y[b] = tokens[s+1:s+T+1], "

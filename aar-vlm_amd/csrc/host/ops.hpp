@@ -23,9 +23,8 @@ Tensor matmul_at_b(const Tensor& a, const Tensor& b);
 // nn.Linear with a bias (aargrad/nn.py:101-105: matmul_a_bt then add_bias)
 // as one GEMM with the bias added in its epilogue; same values and gradients.
 Tensor linear(const Tensor& x, const Tensor& w, const Tensor& b);
-// linear(relu(linear(x, w1, b1)), w2, b2) in three GEMM launches with the
-// bias, the relu and its backward mask in their epilogues; same values and
-// gradients as the composition.
+// linear(relu(linear(x, w1, b1)), w2, b2) with bias + relu in the first
+// GEMM's epilogue; same values and gradients as the composition.
 Tensor mlp_relu(const Tensor& x, const Tensor& w1, const Tensor& b1, const Tensor& w2, const Tensor& b2);
 
 // Row-wise (cppsrc/ops/softmax.cpp:75-96, cppsrc/ops/layernorm.cpp:174-227).

@@ -463,8 +463,8 @@ class GPT:
             x = ag.add(x, ag.matmul_a_bt(a, wout))
             h = ag.layernorm(x, l2w, l2b, 1e-5)
             # the MLP linear -> relu -> linear (nn.Linear with bias) as one fused op:
-            # bias and relu in the first GEMM's epilogue, the relu mask in the
-            # backward's dh GEMM, the second bias in its GEMM's epilogue
+            # bias and relu in the first GEMM's epilogue, the second bias in its
+            # GEMM's epilogue
             x = ag.add(x, ag._core._mlp_relu(h, f1w, f1b, f2w, f2b))
         x = ag.layernorm(x, p[-3], p[-2], 1e-5)
         return ag.matmul_a_bt(x, p[-1])

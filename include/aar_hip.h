@@ -117,7 +117,9 @@ int aar_gemm_f32_bias_relu(int op, int64_t M, int64_t N, int64_t K, const float*
  * output): the relu backward applied in the GEMM epilogue of the next layer's
  * input gradient dY W; bit-identical to aar_gemm_f32 then relu_backward.  op
  * must be AAR_GEMM_NN (else AAR_EUNSUPPORTED).  Replaces matmul_cuda +
- * relu_backward_cuda (cppsrc/ops/matmul.cpp:10, elementwise.cpp:17). */
+ * relu_backward_cuda (cppsrc/ops/matmul.cpp:10, elementwise.cpp:17).  On
+ * MI355X at 16384x1536x384 it runs slower than the GEMM plus the separate
+ * mask pass, so the host MLP op uses those. */
 int aar_gemm_f32_relu_mask(int op, int64_t M, int64_t N, int64_t K, const float* A, const float* B,
                            const float* mask, float* C, void* workspace, size_t workspace_bytes,
                            void* stream);

@@ -1,12 +1,13 @@
 """The fused feed-forward block _mlp_relu(x, W1, b1, W2, b2): bias + relu in
-the first GEMM's epilogue, and in the backward the relu mask (h > 0) in the
-epilogue of dh = g W2.  Against the composition
+the first GEMM's epilogue; the backward takes the relu mask from the saved
+output h.  Against the composition
 linear(relu(linear(x, W1, b1)), W2, b2) of the same backend (aargrad/nn.py:101-122,
 the GPT block's MLP) the values and all five gradients must be bit-identical:
 each epilogue performs the same fp32 operation as the separate op.  Cases
 cover the unsplit DMA path, the register (unaligned) path and split-K with the
-vector and the scalar reduce for both epilogues; one case rechecks the result
-against the oracle at the GEMM tolerance."""
+vector and the scalar reduce; one case rechecks the result against the oracle
+at the GEMM tolerance.  The C-ABI relu-mask GEMM (aar_gemm_f32_relu_mask, which
+the op does not use) is checked against the GEMM followed by relu backward."""
 from __future__ import annotations
 
 import numpy as np
@@ -14,7 +15,9 @@ import pytest
 
 import oracle as O
 from conftest import assert_close, gemm_tol
-from devutil import dev, host
+import ctypes
+
+from devutil import Abi, dev, host
 from test_linear_gpu import _split_count
 
 pytestmark = pytest.mark.gpu
@@ -26,8 +29,8 @@ CASES = [
     ((3, 50), 17, 33, 65),       # unaligned everywhere: register path, scalar epilogue
     ((64,), 4096, 96, 64),       # forward bias+relu under split-K, vector reduce
     ((33,), 4999, 30, 7),        # forward split-K, scalar reduce
-    ((64,), 64, 96, 8192),       # backward mask under split-K (K = 8192 outputs), vector reduce
-    ((33,), 16, 30, 4999),       # backward mask under split-K, scalar reduce
+    ((64,), 64, 96, 8192),       # backward dh GEMM under split-K (K = 8192 outputs), vector reduce
+    ((33,), 16, 30, 4999),       # backward dh GEMM under split-K, scalar reduce
 ]
 
 
@@ -86,3 +89,30 @@ def test_mlp_no_grad_and_errors(gpu):
     assert not out.requires_grad and out.shape == [8, 4]
     with pytest.raises(ValueError):  # W2's in-features must match W1's out-features
         gpu._core._mlp_relu(*(dev(gpu, a) for a in (x, w1, b1, w2[:, :31], b2)))
+
+
+@pytest.mark.parametrize("M,N,K", [(64, 96, 8192), (33, 30, 4999), (150, 65, 17), (512, 256, 256)])
+def test_abi_relu_mask_gemm_matches_gemm_then_relu_backward(gpu, M, N, K):
+    rng = np.random.default_rng(M + N + K)
+    a = rng.standard_normal((M, K)).astype(f32)
+    b = (rng.standard_normal((K, N)) / np.sqrt(K)).astype(f32)
+    h = np.maximum(0, rng.standard_normal((M, N))).astype(f32)
+    abi = Abi()
+    L = abi.L
+    vp, i64 = ctypes.c_void_p, ctypes.c_int64
+    L.aar_gemm_f32_relu_mask.argtypes = [ctypes.c_int, i64, i64, i64, vp, vp, vp, vp, vp, ctypes.c_size_t, vp]
+    L.aar_gemm_f32.argtypes = [ctypes.c_int, i64, i64, i64, vp, vp, vp, vp, ctypes.c_size_t, vp]
+    L.aar_gemm_f32_workspace_bytes.restype = ctypes.c_size_t
+    L.aar_gemm_f32_workspace_bytes.argtypes = [ctypes.c_int, i64, i64, i64]
+    L.aar_relu_bwd_f32.argtypes = [vp, vp, vp, i64, vp]
+    try:
+        pa, pb, ph = abi.put(a), abi.put(b), abi.put(h)
+        wsb = L.aar_gemm_f32_workspace_bytes(0, M, N, K)
+        ws = abi.alloc(wsb) if wsb else None
+        pc, pp, pr = abi.empty(M * N), abi.empty(M * N), abi.empty(M * N)
+        abi.check(L.aar_gemm_f32_relu_mask(0, M, N, K, pa, pb, ph, pc, ws, wsb, None))
+        abi.check(L.aar_gemm_f32(0, M, N, K, pa, pb, pp, ws, wsb, None))
+        abi.check(L.aar_relu_bwd_f32(pp, ph, pr, M * N, None))
+        np.testing.assert_array_equal(abi.get(pc, (M, N)), abi.get(pr, (M, N)))
+    finally:
+        abi.free()
