@@ -440,7 +440,38 @@ multi_update_kernel(MultiArgs A, float alpha, float lr, float beta1, float beta2
   }
 }
 
-// Launch groups of up to kMultiMax non-empty tensors.
+// Byte ranges [p, p + n floats) overlap.
+inline bool spans_overlap(const void* p, const void* q, int64_t n_p, int64_t n_q) {
+  if (!p || !q) return false;
+  const uintptr_t a0 = reinterpret_cast<uintptr_t>(p), b0 = reinterpret_cast<uintptr_t>(q);
+  const uintptr_t a1 = a0 + (uintptr_t)n_p * sizeof(float), b1 = b0 + (uintptr_t)n_q * sizeof(float);
+  return a0 < b1 && b0 < a1;
+}
+
+// Tensor `i` may join the group only if nothing it writes (a, m, v) overlaps
+// anything a member reads or writes, and nothing it reads (b) overlaps what a
+// member writes.  Workgroups of one launch run in no fixed order, so a
+// parameter listed twice (a shared module, a tied weight) must be updated in
+// two launches, one after the other, as the per-parameter loop does.
+inline bool conflicts_with_group(const MultiArgs& A, bool adamw, float* a, const float* b, float* m, float* v,
+                                 int64_t n) {
+  for (int k = 0; k < A.count; ++k) {
+    const int64_t nk = A.n[k];
+    const void* written_k[3] = {A.a[k], adamw ? A.m[k] : nullptr, adamw ? A.v[k] : nullptr};
+    const void* written_i[3] = {a, adamw ? m : nullptr, adamw ? v : nullptr};
+    for (const void* wi : written_i) {
+      if (spans_overlap(wi, A.b[k], n, nk)) return true;
+      for (const void* wk : written_k)
+        if (spans_overlap(wi, wk, n, nk)) return true;
+    }
+    for (const void* wk : written_k)
+      if (spans_overlap(b, wk, n, nk)) return true;
+  }
+  return false;
+}
+
+// Launch groups of up to kMultiMax non-empty tensors whose written ranges are
+// disjoint from every other member's ranges.
 int launch_multi(bool adamw, int count, float* const* a, const float* const* b, float* const* m, float* const* v,
                  const int64_t* n, float alpha, float lr, float beta1, float beta2, float eps, float wd_factor,
                  float bc1, float bc2, hipStream_t st) {
@@ -463,7 +494,8 @@ int launch_multi(bool adamw, int count, float* const* a, const float* const* b, 
   for (int i = 0; i < count; ++i) {
     if (n[i] == 0) continue;
     const int64_t nb = ceil_div(n[i], (int64_t)kMultiChunk);
-    if (A.count == kMultiMax || blocks + nb > INT32_MAX / 2) {
+    if (A.count == kMultiMax || blocks + nb > INT32_MAX / 2 ||
+        conflicts_with_group(A, adamw, a[i], b[i], adamw ? m[i] : nullptr, adamw ? v[i] : nullptr, n[i])) {
       const int rc = flush();
       if (rc != AAR_OK) return rc;
     }

@@ -95,14 +95,16 @@ Tensor add_bias_dev(const Tensor& x, const Tensor& b) {
   if (x.device == Device::CPU) throw_cpu_compute("add_bias");
   Tensor out = Tensor::empty(x.shape, x.dtype, x.device);
   const int64_t D = b.shape[0];
-  check_status(aar_add_bias_f32(fp(x), fp(b), fp(out), D ? n_of(x) / D : 0, D, current_stream()), "add_bias");
+  if (D == 0) return out;  // no columns: nothing to add
+  check_status(aar_add_bias_f32(fp(x), fp(b), fp(out), n_of(x) / D, D, current_stream()), "add_bias");
   return out;
 }
 
 Tensor bias_grad_dev(const Tensor& g, int64_t D) {
   Tensor gc = as_contig(g);
   Tensor db = Tensor::empty({D}, gc.dtype, gc.device);
-  const int64_t rows = D ? n_of(gc) / D : 0;
+  if (D == 0) return db;  // no columns: nothing to sum
+  const int64_t rows = n_of(gc) / D;
   Workspace ws(aar_colsum_workspace_bytes(rows, D));
   check_status(aar_colsum_f32(fp(gc), fp(db), rows, D, ws.data(), ws.bytes(), current_stream()), "bias_grad");
   return db;

@@ -243,11 +243,19 @@ Tensor matmul_at_b_2d(const Tensor& a, const Tensor& b) {
   return gemm_device(AAR_GEMM_TN, a, b, a.shape[1], b.shape[1], a.shape[0]);
 }
 
+// Product of all dims but the last (the flattened row count, also when the
+// last dim is 0).
+int64_t lead_rows(const Tensor& a) {
+  int64_t m = 1;
+  for (size_t i = 0; i + 1 < a.shape.size(); ++i) m *= a.shape[i];
+  return m;
+}
+
 Tensor matmul_no_grad(const Tensor& a, const Tensor& b) {
   if (a.shape.size() == 2) return matmul_2d(a, b);
   const int64_t K = a.shape.back();
   const int64_t N = b.shape[1];
-  const int64_t M_flat = K ? static_cast<int64_t>(a.numel()) / K : 0;
+  const int64_t M_flat = lead_rows(a);
   Tensor out2d = matmul_2d(as_view(a, {M_flat, K}), b);
   std::vector<int64_t> out_shape(a.shape.begin(), a.shape.end() - 1);
   out_shape.push_back(N);
@@ -258,7 +266,7 @@ Tensor matmul_a_bt_no_grad(const Tensor& a, const Tensor& b) {
   if (a.shape.size() == 2) return matmul_a_bt_2d(a, b);
   const int64_t K = a.shape.back();
   const int64_t N = b.shape[0];
-  const int64_t M_flat = K ? static_cast<int64_t>(a.numel()) / K : 0;
+  const int64_t M_flat = lead_rows(a);
   Tensor out2d = matmul_a_bt_2d(as_view(a, {M_flat, K}), b);
   std::vector<int64_t> out_shape(a.shape.begin(), a.shape.end() - 1);
   out_shape.push_back(N);
@@ -269,7 +277,7 @@ Tensor matmul_at_b_no_grad(const Tensor& a, const Tensor& b) {
   if (a.shape.size() == 2 && b.shape.size() == 2) return matmul_at_b_2d(a, b);
   const int64_t M = a.shape.back();
   const int64_t N = b.shape.back();
-  const int64_t K_flat = M ? static_cast<int64_t>(a.numel()) / M : 0;
+  const int64_t K_flat = lead_rows(a);
   return matmul_at_b_2d(as_view(a, {K_flat, M}), as_view(b, {K_flat, N}));
 }
 
@@ -343,8 +351,8 @@ class LinearFunction : public Function {
   Tensor saved_x, saved_w;
   std::vector<Tensor> backward(const Tensor& g) override {
     Tensor gc = as_contig(g);
-    const int64_t N = saved_w.shape[0];
-    const int64_t rows = static_cast<int64_t>(gc.numel()) / N;
+    const int64_t N = saved_w.shape[0], K = saved_w.shape[1];  // linear() routes N == 0 and K == 0 elsewhere
+    const int64_t rows = static_cast<int64_t>(saved_x.numel()) / K;
     Tensor db = Tensor::empty({N}, DType::Fp32, Device::CUDA);
     Workspace ws(aar_colsum_workspace_bytes(rows, N));
     check_status(aar_colsum_f32(fp(gc), fp(db), rows, N, ws.data(), ws.bytes(), current_stream()), "linear backward");
@@ -763,8 +771,9 @@ Tensor linear(const Tensor& x, const Tensor& w, const Tensor& b) {
   if (w.shape[0] != b.shape[0]) throw std::invalid_argument("add_bias: bias size must match x's last dim");
   if (b.dtype != DType::Fp32) throw std::invalid_argument("add_bias: only Fp32 supported");
   if (x.device != b.device) throw std::invalid_argument("add_bias: device mismatch");
-  // An empty contraction is the bias broadcast, not a product: the two-op path.
-  if (x.shape.back() == 0) return add_bias(matmul_a_bt(x, w), b);
+  // An empty contraction is the bias broadcast, not a product, and a layer
+  // with no outputs has nothing to compute: both take the two-op path.
+  if (x.shape.back() == 0 || w.shape[0] == 0) return add_bias(matmul_a_bt(x, w), b);
   Tensor xc = as_contig(x), wc = as_contig(w), bc = as_contig(b);
   if (!xc.requires_grad && !wc.requires_grad && !bc.requires_grad) return linear_no_grad(xc, wc, bc);
   auto fn = std::make_shared<LinearFunction>();
@@ -821,7 +830,7 @@ class MlpReluFunction : public Function {
 
 Tensor mlp_relu(const Tensor& x, const Tensor& w1, const Tensor& b1, const Tensor& w2, const Tensor& b2) {
   if (w1.shape.size() != 2 || w2.shape.size() != 2 || x.shape.empty() || w1.shape[0] == 0 ||
-      x.shape.back() == 0) {
+      w2.shape[0] == 0 || x.shape.back() == 0) {
     return linear(relu(linear(x, w1, b1)), w2, b2);  // the composition's checks and edge cases
   }
   // The checks (and messages) of both layers' matmul_a_bt and add_bias.

@@ -125,13 +125,19 @@ def load_traffic(name: str):
         return None
 
 
-def bench_matmul(ag, steps: int, warmup: int, ev: Events):
-    n = 4096
+def matmul_inputs(ag, n: int = 4096):
+    """The headline step's operands, uploaded once (resident in HBM before
+    any timing starts)."""
     rng = np.random.default_rng(0)
     a = (rng.standard_normal((n, n)) / np.sqrt(n)).astype(np.float32)
     b = (rng.standard_normal((n, n)) / np.sqrt(n)).astype(np.float32)
-    ta = ag.from_numpy(a).to(ag.Device.CUDA)
-    tb = ag.from_numpy(b).to(ag.Device.CUDA)
+    return a, b, ag.from_numpy(a).to(ag.Device.CUDA), ag.from_numpy(b).to(ag.Device.CUDA)
+
+
+def bench_matmul(ag, steps: int, warmup: int, ev: Events, inputs=None):
+    a, b, ta, tb = inputs if inputs is not None else matmul_inputs(ag)
+    n = a.shape[0]
+    rng = np.random.default_rng(1)
     for _ in range(warmup):
         ag.matmul(ta, tb)
     ag.cuda_synchronize()
@@ -518,6 +524,20 @@ def bench_gpt(ag, ev: Events, steps: int = 50, warmup: int = 10, cfg=GPT5):
             "config": "6 layers, d_model 384, 6 heads, ctx 256, batch 64, vocab 65, ReLU MLP, SGD lr 1e-3"}
 
 
+def cpu_pin():
+    """Pin the calling thread (the one that runs the reference CPU code) to one
+    host core: the last core this process may use.  Returns (core, cores the
+    process may use, previous affinity)."""
+    allowed = sorted(os.sched_getaffinity(0))
+    core = allowed[-1]
+    os.sched_setaffinity(0, {core})
+    return core, len(allowed), set(allowed)
+
+
+def cpu_host_note(core: int, n_allowed: int) -> str:
+    return f"host {cpu_model()}, nproc {os.cpu_count()} ({n_allowed} usable), pinned to core {core}"
+
+
 def cpu_baseline_gpt(cfg=GPT5, batch: int = 2):
     """The reference's own CPU GPT step (oracle/_ref, built from its sources)
     on one core at a reduced batch: tokens/s = batch*ctx / t_step."""
@@ -566,9 +586,99 @@ def cpu_baseline_matmul(ab, budget_s: float = 12.0):
         "cores": 1,
         "kind": kind,
         "sample": f"{rows}-row band of the 4096^3 fp32 matmul (naive i-j-k reference loop, {t:.1f} s; "
-                  f"full product extrapolates to {t * n / rows:.0f} s); host {cpu_model()}, "
-                  f"{os.cpu_count()} cores visible, 1 used",
+                  f"full product extrapolates to {t * n / rows:.0f} s)",
     }
+
+
+def _ratio(cpu_ms, gpu_ms):
+    return round(cpu_ms / gpu_ms, 1) if gpu_ms else None
+
+
+def cpu_baselines_configs(sweep, rowwise, flash):
+    """The reference's own CPU path (oracle/_ref) for BASELINE configs 1, 3 and
+    4 on one pinned core, beside the GPU figures of the same run.
+      config 1: matmul / matmul_a_bt / matmul_at_b at 1024^3, in full
+                (cppsrc/ops/matmul.cpp:24-91);
+      config 3: softmax and layernorm fwd and fwd+bwd (autograd) at
+                rows 65536 x cols 384/768 in full; cols 4096 on an 8192-row
+                band x 8, labelled extrapolated (softmax.cpp:15-63,
+                layernorm.cpp:20-157);
+      config 4: the causal attention composite fwd+bwd (flash_attention.cpp:
+                40-45 with bmm/scale/mask/softmax and autograd) on (b,h)
+                slices, x 96 slices, labelled extrapolated: 2 slices at
+                T=1024, 1 at T=4096.
+    Each reference call includes copying its inputs into reference Tensors
+    and its outputs out (memcpy-rate work, small beside the arithmetic).
+    The backward figures are fwd+bwd time minus the forward time."""
+    import oracle
+
+    if not oracle.ref_available():
+        return None
+    rng = np.random.default_rng(0)
+    out = {}
+    # config 1
+    a = rng.standard_normal((1024, 1024)).astype(np.float32)
+    b = rng.standard_normal((1024, 1024)).astype(np.float32)
+    c1 = {}
+    for op in ("nn", "nt", "tn"):
+        t0 = time.perf_counter()
+        oracle.ref_matmul(op, a, b)
+        t = time.perf_counter() - t0
+        gpu_tf = sweep.get(f"{op}_1024x1024x1024")
+        gpu_ms = 2.0 * 1024 ** 3 / (gpu_tf * 1e12) * 1e3 if gpu_tf else None
+        c1[op] = {"cpu_ms": round(t * 1e3, 1), "cpu_GFLOPS": round(2.0 * 1024 ** 3 / t / 1e9, 3),
+                  "gpu_ms": round(gpu_ms, 4) if gpu_ms else None, "gpu_over_cpu": _ratio(t * 1e3, gpu_ms)}
+    out["config1_gemm_1024"] = c1
+    # config 3
+    rows = 65536
+    c3 = {}
+    for cols in (384, 768, 4096):
+        band = rows if cols < 4096 else 8192
+        x = (3 * rng.standard_normal((band, cols))).astype(np.float32)
+        w = (1 + 0.02 * rng.standard_normal(cols)).astype(np.float32)
+        bb = (0.02 * rng.standard_normal(cols)).astype(np.float32)
+        g = rng.standard_normal((band, cols)).astype(np.float32)
+        calls = {"softmax_fwd": lambda: oracle.ref_softmax(x),
+                 "softmax_bwd": lambda: oracle.ref_softmax(x, g),
+                 "layernorm_fwd": lambda: oracle.ref_layernorm(x, w, bb),
+                 "layernorm_bwd": lambda: oracle.ref_layernorm(x, w, bb, 1e-5, g)}
+        tm = {}
+        for name, fn in calls.items():  # best of two (the first run also faults in fresh pages)
+            best = None
+            for _ in range(2):
+                t0 = time.perf_counter()
+                fn()
+                t = time.perf_counter() - t0
+                best = t if best is None else min(best, t)
+            tm[name] = best
+        tm["softmax_bwd"] = max(tm["softmax_bwd"] - tm["softmax_fwd"], 1e-9)
+        tm["layernorm_bwd"] = max(tm["layernorm_bwd"] - tm["layernorm_fwd"], 1e-9)
+        nbytes = {"softmax_fwd": 8.0 * rows * cols, "softmax_bwd": 12.0 * rows * cols,
+                  "layernorm_fwd": 8.0 * rows * cols + 8 * cols + 8 * rows,
+                  "layernorm_bwd": 12.0 * rows * cols + 12 * cols + 8 * rows}
+        for name, t in tm.items():
+            t_full = t * rows / band
+            gpu_ms = rowwise.get(f"{name}_c{cols}", {}).get("ms")
+            c3[f"{name}_c{cols}"] = {"cpu_ms": round(t_full * 1e3, 1),
+                                     "cpu_GB_s": round(nbytes[name] / t_full / 1e9, 3),
+                                     "gpu_ms": gpu_ms, "gpu_over_cpu": _ratio(t_full * 1e3, gpu_ms),
+                                     "sample": "full" if band == rows else f"{band}-row band x {rows // band}, extrapolated"}
+    out["config3_rowwise_65536"] = c3
+    # config 4
+    c4 = {}
+    for T, n_sl in ((1024, 2), (4096, 1)):
+        q, k, v, do = (rng.standard_normal((n_sl, T, 64)).astype(np.float32) for _ in range(4))
+        t0 = time.perf_counter()
+        oracle.ref_attention(q, k, v, True, do)
+        t = (time.perf_counter() - t0) * 96 / n_sl
+        flops = 3.5 * 4.0 * 96 * T * T * 64 / 2.0
+        gpu_ms = flash.get(T)
+        c4[f"t{T}"] = {"cpu_ms": round(t * 1e3, 1), "cpu_GFLOPS": round(flops / t / 1e9, 3),
+                       "gpu_ms": gpu_ms, "gpu_over_cpu": _ratio(t * 1e3, gpu_ms),
+                       "sample": f"{n_sl} of 96 (b,h) slices x {96 // n_sl}, extrapolated",
+                       "flops": "3.5 * 4*B*H*T^2*d/2 (algorithmic, causal)"}
+    out["config4_flash_b8h12d64"] = c4
+    return out
 
 
 def main() -> int:
@@ -617,13 +727,16 @@ def main() -> int:
         log(f"flash T={args.flash_t} fwd+bwd {fa_ms:.3f} ms {fa_flops / (fa_ms * 1e-3) / 1e12:.2f} TFLOPS {fa_dist}")
         return 0
 
-    step_ms, wall, err, ab, mm_dist = bench_matmul(ag, args.steps, args.warmup, ev)
-    tflops = flops / (step_ms * 1e-3) / 1e12
-    log(f"matmul 4096^3: {step_ms:.4f} ms/step, {tflops:.2f} TFLOPS "
-        f"({100 * tflops / PEAK_FP32_MFMA_TFLOPS:.1f}% of fp32 MFMA peak), check err {err:.2e}")
     if args.only == "gemm":
+        step_ms, wall, err, ab, mm_dist = bench_matmul(ag, args.steps, args.warmup, ev)
+        tflops = flops / (step_ms * 1e-3) / 1e12
+        log(f"matmul 4096^3: {step_ms:.4f} ms/step, {tflops:.2f} TFLOPS")
         return 0
 
+    # The other GPU legs run first, so the headline's W warm-up steps start on
+    # a GPU whose clocks have already ramped; its operands are uploaded before
+    # them, so no host-to-device copy idles the GPU right before it.
+    mm_inputs = matmul_inputs(ag)
     fa_ms, fa_flops, fa_dist = bench_flash(ag, args.flash_steps, 10, ev)
     fa_tflops = fa_flops / (fa_ms * 1e-3) / 1e12
     log(f"flash causal B8 H12 T4096 d64 fwd+bwd: {fa_ms:.3f} ms, {fa_tflops:.2f} TFLOPS "
@@ -647,15 +760,35 @@ def main() -> int:
     gpt = bench_gpt(ag, ev)
     log(f"GPT step (config 5): {gpt['tokens_per_s']:.0f} tokens/s, {gpt['ms_per_step']} ms/step, "
         f"{gpt['implied_tflops']} TFLOPS implied")
-    if not args.no_cpu_baseline:
-        gpt["cpu_baseline"] = cpu_baseline_gpt()
-        if gpt["cpu_baseline"]:
-            log(f"GPT step reference CPU (batch 2, 1 core): {gpt['cpu_baseline']['tokens_per_s']} tokens/s")
 
+    step_ms, wall, err, ab, mm_dist = bench_matmul(ag, args.steps, args.warmup, ev, mm_inputs)
+    tflops = flops / (step_ms * 1e-3) / 1e12
+    log(f"matmul 4096^3: {step_ms:.4f} ms/step, {tflops:.2f} TFLOPS "
+        f"({100 * tflops / PEAK_FP32_MFMA_TFLOPS:.1f}% of fp32 MFMA peak), check err {err:.2e}")
+    ag.cuda_synchronize()
+
+    # Reference CPU legs, after all GPU work, on one pinned host core.
     cpu = None
+    cpu_configs = None
     if not args.no_cpu_baseline:
-        cpu = cpu_baseline_matmul(ab)
-        log(f"cpu baseline ({cpu['kind']}): {cpu['value'] * 1e3:.3f} GFLOPS on 1 core")
+        core, n_allowed, prev = cpu_pin()
+        try:
+            note = cpu_host_note(core, n_allowed)
+            cpu = cpu_baseline_matmul(ab)
+            cpu["sample"] += "; " + note
+            log(f"cpu baseline ({cpu['kind']}): {cpu['value'] * 1e3:.3f} GFLOPS on 1 core ({note})")
+            gpt["cpu_baseline"] = cpu_baseline_gpt()
+            if gpt["cpu_baseline"]:
+                gpt["cpu_baseline"]["host"] = note
+                log(f"GPT step reference CPU (batch 2, 1 core): {gpt['cpu_baseline']['tokens_per_s']} tokens/s")
+            cpu_configs = cpu_baselines_configs(sweep, rowwise, {4096: round(fa_ms, 4), 1024: round(fa1_ms, 4)})
+            if cpu_configs is not None:
+                cpu_configs["host"] = note
+                cpu_configs["kind"] = "reference"
+                cpu_configs["cores"] = 1
+                log("reference CPU per config: " + json.dumps(cpu_configs))
+        finally:
+            os.sched_setaffinity(0, prev)
 
     out = {
         "metric": "fp32 matmul TFLOPS @4096^3 (% of FP32 MFMA peak) + flash-attn fwd+bwd TFLOPS",
@@ -703,6 +836,7 @@ def main() -> int:
         "rowwise_hbm": rowwise,
         "attention_ops_and_dropout": extra,
         "gpt_train_step": gpt,
+        "cpu_baselines_per_config": cpu_configs,
         "roofline": {
             "bound": "mfma",
             "achieved": round(tflops, 3),

@@ -102,6 +102,34 @@ def test_linear_empty_contraction_is_bias_broadcast(gpu):
     np.testing.assert_array_equal(host(gpu, tb.grad), np.full(5, 3, f32))
 
 
+def test_linear_zero_width_layer(gpu):
+    # A layer with no outputs (W [0, K], bias [0]): empty output, and the
+    # backward returns an empty dW/db and a zero dX (no division by zero, no
+    # zero-column reduction).
+    rng = np.random.default_rng(8)
+    x = rng.standard_normal((2, 3, 7)).astype(f32)
+    tx, tw, tb = dev(gpu, x, True), dev(gpu, np.zeros((0, 7), f32), True), dev(gpu, np.zeros(0, f32), True)
+    y = gpu._core._linear(tx, tw, tb)
+    assert y.shape == [2, 3, 0]
+    gpu.sum_all(y).backward()
+    np.testing.assert_array_equal(host(gpu, tx.grad), np.zeros_like(x))
+    assert tw.grad.shape == [0, 7] and tb.grad.shape == [0]
+    # the MLP op with a zero-width second layer, and with a zero-width hidden layer
+    w1, b1 = rng.standard_normal((5, 7)).astype(f32), np.zeros(5, f32)
+    for w2, b2 in ((np.zeros((0, 5), f32), np.zeros(0, f32)),):
+        ts = [dev(gpu, a, True) for a in (x, w1, b1, w2, b2)]
+        out = gpu._core._mlp_relu(*ts)
+        assert out.shape == [2, 3, 0]
+        gpu.sum_all(out).backward()
+        np.testing.assert_array_equal(host(gpu, ts[0].grad), np.zeros_like(x))
+    ts = [dev(gpu, a, True) for a in (x, np.zeros((0, 7), f32), np.zeros(0, f32), np.zeros((4, 0), f32),
+                                      np.arange(4, dtype=f32))]
+    out = gpu._core._mlp_relu(*ts)
+    np.testing.assert_array_equal(host(gpu, out), np.broadcast_to(np.arange(4, dtype=f32), (2, 3, 4)))
+    gpu.sum_all(out).backward()
+    np.testing.assert_array_equal(host(gpu, ts[4].grad), np.full(4, 6, f32))
+
+
 @pytest.mark.parametrize("M,N,K", [(64, 96, 8192), (33, 30, 4999), (150, 65, 17), (512, 256, 256)])
 @pytest.mark.parametrize("use_ws,bias_off", [(True, 0), (True, 1), (False, 0)])
 def test_abi_gemm_bias_matches_gemm_then_add_bias(M, N, K, use_ws, bias_off):

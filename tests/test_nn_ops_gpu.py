@@ -134,6 +134,53 @@ def test_multi_tensor_updates_bit_identical(gpu):
         gpu._core._scaled_add_inplace_multi([dev(gpu, np.zeros(3, f32))], [dev(gpu, np.zeros(4, f32))], 1.0)
 
 
+def test_multi_tensor_updates_with_repeated_parameters(gpu, ag):
+    # A parameter listed twice (a shared module or a tied weight: Module.parameters()
+    # does not de-duplicate) must be updated twice in list order, as the
+    # reference's per-parameter loop does (aargrad/optim.py:13-18, :36-54); the
+    # AdamW state is keyed by id(p), so both entries also share m and v.
+    # Several repeats, an overlapping view and large tensors (many workgroups
+    # per tensor) give concurrent updates every chance to race.
+    rng = np.random.default_rng(23)
+    sizes = [70001, 5, 300_000, 4097]
+    init = [rng.standard_normal(n).astype(f32) for n in sizes]
+    grads = [rng.standard_normal(n).astype(f32) for n in sizes]
+    order = [0, 1, 0, 2, 3, 2, 0]
+    # SGD: multi call vs sequential single-tensor calls
+    multi = [dev(gpu, a) for a in init]
+    seq = [dev(gpu, a) for a in init]
+    gdev = [dev(gpu, g) for g in grads]
+    gpu._core._scaled_add_inplace_multi([multi[i] for i in order], [gdev[i] for i in order], -0.25)
+    for i in order:
+        gpu.scaled_add_inplace(seq[i], gdev[i], -0.25)
+    for a, b in zip(multi, seq):
+        np.testing.assert_array_equal(host(gpu, a), host(gpu, b))
+    # AdamW with shared m/v per repeated parameter
+    args = (1e-2, 0.9, 0.999, 1e-8, 0.01, 0.1, 0.001)
+    st_multi = [(dev(gpu, a), dev(gpu, np.zeros_like(a)), dev(gpu, np.zeros_like(a))) for a in init]
+    st_seq = [(dev(gpu, a), dev(gpu, np.zeros_like(a)), dev(gpu, np.zeros_like(a))) for a in init]
+    gpu._core._adamw_step_multi([st_multi[i][0] for i in order], [gdev[i] for i in order],
+                                [st_multi[i][1] for i in order], [st_multi[i][2] for i in order], *args)
+    for i in order:
+        gpu.adamw_step(st_seq[i][0], gdev[i], st_seq[i][1], st_seq[i][2], *args)
+    for a, b in zip(st_multi, st_seq):
+        for x, y in zip(a, b):
+            np.testing.assert_array_equal(host(gpu, x), host(gpu, y))
+    # through optim.SGD with a module shared by two parents
+    lin = ag.nn.Linear(6, 4)
+    lin.to(gpu.Device.CUDA)
+    params = list(lin.parameters()) + list(lin.parameters())
+    x = dev(gpu, rng.standard_normal((3, 6)))
+    gpu.sum_all(lin(x)).backward()
+    before = [host(gpu, p.tensor) for p in lin.parameters()]
+    grads_h = [host(gpu, p.tensor.grad) for p in lin.parameters()]
+    ag.optim.SGD(params, lr=0.5).step()
+    for p, b0, g in zip(lin.parameters(), before, grads_h):
+        ref = b0 + np.float32(-0.5) * g
+        ref = (ref + np.float32(-0.5) * g).astype(f32)
+        np.testing.assert_array_equal(host(gpu, p.tensor), ref)
+
+
 def test_optimizers_take_one_multi_tensor_step(gpu, ag):
     # optim.SGD / optim.AdamW (now one multi-tensor call per step) against the
     # reference optimizers' per-parameter loops (aargrad/optim.py:13-18, :36-54)
