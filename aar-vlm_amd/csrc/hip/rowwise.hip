@@ -22,6 +22,7 @@
 #include <math.h>
 
 #include <algorithm>
+#include <mutex>
 
 #include "common.hpp"
 
@@ -798,10 +799,22 @@ extern "C" size_t aar_layernorm_bwd_workspace_bytes(int64_t rows, int64_t cols) 
   return (size_t)parts * 2 * (size_t)cols * sizeof(float);
 }
 
-extern "C" int aar_layernorm_bwd_f32(const float* gy, const float* x, const float* w,
-                                     const float* mean, const float* rstd, float* dx, float* dw,
-                                     float* db, int64_t rows, int64_t cols, void* workspace,
-                                     size_t workspace_bytes, void* stream) {
+namespace aar {
+namespace {
+
+// 128-bit load path: 16-byte aligned rows and partials.
+bool ln_bwd_vec(const void* gy, const void* x, const void* w, const void* dx, const void* ws, int64_t cols) {
+  return cols % 4 == 0 && aligned16(gy) && aligned16(x) && aligned16(w) && aligned16(dx) && aligned16(ws);
+}
+
+// Workspace the plan for these operands needs (partial rows).
+size_t ln_bwd_need_bytes(int64_t rows, int64_t cols, bool vec) {
+  return (size_t)ln_bwd_parts_for(rows, plan_rows(cols, vec)) * 2 * (size_t)cols * sizeof(float);
+}
+
+int layernorm_bwd_run(const float* gy, const float* x, const float* w, const float* mean, const float* rstd,
+                      float* dx, float* dw, float* db, int64_t rows, int64_t cols, void* workspace,
+                      size_t workspace_bytes, void* stream) {
   if (rows < 0 || cols <= 0) return AAR_EINVAL;
   if (!dw || !db || cols > INT32_MAX) return AAR_EINVAL;
   hipStream_t st = as_stream(stream);
@@ -811,8 +824,7 @@ extern "C" int aar_layernorm_bwd_f32(const float* gy, const float* x, const floa
     return rc;
   }
   if (!gy || !x || !w || !mean || !rstd || !dx) return AAR_EINVAL;
-  const bool vec = cols % 4 == 0 && aligned16(gy) && aligned16(x) && aligned16(w) &&
-                   aligned16(dx) && aligned16(workspace);
+  const bool vec = ln_bwd_vec(gy, x, w, dx, workspace, cols);
   const RowPlan p = plan_rows(cols, vec);
   const int parts = ln_bwd_parts_for(rows, p);
   const size_t need = (size_t)parts * 2 * (size_t)cols * sizeof(float);
@@ -840,4 +852,65 @@ extern "C" int aar_layernorm_bwd_f32(const float* gy, const float* x, const floa
   layernorm_bwd_reduce_kernel<<<dim3((unsigned)ceil_div(2 * cols, kRedCols)), dim3(kRedThreads), 0, st>>>(
       part, dw, db, parts, (int)cols);
   return launch_status();
+}
+
+// Static scratch of the no-allocation entry point: one copy per GPU, held
+// until the process ends.  Host code never passes `scratch` itself to a
+// kernel (on the host the name is a stand-in, not a device address); it uses
+// the per-device address hipGetSymbolAddress returns.
+constexpr size_t kLnBwdScratchBytes = size_t(16) << 20;
+static __device__ __align__(256) unsigned char scratch[kLnBwdScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of the current device's scratch, looked up once per device
+// with that device current.
+int scratch_ptr(void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return static_cast<int>(e);
+  if (dev < 0 || dev >= kMaxDevices) return AAR_EUNSUPPORTED;
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return static_cast<int>(e);
+    if (!p) return AAR_EUNSUPPORTED;
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return AAR_OK;
+}
+
+// Any 16-byte aligned address: stands for the scratch buffer in the
+// alignment test of the plan (the buffer itself is 256-byte aligned).
+inline const void* scratch_align_probe() { return reinterpret_cast<const void*>(uintptr_t(256)); }
+
+}  // namespace
+}  // namespace aar
+
+extern "C" int aar_layernorm_bwd_f32(const float* gy, const float* x, const float* w,
+                                     const float* mean, const float* rstd, float* dx, float* dw,
+                                     float* db, int64_t rows, int64_t cols, void* workspace,
+                                     size_t workspace_bytes, void* stream) {
+  return layernorm_bwd_run(gy, x, w, mean, rstd, dx, dw, db, rows, cols, workspace, workspace_bytes, stream);
+}
+
+extern "C" size_t aar_layernorm_bwd_noalloc_max_bytes(void) { return kLnBwdScratchBytes; }
+
+extern "C" int aar_layernorm_bwd_noalloc_f32(const float* gy, const float* x, const float* w,
+                                             const float* mean, const float* rstd, float* dx, float* dw,
+                                             float* db, int64_t rows, int64_t cols, void* stream) {
+  if (rows < 0 || cols <= 0 || cols > INT32_MAX) return AAR_EINVAL;
+  // The buffer is 256-byte aligned, so the plan follows the operands' alignment.
+  if (rows > 0 && ln_bwd_need_bytes(rows, cols, ln_bwd_vec(gy, x, w, dx, scratch_align_probe(), cols)) >
+                      kLnBwdScratchBytes) {
+    return AAR_ESCRATCH;
+  }
+  void* ws = nullptr;
+  const int rc = scratch_ptr(&ws);
+  if (rc != AAR_OK) return rc;
+  return layernorm_bwd_run(gy, x, w, mean, rstd, dx, dw, db, rows, cols, ws, kLnBwdScratchBytes, stream);
 }

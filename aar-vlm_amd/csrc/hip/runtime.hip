@@ -60,6 +60,7 @@ const char* aar_error_string(int status) {
     case AAR_EWORKSPACE: return "aar: workspace missing or too small";
     case AAR_EUNSUPPORTED: return "aar: shape not supported by the gfx950 kernels";
     case AAR_ENOMEM: return "aar: out of device memory";
+    case AAR_ESCRATCH: return "aar: problem needs more than the no-allocation entry point's static scratch";
     default: break;
   }
   if (status > 0) return hipGetErrorString(static_cast<hipError_t>(status));

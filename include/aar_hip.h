@@ -11,7 +11,8 @@
  *   - Never allocates an output.  Inputs are borrowed and outputs are written
  *     in place; the caller owns all memory.  Entry points that need scratch
  *     memory take an explicit workspace and expose its size through a
- *     *_workspace_bytes() query.
+ *     *_workspace_bytes() query (the one *_noalloc_* entry point uses a
+ *     static per-GPU buffer instead).
  *   - All work is enqueued on `stream` and returns without waiting; results are
  *     visible to the host after aar_stream_synchronize()/aar_synchronize() or a
  *     device-to-host copy.
@@ -35,6 +36,7 @@ extern "C" {
 #define AAR_EWORKSPACE (-2)    /* workspace pointer NULL or too small */
 #define AAR_EUNSUPPORTED (-3)  /* shape outside what the kernels implement */
 #define AAR_ENOMEM (-4)        /* device allocation failed (maps to std::bad_alloc) */
+#define AAR_ESCRATCH (-5)      /* needs more than a no-allocation entry point's static scratch */
 
 /* ---------------------------------------------------------------- runtime */
 
@@ -184,6 +186,27 @@ int aar_layernorm_bwd_f32(const float* gy, const float* x, const float* w,
                           float* dx, float* dw, float* db,
                           int64_t rows, int64_t cols,
                           void* workspace, size_t workspace_bytes, void* stream);
+
+/* No counterpart in the reference: aar_layernorm_bwd_f32 for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  The dgamma/dbeta partial rows go
+ * to a static per-GPU device buffer of aar_layernorm_bwd_noalloc_max_bytes()
+ * (16 MiB, held by each GPU the library runs on until the process ends)
+ * instead of a caller workspace; the call allocates nothing (no hipMalloc,
+ * no allocating library routine).  Same kernels and results as
+ * aar_layernorm_bwd_f32, bit for bit.  A shape whose partial rows exceed
+ * the buffer returns AAR_ESCRATCH before any launch: with 16-byte aligned
+ * operands and a column count divisible by 4, any number of rows fits up to
+ * 4096 columns; unaligned operands or other column counts take the
+ * element-wise plan, which fits up to 2048 columns.  Every
+ * call on one GPU shares that GPU's buffer: calls that overlap on one GPU
+ * (several streams or host threads at once) race and must be serialised by
+ * the caller; calls ordered on one stream are safe. */
+size_t aar_layernorm_bwd_noalloc_max_bytes(void);
+int aar_layernorm_bwd_noalloc_f32(const float* gy, const float* x, const float* w,
+                                  const float* mean, const float* rstd,
+                                  float* dx, float* dw, float* db,
+                                  int64_t rows, int64_t cols, void* stream);
 
 /* ------------------------------------------------------- flash attention */
 
