@@ -8,9 +8,10 @@ Formats (python/shakespeare/scripts/prepare.py:37-47, data.py:7-33):
   * ``train.bin`` / ``val.bin``: the ids as raw little-endian int64, no
     header (read as ``np.memmap(path, dtype=np.int64)``, train.py:148-149).
 
-``CharTokenizer``, ``TokenWindowDataset`` and ``DataLoader`` keep the
-reference classes (data.py:7-71): same arguments, same windows, same shuffle
-order for a seed.  ``DeviceTokenLoader`` yields exactly the batches that
+``CharTokenizer``, ``TokenWindowDataset``, ``default_collate`` and
+``DataLoader`` keep the interface of the reference pipeline's classes
+(data.py:7-71): same arguments, same ids, same windows, same shuffle order for
+a seed.  ``DeviceTokenLoader`` yields exactly the batches that
 ``DataLoader(TokenWindowDataset(tokens, T), batch_size, shuffle, seed=seed)``
 yields, already on the device: the stream is uploaded once and each batch is
 gathered there from its window starts (``_core._token_windows``), so a step
@@ -37,12 +38,24 @@ def write_tokens(ids, path) -> None:
 
 
 class CharTokenizer:
-    """Character vocabulary in ``meta.json`` (data.py:7-33)."""
+    """Character vocabulary (the ``meta.json`` format).  A token id is the
+    character's position in ``vocab``; ``from_text`` sorts the distinct
+    characters, so ids follow code-point order.  ``stoi`` / ``itos`` map
+    characters to ids and back.  Encoding and decoding are vectorised through
+    a code-point lookup table; an unknown character or id raises KeyError."""
 
     def __init__(self, vocab):
         self.vocab = list(vocab)
-        self.stoi = {c: i for i, c in enumerate(self.vocab)}
-        self.itos = {i: c for i, c in enumerate(self.vocab)}
+        self.stoi = dict(zip(self.vocab, range(len(self.vocab))))
+        self.itos = dict(enumerate(self.vocab))
+        single = all(isinstance(c, str) and len(c) == 1 for c in self.vocab)
+        if single and self.vocab:
+            cps = np.fromiter((ord(c) for c in self.vocab), dtype=np.int64, count=len(self.vocab))
+            self._lut = np.full(int(cps.max()) + 1, -1, dtype=np.int64)
+            self._lut[cps] = np.arange(len(self.vocab), dtype=np.int64)
+        else:
+            self._lut = None
+        self._chars = np.array(self.vocab, dtype=object)
 
     @classmethod
     def from_text(cls, text):
@@ -50,26 +63,43 @@ class CharTokenizer:
 
     @classmethod
     def load(cls, path):
-        with open(path) as f:
-            return cls(json.load(f)["vocab"])
+        return cls(json.loads(Path(path).read_text())["vocab"])
 
     def save(self, path):
-        with open(path, "w") as f:
-            json.dump({"vocab": self.vocab, "vocab_size": len(self.vocab)}, f)
+        Path(path).write_text(json.dumps({"vocab": self.vocab, "vocab_size": len(self.vocab)}))
 
     @property
     def vocab_size(self):
         return len(self.vocab)
 
     def encode(self, s):
-        return np.array([self.stoi[c] for c in s], dtype=np.int64)
+        try:
+            raw = s.encode("utf-32-le") if self._lut is not None else None
+        except UnicodeEncodeError:  # lone surrogates: look them up one by one
+            raw = None
+        if raw is None:
+            return np.array([self.stoi[c] for c in s], dtype=np.int64)
+        cps = np.frombuffer(raw, dtype="<u4").astype(np.int64)
+        ids = np.full(cps.shape, -1, dtype=np.int64)
+        known = cps < self._lut.size
+        ids[known] = self._lut[cps[known]]
+        if (ids < 0).any():
+            raise KeyError(chr(int(cps[np.argmax(ids < 0)])))
+        return ids
 
     def decode(self, ids):
-        return "".join(self.itos[int(i)] for i in ids)
+        idx = np.asarray(ids, dtype=np.int64).reshape(-1)
+        bad = (idx < 0) | (idx >= len(self.vocab))
+        if bad.any():
+            raise KeyError(int(idx[np.argmax(bad)]))
+        return "".join(self._chars[idx])
 
 
 class TokenWindowDataset:
-    """Window i: input tokens[i:i+T], target tokens[i+1:i+T+1] (data.py:36-48)."""
+    """Sample i of a token stream: the window tokens[i : i + T + 1] split into
+    ``input`` (its first T tokens) and ``target`` (its last T), int64; there
+    are len(tokens) - T samples.  Negative indices count from the end; indices
+    outside the dataset raise IndexError."""
 
     def __init__(self, tokens, max_seq_len):
         self.tokens = tokens
@@ -79,14 +109,26 @@ class TokenWindowDataset:
         return len(self.tokens) - self.max_seq_len
 
     def __getitem__(self, i):
-        x = np.asarray(self.tokens[i: i + self.max_seq_len], dtype=np.int64)
-        y = np.asarray(self.tokens[i + 1: i + self.max_seq_len + 1], dtype=np.int64)
-        return {"input": x, "target": y}
+        n = len(self)
+        i = int(i) + (n if i < 0 else 0)
+        if not 0 <= i < n:
+            raise IndexError(f"TokenWindowDataset: index out of range for {n} windows")
+        window = np.asarray(self.tokens[i: i + self.max_seq_len + 1], dtype=np.int64)
+        return {"input": window[:-1], "target": window[1:]}
 
 
 def default_collate(batch):
-    keys = batch[0].keys()
-    return {k: np.stack([b[k] for b in batch]) for k in keys}
+    """A list of equal-shaped sample dicts -> one dict of stacked arrays (the
+    batch dimension first), keys in the first sample's order."""
+    first = batch[0]
+    out = {}
+    for key, value in first.items():
+        value = np.asarray(value)
+        stacked = np.empty((len(batch),) + value.shape, dtype=value.dtype)
+        for row, sample in enumerate(batch):
+            stacked[row] = sample[key]
+        out[key] = stacked
+    return out
 
 
 def _batches(rng, n, batch_size, shuffle, drop_last):

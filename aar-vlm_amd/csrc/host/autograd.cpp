@@ -1,9 +1,20 @@
-// Backward engine: iterative DFS topological sort, reverse sweep, gradient
-// fan-in through add_grads.  Follows run_backward / add_grads /
-// accumulate_into_leaf (cppsrc/autograd/backward.cpp:17-113): same order of
-// node visits, same fan-in summation order and the same error messages.  The
-// fan-in sum runs on the GPU through aar_add_f32 (the reference's add_cuda).
+// Reverse-mode sweep over the recorded graph (the behaviour of the reference's
+// run_backward / add_grads, cppsrc/autograd/backward.cpp:17-113).
+//
+// Two phases:
+//  1. `schedule`: the nodes reachable from the root in reverse DFS post-order,
+//     where a node's inputs are explored last input first.  Each node is
+//     entered once, the first time the walk reaches it.
+//  2. `sweep`: nodes run in that order.  Every node owns one pending-gradient
+//     slot (indexed by its position in the schedule); a gradient arriving at a
+//     slot that already holds one is added to it (held + new, on the GPU), so
+//     fan-in sums accumulate in the order the consumers run.  Gradients for
+//     leaves go straight into the leaf's grad slot the same way.
+// This fixes the summation order of every fan-in to the reference's: its
+// stack walk pushes a node's inputs in order and pops the last one first,
+// which is the same post-order.  Error messages match the reference's.
 #include <algorithm>
+#include <optional>
 #include <unordered_map>
 #include <unordered_set>
 
@@ -13,30 +24,102 @@
 
 namespace aar {
 
+namespace {
+// The tensor itself when it is dense row-major, else a dense copy.
+Tensor dense(const Tensor& t) { return t.is_contiguous() ? t : contiguous(t); }
+}  // namespace
+
 Tensor add_grads(const Tensor& a, const Tensor& b) {
   if (a.shape != b.shape) throw std::runtime_error("autograd: grad shape mismatch");
   if (a.device != b.device) throw std::runtime_error("autograd: grad device mismatch");
   if (a.device == Device::CPU) throw_cpu_compute("add_grads");
   if (a.dtype != DType::Fp32 || b.dtype != DType::Fp32)
     throw std::runtime_error("autograd: only Fp32 gradients are supported");
-  Tensor ac = a.is_contiguous() ? a : contiguous(a);
-  Tensor bc = b.is_contiguous() ? b : contiguous(b);
-  Tensor out = Tensor::empty(ac.shape, ac.dtype, ac.device);
-  check_status(aar_add_f32(static_cast<const float*>(ac.data()), static_cast<const float*>(bc.data()),
-                           static_cast<float*>(out.data()), (int64_t)ac.numel(), current_stream()),
+  const Tensor lhs = dense(a);
+  const Tensor rhs = dense(b);
+  Tensor sum = Tensor::empty(lhs.shape, lhs.dtype, lhs.device);
+  check_status(aar_add_f32(static_cast<const float*>(lhs.data()), static_cast<const float*>(rhs.data()),
+                           static_cast<float*>(sum.data()), static_cast<int64_t>(lhs.numel()), current_stream()),
                "add_grads");
-  return out;
+  return sum;
 }
 
 namespace {
 
-void accumulate_into_leaf(Tensor& leaf, const Tensor& grad) {
-  if (!leaf.grad_slot) return;
-  auto& slot = *leaf.grad_slot;
+using FnPtr = std::shared_ptr<Function>;
+
+// Reverse post-order of the graph below `root`.  An explicit cursor per open
+// node walks its inputs from the last to the first; a node is marked when it
+// is opened, so a node reachable along several paths is opened once, from
+// the first path the walk takes.
+std::vector<FnPtr> schedule(const FnPtr& root) {
+  struct Open {
+    Function* fn;
+    size_t remaining;  // inputs not yet looked at: inputs[0, remaining)
+  };
+  std::vector<FnPtr> post;
+  std::unordered_map<Function*, FnPtr> owner;  // keeps each opened node alive and marks it
+  std::vector<Open> path;
+  auto open = [&](const FnPtr& fn) {
+    owner.emplace(fn.get(), fn);
+    path.push_back({fn.get(), fn->inputs.size()});
+  };
+  open(root);
+  while (!path.empty()) {
+    Open& cur = path.back();
+    if (cur.remaining == 0) {
+      post.push_back(owner.at(cur.fn));
+      path.pop_back();
+      continue;
+    }
+    const FnPtr& next = cur.fn->inputs[--cur.remaining].grad_fn;
+    if (next && owner.find(next.get()) == owner.end()) open(next);  // may reallocate `path`
+  }
+  std::reverse(post.begin(), post.end());
+  return post;
+}
+
+// Adds `g` into a pending-gradient slot (first arrival is stored as is).
+void deposit(std::optional<Tensor>& slot, const Tensor& g) {
   if (slot) {
-    slot = std::make_shared<Tensor>(add_grads(*slot, grad));
+    slot = add_grads(*slot, g);
   } else {
-    slot = std::make_shared<Tensor>(grad.is_contiguous() ? grad : contiguous(grad));
+    slot = g;
+  }
+}
+
+// Leaf accumulation: the first gradient is stored contiguous, later ones are
+// added to the stored one.  Leaves that do not track a gradient are skipped.
+void deposit_leaf(Tensor& leaf, const Tensor& g) {
+  if (!leaf.grad_slot) return;
+  std::shared_ptr<Tensor>& held = *leaf.grad_slot;
+  held = std::make_shared<Tensor>(held ? add_grads(*held, g) : dense(g));
+}
+
+void sweep(const std::vector<FnPtr>& nodes, const Tensor& seed) {
+  std::unordered_map<const Function*, size_t> position;
+  position.reserve(nodes.size());
+  for (size_t i = 0; i < nodes.size(); ++i) position.emplace(nodes[i].get(), i);
+  std::vector<std::optional<Tensor>> pending(nodes.size());
+  pending[0] = seed;
+  for (size_t i = 0; i < nodes.size(); ++i) {
+    if (!pending[i]) continue;  // nothing flowed into this node
+    const Tensor upstream = std::move(*pending[i]);
+    pending[i].reset();
+    Function& fn = *nodes[i];
+    const std::vector<Tensor> outs = fn.backward(upstream);
+    if (outs.size() != fn.inputs.size()) {
+      throw std::runtime_error("autograd: backward returned wrong number of grads");
+    }
+    for (size_t k = 0; k < outs.size(); ++k) {
+      Function::Input& in = fn.inputs[k];
+      if (!in.needs_grad) continue;
+      if (in.grad_fn) {
+        deposit(pending[position.at(in.grad_fn.get())], outs[k]);
+      } else {
+        deposit_leaf(in.leaf, outs[k]);
+      }
+    }
   }
 }
 
@@ -44,66 +127,7 @@ void accumulate_into_leaf(Tensor& leaf, const Tensor& grad) {
 
 void run_backward(const Tensor& root, const Tensor& grad_output) {
   if (!root.grad_fn) return;
-
-  struct Frame {
-    std::shared_ptr<Function> fn;
-    bool expanded;
-  };
-  std::vector<Frame> stack;
-  std::vector<std::shared_ptr<Function>> order;
-  std::unordered_set<Function*> visited;
-
-  stack.push_back({root.grad_fn, false});
-  while (!stack.empty()) {
-    Frame& top = stack.back();
-    if (!top.expanded) {
-      if (visited.count(top.fn.get())) {
-        stack.pop_back();
-        continue;
-      }
-      visited.insert(top.fn.get());
-      top.expanded = true;
-      // Copy before pushing: push_back may reallocate and invalidate `top`.
-      std::vector<std::shared_ptr<Function>> next;
-      for (const auto& edge : top.fn->inputs)
-        if (edge.grad_fn && !visited.count(edge.grad_fn.get())) next.push_back(edge.grad_fn);
-      for (auto& n : next) stack.push_back({std::move(n), false});
-    } else {
-      order.push_back(std::move(top.fn));
-      stack.pop_back();
-    }
-  }
-  std::reverse(order.begin(), order.end());
-
-  std::unordered_map<Function*, Tensor> grads;
-  grads[root.grad_fn.get()] = grad_output;
-
-  for (auto& fn : order) {
-    auto it = grads.find(fn.get());
-    if (it == grads.end()) continue;
-    Tensor grad_at = std::move(it->second);
-    grads.erase(it);
-
-    std::vector<Tensor> input_grads = fn->backward(grad_at);
-    if (input_grads.size() != fn->inputs.size()) {
-      throw std::runtime_error("autograd: backward returned wrong number of grads");
-    }
-    for (size_t i = 0; i < fn->inputs.size(); ++i) {
-      auto& edge = fn->inputs[i];
-      if (!edge.needs_grad) continue;
-      const Tensor& g = input_grads[i];
-      if (edge.grad_fn) {
-        auto it2 = grads.find(edge.grad_fn.get());
-        if (it2 == grads.end()) {
-          grads[edge.grad_fn.get()] = g;
-        } else {
-          it2->second = add_grads(it2->second, g);
-        }
-      } else {
-        accumulate_into_leaf(edge.leaf, g);
-      }
-    }
-  }
+  sweep(schedule(root.grad_fn), grad_output);
 }
 
 }  // namespace aar

@@ -18,6 +18,7 @@
 #include <cstring>
 
 #include <new>
+#include <optional>
 
 #include "aar_hip.h"
 
@@ -119,31 +120,34 @@ void copy_contiguous_into_strided(const Tensor& src, Tensor& dst) {
   }
 }
 
-std::vector<int64_t> resolve_new_shape(const std::vector<int64_t>& shape, size_t numel) {
-  std::vector<int64_t> out = shape;
-  int neg_pos = -1;
-  int64_t known = 1;
-  for (size_t i = 0; i < out.size(); ++i) {
-    if (out[i] == -1) {
-      if (neg_pos != -1) throw std::invalid_argument("reshape: at most one -1 dim allowed");
-      neg_pos = static_cast<int>(i);
-    } else if (out[i] < 0) {
+// Target shape of a reshape: every entry is an extent >= 0, except at most
+// one -1 whose extent is whatever makes the element count match.  Entries are
+// checked left to right, so the first offending entry picks the message (the
+// messages are those of the reference's reshape, cppsrc/ops/shape.cpp:15-44).
+std::vector<int64_t> resolve_new_shape(const std::vector<int64_t>& request, size_t numel) {
+  const int64_t total = static_cast<int64_t>(numel);
+  std::optional<size_t> infer_at;
+  int64_t fixed = 1;  // product of the given extents
+  for (size_t i = 0; i < request.size(); ++i) {
+    const int64_t e = request[i];
+    if (e >= 0) {
+      fixed *= e;
+    } else if (e != -1) {
       throw std::invalid_argument("reshape: negative dim other than -1");
+    } else if (infer_at) {
+      throw std::invalid_argument("reshape: at most one -1 dim allowed");
     } else {
-      known *= out[i];
+      infer_at = i;
     }
   }
-  if (neg_pos == -1) {
-    int64_t prod = 1;
-    for (auto d : out) prod *= d;
-    if (static_cast<size_t>(prod) != numel) throw std::invalid_argument("reshape: numel mismatch");
-  } else {
-    if (known == 0 || numel % static_cast<size_t>(known) != 0) {
-      throw std::invalid_argument("reshape: cannot infer -1 dim");
-    }
-    out[neg_pos] = static_cast<int64_t>(numel) / known;
+  if (!infer_at) {
+    if (fixed != total) throw std::invalid_argument("reshape: numel mismatch");
+    return request;
   }
-  return out;
+  if (fixed == 0 || total % fixed != 0) throw std::invalid_argument("reshape: cannot infer -1 dim");
+  std::vector<int64_t> shape = request;
+  shape[*infer_at] = total / fixed;
+  return shape;
 }
 
 // ------------------------------------------------------------ view Functions

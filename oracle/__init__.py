@@ -122,7 +122,8 @@ def ref():
         R.ref_dropout.argtypes = [_f32p, _f32p, vp, _i64, ctypes.c_float, ctypes.c_uint64]
         R.ref_causal_mask.argtypes = [_f32p, vp, _f32p, vp, _i64, _i64]
         R.ref_bmm.argtypes = [ctypes.c_int, _f32p, _f32p, _f32p, _i64, _i64, _i64, _i64]
-        for f in (R.ref_dropout, R.ref_causal_mask, R.ref_bmm):
+        R.ref_fanin_graph.argtypes = [_f32p, _f32p, _f32p, _f32p, _i64]
+        for f in (R.ref_dropout, R.ref_causal_mask, R.ref_bmm, R.ref_fanin_graph):
             f.restype = ctypes.c_int
         for f in (R.ref_matmul, R.ref_softmax, R.ref_layernorm, R.ref_attention, R.ref_elementwise,
                   R.ref_add_bias, R.ref_sum_all, R.ref_embedding, R.ref_cross_entropy, R.ref_adamw):
@@ -567,6 +568,19 @@ def ref_bmm(op: str, a, b) -> np.ndarray:
     if ref().ref_bmm(BMM_OPS.index(op), a, b, c, Bn, M, N, K) != 0:
         raise RuntimeError("reference bmm failed")
     return c
+
+
+def ref_fanin_graph(x, w, g):
+    """x.grad of the reference driver's fan-in graph (h = x*w0; u = h*w1;
+    v = 0.75*h; z = h*w2; t = x*w3; root = ((u+v)+z)+t) through the
+    reference's own autograd; w is [4, n]."""
+    x, w, g = _c(x), _c(w), _c(g)
+    n = x.size
+    assert w.shape == (4, n) and g.size == n
+    dx = np.empty_like(x)
+    if ref().ref_fanin_graph(x, w, g, dx, n) != 0:
+        raise RuntimeError("reference fan-in graph failed")
+    return dx
 
 
 def ref_lm_step(cfg, params, m, v, ids, targets, *, dropout, seed, lr, betas, eps, wd, t, grads=False):

@@ -412,4 +412,29 @@ int ref_lm_step(int64_t vocab, int64_t ctx, int64_t layers, int64_t d, int64_t h
   }
 }
 
+// A fixed graph with gradient fan-in, run through the reference's ops and
+// autograd (cppsrc/autograd/backward.cpp:50-113), for pinning the order in
+// which fan-in gradients are summed:
+//   h = x * w0;  u = h * w1;  v = scale(h, 0.75);  z = h * w2;
+//   t = x * w3;  root = ((u + v) + z) + t;  root.backward(g)
+// h receives three gradients (an interior fan-in), x two (a leaf fan-in).
+// w is [4][n]; writes x.grad [n].
+int ref_fanin_graph(const float* x, const float* w, const float* g, float* dx, int64_t n) {
+  try {
+    Tensor tx = make(x, {n}, true);
+    Tensor w0 = make(w, {n}), w1 = make(w + n, {n}), w2 = make(w + 2 * n, {n}), w3 = make(w + 3 * n, {n});
+    Tensor h = vlm::mul(tx, w0);
+    Tensor u = vlm::mul(h, w1);
+    Tensor v = vlm::scale(h, 0.75f);
+    Tensor z = vlm::mul(h, w2);
+    Tensor t = vlm::mul(tx, w3);
+    Tensor root = vlm::add(vlm::add(vlm::add(u, v), z), t);
+    root.backward(make(g, {n}));
+    out(*tx.grad(), dx);
+    return 0;
+  } catch (const std::exception&) {
+    return -1;
+  }
+}
+
 }  // extern "C"

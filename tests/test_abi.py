@@ -147,6 +147,21 @@ def test_factories_and_numpy_round_trip(ag):
     assert repr(ag.from_numpy(np.zeros((2, 3), np.float32))) == "Tensor(shape=[2, 3], dtype=Fp32, device=CPU)"
 
 
+def test_reshape_shape_rules(ag):
+    # the reference reshape's rules and messages (cppsrc/ops/shape.cpp:15-44):
+    # one inferred -1 at most, no other negative extent, the first offending
+    # entry from the left picks the message
+    t = ag.from_numpy(np.arange(24, dtype=np.float32))
+    assert ag.reshape(t, [2, -1, 3]).shape == [2, 4, 3]
+    assert ag.reshape(t, [24]).shape == [24]
+    assert ag.reshape(ag.from_numpy(np.zeros((0, 3), np.float32)), [3, 0]).shape == [3, 0]
+    for shape, msg in (([5, -1], "cannot infer"), ([0, -1], "cannot infer"), ([5, 5], "numel mismatch"),
+                       ([-1, -1], "at most one -1"), ([-2, 12], "negative dim other than -1"),
+                       ([-1, -1, -2], "at most one -1"), ([-2, -1, -1], "negative dim other than -1")):
+        with pytest.raises(ValueError, match=msg):
+            ag.reshape(t, shape)
+
+
 def test_views_on_host(ag):
     a = np.arange(24, dtype=np.float32).reshape(2, 3, 4)
     t = ag.from_numpy(a)

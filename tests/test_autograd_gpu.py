@@ -26,6 +26,28 @@ def test_device_round_trip_and_zeros(gpu):
     gpu.cuda_synchronize()
 
 
+@pytest.mark.skipif(not O.ref_available(), reason="oracle/_ref not built (no reference tree)")
+def test_fanin_order_bit_identical_to_reference_autograd(gpu):
+    """h = x*w0 feeds three consumers (u = h*w1, v = 0.75*h, z = h*w2) and x
+    also feeds t = x*w3; root = ((u + v) + z) + t.  Every product and sum is a
+    single fp32 operation on both sides, so x.grad agrees bit for bit with the
+    reference's own autograd (oracle/_ref) only if both sum the three
+    gradients of h, and then the two of x, in the same order."""
+    rng = np.random.default_rng(31)
+    n = 4099
+    x = rng.standard_normal(n).astype(f32)
+    w = rng.standard_normal((4, n)).astype(f32)
+    g = rng.standard_normal(n).astype(f32)
+    tx = dev(gpu, x, True)
+    w0, w1, w2, w3 = (dev(gpu, w[i]) for i in range(4))
+    h = gpu.mul(tx, w0)
+    u, v, z = gpu.mul(h, w1), gpu.scale(h, 0.75), gpu.mul(h, w2)
+    t = gpu.mul(tx, w3)
+    root = gpu.add(gpu.add(gpu.add(u, v), z), t)
+    root.backward(dev(gpu, g))
+    np.testing.assert_array_equal(host(gpu, tx.grad), O.ref_fanin_graph(x, w, g))
+
+
 def test_add_and_fan_in(gpu):
     rng = np.random.default_rng(0)
     a, b = rng.standard_normal((64, 33)).astype(f32), rng.standard_normal((64, 33)).astype(f32)

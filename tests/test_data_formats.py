@@ -53,6 +53,46 @@ def test_meta_json_layout(tmp_path):
     assert D.CharTokenizer.load(tmp_path / "meta.json").vocab == tok.vocab
 
 
+def test_tokenizer_encode_decode_rules():
+    # ids are positions in vocab (meta.json); unknown characters and ids raise
+    # KeyError, as the reference's dict lookups do (data.py:7-33)
+    tok = D.CharTokenizer(["b", "a", "\u00e9", "\n", "z"])
+    np.testing.assert_array_equal(tok.encode("ab\u00e9\nz"), [1, 0, 2, 3, 4])
+    assert tok.encode("").dtype == np.int64 and tok.encode("").shape == (0,)
+    assert tok.decode([4, 3, 2, 1, 0]) == "z\n\u00e9ab"
+    assert tok.decode(np.array([[0, 1]])) == "ba"
+    assert tok.stoi["z"] == 4 and tok.itos[2] == "\u00e9" and tok.vocab_size == 5
+    for bad in ("abc", "\u2603", "a\U0001F600"):
+        with pytest.raises(KeyError):
+            tok.encode(bad)
+    for bad in ([5], [-1]):
+        with pytest.raises(KeyError):
+            tok.decode(bad)
+    # the shipped vocabulary: every character of the validation text round-trips
+    text = (FIX / "val_head.txt").read_text()
+    ship = D.CharTokenizer.load(FIX / "meta.json")
+    assert ship.decode(ship.encode(text)) == text
+    np.testing.assert_array_equal(ship.encode(text), [ship.stoi[c] for c in text])
+
+
+def test_dataset_indexing_and_collate():
+    ids = np.arange(20, dtype=np.int64)
+    ds = D.TokenWindowDataset(ids, 4)
+    assert len(ds) == 16
+    np.testing.assert_array_equal(ds[-1]["input"], ids[15:19])
+    np.testing.assert_array_equal(ds[-1]["target"], ids[16:20])
+    for bad in (16, -17):
+        with pytest.raises(IndexError):
+            ds[bad]
+    assert [s["input"][0] for s in ds] == list(range(16))  # iteration stops at the end
+    batch = [ds[i] for i in (3, 0, 7)]
+    got = D.default_collate(batch)
+    assert list(got) == ["input", "target"]
+    for k in got:
+        np.testing.assert_array_equal(got[k], np.stack([b[k] for b in batch]))
+        assert got[k].dtype == np.int64 and got[k].shape == (3, 4)
+
+
 def test_window_dataset_and_loader():
     ids = np.arange(100, dtype=np.int64) * 3
     ds = D.TokenWindowDataset(ids, 8)

@@ -180,3 +180,38 @@ def test_ref_lm_step_matches_oracle_forward():
     assert abs(loss0 - want) <= 1e-5 * max(abs(want), 1)
     losses = [O.ref_lm_step(cfg, params, m, v, ids, tgt, t=t, **kw) for t in range(2, 6)]
     assert losses[-1] < loss0
+
+
+def _fanin_inputs(n=4099, seed=31):
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal(n).astype(f32)
+    w = rng.standard_normal((4, n)).astype(f32)
+    g = rng.standard_normal(n).astype(f32)
+    return x, w, g
+
+
+def _fanin_in_order(x, w, g, order):
+    """x.grad of the fan-in graph with h's three incoming gradients summed in
+    `order` (indices into (g*w1, g*0.75, g*w2)), in float32."""
+    parts = [g * w[1], g * f32(0.75), g * w[2]]
+    acc = parts[order[0]]
+    for i in order[1:]:
+        acc = (acc + parts[i]).astype(f32)
+    return (acc * w[0] + g * w[3]).astype(f32)
+
+
+@needs_ref
+def test_reference_fanin_summation_order():
+    # The reference's autograd (cppsrc/autograd/backward.cpp:50-113) runs the
+    # nodes in reverse DFS post-order, a node's inputs pushed in order and the
+    # last popped first.  For root = ((u + v) + z) + t that runs u, v, z (the
+    # consumers of h) in that order, so h's gradient is ((g*w1 + 0.75 g) + g*w2),
+    # and then x's: (h_grad * w0) + g*w3.  Bit-exact against the reference.
+    x, w, g = _fanin_inputs()
+    got = O.ref_fanin_graph(x, w, g)
+    np.testing.assert_array_equal(got, _fanin_in_order(x, w, g, (0, 1, 2)))
+    # the inputs separate the orders: any other summation order differs somewhere
+    for other in ((0, 2, 1), (1, 0, 2), (1, 2, 0), (2, 0, 1), (2, 1, 0)):
+        alt = _fanin_in_order(x, w, g, other)
+        if other != (1, 0, 2):  # (a + b) + c == (b + a) + c bit for bit
+            assert not np.array_equal(alt, got), other
