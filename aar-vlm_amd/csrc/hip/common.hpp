@@ -85,6 +85,44 @@ __device__ __forceinline__ float wave_max(float v) {
   return fmaxf(lo, hi);
 }
 
+// ---------------------------------------------------------------- HBM -> LDS DMA
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+// One 16-byte-per-lane HBM -> LDS DMA (global_load_lds_dwordx4): lane i
+// writes the 16 bytes at g into LDS at lds + 16 * i; `lds` must be
+// wave-uniform.  The builtin only exists for the device target; the host
+// pass, which never runs this code, sees an empty body so kernel host stubs
+// are still emitted.
+__device__ __forceinline__ void dma16(const void* g, lds_void_t* lds) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  __builtin_amdgcn_global_load_lds(g, lds, 16, 0, 0);
+#endif
+}
+
+// The same with 4 bytes per lane (lane i writes lds + 4 * i).
+__device__ __forceinline__ void dma4(const void* g, lds_void_t* lds) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  __builtin_amdgcn_global_load_lds(g, lds, 4, 0, 0);
+#endif
+}
+
+// s_waitcnt vmcnt(N) lgkmcnt(0) (expcnt untouched): this wave's DMAs and
+// loads but the last N are done, and its LDS accesses are complete.
+template <int N>
+__device__ __forceinline__ void wait_vm_lgkm0() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4));
+}
+
+// Workgroup barrier without a memory fence (DMA buffers are ordered by the
+// explicit waits); the empty asm statements keep the compiler from moving
+// LDS accesses across it.
+__device__ __forceinline__ void ring_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 // ---------------------------------------------------------------- host helpers
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }

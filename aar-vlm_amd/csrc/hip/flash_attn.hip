@@ -38,6 +38,7 @@
 #include <math.h>
 
 #include <algorithm>
+#include <atomic>
 #include <initializer_list>
 #include <stdint.h>
 
@@ -628,6 +629,237 @@ flash_bwd_dkdv_kernel(FaIn Qv, FaIn Kv, FaIn Vv, FaIn dOv, const float* __restri
   }
 }
 
+// ------------------------------------------------------ backward 1, paired
+// The dK/dV pass over 64-key workgroups for grids of about one round: four
+// waves as 2 key tiles x 2 query phases.  Per iteration the workgroup stages
+// two query tiles (t and t + 1) of Q, dO, lse and D; wave (a, p) takes query
+// tile t + p against key tile a, so the two phases of a key tile walk the
+// query range in step and each works half of it.  Against 128-key
+// workgroups this halves the longest work item and the idle diagonal steps
+// (causal T = 256, 384 heads: 8 instead of 12 rounds of tile work on 512
+// slots).  At the end phase 1 hands its dK/dV accumulators to phase 0
+// through LDS, and phase 0 adds them (phase 0 + phase 1, a fixed order):
+// deterministic, no atomics.  Stored dS tiles are written exactly as by
+// flash_bwd_dkdv_kernel.
+//
+// Q and dO tiles go HBM -> LDS by DMA (no staging registers: the 128-key
+// kernel already uses all 256 VGPRs of a 2-wave-per-SIMD launch).  A tile is
+// [32][DP] unpadded; float4 group g of row r sits at group g ^ (r & 15)
+// (DP = 64: 16 groups per row), so the 128-bit row reads (32 rows, one group)
+// and the 32-bit column reads (one row, 32 columns) are bank-conflict free.
+// Rows past T are clamped onto row T - 1 (their P is 0 through lse = +inf).
+// Requires d == DP == 64 and 16-byte aligned rows.
+struct FaDmaTile64 {
+  static constexpr int kGroups = 16;
+  static constexpr int kFloats = kTile * 64;
+  static constexpr int kPerWave = kTile * kGroups / (kWave * 4);  // 2 DMA instructions per wave (4 waves)
+
+  __device__ __forceinline__ static void issue(const float* __restrict__ base, int64_t st, int row0, int T,
+                                               float* stage, int wave, int lane) {
+#pragma unroll
+    for (int i = 0; i < kPerWave; ++i) {
+      const int u = (wave * kPerWave + i) * kWave + lane;
+      const int r = u / kGroups;
+      const int g = (u % kGroups) ^ (r & 15);
+      const int row = min(row0 + r, T - 1);
+      dma16(base + (int64_t)row * st + g * 4, (lds_void_t*)(stage + (wave * kPerWave + i) * kWave * 4));
+    }
+  }
+  // float4 group `grp` of row `row`
+  __device__ __forceinline__ static f32x4 group(const float* S, int row, int grp) {
+    return *reinterpret_cast<const f32x4*>(S + (row * kGroups + (grp ^ (row & 15))) * 4);
+  }
+  // Column reads of the dV/dK products: lane (lr, h) reads row
+  // q = 8*(st/4) + 4h + st%4, column 32b + lr.  The float offset splits into a
+  // lane part that depends on st only through st % 4 (lane_off(k), four
+  // values per lane) and a compile-time part (ct_off).
+  __device__ __forceinline__ static int lane_off(int k, int lr, int h) {
+    return 4 * h * 64 + ((((lr >> 2) ^ (4 * h)) ^ k) << 2) + (lr & 3);
+  }
+  __host__ __device__ static constexpr int ct_off(int st, int b) {
+    return (8 * (st >> 2) + (st & 3)) * 64 + ((b ^ ((st >> 2) & 1)) << 5);
+  }
+};
+
+template <int DP, bool CAUSAL, bool STORE_DS>
+__global__ void __launch_bounds__(kFaThreads, DP <= 64 && (CAUSAL || !STORE_DS) ? 2 : 1)
+flash_bwd_dkdv_pair_kernel(FaIn Qv, FaIn Kv, FaIn Vv, FaIn dOv, const float* __restrict__ Lse,
+                           const float* __restrict__ Dv, FaOut dKv, FaOut dVv, float* __restrict__ dS, int T,
+                           int d, int H, int nkb, int BH, float scale, float scale_log2) {
+  static_assert(DP == 64, "the paired kernel is built for head dim 64");
+  constexpr int NC = DP / 8;
+  constexpr int NB = DP / 32;
+  constexpr int kKeys = 2 * kTile;  // keys per workgroup
+  using Tile = FaDmaTile64;
+  __shared__ __attribute__((aligned(16))) float qs[2][2][Tile::kFloats];
+  __shared__ __attribute__((aligned(16))) float dos[2][2][Tile::kFloats];
+  __shared__ __attribute__((aligned(16))) float ls[2][2 * kTile];    // raw lse of the 64 staged rows
+  __shared__ __attribute__((aligned(16))) float dsum[2][2 * kTile];  // D of the 64 staged rows
+  static_assert(2 * kTile == kWave, "one 4-byte DMA per staged statistic");
+  static_assert(Tile::kFloats >= NB * 16 * kWave, "phase hand-over of one key tile fits in one staged tile");
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int lr = lane & 31, h = lane >> 5;
+  const int kt_local = wave & 1;  // key tile of this wave
+  const int phase = wave >> 1;    // query tile t + phase of each staged pair
+  const int kb = (int)(blockIdx.x / BH);  // longest work first under the causal mask
+  const int bh = blockIdx.x % BH;
+  const float* __restrict__ Q = Qv.head(bh, H);
+  const float* __restrict__ K = Kv.head(bh, H);
+  const float* __restrict__ V = Vv.head(bh, H);
+  const float* __restrict__ dO = dOv.head(bh, H);
+  const int k0 = kb * kKeys + kt_local * kTile;  // first key of this wave
+  const int kj = k0 + lr;
+  const bool key_ok = kj < T;
+
+  f32x4 kr[NC], vr[NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const int dd = 8 * c + 4 * h;
+    kr[c] = key_ok ? *reinterpret_cast<const f32x4*>(K + (int64_t)kj * Kv.st + dd) : f32x4{0.f, 0.f, 0.f, 0.f};
+    vr[c] = key_ok ? *reinterpret_cast<const f32x4*>(V + (int64_t)kj * Vv.st + dd) : f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  f32x16 dk[NB], dv[NB];
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    dk[b] = zero16();
+    dv[b] = zero16();
+  }
+
+  const int t0 = CAUSAL ? kb * 2 : 0;  // first query tile with work (64 keys = 2 tiles)
+  const int ntiles = (T + kTile - 1) / kTile;
+  float* dS_head = STORE_DS ? dS + (int64_t)bh * ds_pairs(ntiles, CAUSAL) * kDsTile : nullptr;
+  const int ds_lane = lr * kTile + 4 * h;
+  const int ktile = k0 / kTile;
+  const float* Lb = Lse + (int64_t)bh * T;
+  const float* Db = Dv + (int64_t)bh * T;
+
+  // Stages query tiles t, t + 1 into buffer `buf`, all by DMA: Q and dO tiles
+  // (two instructions per wave each), and the raw lse and D of the 64 rows
+  // (one 4-byte-per-lane instruction each, waves 0 and 1; rows past T read
+  // row T - 1 and are masked where P is formed).  No staging registers.
+  auto issue_tiles = [&](int t, int buf) {
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      Tile::issue(Q, Qv.st, (t + p) * kTile, T, qs[buf][p], wave, lane);
+      Tile::issue(dO, dOv.st, (t + p) * kTile, T, dos[buf][p], wave, lane);
+    }
+    if (wave < 2) {
+      // __lane_id() recomputes the lane index here (kept live, it would be
+      // spilled, and its reload would wait for every DMA in flight)
+      const int q = min(t * kTile + (int)__lane_id(), T - 1);
+      dma4((wave == 0 ? Lb : Db) + q, (lds_void_t*)(wave == 0 ? ls[buf] : dsum[buf]));
+    }
+  };
+  // Lane offset of the column reads for st % 4 == 0; the one for st % 4 == k
+  // is col_off ^ (k << 2) (see FaDmaTile64::lane_off: the XOR only touches
+  // bits 2-3 of its field).
+  const int col_off = Tile::lane_off(0, lr, h);
+  if (t0 < ntiles) issue_tiles(t0, 0);
+  wait_vm_lgkm0<0>();
+  ring_barrier();
+
+  for (int t = t0; t < ntiles; t += 2) {
+    const int cur = ((t - t0) >> 1) & 1;
+    const int qt0 = (t + phase) * kTile;  // this wave's query tile
+    const bool has_next = t + 2 < ntiles;
+    if (has_next) issue_tiles(t + 2, cur ^ 1);
+    if (qt0 < T && (!CAUSAL || qt0 + kTile - 1 >= k0)) {
+      const float* qt = qs[cur][phase];
+      const float* dot = dos[cur][phase];
+      f32x16 s = zero16(), dp = zero16();
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        const f32x4 qf = Tile::group(qt, lr, 2 * c + h);
+        const f32x4 df = Tile::group(dot, lr, 2 * c + h);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          s = mfma32(qf[e], kr[c][e], s);
+          dp = mfma32(df[e], vr[c][e], dp);
+        }
+      }
+      // s, dp: lane = key kj, register r = query qt0 + acc_row(r, h).
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const f32x4 l4 = *reinterpret_cast<const f32x4*>(&ls[cur][phase * kTile + 8 * g + 4 * h]);
+        const f32x4 d4 = *reinterpret_cast<const f32x4*>(&dsum[cur][phase * kTile + 8 * g + 4 * h]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int r = 4 * g + e;
+          const int q = qt0 + acc_row(r, h);
+          float p = fast_exp2(s[r] * scale_log2 - l4[e] * kLog2e);
+          // Keys past the end (zero-filled K) and queries past the end get
+          // P = 0, so a stored dS tile is exactly zero there.
+          if ((CAUSAL && kj > q) || !key_ok || q >= T) p = 0.f;
+          s[r] = p;
+          dp[r] = p * (dp[r] - d4[e]);
+        }
+      }
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+#pragma unroll
+        for (int st = 0; st < 16; ++st) {
+          const int q = acc_row(st, h);
+          const int o = Tile::ct_off(st, b) + (col_off ^ ((st & 3) << 2));
+          dv[b] = mfma32(dot[o], s[st], dv[b]);
+          dk[b] = mfma32(qt[o], dp[st], dk[b]);
+        }
+      }
+      if (STORE_DS && k0 < T) {
+        float* tile = dS_head + ds_pair(t + phase, ktile, ntiles, CAUSAL) * kDsTile + ds_lane;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const f32x4 v = {dp[4 * g], dp[4 * g + 1], dp[4 * g + 2], dp[4 * g + 3]};
+          *reinterpret_cast<f32x4*>(tile + 8 * g) = v;
+        }
+      }
+    }
+    wait_vm_lgkm0<0>();
+    ring_barrier();
+  }
+
+  // Phase 1 hands its accumulators to phase 0 of the same key tile through
+  // the staging buffers (every wave is past the loop's last barrier, no DMA
+  // is in flight): dK in qs[0][kt_local], dV in dos[0][kt_local], lane-major
+  // so the writes and reads are conflict free.
+  float* hk = qs[0][kt_local];
+  float* hv = dos[0][kt_local];
+  if (phase == 1) {
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        hk[(b * 16 + r) * kWave + lane] = dk[b][r];
+        hv[(b * 16 + r) * kWave + lane] = dv[b][r];
+      }
+    }
+  }
+  __syncthreads();
+  if (phase == 1 || !key_ok) return;
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      dk[b][r] += hk[(b * 16 + r) * kWave + lane];
+      dv[b][r] += hv[(b * 16 + r) * kWave + lane];
+    }
+  }
+  float* krow = dKv.head(bh, H) + (int64_t)kj * dKv.st;
+  float* vrow = dVv.head(bh, H) + (int64_t)kj * dVv.st;
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int dd = b * 32 + 8 * g + 4 * h;
+      f32x4 a = {dk[b][4 * g] * scale, dk[b][4 * g + 1] * scale, dk[b][4 * g + 2] * scale,
+                 dk[b][4 * g + 3] * scale};
+      f32x4 c = {dv[b][4 * g], dv[b][4 * g + 1], dv[b][4 * g + 2], dv[b][4 * g + 3]};
+      *reinterpret_cast<f32x4*>(krow + dd) = a;
+      *reinterpret_cast<f32x4*>(vrow + dd) = c;
+    }
+  }
+}
+
 // ------------------------------------------------------------- backward 2
 
 template <int DP, bool CAUSAL, bool VEC>
@@ -964,12 +1196,68 @@ struct BwdArgs {
   float* dS;  // stored-dS path when non-null
   int T, d, H, BH;
   float scale;
+  int key_block;  // keys per dK/dV workgroup: 64 (paired kernel) or 128
   hipStream_t st;
 };
+
+// Workgroups of a dK/dV kernel resident on one CU at once.
+template <int DP, bool C, bool VEC, bool PAIR>
+int fa_dkdv_resident() {
+  static const int n = [] {
+    int b = 0;
+    hipError_t e;
+    if constexpr (PAIR) {
+      e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, flash_bwd_dkdv_pair_kernel<DP, C, true>, kFaThreads, 0);
+    } else {
+      e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, flash_bwd_dkdv_kernel<DP, C, VEC, true>, kFaThreads,
+                                                       0);
+    }
+    if (e != hipSuccess) b = 1;
+    return b > 0 ? b : 1;
+  }();
+  return n;
+}
+
+// Keys per dK/dV workgroup.  128-key workgroups hold four key tiles that
+// share each staged query tile; when their grid is at most two rounds of
+// resident workgroups (short sequences, few heads) its longest items set the
+// time, and the paired 64-key kernel (half the longest item) is used instead.
+// The paired kernel stages its tiles by DMA in a layout built for d = 64
+// exactly, with 128-bit operands; other shapes take 128-key workgroups.  A process-wide
+// override (aar_flash_set_bwd_key_block) serves tuning and tests.
+std::atomic<int> g_bwd_key_block_override{0};
+int fa_bwd_key_block(int64_t bh, int64_t T, int64_t d, bool causal, bool vec) {
+  if (d != 64 || !vec) return 128;
+  const int forced = g_bwd_key_block_override.load(std::memory_order_relaxed);
+  if (forced) return forced;
+  const int resident =
+      causal ? fa_dkdv_resident<64, true, true, false>() : fa_dkdv_resident<64, false, true, false>();
+  const int64_t slots = (int64_t)device_cu_count() * resident;
+  const int64_t grid = bh * ((T + kBlock - 1) / kBlock);
+  return grid <= 2 * slots ? 64 : 128;
+}
 
 template <int DP, bool C, bool VEC>
 struct BwdLaunch {
   static int run(const BwdArgs& a) {
+    if constexpr (DP == 64 && VEC) {
+      const int64_t nb2 = (a.T + 2 * kTile - 1) / (2 * kTile);
+      // (a dispatch holds the grid as a 32-bit work-item count)
+      if (a.key_block == 64 && a.d == DP && nb2 * a.BH * kFaThreads <= (int64_t)UINT32_MAX) {
+        if (a.dS) {
+          flash_bwd_dkdv_pair_kernel<DP, C, true><<<dim3((unsigned)(nb2 * a.BH)), dim3(kFaThreads), 0, a.st>>>(
+              a.q, a.k, a.v, a.dout, a.lse, a.D, a.dk, a.dv, a.dS, a.T, a.d, a.H, (int)nb2, a.BH, a.scale,
+              a.scale * kLog2e);
+        } else {
+          flash_bwd_dkdv_pair_kernel<DP, C, false><<<dim3((unsigned)(nb2 * a.BH)), dim3(kFaThreads), 0, a.st>>>(
+              a.q, a.k, a.v, a.dout, a.lse, a.D, a.dk, a.dv, nullptr, a.T, a.d, a.H, (int)nb2, a.BH, a.scale,
+              a.scale * kLog2e);
+        }
+        const int rc = launch_status();
+        if (rc != AAR_OK) return rc;
+        return run_dq(a);
+      }
+    }
     const int nb = (a.T + kBlock - 1) / kBlock;
     if (a.dS) {
       flash_bwd_dkdv_kernel<DP, C, VEC, true><<<dim3((unsigned)(nb * a.BH)), dim3(kFaThreads), 0, a.st>>>(
@@ -980,8 +1268,15 @@ struct BwdLaunch {
           a.q, a.k, a.v, a.dout, a.lse, a.D, a.dk, a.dv, nullptr, a.T, a.d, a.H, nb, a.BH, a.scale,
           a.scale * kLog2e);
     }
-    int rc = launch_status();
+    const int rc = launch_status();
     if (rc != AAR_OK) return rc;
+    return run_dq(a);
+  }
+
+  // The dQ pass (128-query workgroups), from the stored dS tiles or by
+  // recomputing P and dP.
+  static int run_dq(const BwdArgs& a) {
+    const int nb = (a.T + kBlock - 1) / kBlock;
     if (a.dS) {
       flash_bwd_dq_ds_kernel<DP, C, VEC><<<dim3((unsigned)(nb * a.BH)), dim3(kFaThreads), 0, a.st>>>(
           a.k, a.dS, a.dq, a.T, a.d, a.H, nb, a.BH, a.scale);
@@ -1097,7 +1392,7 @@ extern "C" int aar_flash_bwd_strided_f32(const float* q, const float* k, const f
             fa_out(dq, strides + 15),   fa_out(dk, strides + 18),   fa_out(dv, strides + 21),
             dS,                         (int)T,                     (int)d,
             (int)H,                     (int)bh,                    scale,
-            st};
+            fa_bwd_key_block(bh, T, d, causal != 0, vec),  st};
   return dispatch_fa<BwdLaunch>(pad_dim(d), causal != 0, vec, a);
 }
 
@@ -1114,4 +1409,38 @@ extern "C" int aar_flash_bwd_f32(const float* q, const float* k, const float* v,
   }
   return aar_flash_bwd_strided_f32(q, k, v, o, lse, dout, dq, dk, dv, 1, bh, T, d, strides, causal, scale,
                                    workspace, workspace_bytes, stream);
+}
+
+extern "C" int aar_flash_fwd_plan(int64_t bh, int64_t T, int64_t d, int causal, int vec, size_t workspace_bytes,
+                                  int* split_blocks) {
+  if (!split_blocks || bh <= 0 || T <= 0 || d <= 0) return AAR_EINVAL;
+  if (d > 128) return AAR_EINVAL;
+  if (!fa_shape_ok(bh, T, d)) return AAR_EUNSUPPORTED;
+  *split_blocks = 0;
+  if (!causal || workspace_bytes < fa_fwd_split_bytes(bh, T, d) || fa_fwd_split_bytes(bh, T, d) == 0) return AAR_OK;
+  const int64_t nqb = (T + kBlock - 1) / kBlock;
+  const int dp = pad_dim(d);
+  int resident = 1;
+#define AAR_RES(DPV) \
+  if (dp == DPV) resident = vec ? fa_fwd_resident<DPV, true>() : fa_fwd_resident<DPV, false>();
+  AAR_RES(32)
+  AAR_RES(64)
+  AAR_RES(128)
+#undef AAR_RES
+  *split_blocks = fa_fwd_split_blocks(bh, nqb, (int64_t)device_cu_count() * resident);
+  return AAR_OK;
+}
+
+extern "C" int aar_flash_bwd_plan(int64_t bh, int64_t T, int64_t d, int causal, int vec, int* key_block) {
+  if (!key_block || bh <= 0 || T <= 0 || d <= 0) return AAR_EINVAL;
+  if (d > 128) return AAR_EINVAL;
+  if (!fa_shape_ok(bh, T, d)) return AAR_EUNSUPPORTED;
+  *key_block = fa_bwd_key_block(bh, T, d, causal != 0, vec != 0);
+  return AAR_OK;
+}
+
+extern "C" int aar_flash_set_bwd_key_block(int key_block) {
+  if (key_block != 0 && key_block != 64 && key_block != 128) return AAR_EINVAL;
+  g_bwd_key_block_override.store(key_block, std::memory_order_relaxed);
+  return AAR_OK;
 }

@@ -293,16 +293,6 @@ gemm_f32_kernel(const float* __restrict__ A, const float* __restrict__ B, float*
 // written to the same layout.  The ring is synchronised by an explicit
 // s_waitcnt on this wave's outstanding DMAs plus s_barrier.
 
-typedef __attribute__((address_space(3))) void lds_void_t;
-
-// One 16-byte-per-lane HBM -> LDS DMA (LDS address = lds + 16 * lane).  The
-// builtin only exists for the device target; the host pass, which never runs
-// this code, sees an empty body so the kernel's host stub is still emitted.
-__device__ __forceinline__ void dma16(const void* g, lds_void_t* lds) {
-#if defined(__HIP_DEVICE_COMPILE__)
-  __builtin_amdgcn_global_load_lds(g, lds, 16, 0, 0);
-#endif
-}
 
 // Row swizzle of the K-contiguous layout: rows that one 8- or 16-lane LDS
 // pass reads (8 or 16 consecutive rows, same q) land in distinct banks.
@@ -394,21 +384,7 @@ struct DmaTile {
   }
 };
 
-// s_waitcnt vmcnt(N) lgkmcnt(0) (expcnt untouched).
-template <int N>
-__device__ __forceinline__ void wait_vm_lgkm0() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4));
-}
 
-// Workgroup barrier without a memory fence (the DMA ring is ordered by the
-// explicit waits); the empty asm statements keep the compiler from moving
-// LDS accesses across it.
-__device__ __forceinline__ void ring_barrier() {
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-}
 
 template <int BM, int BN, int BK, int WM, int WN, int WPE, int S, bool A_KC, bool B_KC, int EPI>
 __global__ void __launch_bounds__((BM / WM) * (BN / WN) * 64, WPE)

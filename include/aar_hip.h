@@ -270,6 +270,22 @@ int aar_flash_bwd_strided_f32(const float* q, const float* k, const float* v,
                               const int64_t* strides, int causal, float scale,
                               void* workspace, size_t workspace_bytes, void* stream);
 
+/* Plans the flash calls would take on the current device (tuning and tests;
+ * no counterpart in the reference, whose kernels have one launch shape,
+ * cppsrc/ops/flash_attention.cu:227-280).  vec: 1 when the operands take the
+ * 128-bit path (16-byte aligned, d and all strides multiples of 4).
+ * aar_flash_fwd_plan: query blocks per head that the causal strided forward
+ * splits over two workgroups given `workspace_bytes` of workspace (0: none).
+ * aar_flash_bwd_plan: keys per dK/dV workgroup, 64 (the paired kernel: two
+ * query phases per key tile, for grids of about one round) or 128.
+ * aar_flash_set_bwd_key_block forces that choice for later calls in this
+ * process (64 or 128; 0 restores the plan; head dims above 64 always take
+ * 128); backward calls running on other threads meanwhile may see either. */
+int aar_flash_fwd_plan(int64_t bh, int64_t T, int64_t d, int causal, int vec, size_t workspace_bytes,
+                       int* split_blocks);
+int aar_flash_bwd_plan(int64_t bh, int64_t T, int64_t d, int causal, int vec, int* key_block);
+int aar_flash_set_bwd_key_block(int key_block);
+
 /* Strided fp32 copy of an ndim <= 8 view: dst[idx] = src[idx] for every index
  * of `shape`, element offsets given by the two stride arrays (host arrays, read
  * during the call).  Replaces contiguous_cuda / copy_contiguous_into_strided_cuda

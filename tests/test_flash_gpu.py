@@ -413,3 +413,108 @@ def test_abi_forward_key_range_split(gpu, bh, T, d, offset):
     # below the tolerance
     assert_close(o_split, o_whole, 1e-5, "O split vs whole")
     assert_close(l_split, l_whole, 1e-5, "lse split vs whole")
+
+
+def _flash_plans():
+    L = Abi().L
+    ip = ctypes.POINTER(ctypes.c_int)
+    L.aar_flash_bwd_plan.argtypes = [ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int, ctypes.c_int, ip]
+    L.aar_flash_fwd_plan.argtypes = [ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int, ctypes.c_int,
+                                     ctypes.c_size_t, ip]
+    L.aar_flash_fwd_workspace_bytes.restype = ctypes.c_size_t
+    L.aar_flash_fwd_workspace_bytes.argtypes = [ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int]
+    L.aar_flash_set_bwd_key_block.argtypes = [ctypes.c_int]
+    return L
+
+
+def _bwd_plan(L, bh, T, d, causal, vec=1):
+    out = ctypes.c_int()
+    assert L.aar_flash_bwd_plan(bh, T, d, int(causal), vec, ctypes.byref(out)) == 0
+    return out.value
+
+
+def test_flash_plans(gpu):
+    """The plan queries: the paired 64-key dK/dV kernel for grids of about one
+    round with d = 64 on the 128-bit path, 128-key workgroups otherwise;
+    the forward's key-range split for under-filled causal grids only."""
+    L = _flash_plans()
+    assert _bwd_plan(L, 384, 256, 64, True) == 64     # the GPT step's attention
+    assert _bwd_plan(L, 96, 1024, 64, True) == 64     # BASELINE config 4, T = 1024
+    assert _bwd_plan(L, 96, 4096, 64, True) == 128    # BASELINE config 4, T = 4096
+    assert _bwd_plan(L, 8, 300, 64, False) == 64
+    for d in (32, 48, 100, 128):                      # other head dims
+        assert _bwd_plan(L, 8, 256, d, True) == 128
+    assert _bwd_plan(L, 8, 256, 64, True, vec=0) == 128
+    out = ctypes.c_int()
+    assert L.aar_flash_bwd_plan(8, 256, 200, 1, 1, ctypes.byref(out)) == -1
+    assert L.aar_flash_set_bwd_key_block(96) == -1
+    try:
+        assert L.aar_flash_set_bwd_key_block(128) == 0
+        assert _bwd_plan(L, 384, 256, 64, True) == 128
+        assert L.aar_flash_set_bwd_key_block(64) == 0
+        assert _bwd_plan(L, 96, 4096, 64, True) == 64
+        assert _bwd_plan(L, 8, 256, 128, True) == 128  # other head dims never pair
+        assert _bwd_plan(L, 8, 256, 32, True) == 128
+    finally:
+        L.aar_flash_set_bwd_key_block(0)
+    # forward split: with its workspace, a small causal grid splits, a full one does not
+    for bh, T, want_split in ((2, 2048, True), (12, 1024, True), (96, 1024, True), (192, 512, False),
+                              (96, 4096, False)):
+        wsb = L.aar_flash_fwd_workspace_bytes(bh, T, 64, 1)
+        assert L.aar_flash_fwd_plan(bh, T, 64, 1, 1, wsb, ctypes.byref(out)) == 0
+        assert (out.value > 0) == want_split, (bh, T, out.value)
+        assert L.aar_flash_fwd_plan(bh, T, 64, 1, 1, 0, ctypes.byref(out)) == 0 and out.value == 0
+        assert L.aar_flash_fwd_plan(bh, T, 64, 0, 1, wsb, ctypes.byref(out)) == 0 and out.value == 0
+
+
+@pytest.mark.parametrize("key_block", [64, 128])
+@pytest.mark.parametrize("bh,T,d,causal", [(3, 77, 64, True), (2, 45, 64, False), (1, 1, 64, True),
+                                           (2, 33, 64, True), (2, 257, 64, True), (4, 64, 64, True),
+                                           (2, 96, 64, False), (1, 300, 64, False), (2, 130, 64, True),
+                                           (5, 31, 64, True), (2, 65, 64, False)])
+def test_dkdv_key_blocks_vs_oracle(gpu, key_block, bh, T, d, causal):
+    """Both dK/dV decompositions (forced) against the oracle through both
+    backward paths; the stored-dS and recompute paths share the dK/dV kernel
+    and agree bit for bit."""
+    L = _flash_plans()
+    rng = np.random.default_rng(bh * 977 + T + d + causal)
+    q, k, v, do = (rng.standard_normal((bh, T, d)).astype(f32) for _ in range(4))
+    try:
+        assert L.aar_flash_set_bwd_key_block(key_block) == 0
+        assert _bwd_plan(L, bh, T, d, causal) == key_block
+        o, slow, fast = _abi_bwd_both_paths(q, k, v, do, causal)
+    finally:
+        L.aar_flash_set_bwd_key_block(0)
+    assert_close(o, O.attention(q, k, v, causal), TOL, "O")
+    ref = O.attention_backward(q, k, v, do, causal)
+    for g, r, n in zip(fast, ref, ("dq", "dk", "dv")):
+        assert_close(g, r, TOL, f"{n} (key block {key_block})")
+    for a, b in zip(fast, slow):
+        np.testing.assert_array_equal(a, b)
+
+
+def test_paired_dkdv_at_config5_shape_and_reruns(gpu):
+    """The paired kernel at the GPT step's attention shape (planned there), on
+    the packed-qkv strided views, against the oracle on sampled heads and
+    bit-identical on a rerun."""
+    L = _flash_plans()
+    B, T, H, d = 64, 256, 6, 64
+    assert _bwd_plan(L, B * H, T, d, True) == 64
+    rng = np.random.default_rng(12)
+    D = H * d
+    qkv = rng.standard_normal((B, T, 3 * D)).astype(f32)
+    do = rng.standard_normal((B, T, D)).astype(f32)
+    grads = []
+    for _ in range(2):
+        t = dev(gpu, qkv, True)
+        gpu._core._flash_attention_qkv(t, H, True).backward(dev(gpu, do))
+        grads.append(host(gpu, t.grad))
+    np.testing.assert_array_equal(grads[0], grads[1])
+    g = grads[0].reshape(B, T, 3, H, d)
+    heads = qkv.reshape(B, T, 3, H, d)
+    dob = do.reshape(B, T, H, d)
+    for b, h in ((0, 0), (40, 5)):
+        q, k, v = (np.ascontiguousarray(heads[b, :, i, h])[None] for i in range(3))
+        rq, rk, rv = O.attention_backward(q, k, v, np.ascontiguousarray(dob[b, :, h])[None], True)
+        for i, ref in enumerate((rq, rk, rv)):
+            assert_close(g[b, :, i, h][None], ref, TOL, f"d{'qkv'[i]} ({b},{h})")
