@@ -453,7 +453,11 @@ flash_fwd_combine_kernel(FaSplit sp, FaOut Ov, float* __restrict__ Lse, int T, i
 
 // ------------------------------------------------------------- backward 0
 
-// D[bh*T + t] = sum_c dO[bh][t][c] * O[bh][t][c]; 16 lanes per row.
+// D[bh*T + t] = sum_c dO[bh][t][c] * O[bh][t][c]; 16 lanes per row.  VEC
+// (d % 4 == 0, 16-byte aligned rows): each lane takes float4 groups sub,
+// sub + 16, ... with 128-bit loads (one per operand for d <= 64), so a row
+// is two contiguous 256-byte reads; else element-wise.
+template <bool VEC>
 __global__ void __launch_bounds__(256)
 flash_bwd_dot_kernel(FaIn dOv, FaIn Ov, float* __restrict__ D, int64_t rows, int T, int H, int d) {
   const int64_t row = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 4;
@@ -463,7 +467,15 @@ flash_bwd_dot_kernel(FaIn dOv, FaIn Ov, float* __restrict__ D, int64_t rows, int
     const int bh = (int)(row / T), t = (int)(row % T);
     const float* a = dOv.head(bh, H) + (int64_t)t * dOv.st;
     const float* b = Ov.head(bh, H) + (int64_t)t * Ov.st;
-    for (int c = sub; c < d; c += 16) acc += a[c] * b[c];
+    if (VEC) {
+      for (int c = 4 * sub; c < d; c += 64) {
+        const f32x4 x = *reinterpret_cast<const f32x4*>(a + c);
+        const f32x4 y = *reinterpret_cast<const f32x4*>(b + c);
+        acc += x[0] * y[0] + x[1] * y[1] + x[2] * y[2] + x[3] * y[3];
+      }
+    } else {
+      for (int c = sub; c < d; c += 16) acc += a[c] * b[c];
+    }
   }
   acc += dpp_quad_xor1(acc);
   acc += dpp_quad_xor2(acc);
@@ -1060,6 +1072,126 @@ flash_bwd_dq_ds_kernel(FaIn Kv, const float* __restrict__ dS, FaOut dQv, int T, 
   }
 }
 
+// dQ from the stored dS tiles over 64-query workgroups, for the grids that
+// take the paired dK/dV kernel: four waves as 2 query tiles x 2 key phases.
+// Per iteration the workgroup stages key tiles t and t + 1 (transposed, as
+// above); wave (a, p) takes key tile t + p for query tile a, so the two
+// phases of a query tile split its key range and the longest work item is
+// half that of a 128-query workgroup.  At the end phase 1 hands its dQ
+// accumulators to phase 0 through LDS and phase 0 adds them (phase 0 +
+// phase 1, a fixed order; deterministic).
+template <int DP, bool CAUSAL, bool VEC>
+__global__ void __launch_bounds__(kFaThreads, 4)
+flash_bwd_dq_ds_pair_kernel(FaIn Kv, const float* __restrict__ dS, FaOut dQv, int T, int d, int H, int nqb,
+                            int BH, float scale) {
+  constexpr int NB = DP / 32;
+  constexpr int kQueries = 2 * kTile;  // queries per workgroup
+  __shared__ __attribute__((aligned(16))) float kts[2][2][DP * kLdt];  // key tiles t, t+1, transposed
+  static_assert(2 * DP * kLdt >= 2 * NB * 16 * kWave, "phase hand-over fits in one staged tile pair");
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int lr = lane & 31, h = lane >> 5;
+  const int qt_local = wave & 1;  // query tile of this wave
+  const int phase = wave >> 1;    // key tile t + phase of each staged pair
+  const int qb = CAUSAL ? nqb - 1 - (int)(blockIdx.x / BH) : (int)(blockIdx.x / BH);  // longest first
+  const int bh = blockIdx.x % BH;
+  const float* __restrict__ K = Kv.head(bh, H);
+  const int q0 = qb * kQueries + qt_local * kTile;
+  const int qi = q0 + lr;
+  const int qtile = q0 / kTile;
+  const int nt = (T + kTile - 1) / kTile;
+  const bool active = q0 < T;  // tiles past the end were never stored
+  const float* __restrict__ dS_head = dS + (int64_t)bh * ds_pairs(nt, CAUSAL) * kDsTile + 4 * h * kTile + lr;
+
+  f32x16 dq[NB];
+#pragma unroll
+  for (int b = 0; b < NB; ++b) dq[b] = zero16();
+
+  const int kv_end = CAUSAL ? min(T, qb * kQueries + kQueries) : T;
+  const int ntiles = (kv_end + kTile - 1) / kTile;
+  auto has_work = [&](int t) { return active && t < ntiles && (!CAUSAL || t <= qtile); };
+  auto load_ds = [&](int t, float (&r)[16]) {
+    const float* tile = dS_head + ds_pair(qtile, t, nt, CAUSAL) * kDsTile;
+#pragma unroll
+    for (int st = 0; st < 16; ++st) r[st] = tile[(8 * (st >> 2) + (st & 3)) * kTile];
+  };
+
+  constexpr bool kSwz = kKtSwizzle<DP, CAUSAL>;
+  TileCopy<DP, VEC> kc0, kc1;
+  kc0.load(K, Kv.st, 0, T, d, tid);
+  kc1.load(K, Kv.st, kTile, T, d, tid);
+  kc0.template store_t<kLdt, kSwz>(kts[0][0], tid);
+  kc1.template store_t<kLdt, kSwz>(kts[0][1], tid);
+  float dsr[16];
+  if (has_work(phase)) load_ds(phase, dsr);
+  __syncthreads();
+
+  for (int t = 0; t < ntiles; t += 2) {
+    const int cur = (t >> 1) & 1;
+    const bool has_next = t + 2 < ntiles;
+    if (has_next) {
+      kc0.load(K, Kv.st, (t + 2) * kTile, T, d, tid);
+      kc1.load(K, Kv.st, (t + 3) * kTile, T, d, tid);
+    }
+    float nxt[16];
+    if (has_work(t + 2 + phase)) load_ds(t + 2 + phase, nxt);
+    if (has_work(t + phase)) {
+      const float* kt = kts[cur][phase];
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          // K^T[b*32 + lr][keys 8g + 4h .. +3]: one 128-bit read feeds 4 steps
+          const int kc_col = b * 32 + lr;
+          const f32x4 kf = *reinterpret_cast<const f32x4*>(kt + kc_col * kLdt + vt_swz<kSwz>(kc_col, 8 * g + 4 * h));
+#pragma unroll
+          for (int e = 0; e < 4; ++e) dq[b] = mfma32(kf[e], dsr[4 * g + e], dq[b]);
+        }
+      }
+    }
+    if (has_next) {
+      kc0.template store_t<kLdt, kSwz>(kts[cur ^ 1][0], tid);
+      kc1.template store_t<kLdt, kSwz>(kts[cur ^ 1][1], tid);
+    }
+    if (has_work(t + 2 + phase)) {
+#pragma unroll
+      for (int st = 0; st < 16; ++st) dsr[st] = nxt[st];
+    }
+    __syncthreads();
+  }
+
+  // Phase 1 hands its dQ accumulators to phase 0 of the same query tile
+  // through the staging buffers (every wave is past the loop's last barrier),
+  // lane-major so the writes and reads are conflict free.
+  float* hq = &kts[0][0][0] + qt_local * (NB * 16 * kWave);
+  if (phase == 1) {
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) hq[(b * 16 + r) * kWave + lane] = dq[b][r];
+    }
+  }
+  __syncthreads();
+  if (phase == 1 || qi >= T) return;
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) dq[b][r] += hq[(b * 16 + r) * kWave + lane];
+  }
+  float* qrow = dQv.head(bh, H) + (int64_t)qi * dQv.st;
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int dd = b * 32 + 8 * g + 4 * h;
+      if (dd >= d) continue;
+      f32x4 v = {dq[b][4 * g] * scale, dq[b][4 * g + 1] * scale, dq[b][4 * g + 2] * scale,
+                 dq[b][4 * g + 3] * scale};
+      store4<VEC>(qrow + dd, v, d - dd);
+    }
+  }
+}
+
 // ------------------------------------------------------------ dispatching
 
 int pad_dim(int64_t d) { return d <= 32 ? 32 : (d <= 64 ? 64 : 128); }
@@ -1277,6 +1409,14 @@ struct BwdLaunch {
   // recomputing P and dP.
   static int run_dq(const BwdArgs& a) {
     const int nb = (a.T + kBlock - 1) / kBlock;
+    if constexpr (DP == 64) {
+      const int64_t nb2 = (a.T + 2 * kTile - 1) / (2 * kTile);
+      if (a.dS && a.key_block == 64 && nb2 * a.BH * kFaThreads <= (int64_t)UINT32_MAX) {
+        flash_bwd_dq_ds_pair_kernel<DP, C, VEC><<<dim3((unsigned)(nb2 * a.BH)), dim3(kFaThreads), 0, a.st>>>(
+            a.k, a.dS, a.dq, a.T, a.d, a.H, (int)nb2, a.BH, a.scale);
+        return launch_status();
+      }
+    }
     if (a.dS) {
       flash_bwd_dq_ds_kernel<DP, C, VEC><<<dim3((unsigned)(nb * a.BH)), dim3(kFaThreads), 0, a.st>>>(
           a.k, a.dS, a.dq, a.T, a.d, a.H, nb, a.BH, a.scale);
@@ -1379,7 +1519,9 @@ extern "C" int aar_flash_bwd_strided_f32(const float* q, const float* k, const f
   hipStream_t st = as_stream(stream);
   float* D = static_cast<float*>(workspace);
   const int64_t rows = bh * T;
-  flash_bwd_dot_kernel<<<dim3((unsigned)ceil_div(rows * 16, (int64_t)256)), dim3(256), 0, st>>>(
+  const bool dot_vec = fa_vec_ok(d, {o, dout}, strides + 9, 6);
+  auto dot_kernel = dot_vec ? flash_bwd_dot_kernel<true> : flash_bwd_dot_kernel<false>;
+  dot_kernel<<<dim3((unsigned)ceil_div(rows * 16, (int64_t)256)), dim3(256), 0, st>>>(
       fa_in(dout, strides + 12), fa_in(o, strides + 9), D, rows, (int)T, (int)H, (int)d);
   int rc = launch_status();
   if (rc != AAR_OK) return rc;

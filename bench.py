@@ -160,8 +160,8 @@ def bench_matmul(ag, steps: int, warmup: int, ev: Events, inputs=None):
     return ms / steps, wall, err, (a, b), dist
 
 
-def bench_flash(ag, steps: int, warmup: int, ev: Events, T: int = 4096):
-    B, H, d = 8, 12, 64
+def bench_flash(ag, steps: int, warmup: int, ev: Events, T: int = 4096, B: int = 8, H: int = 12):
+    d = 64
     rng = np.random.default_rng(0)
     q, k, v, do = (rng.standard_normal((B, H, T, d)).astype(np.float32) for _ in range(4))
     tq, tk, tv = (ag.from_numpy(x).to(ag.Device.CUDA) for x in (q, k, v))
@@ -688,8 +688,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=60)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--flash-steps", type=int, default=50)
-    ap.add_argument("--flash-t", type=int, default=4096, choices=[1024, 4096],
-                    help="sequence length of the --only flash run (BASELINE config 4 has both)")
+    ap.add_argument("--flash-t", type=int, default=4096, choices=[256, 1024, 4096],
+                    help="sequence length of the --only flash run (BASELINE config 4 has 1024 and 4096 at "
+                         "B8 H12; 256 is config 5's attention, B64 H6)")
     ap.add_argument("--only", choices=["all", "gemm", "flash", "rowwise", "extra", "copy", "gpt", "sweep"], default="all",
                     help="run one part (profiling runs); the JSON line is printed for 'all'")
     args = ap.parse_args()
@@ -723,7 +724,8 @@ def main() -> int:
         log(json.dumps(bench_gpt(ag, ev)))
         return 0
     if args.only == "flash":
-        fa_ms, fa_flops, fa_dist = bench_flash(ag, args.flash_steps, 10, ev, T=args.flash_t)
+        bh = (64, 6) if args.flash_t == 256 else (8, 12)
+        fa_ms, fa_flops, fa_dist = bench_flash(ag, args.flash_steps, 10, ev, T=args.flash_t, B=bh[0], H=bh[1])
         log(f"flash T={args.flash_t} fwd+bwd {fa_ms:.3f} ms {fa_flops / (fa_ms * 1e-3) / 1e12:.2f} TFLOPS {fa_dist}")
         return 0
 
@@ -745,6 +747,11 @@ def main() -> int:
     fa1_tflops = fa1_flops / (fa1_ms * 1e-3) / 1e12
     log(f"flash causal B8 H12 T1024 d64 fwd+bwd: {fa1_ms:.3f} ms, {fa1_tflops:.2f} TFLOPS "
         f"({100 * fa1_tflops / PEAK_FP32_MFMA_TFLOPS:.1f}%)")
+
+    fa5_ms, fa5_flops, fa5_dist = bench_flash(ag, args.flash_steps, 10, ev, T=256, B=64, H=6)
+    fa5_tflops = fa5_flops / (fa5_ms * 1e-3) / 1e12
+    log(f"flash causal B64 H6 T256 d64 (config 5 attention) fwd+bwd: {fa5_ms:.4f} ms, {fa5_tflops:.2f} TFLOPS "
+        f"({100 * fa5_tflops / PEAK_FP32_MFMA_TFLOPS:.1f}%)")
 
     sweep = bench_gemm_sweep(ev)
     log("GEMM sweep TFLOPS: " + ", ".join(f"{k} {v}" for k, v in sweep.items()))
@@ -831,6 +838,14 @@ def main() -> int:
             "ms_per_step_median": fa1_dist["median_ms"],
             "ms_per_step_p99": fa1_dist["p99_ms"],
             "config": "causal, B8 H12 T1024 d64, fwd+bwd",
+        },
+        "flash_attn_fwd_bwd_config5_t256": {
+            "tflops": round(fa5_tflops, 3),
+            "pct_of_fp32_mfma_peak": round(100 * fa5_tflops / PEAK_FP32_MFMA_TFLOPS, 2),
+            "ms_per_step": round(fa5_ms, 4),
+            "ms_per_step_median": fa5_dist["median_ms"],
+            "ms_per_step_p99": fa5_dist["p99_ms"],
+            "config": "causal, B64 H6 T256 d64 (one GPT-step layer's attention), fwd+bwd",
         },
         "gemm_sweep_tflops": sweep,
         "rowwise_hbm": rowwise,
