@@ -5,13 +5,19 @@ numpy front end over two CPU libraries:
     (``aar_oracle.c``), always available once ``make -C oracle`` has run;
   * ``_ref/libaar_ref.so``: the reference's own CPU implementation compiled from
     its sources (``ref_driver.cpp`` + the reference tree), present only where
-    the reference tree was available at build time.
+    the reference tree was available at build time;
+  * ``_ref/libaar_glue.so``: the same reference sources and driver with the
+    reference's device entry points bound to libaar_hip.so (``hip_backend.cpp``).
+    Inside ``reference_on_device()`` the ``ref_*`` wrappers call it, so the
+    reference's own C++ runs its ops on the GPU; it checks the integration
+    boundary, and the CPU build stays the checker.
 
 Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import
 this package, and only as the checker: the product never uses it.
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes
 import os
 import subprocess
@@ -22,6 +28,7 @@ import numpy as np
 HERE = Path(__file__).resolve().parent
 LIB_PATH = HERE / "_build" / "liboracle.so"
 REF_PATH = HERE / "_ref" / "libaar_ref.so"
+GLUE_PATH = HERE / "_ref" / "libaar_glue.so"
 
 _f32p = np.ctypeslib.ndpointer(dtype=np.float32, flags="C_CONTIGUOUS")
 _f64p = np.ctypeslib.ndpointer(dtype=np.float64, flags="C_CONTIGUOUS")
@@ -30,6 +37,8 @@ _i64 = ctypes.c_int64
 
 _lib = None
 _ref = None
+_glue = None
+_front = None  # the library the ref_* wrappers call inside reference_on_device()
 
 
 def build(reference: str | None = None) -> None:
@@ -93,43 +102,71 @@ def ref_available() -> bool:
     return REF_PATH.exists()
 
 
+def glue_available() -> bool:
+    return GLUE_PATH.exists()
+
+
 def ref():
-    """The reference's own CPU build, or None when it was not built here."""
+    """The library the ref_* wrappers call: the reference's own CPU build (None
+    when it was not built here), or libaar_glue.so inside reference_on_device()."""
     global _ref
+    if _front is not None:
+        return _front
     if _ref is None and REF_PATH.exists():
-        R = ctypes.CDLL(str(REF_PATH))
-        vp = ctypes.c_void_p
-        R.ref_matmul.argtypes = [ctypes.c_int, _f32p, _f32p, _f32p, _i64, _i64, _i64]
-        R.ref_softmax.argtypes = [_f32p, vp, _f32p, vp, _i64, _i64]
-        R.ref_layernorm.argtypes = [_f32p, _f32p, _f32p, vp, _f32p, vp, vp, vp, _i64, _i64, ctypes.c_float]
-        R.ref_attention.argtypes = [_f32p, _f32p, _f32p, vp, _f32p, vp, vp, vp, _i64, _i64, _i64, ctypes.c_int]
-        R.ref_elementwise.argtypes = [ctypes.c_int, _f32p, vp, ctypes.c_float, vp, _f32p, vp, _i64]
-        R.ref_add_bias.argtypes = [_f32p, _f32p, vp, _f32p, vp, _i64, _i64]
-        R.ref_sum_all.argtypes = [_f32p, _i64, ctypes.POINTER(ctypes.c_float)]
-        R.ref_embedding.argtypes = [_f32p, _i64p, vp, _f32p, vp, _i64, _i64, _i64]
-        R.ref_cross_entropy.argtypes = [_f32p, _i64p, _i64, _i64, _i64, ctypes.c_float,
-                                        ctypes.POINTER(ctypes.c_float), vp]
-        R.ref_adamw.argtypes = [_f32p, _f32p, _f32p, _f32p, _i64] + [ctypes.c_float] * 7
-        R.ref_gpt_step.argtypes = [_i64] * 6 + [ctypes.POINTER(ctypes.c_void_p), _i64p, _i64p, ctypes.c_float,
-                                                 ctypes.POINTER(ctypes.c_float)]
-        R.ref_gpt_step.restype = ctypes.c_int
-        pp = ctypes.POINTER(ctypes.c_void_p)
-        R.ref_lm_step.argtypes = [_i64] * 6 + [ctypes.c_float, _i64, pp, pp, pp, _i64p, _i64p] + \
-            [ctypes.c_float] * 7 + [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p]
-        R.ref_lm_step.restype = ctypes.c_int
-        R.ref_philox_uniform.argtypes = [ctypes.c_uint64, ctypes.c_uint64]
-        R.ref_philox_uniform.restype = ctypes.c_float
-        R.ref_dropout.argtypes = [_f32p, _f32p, vp, _i64, ctypes.c_float, ctypes.c_uint64]
-        R.ref_causal_mask.argtypes = [_f32p, vp, _f32p, vp, _i64, _i64]
-        R.ref_bmm.argtypes = [ctypes.c_int, _f32p, _f32p, _f32p, _i64, _i64, _i64, _i64]
-        R.ref_fanin_graph.argtypes = [_f32p, _f32p, _f32p, _f32p, _i64]
-        for f in (R.ref_dropout, R.ref_causal_mask, R.ref_bmm, R.ref_fanin_graph):
-            f.restype = ctypes.c_int
-        for f in (R.ref_matmul, R.ref_softmax, R.ref_layernorm, R.ref_attention, R.ref_elementwise,
-                  R.ref_add_bias, R.ref_sum_all, R.ref_embedding, R.ref_cross_entropy, R.ref_adamw):
-            f.restype = ctypes.c_int
-        _ref = R
+        _ref = _bind_driver(ctypes.CDLL(str(REF_PATH)))
     return _ref
+
+
+@contextlib.contextmanager
+def reference_on_device():
+    """Within the block the ref_* wrappers run the reference's ops, autograd and
+    optimizer steps with every operand on Device::CUDA: libaar_glue.so, the
+    reference's C++ with its device entry points bound to libaar_hip.so."""
+    global _glue, _front
+    if _glue is None:
+        if not GLUE_PATH.exists():
+            raise RuntimeError(f"{GLUE_PATH} is not built")
+        _glue = _bind_driver(ctypes.CDLL(str(GLUE_PATH)))
+    prev, _front = _front, _glue
+    try:
+        yield
+    finally:
+        _front = prev
+
+
+def _bind_driver(R):
+    """Argument types of ref_driver.cpp's entry points (both builds)."""
+    vp = ctypes.c_void_p
+    R.ref_matmul.argtypes = [ctypes.c_int, _f32p, _f32p, _f32p, _i64, _i64, _i64]
+    R.ref_softmax.argtypes = [_f32p, vp, _f32p, vp, _i64, _i64]
+    R.ref_layernorm.argtypes = [_f32p, _f32p, _f32p, vp, _f32p, vp, vp, vp, _i64, _i64, ctypes.c_float]
+    R.ref_attention.argtypes = [_f32p, _f32p, _f32p, vp, _f32p, vp, vp, vp, _i64, _i64, _i64, ctypes.c_int]
+    R.ref_elementwise.argtypes = [ctypes.c_int, _f32p, vp, ctypes.c_float, vp, _f32p, vp, _i64]
+    R.ref_add_bias.argtypes = [_f32p, _f32p, vp, _f32p, vp, _i64, _i64]
+    R.ref_sum_all.argtypes = [_f32p, _i64, ctypes.POINTER(ctypes.c_float)]
+    R.ref_embedding.argtypes = [_f32p, _i64p, vp, _f32p, vp, _i64, _i64, _i64]
+    R.ref_cross_entropy.argtypes = [_f32p, _i64p, _i64, _i64, _i64, ctypes.c_float,
+                                    ctypes.POINTER(ctypes.c_float), vp]
+    R.ref_adamw.argtypes = [_f32p, _f32p, _f32p, _f32p, _i64] + [ctypes.c_float] * 7
+    R.ref_gpt_step.argtypes = [_i64] * 6 + [ctypes.POINTER(ctypes.c_void_p), _i64p, _i64p, ctypes.c_float,
+                                             ctypes.POINTER(ctypes.c_float)]
+    R.ref_gpt_step.restype = ctypes.c_int
+    pp = ctypes.POINTER(ctypes.c_void_p)
+    R.ref_lm_step.argtypes = [_i64] * 6 + [ctypes.c_float, _i64, pp, pp, pp, _i64p, _i64p] + \
+        [ctypes.c_float] * 7 + [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p]
+    R.ref_lm_step.restype = ctypes.c_int
+    R.ref_philox_uniform.argtypes = [ctypes.c_uint64, ctypes.c_uint64]
+    R.ref_philox_uniform.restype = ctypes.c_float
+    R.ref_dropout.argtypes = [_f32p, _f32p, vp, _i64, ctypes.c_float, ctypes.c_uint64]
+    R.ref_causal_mask.argtypes = [_f32p, vp, _f32p, vp, _i64, _i64]
+    R.ref_bmm.argtypes = [ctypes.c_int, _f32p, _f32p, _f32p, _i64, _i64, _i64, _i64]
+    R.ref_fanin_graph.argtypes = [_f32p, _f32p, _f32p, _f32p, _i64]
+    for f in (R.ref_dropout, R.ref_causal_mask, R.ref_bmm, R.ref_fanin_graph):
+        f.restype = ctypes.c_int
+    for f in (R.ref_matmul, R.ref_softmax, R.ref_layernorm, R.ref_attention, R.ref_elementwise,
+              R.ref_add_bias, R.ref_sum_all, R.ref_embedding, R.ref_cross_entropy, R.ref_adamw):
+        f.restype = ctypes.c_int
+    return R
 
 
 def _c(a) -> np.ndarray:

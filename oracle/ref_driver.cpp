@@ -7,6 +7,12 @@
 // bench.py as the "reference" CPU baseline.  Every function goes through the
 // reference's public ops (vlm::matmul, vlm::softmax, ...) on Device::CPU, with
 // autograd where the reference computes gradients that way.
+//
+// Compiled a second time with -DREF_DRIVER_ON_DEVICE into
+// oracle/_ref/libaar_glue.so: the same entry points then put every operand on
+// Device::CUDA, so the reference's own ops, autograd and optimizer steps run
+// on the MI355X kernels through hip_backend.cpp and libaar_hip.so.  Host data
+// only enters and leaves through make / make_ids / out / scalar.
 #include <cstdint>
 #include <cstring>
 #include <exception>
@@ -27,21 +33,53 @@
 #include "ops/shape.hpp"
 #include "ops/softmax.hpp"
 
+using vlm::Device;
 using vlm::DType;
 using vlm::Tensor;
 
 namespace {
 
-Tensor make(const float* src, std::vector<int64_t> shape, bool requires_grad = false) {
-  Tensor t = Tensor::empty(std::move(shape), DType::Fp32);
+#ifdef REF_DRIVER_ON_DEVICE
+constexpr Device kDevice = Device::CUDA;
+#else
+constexpr Device kDevice = Device::CPU;
+#endif
+
+// A tensor on kDevice holding a copy of `src` (host memory).
+Tensor upload(const void* src, std::vector<int64_t> shape, DType dtype) {
+  Tensor t = Tensor::empty(std::move(shape), dtype);
   if (t.nbytes()) std::memcpy(t.data(), src, t.nbytes());
+  return kDevice == Device::CPU ? t : t.to(kDevice);
+}
+
+Tensor make(const float* src, std::vector<int64_t> shape, bool requires_grad = false) {
+  Tensor t = upload(src, std::move(shape), DType::Fp32);
   if (requires_grad) t.set_requires_grad(true);
   return t;
 }
 
+Tensor make_ids(const int64_t* src, std::vector<int64_t> shape) {
+  return upload(src, std::move(shape), DType::Int64);
+}
+
+// Copies a contiguous result (every op here returns one) to host memory.
 void out(const Tensor& t, float* dst) {
-  Tensor c = t.is_contiguous() ? t : t;  // every op here returns contiguous storage
-  if (c.nbytes()) std::memcpy(dst, c.data(), c.nbytes());
+  const Tensor h = t.device == Device::CPU ? t : t.to(Device::CPU);
+  if (h.nbytes()) std::memcpy(dst, h.data(), h.nbytes());
+}
+
+float scalar(const Tensor& t) {
+  float v = 0.0f;
+  out(t, &v);
+  return v;
+}
+
+// Position ids 0..T-1 for each of B rows.
+Tensor positions(int64_t B, int64_t T) {
+  std::vector<int64_t> pos(static_cast<size_t>(B * T));
+  for (int64_t b = 0; b < B; ++b)
+    for (int64_t t = 0; t < T; ++t) pos[b * T + t] = t;
+  return make_ids(pos.data(), {B, T});
 }
 
 }  // namespace
@@ -169,8 +207,7 @@ int ref_add_bias(const float* x, const float* bias, const float* g, float* y, fl
 
 int ref_sum_all(const float* x, int64_t n, float* result) {
   try {
-    Tensor s = vlm::sum_all(make(x, {n}));
-    *result = *static_cast<const float*>(s.data());
+    *result = scalar(vlm::sum_all(make(x, {n})));
     return 0;
   } catch (const std::exception&) {
     return -1;
@@ -181,9 +218,7 @@ int ref_embedding(const float* w, const int64_t* ids, const float* g, float* y, 
                   int64_t vocab, int64_t dim) {
   try {
     Tensor tw = make(w, {vocab, dim}, g != nullptr);
-    Tensor ti = Tensor::empty({n}, DType::Int64);
-    std::memcpy(ti.data(), ids, n * sizeof(int64_t));
-    Tensor ty = vlm::embedding(tw, ti);
+    Tensor ty = vlm::embedding(tw, make_ids(ids, {n}));
     out(ty, y);
     if (g) {
       ty.backward(make(g, {n, dim}));
@@ -201,14 +236,10 @@ int ref_cross_entropy(const float* logits, const int64_t* targets, int64_t n, in
                       int64_t ignore_index, float go, float* loss, float* dlogits) {
   try {
     Tensor tl = make(logits, {n, vocab}, dlogits != nullptr);
-    Tensor tt = Tensor::empty({n}, DType::Int64);
-    std::memcpy(tt.data(), targets, n * sizeof(int64_t));
-    Tensor l = vlm::cross_entropy(tl, tt, ignore_index);
-    *loss = *static_cast<const float*>(l.data());
+    Tensor l = vlm::cross_entropy(tl, make_ids(targets, {n}), ignore_index);
+    *loss = scalar(l);
     if (dlogits) {
-      Tensor seed = Tensor::empty({}, DType::Fp32);
-      *static_cast<float*>(seed.data()) = go;
-      l.backward(seed);
+      l.backward(make(&go, {}));
       out(*tl.grad(), dlogits);
     }
     return 0;
@@ -302,13 +333,9 @@ int ref_gpt_step(int64_t vocab, int64_t ctx, int64_t layers, int64_t d, int64_t 
     std::vector<Tensor> P;
     for (size_t i = 0; i < shapes.size(); ++i) P.push_back(make(params[i], shapes[i], true));
 
-    Tensor tids = Tensor::empty({B, T}, DType::Int64);
-    std::memcpy(tids.data(), ids, B * T * sizeof(int64_t));
-    Tensor pos = Tensor::empty({B, T}, DType::Int64);
-    for (int64_t b = 0; b < B; ++b)
-      for (int64_t t = 0; t < T; ++t) static_cast<int64_t*>(pos.data())[b * T + t] = t;
-    Tensor tgt = Tensor::empty({B * T}, DType::Int64);
-    std::memcpy(tgt.data(), targets, B * T * sizeof(int64_t));
+    const Tensor tids = make_ids(ids, {B, T});
+    const Tensor pos = positions(B, T);
+    const Tensor tgt = make_ids(targets, {B * T});
 
     Tensor x = vlm::add(vlm::embedding(P[0], tids), vlm::embedding(P[1], pos));
     for (int64_t i = 0; i < layers; ++i) {
@@ -328,7 +355,7 @@ int ref_gpt_step(int64_t vocab, int64_t ctx, int64_t layers, int64_t d, int64_t 
     x = vlm::layernorm(x, P[n - 3], P[n - 2], 1e-5f);
     Tensor logits = vlm::matmul_a_bt(x, P[n - 1]);
     Tensor loss = vlm::cross_entropy(vlm::reshape(logits, {B * T, vocab}), tgt, -100);
-    *loss_out = *static_cast<const float*>(loss.data());
+    *loss_out = scalar(loss);
     loss.backward();
     for (size_t i = 0; i < n; ++i) {
       vlm::scaled_add_inplace(P[i], *P[i].grad(), -lr);
@@ -369,13 +396,9 @@ int ref_lm_step(int64_t vocab, int64_t ctx, int64_t layers, int64_t d, int64_t h
       M.push_back(make(m_state[i], shapes[i]));
       V.push_back(make(v_state[i], shapes[i]));
     }
-    Tensor tids = Tensor::empty({B, T}, DType::Int64);
-    std::memcpy(tids.data(), ids, B * T * sizeof(int64_t));
-    Tensor pos = Tensor::empty({B, T}, DType::Int64);
-    for (int64_t b = 0; b < B; ++b)
-      for (int64_t t = 0; t < T; ++t) static_cast<int64_t*>(pos.data())[b * T + t] = t;
-    Tensor tgt = Tensor::empty({B * T}, DType::Int64);
-    std::memcpy(tgt.data(), targets, B * T * sizeof(int64_t));
+    const Tensor tids = make_ids(ids, {B, T});
+    const Tensor pos = positions(B, T);
+    const Tensor tgt = make_ids(targets, {B * T});
     if (seed >= 0) vlm::manual_seed((uint64_t)seed);
     auto drop = [&](const Tensor& x) { return dropout > 0.0f ? vlm::dropout(x, dropout) : x; };
 
@@ -397,7 +420,7 @@ int ref_lm_step(int64_t vocab, int64_t ctx, int64_t layers, int64_t d, int64_t h
     x = vlm::layernorm(x, P[n - 3], P[n - 2], 1e-5f);
     Tensor logits = vlm::matmul_a_bt(x, P[n - 1]);
     Tensor loss = vlm::cross_entropy(vlm::reshape(logits, {B * T, vocab}), tgt, -100);
-    *loss_out = *static_cast<const float*>(loss.data());
+    *loss_out = scalar(loss);
     loss.backward();
     for (size_t i = 0; i < n; ++i) {
       if (grads_out) out(*P[i].grad(), grads_out[i]);
