@@ -292,6 +292,15 @@ gemm_f32_kernel(const float* __restrict__ A, const float* __restrict__ B, float*
 // A ragged last K tile is loaded through registers with K predicates and
 // written to the same layout.  The ring is synchronised by an explicit
 // s_waitcnt on this wave's outstanding DMAs plus s_barrier.
+//
+// K groups (KG > 1): the workgroup runs KG groups of NW waves over one output
+// tile, group g taking the g-th of KG consecutive runs of the block's K tiles
+// through its own ring.  This multiplies the waves per SIMD of a grid of about
+// one workgroup per CU (1024^3 on 64x64 tiles, 2048^3 on 128x128, the N = 384
+// input gradients of the GPT step) without a second launch or a workspace.
+// The groups share the ring barriers (a group out of tiles still takes
+// part); at the end groups 1..KG-1 write their accumulators to LDS and group 0
+// adds them in group order and stores: deterministic, no atomics.
 
 
 // Row swizzle of the K-contiguous layout: rows that one 8- or 16-lane LDS
@@ -307,7 +316,7 @@ template <int BR, int BK, int NW, bool KC>
 struct DmaTile {
   static constexpr int kUnits = BR * BK / 4;
   static_assert(kUnits % (64 * NW) == 0, "tile must divide into whole wave DMAs");
-  static_assert(KC || BR >= 64, "row-contiguous swizzle needs BR >= 64");
+  static_assert(KC || BR % 64 == 0, "row-contiguous swizzle pairs float4 groups p and p ^ 8 within BR");
   static constexpr int kPerWave = kUnits / (64 * NW);  // DMA instructions per wave per tile
   static constexpr int kFloats = BR * BK;
 
@@ -386,29 +395,33 @@ struct DmaTile {
 
 
 
-template <int BM, int BN, int BK, int WM, int WN, int WPE, int S, bool A_KC, bool B_KC, int EPI>
-__global__ void __launch_bounds__((BM / WM) * (BN / WN) * 64, WPE)
+template <int BM, int BN, int BK, int WM, int WN, int WPE, int S, bool A_KC, bool B_KC, int EPI, int KG>
+__global__ void __launch_bounds__((BM / WM) * (BN / WN) * KG * 64, WPE)
 gemm_f32_dma_kernel(const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C,
                     int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc,
                     int64_t k_per_split, int64_t split_stride, int tiles_m, int tiles_n, int64_t sA,
                     int64_t sB, int64_t sC, GemmEpi ep) {
   constexpr int NWM = BM / WM;
-  constexpr int NW = NWM * (BN / WN);
+  constexpr int NW = NWM * (BN / WN);  // waves per K group
   constexpr int TM = WM / 32;
   constexpr int TN = WN / 32;
   constexpr int NC = BK / 8;
   static_assert(S >= 2 && S <= 4, "ring depth 2..4");
+  static_assert(KG >= 1 && NW * KG <= 16, "at most 1024 threads per workgroup");
   using TA = DmaTile<BM, BK, NW, A_KC>;
   using TB = DmaTile<BN, BK, NW, B_KC>;
   constexpr int kStage = TA::kFloats + TB::kFloats;
   constexpr int kPerTile = TA::kPerWave + TB::kPerWave;  // DMA instructions per wave per tile
   static_assert((S - 2) * kPerTile < 64, "outstanding DMAs exceed the vmcnt range");
+  constexpr int kAccFloats = TM * TN * 16 * 64;  // one wave's accumulators
+  static_assert((KG - 1) * NW * kAccFloats <= KG * S * kStage, "K-group hand-over fits in the rings");
 
-  __shared__ __attribute__((aligned(16))) float smem[S * kStage];
+  __shared__ __attribute__((aligned(16))) float smem[KG * S * kStage];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int grp = (tid >> 6) / NW;  // K group
+  const int wave = (tid >> 6) % NW;  // wave within the group
   const int lr = lane & 31;
   const int h = lane >> 5;
   const int wm0 = (wave % NWM) * WM;
@@ -419,10 +432,18 @@ gemm_f32_dma_kernel(const float* __restrict__ A, const float* __restrict__ B, fl
   const int64_t m0 = (int64_t)tm * BM;
   const int64_t n0 = (int64_t)tn * BN;
 
-  const int64_t kbeg = (int64_t)blockIdx.y * k_per_split;
-  const int64_t kend = min(K, kbeg + k_per_split);
-  const int ntiles = kend > kbeg ? (int)ceil_div(kend - kbeg, (int64_t)BK) : 0;
-  const bool ragged = kend > kbeg && ((kend - kbeg) % BK) != 0;
+  // This block's K range, then this group's run of its tiles: groups take
+  // ceil(tiles / KG) tiles each, in order; the ragged last tile belongs to the
+  // group that reaches the range end.
+  const int64_t kbeg0 = (int64_t)blockIdx.y * k_per_split;
+  const int64_t kend = min(K, kbeg0 + k_per_split);
+  const int nt_all = kend > kbeg0 ? (int)ceil_div(kend - kbeg0, (int64_t)BK) : 0;
+  const int ntg = KG == 1 ? nt_all : (nt_all + KG - 1) / KG;  // loop trips, the same for every group
+  const int t0 = grp * ntg;
+  const int ntiles = max(0, min(nt_all - t0, ntg));
+  const int64_t kbeg = kbeg0 + (int64_t)t0 * BK;
+  const bool ragged = ntiles > 0 && t0 + ntiles == nt_all && ((kend - kbeg0) % BK) != 0;
+  float* const ring = smem + grp * (S * kStage);
   C += (int64_t)blockIdx.y * split_stride;
   // batched launches: one grid layer per matrix (blockIdx.z)
   A += (int64_t)blockIdx.z * sA;
@@ -443,7 +464,7 @@ gemm_f32_dma_kernel(const float* __restrict__ A, const float* __restrict__ B, fl
   tb.init(ldb, n0, N, wave, lane);
   auto issue = [&](int t) {
     const int64_t k0 = kbeg + (int64_t)t * BK;
-    float* st = smem + (t % S) * kStage;
+    float* st = ring + (t % S) * kStage;
     if (ragged && t == ntiles - 1) {
       ta.tail(A, lda, m0, k0, kend, st, wave, lane);
       tb.tail(B, ldb, n0, k0, kend, st + TA::kFloats, wave, lane);
@@ -456,7 +477,7 @@ gemm_f32_dma_kernel(const float* __restrict__ A, const float* __restrict__ B, fl
   for (int p = 0; p < S - 1; ++p)
     if (p < ntiles) issue(p);
 
-  for (int t = 0; t < ntiles; ++t) {
+  for (int t = 0; t < ntg; ++t) {
     // Tile t has landed once at most the DMAs of the tiles issued after it
     // (t+1 .. t+S-2) are outstanding.  A ragged tile's register loads wait
     // for every earlier DMA before its LDS stores, so counting it as a full
@@ -466,10 +487,15 @@ gemm_f32_dma_kernel(const float* __restrict__ A, const float* __restrict__ B, fl
     else if (S >= 3 && ahead == 1) wait_vm_lgkm0<(S >= 3 ? 1 : 0) * kPerTile>();
     else wait_vm_lgkm0<0>();
     ring_barrier();
+    if (KG > 1 && t >= ntiles) continue;  // this group is out of tiles; it still meets the barriers
     if (t + S - 1 < ntiles) issue(t + S - 1);  // refills the stage computed in iteration t-1
 
-    const float* as = smem + (t % S) * kStage;
+    const float* as = ring + (t % S) * kStage;
     const float* bs = as + TA::kFloats;
+    // With K groups four waves share a SIMD; the one issuing matrix ops
+    // keeps priority over those issuing loads (measured +2.5 % at 1024^3;
+    // the one-group kernels lose slightly with it).
+    if constexpr (KG > 1) __builtin_amdgcn_s_setprio(1);
     f32x4 af[2][TM], bf[2][TN];
 #pragma unroll
     for (int i = 0; i < TM; ++i) af[0][i] = TA::frag(as, wm0 + 32 * i + lr, 0, h);
@@ -491,6 +517,43 @@ gemm_f32_dma_kernel(const float* __restrict__ A, const float* __restrict__ B, fl
 #pragma unroll
           for (int j = 0; j < TN; ++j)
             acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[p][i][s], bf[p][j][s], acc[i][j], 0, 0, 0);
+    }
+    if constexpr (KG > 1) __builtin_amdgcn_s_setprio(0);
+  }
+
+  if constexpr (KG > 1) {
+    // Hand-over: every wave's DMAs have landed (the last trip waits for all),
+    // and the barrier ends every read of the rings, which the partial sums
+    // then overwrite.  Lane-major float4s: conflict-free stores and loads.
+    __syncthreads();
+    if (grp > 0) {
+      float* dst = smem + ((grp - 1) * NW + wave) * kAccFloats + lane * 4;
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            *reinterpret_cast<f32x4*>(dst + ((i * TN + j) * 4 + q) * 256) =
+                f32x4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+    }
+    __syncthreads();
+    if (grp > 0) return;
+#pragma unroll
+    for (int g = 1; g < KG; ++g) {
+      const float* src = smem + ((g - 1) * NW + wave) * kAccFloats + lane * 4;
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const f32x4 v = *reinterpret_cast<const f32x4*>(src + ((i * TN + j) * 4 + q) * 256);
+            acc[i][j][4 * q] += v[0];
+            acc[i][j][4 * q + 1] += v[1];
+            acc[i][j][4 * q + 2] += v[2];
+            acc[i][j][4 * q + 3] += v[3];
+          }
     }
   }
 
@@ -552,9 +615,10 @@ struct Cfg {
   int bm, bn, bk, wm, wn, resident, stages;
   float eff;
   int slots, ops;
+  int kg = 1;  // K groups of the DMA path
 };
 constexpr Cfg kCfgs[] = {
-    {256, 256, 32, 64, 128, 1, 2, 0.895f, 1, kAllOps},  // 0: 8 waves, 2 waves/SIMD; BK 32 halves the barriers
+    {256, 256, 32, 64, 128, 1, 2, 0.866f, 1, kAllOps},  // 0: 8 waves, 2 waves/SIMD; BK 32 halves the barriers
     {256, 128, 16, 128, 64, 2, 3, 0.83f, 2, kAllOps},   // 1
     {128, 256, 16, 64, 128, 2, 3, 0.83f, 2, kAllOps},   // 2
     {128, 128, 16, 64, 64, 2, 3, 0.84f, 2, kAllOps},    // 3
@@ -567,6 +631,14 @@ constexpr Cfg kCfgs[] = {
     // with one workgroup per CU, hence one model slot; as NT it loses at
     // N = 1152, so it is not planned there.
     {128, 192, 32, 64, 96, 2, 2, 0.87f, 1, 1 << AAR_GEMM_NN},
+    // 9-12: K groups (see gemm_f32_dma_kernel), for grids of about one
+    // workgroup per CU.  12 has a 96-wide N tile for thin outputs (the GPT
+    // head, N = 65); its row-contiguous DMA layout needs BN % 64 == 0, so it
+    // serves NT only.
+    {64, 64, 32, 32, 32, 1, 2, 0.587f, 1, kAllOps, 4},           // 9: 16 waves
+    {128, 128, 32, 64, 64, 1, 2, 0.826f, 1, kAllOps, 2},         // 10: 8 waves
+    {64, 64, 32, 32, 32, 1, 3, 0.60f, 1, kAllOps, 2},            // 11: 8 waves
+    {64, 96, 32, 32, 96, 1, 2, 0.55f, 1, 1 << AAR_GEMM_NT, 4},   // 12: 8 waves
 };
 constexpr int kNumCfgs = sizeof(kCfgs) / sizeof(kCfgs[0]);
 constexpr int kMaxSplits = 64;
@@ -582,8 +654,11 @@ int64_t split_chunk(int64_t K, int splits, int bk) { return ceil_div(ceil_div(K,
 // Cost model: blocks are spread evenly over the CUs; a CU holding fewer
 // blocks than it has resident slots runs at reduced efficiency (down to 60%
 // of `eff` with one block); split-K adds the partial-sum traffic and the
-// reduction launch.  Fitted to measured throughput of every configuration on
-// the square, MLP and weight-gradient shapes of the GPT step.
+// reduction launch.  `eff` is fitted to the measured time of every
+// (configuration, split) pair on the square, MLP and weight-gradient shapes
+// of the GPT step plus a held-out shape set; the split counts tried are the
+// measured ones.
+constexpr int kPlanSplits[] = {1, 2, 3, 4, 6, 8, 12, 16, 24, 32};
 Plan plan_gemm(int op, int64_t M, int64_t N, int64_t K, size_t ws_bytes, bool allow_split, int64_t batch = 1) {
   const int cus = device_cu_count();
   const double cu_flops = 157.3e12 / 256;  // fp32 MFMA FLOP/s per CU
@@ -593,7 +668,7 @@ Plan plan_gemm(int op, int64_t M, int64_t N, int64_t K, size_t ws_bytes, bool al
     const Cfg& cf = kCfgs[c];
     if (!(cf.ops & (1 << op))) continue;
     const int64_t tiles = ceil_div(M, (int64_t)cf.bm) * ceil_div(N, (int64_t)cf.bn) * batch;
-    for (int splits = 1; splits <= kMaxSplits; splits *= 2) {
+    for (const int splits : kPlanSplits) {
       if (splits > 1) {
         if (!allow_split) break;
         if (K / splits < 256) break;
@@ -620,25 +695,28 @@ struct Batch {
 };
 constexpr Batch kSingle{1, 0, 0, 0};
 
-template <int BM, int BN, int BK, int WM, int WN, int RES, int STAGES, bool A_KC, bool B_KC>
+template <int BM, int BN, int BK, int WM, int WN, int RES, int STAGES, int KG, bool A_KC, bool B_KC>
 int launch_cfg(bool vec, const float* A, const float* B, float* C, int64_t M, int64_t N, int64_t K,
                int64_t lda, int64_t ldb, int64_t ldc, int splits, int64_t kps, int64_t split_stride,
                const Batch& bt, int epi, const GemmEpi& ep, hipStream_t st) {
   constexpr int kWaves = (BM / WM) * (BN / WN);
-  constexpr int kWpe = (RES * kWaves + 3) / 4;
+  constexpr int kWpe = (RES * kWaves * KG + 3) / 4;  // DMA path: KG groups of kWaves waves
+  constexpr int kWpeReg = (RES * kWaves + 3) / 4;    // register path: one group
   const int tiles_m = (int)ceil_div(M, (int64_t)BM);
   const int tiles_n = (int)ceil_div(N, (int64_t)BN);
   // A dispatch holds each grid extent as a 32-bit work-item count.
-  if ((int64_t)tiles_m * tiles_n * kWaves * 64 > (int64_t)UINT32_MAX) return AAR_EUNSUPPORTED;
+  if ((int64_t)tiles_m * tiles_n * kWaves * KG * 64 > (int64_t)UINT32_MAX) return AAR_EUNSUPPORTED;
   dim3 grid((unsigned)(tiles_m * tiles_n), (unsigned)splits, (unsigned)bt.count);
-  dim3 block(kWaves * 64);
   auto go = [&](auto epi_tag) {
     constexpr int E = decltype(epi_tag)::value;
-    if (vec)
-      gemm_f32_dma_kernel<BM, BN, BK, WM, WN, kWpe, STAGES, A_KC, B_KC, E><<<grid, block, 0, st>>>(
+    if constexpr ((!A_KC && BM % 64 != 0) || (!B_KC && BN % 64 != 0)) {
+      if (vec) return AAR_EUNSUPPORTED;  // no DMA layout for this row-contiguous tile
+    } else if (vec) {
+      gemm_f32_dma_kernel<BM, BN, BK, WM, WN, kWpe, STAGES, A_KC, B_KC, E, KG><<<grid, dim3(kWaves * KG * 64), 0, st>>>(
           A, B, C, M, N, K, lda, ldb, ldc, kps, split_stride, tiles_m, tiles_n, bt.sA, bt.sB, bt.sC, ep);
-    else
-      gemm_f32_kernel<BM, BN, BK, WM, WN, kWpe, A_KC, B_KC, E><<<grid, block, 0, st>>>(
+      return launch_status();
+    }
+    gemm_f32_kernel<BM, BN, BK, WM, WN, kWpeReg, A_KC, B_KC, E><<<grid, dim3(kWaves * 64), 0, st>>>(
           A, B, C, M, N, K, lda, ldb, ldc, kps, split_stride, tiles_m, tiles_n, bt.sA, bt.sB, bt.sC, ep);
     return launch_status();
   };
@@ -664,8 +742,8 @@ int launch_op(int cfg, bool vec, const float* A, const float* B, float* C, int64
 #define AAR_GEMM_CFG(I)                                                                                   \
   case I:                                                                                                 \
     return launch_cfg<kCfgs[I].bm, kCfgs[I].bn, kCfgs[I].bk, kCfgs[I].wm, kCfgs[I].wn, kCfgs[I].resident, \
-                      kCfgs[I].stages, A_KC, B_KC>(vec, A, B, C, M, N, K, lda, ldb, ldc, splits, kps, split_stride, \
-                                                   bt, epi, ep, st);
+                      kCfgs[I].stages, kCfgs[I].kg, A_KC, B_KC>(vec, A, B, C, M, N, K, lda, ldb, ldc, splits, kps, \
+                                                                split_stride, bt, epi, ep, st);
   switch (cfg) {
     AAR_GEMM_CFG(0)
     AAR_GEMM_CFG(1)
@@ -676,12 +754,16 @@ int launch_op(int cfg, bool vec, const float* A, const float* B, float* C, int64
     AAR_GEMM_CFG(6)
     AAR_GEMM_CFG(7)
     AAR_GEMM_CFG(8)
+    AAR_GEMM_CFG(9)
+    AAR_GEMM_CFG(10)
+    AAR_GEMM_CFG(11)
+    AAR_GEMM_CFG(12)
     default:
       return AAR_EINVAL;
   }
 #undef AAR_GEMM_CFG
 }
-static_assert(kNumCfgs == 9, "launch_op lists every configuration");
+static_assert(kNumCfgs == 13, "launch_op lists every configuration");
 
 // 128-bit loads need 16-byte aligned operands whose contiguous extents and
 // leading dimensions are multiples of 4, and the 32-bit per-thread offsets

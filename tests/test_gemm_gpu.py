@@ -209,11 +209,18 @@ def test_every_tile_config_vs_oracle(gpu, op):
             ref = O.matmul(name, a, b)
             pa, pb = abi.put(a), abi.put(b)
             ws = abi.alloc(4 * 4 * M * N)
+            vec = M % 4 == 0 and N % 4 == 0 and K % 4 == 0
             for (cfg, bm, bn, bk) in cfgs:
+                # the 128-bit path stages a row-contiguous operand (A of TN, B of NN and TN)
+                # with a layout that needs the tile extent to be a multiple of 64
+                no_dma = vec and ((op == 2 and bm % 64) or (op in (0, 2) and bn % 64))
                 for splits in (1, 3):
                     pc = abi.empty(M * N)
-                    abi.check(abi.L.aar_gemm_f32_with_config(op, M, N, K, pa, pb, pc, ws, 16 * M * N, cfg,
-                                                             splits, None))
+                    rc = abi.L.aar_gemm_f32_with_config(op, M, N, K, pa, pb, pc, ws, 16 * M * N, cfg, splits, None)
+                    if no_dma:
+                        assert rc == -3, (cfg, op, rc)
+                        continue
+                    abi.check(rc)
                     assert_close(abi.get(pc, (M, N)), ref, gemm_tol(K), f"{name} cfg {cfg} ({bm}x{bn}x{bk}) "
                                  f"splits {splits} shape {(M, N, K)}")
     finally:
