@@ -420,6 +420,203 @@ flash_fwd_kernel(FaIn Qv, FaIn Kv, FaIn Vv, FaOut Ov, float* __restrict__ Lse, i
   }
 }
 
+// ------------------------------------------------------ forward, paired
+// Causal forward over 64-query workgroups for short sequences, where the
+// 128-query grid is about one round of resident workgroups and its longest
+// items (the last query block, every key tile in turn) set the time: four
+// waves as 2 query tiles x 2 key phases.  Each iteration stages key tiles t
+// and t + 1 (K rows and V^T, as flash_fwd_kernel); wave (a, p) runs the
+// online softmax of query tile a over key tile t + p, so the two phases of a
+// query tile split its key range and the longest chain of tiles is half that
+// of the 128-query kernel.  At the end phase 1 hands (m, l, O) to phase 0
+// through LDS, and phase 0 merges the two partial softmaxes in a fixed order
+// (m = max(m0, m1), w_p = 2^(m_p - m), l = w0 l0 + w1 l1, O = w0 O0 + w1 O1;
+// deterministic), normalises and stores O and lse.  The tiles of the next
+// pair are loaded into registers during the iteration and stored after a
+// barrier (one LDS stage, two barriers per pair of tiles).
+template <int DP, bool CAUSAL, bool VEC>
+__global__ void __launch_bounds__(kFaThreads, DP <= 64 ? 3 : 1)
+flash_fwd_pair_kernel(FaIn Qv, FaIn Kv, FaIn Vv, FaOut Ov, float* __restrict__ Lse, int T, int d, int H,
+                      int nqb, int BH, float scale_log2) {
+  constexpr int NC = DP / 8;   // head-dim chunks
+  constexpr int NB = DP / 32;  // head-dim output blocks
+  constexpr int LD = DP + 4;
+  constexpr bool kSwz = kVtSwizzle<DP, CAUSAL>;
+  constexpr int kQueries = 2 * kTile;  // queries per workgroup
+  constexpr int kKs = kTile * LD;      // one staged K tile (rows)
+  constexpr int kVts = DP * kLdt;      // one staged V tile (transposed)
+  constexpr int kHand = (NB * 16 + 2) * kWave;  // one wave's O, m and l, lane-major
+  __shared__ __attribute__((aligned(16))) float smem[2 * kKs + 2 * kVts];
+  static_assert(2 * kHand <= 2 * kKs + 2 * kVts, "phase hand-over fits in the staging buffers");
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int lr = lane & 31, h = lane >> 5;
+  const int qt_local = wave & 1;  // query tile of this wave
+  const int phase = wave >> 1;    // key tile t + phase of each staged pair
+  const int qb = CAUSAL ? nqb - 1 - (int)(blockIdx.x / BH) : (int)(blockIdx.x / BH);  // longest first
+  const int bh = blockIdx.x % BH;
+  const float* __restrict__ Q = Qv.head(bh, H);
+  const float* __restrict__ K = Kv.head(bh, H);
+  const float* __restrict__ V = Vv.head(bh, H);
+  const int q0 = qb * kQueries + qt_local * kTile;  // first query of this wave
+  const int qi = q0 + lr;                           // this lane's query
+  float* const ks = smem;
+  float* const vts = smem + 2 * kKs;
+
+  f32x4 qr[NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const int dd = 8 * c + 4 * h;
+    qr[c] = qi < T ? load4<VEC>(Q + (int64_t)qi * Qv.st + dd, d - dd) : f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  f32x16 o[NB];
+#pragma unroll
+  for (int b = 0; b < NB; ++b) o[b] = zero16();
+  float m = -INFINITY, l = 0.f;
+
+  const int kv_end = CAUSAL ? min(T, qb * kQueries + kQueries) : T;
+  const int ntiles = (kv_end + kTile - 1) / kTile;
+  // Last key tile that holds a key this wave's queries may see.
+  const int wlast = CAUSAL ? min(ntiles - 1, (q0 + kTile - 1) / kTile) : ntiles - 1;
+
+  // S^T tile from K rows in LDS: lane = query, register r = key acc_row(r, h).
+  auto qk = [&](const float* kt) {
+    f32x16 sc = zero16();
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const f32x4 kf = *reinterpret_cast<const f32x4*>(kt + lr * LD + 8 * c + 4 * h);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) sc = mfma32(kf[e], qr[c][e], sc);
+    }
+    return sc;
+  };
+  // Online softmax of one key tile (S in sc) and O += V_t P_t.
+  auto soft_pv = [&](f32x16 sc, const float* vt, int kv0) {
+    float mx = -INFINITY;
+    if ((CAUSAL && kv0 + kTile - 1 > q0) || kv0 + kTile > T) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int key = kv0 + acc_row(r, h);
+        float v = sc[r] * scale_log2;
+        if (key >= T || (CAUSAL && key > qi)) v = -INFINITY;
+        sc[r] = v;
+        mx = fmaxf(mx, v);
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        sc[r] *= scale_log2;
+        mx = fmaxf(mx, sc[r]);
+      }
+    }
+    mx = half_swap_max(mx);
+    const float m_new = fmaxf(m, mx);
+    const float m_use = m_new == -INFINITY ? 0.f : m_new;
+    const float alpha = fast_exp2(m - m_use);
+    float ps = 0.f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const float pr = fast_exp2(sc[r] - m_use);
+      sc[r] = pr;
+      ps += pr;
+    }
+    ps = half_swap_sum(ps);
+    l = l * alpha + ps;
+    m = m_new;
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[b][r] *= alpha;
+    }
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int vc = b * 32 + lr;
+        const f32x4 vf = *reinterpret_cast<const f32x4*>(vt + vc * kLdt + vt_swz<kSwz>(vc, 8 * g + 4 * h));
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[b] = mfma32(vf[e], sc[4 * g + e], o[b]);
+      }
+    }
+  };
+
+  TileCopy<DP, VEC> kc0, kc1, vc0, vc1;
+  kc0.load(K, Kv.st, 0, T, d, tid);
+  vc0.load(V, Vv.st, 0, T, d, tid);
+  if (ntiles > 1) {
+    kc1.load(K, Kv.st, kTile, T, d, tid);
+    vc1.load(V, Vv.st, kTile, T, d, tid);
+  }
+  kc0.template store<LD>(ks, tid);
+  vc0.template store_t<kLdt, kSwz>(vts, tid);
+  if (ntiles > 1) {
+    kc1.template store<LD>(ks + kKs, tid);
+    vc1.template store_t<kLdt, kSwz>(vts + kVts, tid);
+  }
+  __syncthreads();
+
+  for (int t = 0; t < ntiles; t += 2) {
+    const bool next0 = t + 2 < ntiles, next1 = t + 3 < ntiles;
+    if (next0) {
+      kc0.load(K, Kv.st, (t + 2) * kTile, T, d, tid);
+      vc0.load(V, Vv.st, (t + 2) * kTile, T, d, tid);
+    }
+    if (next1) {
+      kc1.load(K, Kv.st, (t + 3) * kTile, T, d, tid);
+      vc1.load(V, Vv.st, (t + 3) * kTile, T, d, tid);
+    }
+    if (t + phase <= wlast) soft_pv(qk(ks + phase * kKs), vts + phase * kVts, (t + phase) * kTile);
+    __syncthreads();  // every read of the staged pair is done
+    if (next0) {
+      kc0.template store<LD>(ks, tid);
+      vc0.template store_t<kLdt, kSwz>(vts, tid);
+    }
+    if (next1) {
+      kc1.template store<LD>(ks + kKs, tid);
+      vc1.template store_t<kLdt, kSwz>(vts + kVts, tid);
+    }
+    __syncthreads();
+  }
+
+  // Phase 1 hands (O, m, l) of its query tile to phase 0 (every wave is past
+  // the loop's last barrier, so the staging buffers are free).
+  float* const hs = smem + qt_local * kHand;
+  if (phase == 1) {
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) hs[(b * 16 + r) * kWave + lane] = o[b][r];
+    }
+    hs[(NB * 16) * kWave + lane] = m;
+    hs[(NB * 16 + 1) * kWave + lane] = l;
+  }
+  __syncthreads();
+  if (phase == 1 || qi >= T) return;
+  const float m1 = hs[(NB * 16) * kWave + lane], l1 = hs[(NB * 16 + 1) * kWave + lane];
+  const float mm = fmaxf(m, m1);
+  const float mu = mm == -INFINITY ? 0.f : mm;
+  const float w0 = fast_exp2(m - mu), w1 = fast_exp2(m1 - mu);
+  l = w0 * l + w1 * l1;
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[b][r] = w0 * o[b][r] + w1 * hs[(b * 16 + r) * kWave + lane];
+  }
+  m = mm;
+  const float inv_l = 1.0f / l;
+  float* orow = Ov.head(bh, H) + (int64_t)qi * Ov.st;
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int dd = b * 32 + 8 * g + 4 * h;
+      f32x4 v = {o[b][4 * g] * inv_l, o[b][4 * g + 1] * inv_l, o[b][4 * g + 2] * inv_l, o[b][4 * g + 3] * inv_l};
+      if (dd < d) store4<VEC>(orow + dd, v, d - dd);
+    }
+  }
+  if (h == 0) Lse[(int64_t)bh * T + qi] = (m + log2f(l)) * kLn2;
+}
+
 // Merge of the two halves of every split row: with L_p = m_p + log2(l_p) and
 // M = max(L_0, L_1), w_p = 2^(L_p - M),
 //   O = (w_0 O_0 + w_1 O_1) / (w_0 + w_1),   lse = (M + log2(w_0 + w_1)) ln 2,
@@ -1290,9 +1487,34 @@ int fa_fwd_resident() {
   return n;
 }
 
+// Queries per forward workgroup.  The 128-query kernel's longest items (the
+// last query block of each head, every key tile in turn) set the time when
+// its whole grid is one round of resident workgroups and the sequence is
+// short; there the paired 64-query kernel (two key phases per query tile)
+// halves that chain.  The paired kernel is built for causal d = 64 with
+// 128-bit operands; other shapes take 128.  A process-wide override
+// (aar_flash_set_fwd_query_block) serves tuning and tests.
+std::atomic<int> g_fwd_query_block_override{0};
+int fa_fwd_query_block(int64_t bh, int64_t T, int64_t d, bool causal, bool vec) {
+  if (!causal || pad_dim(d) != 64 || !vec) return kBlock;
+  const int forced = g_fwd_query_block_override.load(std::memory_order_relaxed);
+  if (forced) return forced;
+  const int64_t slots = (int64_t)device_cu_count() * fa_fwd_resident<64, true>();
+  const int64_t grid = bh * ((T + kBlock - 1) / kBlock);
+  return (T <= 512 && grid <= slots) ? 64 : kBlock;
+}
+
 template <int DP, bool C, bool VEC>
 struct FwdLaunch {
   static int run(const FwdArgs& a) {
+    if constexpr (C && VEC && DP == 64) {
+      if (fa_fwd_query_block(a.BH, a.T, a.d, true, true) == 64) {
+        const int nqb64 = (a.T + 2 * kTile - 1) / (2 * kTile);
+        flash_fwd_pair_kernel<DP, C, VEC><<<dim3((unsigned)(nqb64 * a.BH)), dim3(kFaThreads), 0, a.st>>>(
+            a.q, a.k, a.v, a.o, a.lse, a.T, a.d, a.H, nqb64, a.BH, a.scale * kLog2e);
+        return launch_status();
+      }
+    }
     const int nqb = (a.T + kBlock - 1) / kBlock;
     FaSplit sp{};
     if (C && a.ws && aligned16(a.ws) && a.ws_bytes >= fa_fwd_split_bytes(a.BH, a.T, a.d)) {
@@ -1584,5 +1806,19 @@ extern "C" int aar_flash_bwd_plan(int64_t bh, int64_t T, int64_t d, int causal, 
 extern "C" int aar_flash_set_bwd_key_block(int key_block) {
   if (key_block != 0 && key_block != 64 && key_block != 128) return AAR_EINVAL;
   g_bwd_key_block_override.store(key_block, std::memory_order_relaxed);
+  return AAR_OK;
+}
+
+extern "C" int aar_flash_fwd_query_block(int64_t bh, int64_t T, int64_t d, int causal, int vec, int* query_block) {
+  if (!query_block || bh <= 0 || T <= 0 || d <= 0) return AAR_EINVAL;
+  if (d > 128) return AAR_EINVAL;
+  if (!fa_shape_ok(bh, T, d)) return AAR_EUNSUPPORTED;
+  *query_block = fa_fwd_query_block(bh, T, d, causal != 0, vec != 0);
+  return AAR_OK;
+}
+
+extern "C" int aar_flash_set_fwd_query_block(int query_block) {
+  if (query_block != 0 && query_block != 64 && query_block != 128) return AAR_EINVAL;
+  g_fwd_query_block_override.store(query_block, std::memory_order_relaxed);
   return AAR_OK;
 }

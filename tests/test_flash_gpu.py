@@ -441,7 +441,15 @@ def _flash_plans():
     L.aar_flash_fwd_workspace_bytes.restype = ctypes.c_size_t
     L.aar_flash_fwd_workspace_bytes.argtypes = [ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int]
     L.aar_flash_set_bwd_key_block.argtypes = [ctypes.c_int]
+    L.aar_flash_fwd_query_block.argtypes = L.aar_flash_bwd_plan.argtypes
+    L.aar_flash_set_fwd_query_block.argtypes = [ctypes.c_int]
     return L
+
+
+def _fwd_qb(L, bh, T, d, causal, vec=1):
+    out = ctypes.c_int()
+    assert L.aar_flash_fwd_query_block(bh, T, d, int(causal), vec, ctypes.byref(out)) == 0
+    return out.value
 
 
 def _bwd_plan(L, bh, T, d, causal, vec=1):
@@ -482,6 +490,57 @@ def test_flash_plans(gpu):
         assert (out.value > 0) == want_split, (bh, T, out.value)
         assert L.aar_flash_fwd_plan(bh, T, 64, 1, 1, 0, ctypes.byref(out)) == 0 and out.value == 0
         assert L.aar_flash_fwd_plan(bh, T, 64, 0, 1, wsb, ctypes.byref(out)) == 0 and out.value == 0
+    # forward query blocks: the paired 64-query kernel for short causal d = 64 grids of one round
+    assert _fwd_qb(L, 384, 256, 64, True) == 64      # the GPT step's attention
+    assert _fwd_qb(L, 8, 100, 64, True) == 64
+    assert _fwd_qb(L, 8, 512, 48, True) == 64        # head dims 33..64 share the d = 64 kernels
+    assert _fwd_qb(L, 96, 1024, 64, True) == 128     # longer sequences split the key range instead
+    assert _fwd_qb(L, 96, 4096, 64, True) == 128
+    assert _fwd_qb(L, 4096, 256, 64, True) == 128    # several rounds of 128-query workgroups
+    assert _fwd_qb(L, 8, 256, 64, False) == 128
+    for d in (32, 100, 128):
+        assert _fwd_qb(L, 8, 256, d, True) == 128
+    assert _fwd_qb(L, 8, 256, 64, True, vec=0) == 128
+    assert L.aar_flash_fwd_query_block(8, 256, 200, 1, 1, ctypes.byref(out)) == -1
+    assert L.aar_flash_set_fwd_query_block(96) == -1
+    try:
+        assert L.aar_flash_set_fwd_query_block(128) == 0
+        assert _fwd_qb(L, 384, 256, 64, True) == 128
+        assert L.aar_flash_set_fwd_query_block(64) == 0
+        assert _fwd_qb(L, 96, 4096, 64, True) == 64
+        assert _fwd_qb(L, 8, 256, 128, True) == 128   # other head dims never pair
+        assert _fwd_qb(L, 8, 256, 64, False) == 128   # nor non-causal attention
+    finally:
+        L.aar_flash_set_fwd_query_block(0)
+
+
+@pytest.mark.parametrize("query_block", [64, 128])
+@pytest.mark.parametrize("bh,T,d", [(3, 77, 64), (1, 1, 64), (2, 33, 64), (2, 257, 64), (4, 64, 64),
+                                    (2, 130, 48), (5, 31, 64), (3, 200, 64), (1, 511, 64), (2, 96, 64)])
+def test_fwd_query_blocks_vs_oracle(gpu, query_block, bh, T, d):
+    """Both causal forward decompositions (forced) against the oracle: O and
+    lse, then the backward through the forward's lse.  The paired kernel
+    merges two key phases per query tile in a fixed order, so a rerun is bit
+    identical."""
+    L = _flash_plans()
+    rng = np.random.default_rng(bh * 131 + T + d + query_block)
+    q, k, v, do = (rng.standard_normal((bh, T, d)).astype(f32) for _ in range(4))
+    try:
+        assert L.aar_flash_set_fwd_query_block(query_block) == 0
+        assert _fwd_qb(L, bh, T, d, True) == query_block
+        runs = [gpu._core._flash_attention_fwd(dev(gpu, q), dev(gpu, k), dev(gpu, v), True) for _ in range(2)]
+        tq, tk, tv = dev(gpu, q, True), dev(gpu, k, True), dev(gpu, v, True)
+        gpu.flash_attention(tq, tk, tv, True).backward(dev(gpu, do))
+        grads = [host(gpu, t.grad) for t in (tq, tk, tv)]
+    finally:
+        L.aar_flash_set_fwd_query_block(0)
+    (o, lse), (o2, lse2) = [(host(gpu, a), host(gpu, b)) for a, b in runs]
+    np.testing.assert_array_equal(o, o2)
+    np.testing.assert_array_equal(lse, lse2)
+    assert_close(o, O.attention(q, k, v, True), TOL, f"O (query block {query_block})")
+    assert_close(lse, O.attention_lse(q, k, True), TOL, f"lse (query block {query_block})")
+    for g, r, n in zip(grads, O.attention_backward(q, k, v, do, True), ("dq", "dk", "dv")):
+        assert_close(g, r, TOL, f"{n} (query block {query_block})")
 
 
 @pytest.mark.parametrize("key_block", [64, 128])
