@@ -106,6 +106,30 @@ __device__ __forceinline__ void dma4(const void* g, lds_void_t* lds) {
 #endif
 }
 
+// The same two DMAs issued as inline assembly, which the compiler's wait
+// insertion does not see.  For the builtins it assumes an LDS read may alias
+// any DMA in flight unless it can tell their buffers apart, and waits for all
+// of them (vmcnt(0)) before the read; with a double-buffered stage indexed at
+// run time it cannot, so the next tile's DMA latency lands on every
+// iteration.  Callers of these forms order the DMAs themselves: an explicit
+// wait_vm_lgkm0 and barrier before any wave reads the staged buffer, and none
+// of their own vector-memory operations between the DMAs and that wait that
+// the wait's count does not allow for.  M0 (the LDS base) is an asm operand,
+// so the compiler writes it.
+__device__ __forceinline__ void dma16_untracked(const void* g, lds_void_t* lds) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  const unsigned m0 = __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)lds);
+  asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(g), "{m0}"(m0) : "memory");
+#endif
+}
+
+__device__ __forceinline__ void dma4_untracked(const void* g, lds_void_t* lds) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  const unsigned m0 = __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)lds);
+  asm volatile("global_load_lds_dword %0, off" ::"v"(g), "{m0}"(m0) : "memory");
+#endif
+}
+
 // s_waitcnt vmcnt(N) lgkmcnt(0) (expcnt untouched): this wave's DMAs and
 // loads but the last N are done, and its LDS accesses are complete.
 template <int N>

@@ -857,6 +857,9 @@ flash_bwd_dkdv_kernel(FaIn Qv, FaIn Kv, FaIn Vv, FaIn dOv, const float* __restri
 // (DP = 64: 16 groups per row), so the 128-bit row reads (32 rows, one group)
 // and the 32-bit column reads (one row, 32 columns) are bank-conflict free.
 // Rows past T are clamped onto row T - 1 (their P is 0 through lse = +inf).
+// The DMAs are the untracked form: the loop's own wait and barrier at the end
+// of each pair order them, and the next pair's DMA runs under this pair's
+// MFMA work instead of before its first LDS read.
 // Requires d == DP == 64 and 16-byte aligned rows.
 struct FaDmaTile64 {
   static constexpr int kGroups = 16;
@@ -871,7 +874,7 @@ struct FaDmaTile64 {
       const int r = u / kGroups;
       const int g = (u % kGroups) ^ (r & 15);
       const int row = min(row0 + r, T - 1);
-      dma16(base + (int64_t)row * st + g * 4, (lds_void_t*)(stage + (wave * kPerWave + i) * kWave * 4));
+      dma16_untracked(base + (int64_t)row * st + g * 4, (lds_void_t*)(stage + (wave * kPerWave + i) * kWave * 4));
     }
   }
   // float4 group `grp` of row `row`
@@ -953,12 +956,10 @@ flash_bwd_dkdv_pair_kernel(FaIn Qv, FaIn Kv, FaIn Vv, FaIn dOv, const float* __r
       Tile::issue(Q, Qv.st, (t + p) * kTile, T, qs[buf][p], wave, lane);
       Tile::issue(dO, dOv.st, (t + p) * kTile, T, dos[buf][p], wave, lane);
     }
-    if (wave < 2) {
-      // __lane_id() recomputes the lane index here (kept live, it would be
-      // spilled, and its reload would wait for every DMA in flight)
-      const int q = min(t * kTile + (int)__lane_id(), T - 1);
-      dma4((wave == 0 ? Lb : Db) + q, (lds_void_t*)(wave == 0 ? ls[buf] : dsum[buf]));
-    }
+    // __lane_id() recomputes the lane index here (kept live, it would be
+    // spilled, and its reload would wait for every DMA in flight)
+    if (wave == 0) dma4_untracked(Lb + min(t * kTile + (int)__lane_id(), T - 1), (lds_void_t*)ls[buf]);
+    if (wave == 1) dma4_untracked(Db + min(t * kTile + (int)__lane_id(), T - 1), (lds_void_t*)dsum[buf]);
   };
   // Lane offset of the column reads for st % 4 == 0; the one for st % 4 == k
   // is col_off ^ (k << 2) (see FaDmaTile64::lane_off: the XOR only touches
@@ -973,7 +974,8 @@ flash_bwd_dkdv_pair_kernel(FaIn Qv, FaIn Kv, FaIn Vv, FaIn dOv, const float* __r
     const int qt0 = (t + phase) * kTile;  // this wave's query tile
     const bool has_next = t + 2 < ntiles;
     if (has_next) issue_tiles(t + 2, cur ^ 1);
-    if (qt0 < T && (!CAUSAL || qt0 + kTile - 1 >= k0)) {
+    const bool work = qt0 < T && (!CAUSAL || qt0 + kTile - 1 >= k0);
+    if (work) {
       const float* qt = qs[cur][phase];
       const float* dot = dos[cur][phase];
       f32x16 s = zero16(), dp = zero16();
@@ -1023,7 +1025,15 @@ flash_bwd_dkdv_pair_kernel(FaIn Qv, FaIn Kv, FaIn Vv, FaIn dOv, const float* __r
         }
       }
     }
-    wait_vm_lgkm0<0>();
+    // The next pair's DMAs were issued before this tile's four dS stores, and
+    // vector memory operations retire in issue order: a wave that stored
+    // waits for all but the last four (every DMA), without waiting for its
+    // stores to reach memory.
+    if (STORE_DS && work && k0 < T) {
+      wait_vm_lgkm0<4>();
+    } else {
+      wait_vm_lgkm0<0>();
+    }
     ring_barrier();
   }
 
