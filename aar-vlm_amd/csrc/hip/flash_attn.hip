@@ -420,34 +420,77 @@ flash_fwd_kernel(FaIn Qv, FaIn Kv, FaIn Vv, FaOut Ov, float* __restrict__ Lse, i
   }
 }
 
+// ------------------------------------------------- DMA-staged 32 x 64 tiles
+// The paired kernels stage their [32][64] operand tiles HBM -> LDS by DMA:
+// no staging registers, no LDS stores.  A tile is [32][64] unpadded; float4
+// group g of row r sits at group g ^ (r & 15) (16 groups per row), so the
+// 128-bit row reads (32 rows, one group) and the 32-bit column reads (one
+// row, 32 columns) are bank-conflict free.  Rows past T are clamped onto row
+// T - 1: the caller masks them.  The DMAs are the untracked form: each
+// kernel's loop orders them with its own wait and barrier at the end of an
+// iteration, so the next iteration's DMA runs under the current MFMA work
+// instead of before its first LDS read.  Requires d == 64 and 16-byte
+// aligned rows.
+struct FaDmaTile64 {
+  static constexpr int kGroups = 16;
+  static constexpr int kFloats = kTile * 64;
+  static constexpr int kPerWave = kTile * kGroups / (kWave * 4);  // 2 DMA instructions per wave (4 waves)
+
+  __device__ __forceinline__ static void issue(const float* __restrict__ base, int64_t st, int row0, int T,
+                                               float* stage, int wave, int lane) {
+#pragma unroll
+    for (int i = 0; i < kPerWave; ++i) {
+      const int u = (wave * kPerWave + i) * kWave + lane;
+      const int r = u / kGroups;
+      const int g = (u % kGroups) ^ (r & 15);
+      const int row = min(row0 + r, T - 1);
+      dma16_untracked(base + (int64_t)row * st + g * 4, (lds_void_t*)(stage + (wave * kPerWave + i) * kWave * 4));
+    }
+  }
+  // float4 group `grp` of row `row`
+  __device__ __forceinline__ static f32x4 group(const float* S, int row, int grp) {
+    return *reinterpret_cast<const f32x4*>(S + (row * kGroups + (grp ^ (row & 15))) * 4);
+  }
+  // Column reads of the dV/dK products: lane (lr, h) reads row
+  // q = 8*(st/4) + 4h + st%4, column 32b + lr.  The float offset splits into a
+  // lane part that depends on st only through st % 4 (lane_off(k), four
+  // values per lane) and a compile-time part (ct_off).
+  __device__ __forceinline__ static int lane_off(int k, int lr, int h) {
+    return 4 * h * 64 + ((((lr >> 2) ^ (4 * h)) ^ k) << 2) + (lr & 3);
+  }
+  __host__ __device__ static constexpr int ct_off(int st, int b) {
+    return (8 * (st >> 2) + (st & 3)) * 64 + ((b ^ ((st >> 2) & 1)) << 5);
+  }
+};
+
 // ------------------------------------------------------ forward, paired
 // Causal forward over 64-query workgroups for short sequences, where the
 // 128-query grid is about one round of resident workgroups and its longest
 // items (the last query block, every key tile in turn) set the time: four
 // waves as 2 query tiles x 2 key phases.  Each iteration stages key tiles t
-// and t + 1 (K rows and V^T, as flash_fwd_kernel); wave (a, p) runs the
-// online softmax of query tile a over key tile t + p, so the two phases of a
-// query tile split its key range and the longest chain of tiles is half that
-// of the 128-query kernel.  At the end phase 1 hands (m, l, O) to phase 0
-// through LDS, and phase 0 merges the two partial softmaxes in a fixed order
-// (m = max(m0, m1), w_p = 2^(m_p - m), l = w0 l0 + w1 l1, O = w0 O0 + w1 O1;
-// deterministic), normalises and stores O and lse.  The tiles of the next
-// pair are loaded into registers during the iteration and stored after a
-// barrier (one LDS stage, two barriers per pair of tiles).
-template <int DP, bool CAUSAL, bool VEC>
-__global__ void __launch_bounds__(kFaThreads, DP <= 64 ? 3 : 1)
-flash_fwd_pair_kernel(FaIn Qv, FaIn Kv, FaIn Vv, FaOut Ov, float* __restrict__ Lse, int T, int d, int H,
-                      int nqb, int BH, float scale_log2) {
+// and t + 1 of K and V by DMA (FaDmaTile64, double-buffered); wave (a, p)
+// runs the online softmax of query tile a over key tile t + p, so the two
+// phases of a query tile split its key range and the longest chain of tiles
+// is half that of the 128-query kernel.  S^T takes 128-bit K row reads; O +=
+// V^T P takes one 32-bit V column read per MFMA (the layout of the dK/dV
+// pair kernel's dO^T P product).  At the end phase 1 hands (m, l, O) to
+// phase 0 through LDS, and phase 0 merges the two partial softmaxes in a
+// fixed order (m = max(m0, m1), w_p = 2^(m_p - m), l = w0 l0 + w1 l1,
+// O = w0 O0 + w1 O1; deterministic), normalises and stores O and lse.
+// Requires d == DP == 64 and 16-byte aligned rows.
+template <int DP, bool CAUSAL>
+__global__ void __launch_bounds__(kFaThreads, 2)
+flash_fwd_pair_kernel(FaIn Qv, FaIn Kv, FaIn Vv, FaOut Ov, float* __restrict__ Lse, int T, int H, int nqb,
+                      int BH, float scale_log2) {
+  static_assert(DP == 64, "the paired forward is built for head dim 64");
   constexpr int NC = DP / 8;   // head-dim chunks
   constexpr int NB = DP / 32;  // head-dim output blocks
-  constexpr int LD = DP + 4;
-  constexpr bool kSwz = kVtSwizzle<DP, CAUSAL>;
-  constexpr int kQueries = 2 * kTile;  // queries per workgroup
-  constexpr int kKs = kTile * LD;      // one staged K tile (rows)
-  constexpr int kVts = DP * kLdt;      // one staged V tile (transposed)
+  constexpr int kQueries = 2 * kTile;           // queries per workgroup
   constexpr int kHand = (NB * 16 + 2) * kWave;  // one wave's O, m and l, lane-major
-  __shared__ __attribute__((aligned(16))) float smem[2 * kKs + 2 * kVts];
-  static_assert(2 * kHand <= 2 * kKs + 2 * kVts, "phase hand-over fits in the staging buffers");
+  using Tile = FaDmaTile64;
+  __shared__ __attribute__((aligned(16))) float ks[2][2][Tile::kFloats];
+  __shared__ __attribute__((aligned(16))) float vs[2][2][Tile::kFloats];
+  static_assert(2 * kHand <= 4 * Tile::kFloats, "phase hand-over fits in the K staging buffers");
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int lr = lane & 31, h = lane >> 5;
@@ -460,14 +503,12 @@ flash_fwd_pair_kernel(FaIn Qv, FaIn Kv, FaIn Vv, FaOut Ov, float* __restrict__ L
   const float* __restrict__ V = Vv.head(bh, H);
   const int q0 = qb * kQueries + qt_local * kTile;  // first query of this wave
   const int qi = q0 + lr;                           // this lane's query
-  float* const ks = smem;
-  float* const vts = smem + 2 * kKs;
 
   f32x4 qr[NC];
 #pragma unroll
   for (int c = 0; c < NC; ++c) {
     const int dd = 8 * c + 4 * h;
-    qr[c] = qi < T ? load4<VEC>(Q + (int64_t)qi * Qv.st + dd, d - dd) : f32x4{0.f, 0.f, 0.f, 0.f};
+    qr[c] = qi < T ? *reinterpret_cast<const f32x4*>(Q + (int64_t)qi * Qv.st + dd) : f32x4{0.f, 0.f, 0.f, 0.f};
   }
   f32x16 o[NB];
 #pragma unroll
@@ -478,19 +519,21 @@ flash_fwd_pair_kernel(FaIn Qv, FaIn Kv, FaIn Vv, FaOut Ov, float* __restrict__ L
   const int ntiles = (kv_end + kTile - 1) / kTile;
   // Last key tile that holds a key this wave's queries may see.
   const int wlast = CAUSAL ? min(ntiles - 1, (q0 + kTile - 1) / kTile) : ntiles - 1;
+  // Lane offset of the V column reads for st % 4 == 0 (st % 4 == k: XOR k << 2).
+  const int col_off = Tile::lane_off(0, lr, h);
 
-  // S^T tile from K rows in LDS: lane = query, register r = key acc_row(r, h).
+  // S^T tile from a staged K tile: lane = query, register r = key acc_row(r, h).
   auto qk = [&](const float* kt) {
     f32x16 sc = zero16();
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
-      const f32x4 kf = *reinterpret_cast<const f32x4*>(kt + lr * LD + 8 * c + 4 * h);
+      const f32x4 kf = Tile::group(kt, lr, 2 * c + h);
 #pragma unroll
       for (int e = 0; e < 4; ++e) sc = mfma32(kf[e], qr[c][e], sc);
     }
     return sc;
   };
-  // Online softmax of one key tile (S in sc) and O += V_t P_t.
+  // Online softmax of one key tile (S in sc) and O += V_t^T P_t.
   auto soft_pv = [&](f32x16 sc, const float* vt, int kv0) {
     float mx = -INFINITY;
     if ((CAUSAL && kv0 + kTile - 1 > q0) || kv0 + kTile > T) {
@@ -528,59 +571,42 @@ flash_fwd_pair_kernel(FaIn Qv, FaIn Kv, FaIn Vv, FaOut Ov, float* __restrict__ L
 #pragma unroll
       for (int r = 0; r < 16; ++r) o[b][r] *= alpha;
     }
+    // Lane (lr, h) of step st reads V row acc_row(st, h), column 32 b + lr.
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int vc = b * 32 + lr;
-        const f32x4 vf = *reinterpret_cast<const f32x4*>(vt + vc * kLdt + vt_swz<kSwz>(vc, 8 * g + 4 * h));
-#pragma unroll
-        for (int e = 0; e < 4; ++e) o[b] = mfma32(vf[e], sc[4 * g + e], o[b]);
+      for (int st = 0; st < 16; ++st) {
+        const int off = Tile::ct_off(st, b) + (col_off ^ ((st & 3) << 2));
+        o[b] = mfma32(vt[off], sc[st], o[b]);
       }
     }
   };
 
-  TileCopy<DP, VEC> kc0, kc1, vc0, vc1;
-  kc0.load(K, Kv.st, 0, T, d, tid);
-  vc0.load(V, Vv.st, 0, T, d, tid);
-  if (ntiles > 1) {
-    kc1.load(K, Kv.st, kTile, T, d, tid);
-    vc1.load(V, Vv.st, kTile, T, d, tid);
-  }
-  kc0.template store<LD>(ks, tid);
-  vc0.template store_t<kLdt, kSwz>(vts, tid);
-  if (ntiles > 1) {
-    kc1.template store<LD>(ks + kKs, tid);
-    vc1.template store_t<kLdt, kSwz>(vts + kVts, tid);
-  }
-  __syncthreads();
+  auto issue_tiles = [&](int t, int buf) {
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      Tile::issue(K, Kv.st, (t + p) * kTile, T, ks[buf][p], wave, lane);
+      Tile::issue(V, Vv.st, (t + p) * kTile, T, vs[buf][p], wave, lane);
+    }
+  };
+  issue_tiles(0, 0);
+  wait_vm_lgkm0<0>();
+  ring_barrier();
 
   for (int t = 0; t < ntiles; t += 2) {
-    const bool next0 = t + 2 < ntiles, next1 = t + 3 < ntiles;
-    if (next0) {
-      kc0.load(K, Kv.st, (t + 2) * kTile, T, d, tid);
-      vc0.load(V, Vv.st, (t + 2) * kTile, T, d, tid);
-    }
-    if (next1) {
-      kc1.load(K, Kv.st, (t + 3) * kTile, T, d, tid);
-      vc1.load(V, Vv.st, (t + 3) * kTile, T, d, tid);
-    }
-    if (t + phase <= wlast) soft_pv(qk(ks + phase * kKs), vts + phase * kVts, (t + phase) * kTile);
-    __syncthreads();  // every read of the staged pair is done
-    if (next0) {
-      kc0.template store<LD>(ks, tid);
-      vc0.template store_t<kLdt, kSwz>(vts, tid);
-    }
-    if (next1) {
-      kc1.template store<LD>(ks + kKs, tid);
-      vc1.template store_t<kLdt, kSwz>(vts + kVts, tid);
-    }
-    __syncthreads();
+    const int cur = (t >> 1) & 1;
+    if (t + 2 < ntiles) issue_tiles(t + 2, cur ^ 1);
+    if (t + phase <= wlast) soft_pv(qk(ks[cur][phase]), vs[cur][phase], (t + phase) * kTile);
+    // This wave's DMAs for the next pair have landed, and (after the
+    // barrier) every wave's have and every read of this pair is done.
+    wait_vm_lgkm0<0>();
+    ring_barrier();
   }
 
   // Phase 1 hands (O, m, l) of its query tile to phase 0 (every wave is past
-  // the loop's last barrier, so the staging buffers are free).
-  float* const hs = smem + qt_local * kHand;
+  // the loop's last barrier and no DMA is in flight, so the K buffers are
+  // free).
+  float* const hs = &ks[0][0][0] + qt_local * kHand;
   if (phase == 1) {
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
@@ -611,7 +637,7 @@ flash_fwd_pair_kernel(FaIn Qv, FaIn Kv, FaIn Vv, FaOut Ov, float* __restrict__ L
     for (int g = 0; g < 4; ++g) {
       const int dd = b * 32 + 8 * g + 4 * h;
       f32x4 v = {o[b][4 * g] * inv_l, o[b][4 * g + 1] * inv_l, o[b][4 * g + 2] * inv_l, o[b][4 * g + 3] * inv_l};
-      if (dd < d) store4<VEC>(orow + dd, v, d - dd);
+      *reinterpret_cast<f32x4*>(orow + dd) = v;
     }
   }
   if (h == 0) Lse[(int64_t)bh * T + qi] = (m + log2f(l)) * kLn2;
@@ -851,47 +877,11 @@ flash_bwd_dkdv_kernel(FaIn Qv, FaIn Kv, FaIn Vv, FaIn dOv, const float* __restri
 // deterministic, no atomics.  Stored dS tiles are written exactly as by
 // flash_bwd_dkdv_kernel.
 //
-// Q and dO tiles go HBM -> LDS by DMA (no staging registers: the 128-key
-// kernel already uses all 256 VGPRs of a 2-wave-per-SIMD launch).  A tile is
-// [32][DP] unpadded; float4 group g of row r sits at group g ^ (r & 15)
-// (DP = 64: 16 groups per row), so the 128-bit row reads (32 rows, one group)
-// and the 32-bit column reads (one row, 32 columns) are bank-conflict free.
-// Rows past T are clamped onto row T - 1 (their P is 0 through lse = +inf).
-// The DMAs are the untracked form: the loop's own wait and barrier at the end
-// of each pair order them, and the next pair's DMA runs under this pair's
-// MFMA work instead of before its first LDS read.
-// Requires d == DP == 64 and 16-byte aligned rows.
-struct FaDmaTile64 {
-  static constexpr int kGroups = 16;
-  static constexpr int kFloats = kTile * 64;
-  static constexpr int kPerWave = kTile * kGroups / (kWave * 4);  // 2 DMA instructions per wave (4 waves)
-
-  __device__ __forceinline__ static void issue(const float* __restrict__ base, int64_t st, int row0, int T,
-                                               float* stage, int wave, int lane) {
-#pragma unroll
-    for (int i = 0; i < kPerWave; ++i) {
-      const int u = (wave * kPerWave + i) * kWave + lane;
-      const int r = u / kGroups;
-      const int g = (u % kGroups) ^ (r & 15);
-      const int row = min(row0 + r, T - 1);
-      dma16_untracked(base + (int64_t)row * st + g * 4, (lds_void_t*)(stage + (wave * kPerWave + i) * kWave * 4));
-    }
-  }
-  // float4 group `grp` of row `row`
-  __device__ __forceinline__ static f32x4 group(const float* S, int row, int grp) {
-    return *reinterpret_cast<const f32x4*>(S + (row * kGroups + (grp ^ (row & 15))) * 4);
-  }
-  // Column reads of the dV/dK products: lane (lr, h) reads row
-  // q = 8*(st/4) + 4h + st%4, column 32b + lr.  The float offset splits into a
-  // lane part that depends on st only through st % 4 (lane_off(k), four
-  // values per lane) and a compile-time part (ct_off).
-  __device__ __forceinline__ static int lane_off(int k, int lr, int h) {
-    return 4 * h * 64 + ((((lr >> 2) ^ (4 * h)) ^ k) << 2) + (lr & 3);
-  }
-  __host__ __device__ static constexpr int ct_off(int st, int b) {
-    return (8 * (st >> 2) + (st & 3)) * 64 + ((b ^ ((st >> 2) & 1)) << 5);
-  }
-};
+// Q and dO tiles go HBM -> LDS by DMA in the FaDmaTile64 layout (no staging
+// registers: the 128-key kernel already uses all 256 VGPRs of a
+// 2-wave-per-SIMD launch), double-buffered; the lse and D of the staged rows
+// by 4-byte DMAs.  Rows past T are clamped onto row T - 1 (their P is 0
+// through lse = +inf).  Requires d == DP == 64 and 16-byte aligned rows.
 
 template <int DP, bool CAUSAL, bool STORE_DS>
 __global__ void __launch_bounds__(kFaThreads, DP <= 64 && (CAUSAL || !STORE_DS) ? 2 : 1)
@@ -1501,12 +1491,13 @@ int fa_fwd_resident() {
 // last query block of each head, every key tile in turn) set the time when
 // its whole grid is one round of resident workgroups and the sequence is
 // short; there the paired 64-query kernel (two key phases per query tile)
-// halves that chain.  The paired kernel is built for causal d = 64 with
-// 128-bit operands; other shapes take 128.  A process-wide override
-// (aar_flash_set_fwd_query_block) serves tuning and tests.
+// halves that chain.  The paired kernel stages its tiles by DMA in a layout
+// built for causal d = 64 exactly, with 128-bit operands; other shapes take
+// 128.  A process-wide override (aar_flash_set_fwd_query_block) serves tuning
+// and tests.
 std::atomic<int> g_fwd_query_block_override{0};
 int fa_fwd_query_block(int64_t bh, int64_t T, int64_t d, bool causal, bool vec) {
-  if (!causal || pad_dim(d) != 64 || !vec) return kBlock;
+  if (!causal || d != 64 || !vec) return kBlock;
   const int forced = g_fwd_query_block_override.load(std::memory_order_relaxed);
   if (forced) return forced;
   const int64_t slots = (int64_t)device_cu_count() * fa_fwd_resident<64, true>();
@@ -1518,10 +1509,11 @@ template <int DP, bool C, bool VEC>
 struct FwdLaunch {
   static int run(const FwdArgs& a) {
     if constexpr (C && VEC && DP == 64) {
-      if (fa_fwd_query_block(a.BH, a.T, a.d, true, true) == 64) {
-        const int nqb64 = (a.T + 2 * kTile - 1) / (2 * kTile);
-        flash_fwd_pair_kernel<DP, C, VEC><<<dim3((unsigned)(nqb64 * a.BH)), dim3(kFaThreads), 0, a.st>>>(
-            a.q, a.k, a.v, a.o, a.lse, a.T, a.d, a.H, nqb64, a.BH, a.scale * kLog2e);
+      const int64_t nqb64 = (a.T + 2 * kTile - 1) / (2 * kTile);
+      // (a dispatch holds the grid as a 32-bit work-item count)
+      if (fa_fwd_query_block(a.BH, a.T, a.d, true, true) == 64 && nqb64 * a.BH * kFaThreads <= (int64_t)UINT32_MAX) {
+        flash_fwd_pair_kernel<DP, C><<<dim3((unsigned)(nqb64 * a.BH)), dim3(kFaThreads), 0, a.st>>>(
+            a.q, a.k, a.v, a.o, a.lse, a.T, a.H, (int)nqb64, a.BH, a.scale * kLog2e);
         return launch_status();
       }
     }

@@ -286,7 +286,7 @@ int aar_flash_bwd_strided_f32(const float* q, const float* k, const float* v,
  * 128-query grid is one round) or 128; when it is 64 the forward does not
  * split and aar_flash_fwd_plan's count does not apply.
  * aar_flash_set_fwd_query_block forces it likewise (64 or 128; 0 restores
- * the plan; only causal head dims 33..64 with 128-bit operands can take 64). */
+ * the plan; only causal d = 64 with 128-bit operands can take 64). */
 int aar_flash_fwd_plan(int64_t bh, int64_t T, int64_t d, int causal, int vec, size_t workspace_bytes,
                        int* split_blocks);
 int aar_flash_bwd_plan(int64_t bh, int64_t T, int64_t d, int causal, int vec, int* key_block);

@@ -493,12 +493,12 @@ def test_flash_plans(gpu):
     # forward query blocks: the paired 64-query kernel for short causal d = 64 grids of one round
     assert _fwd_qb(L, 384, 256, 64, True) == 64      # the GPT step's attention
     assert _fwd_qb(L, 8, 100, 64, True) == 64
-    assert _fwd_qb(L, 8, 512, 48, True) == 64        # head dims 33..64 share the d = 64 kernels
+    assert _fwd_qb(L, 8, 512, 48, True) == 128       # the paired kernel's DMA layout is d = 64 exactly
     assert _fwd_qb(L, 96, 1024, 64, True) == 128     # longer sequences split the key range instead
     assert _fwd_qb(L, 96, 4096, 64, True) == 128
     assert _fwd_qb(L, 4096, 256, 64, True) == 128    # several rounds of 128-query workgroups
     assert _fwd_qb(L, 8, 256, 64, False) == 128
-    for d in (32, 100, 128):
+    for d in (32, 48, 63, 100, 128):
         assert _fwd_qb(L, 8, 256, d, True) == 128
     assert _fwd_qb(L, 8, 256, 64, True, vec=0) == 128
     assert L.aar_flash_fwd_query_block(8, 256, 200, 1, 1, ctypes.byref(out)) == -1
@@ -509,6 +509,7 @@ def test_flash_plans(gpu):
         assert L.aar_flash_set_fwd_query_block(64) == 0
         assert _fwd_qb(L, 96, 4096, 64, True) == 64
         assert _fwd_qb(L, 8, 256, 128, True) == 128   # other head dims never pair
+        assert _fwd_qb(L, 8, 256, 48, True) == 128
         assert _fwd_qb(L, 8, 256, 64, False) == 128   # nor non-causal attention
     finally:
         L.aar_flash_set_fwd_query_block(0)
@@ -516,7 +517,8 @@ def test_flash_plans(gpu):
 
 @pytest.mark.parametrize("query_block", [64, 128])
 @pytest.mark.parametrize("bh,T,d", [(3, 77, 64), (1, 1, 64), (2, 33, 64), (2, 257, 64), (4, 64, 64),
-                                    (2, 130, 48), (5, 31, 64), (3, 200, 64), (1, 511, 64), (2, 96, 64)])
+                                    (2, 130, 48), (5, 31, 64), (3, 200, 64), (1, 511, 64), (2, 96, 64),
+                                    (2, 448, 64), (1, 320, 64)])
 def test_fwd_query_blocks_vs_oracle(gpu, query_block, bh, T, d):
     """Both causal forward decompositions (forced) against the oracle: O and
     lse, then the backward through the forward's lse.  The paired kernel
@@ -527,7 +529,7 @@ def test_fwd_query_blocks_vs_oracle(gpu, query_block, bh, T, d):
     q, k, v, do = (rng.standard_normal((bh, T, d)).astype(f32) for _ in range(4))
     try:
         assert L.aar_flash_set_fwd_query_block(query_block) == 0
-        assert _fwd_qb(L, bh, T, d, True) == query_block
+        assert _fwd_qb(L, bh, T, d, True) == (query_block if d == 64 else 128)  # pairs at d = 64 only
         runs = [gpu._core._flash_attention_fwd(dev(gpu, q), dev(gpu, k), dev(gpu, v), True) for _ in range(2)]
         tq, tk, tv = dev(gpu, q, True), dev(gpu, k, True), dev(gpu, v, True)
         gpu.flash_attention(tq, tk, tv, True).backward(dev(gpu, do))
