@@ -1271,20 +1271,26 @@ flash_bwd_dq_ds_kernel(FaIn Kv, const float* __restrict__ dS, FaOut dQv, int T, 
 
 // dQ from the stored dS tiles over 64-query workgroups, for the grids that
 // take the paired dK/dV kernel: four waves as 2 query tiles x 2 key phases.
-// Per iteration the workgroup stages key tiles t and t + 1 (transposed, as
-// above); wave (a, p) takes key tile t + p for query tile a, so the two
-// phases of a query tile split its key range and the longest work item is
-// half that of a 128-query workgroup.  At the end phase 1 hands its dQ
-// accumulators to phase 0 through LDS and phase 0 adds them (phase 0 +
-// phase 1, a fixed order; deterministic).
-template <int DP, bool CAUSAL, bool VEC>
+// Per iteration the workgroup stages key tiles t and t + 1 by DMA
+// (FaDmaTile64, double-buffered); wave (a, p) takes key tile t + p for query
+// tile a, so the two phases of a query tile split its key range and the
+// longest work item is half that of a 128-query workgroup.  dQ^T += K^T dS^T
+// reads K columns with 32-bit conflict-free reads (the layout of the dK/dV
+// pair kernel's dO^T P product); each wave's dS tile of the next pair is
+// loaded into registers during the current one.  At the end phase 1 hands
+// its dQ accumulators to phase 0 through LDS and phase 0 adds them (phase 0
+// + phase 1, a fixed order; deterministic).  Requires d == DP == 64 and
+// 16-byte aligned rows.
+template <int DP, bool CAUSAL>
 __global__ void __launch_bounds__(kFaThreads, 4)
-flash_bwd_dq_ds_pair_kernel(FaIn Kv, const float* __restrict__ dS, FaOut dQv, int T, int d, int H, int nqb,
-                            int BH, float scale) {
+flash_bwd_dq_ds_pair_kernel(FaIn Kv, const float* __restrict__ dS, FaOut dQv, int T, int H, int nqb, int BH,
+                            float scale) {
+  static_assert(DP == 64, "the paired dQ kernel is built for head dim 64");
   constexpr int NB = DP / 32;
   constexpr int kQueries = 2 * kTile;  // queries per workgroup
-  __shared__ __attribute__((aligned(16))) float kts[2][2][DP * kLdt];  // key tiles t, t+1, transposed
-  static_assert(2 * DP * kLdt >= 2 * NB * 16 * kWave, "phase hand-over fits in one staged tile pair");
+  using Tile = FaDmaTile64;
+  __shared__ __attribute__((aligned(16))) float ks[2][2][Tile::kFloats];  // key tiles t, t+1 of a stage
+  static_assert(2 * NB * 16 * kWave <= 4 * Tile::kFloats, "phase hand-over fits in the staging buffers");
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int lr = lane & 31, h = lane >> 5;
@@ -1307,60 +1313,60 @@ flash_bwd_dq_ds_pair_kernel(FaIn Kv, const float* __restrict__ dS, FaOut dQv, in
   const int kv_end = CAUSAL ? min(T, qb * kQueries + kQueries) : T;
   const int ntiles = (kv_end + kTile - 1) / kTile;
   auto has_work = [&](int t) { return active && t < ntiles && (!CAUSAL || t <= qtile); };
+  // Lane (lr, h) of step st needs dS^T[key acc_row(st, h)][query lr] of the
+  // key-major stored tile.
   auto load_ds = [&](int t, float (&r)[16]) {
     const float* tile = dS_head + ds_pair(qtile, t, nt, CAUSAL) * kDsTile;
 #pragma unroll
     for (int st = 0; st < 16; ++st) r[st] = tile[(8 * (st >> 2) + (st & 3)) * kTile];
   };
+  auto issue_tiles = [&](int t, int buf) {
+#pragma unroll
+    for (int p = 0; p < 2; ++p) Tile::issue(K, Kv.st, (t + p) * kTile, T, ks[buf][p], wave, lane);
+  };
+  // Lane offset of the K column reads for st % 4 == 0 (st % 4 == k: XOR k << 2).
+  const int col_off = Tile::lane_off(0, lr, h);
 
-  constexpr bool kSwz = kKtSwizzle<DP, CAUSAL>;
-  TileCopy<DP, VEC> kc0, kc1;
-  kc0.load(K, Kv.st, 0, T, d, tid);
-  kc1.load(K, Kv.st, kTile, T, d, tid);
-  kc0.template store_t<kLdt, kSwz>(kts[0][0], tid);
-  kc1.template store_t<kLdt, kSwz>(kts[0][1], tid);
+  issue_tiles(0, 0);
   float dsr[16];
   if (has_work(phase)) load_ds(phase, dsr);
-  __syncthreads();
+  wait_vm_lgkm0<0>();
+  ring_barrier();
 
   for (int t = 0; t < ntiles; t += 2) {
     const int cur = (t >> 1) & 1;
-    const bool has_next = t + 2 < ntiles;
-    if (has_next) {
-      kc0.load(K, Kv.st, (t + 2) * kTile, T, d, tid);
-      kc1.load(K, Kv.st, (t + 3) * kTile, T, d, tid);
-    }
+    if (t + 2 < ntiles) issue_tiles(t + 2, cur ^ 1);
+    const bool next_work = has_work(t + 2 + phase);
     float nxt[16];
-    if (has_work(t + 2 + phase)) load_ds(t + 2 + phase, nxt);
+    if (next_work) load_ds(t + 2 + phase, nxt);
     if (has_work(t + phase)) {
-      const float* kt = kts[cur][phase];
+      const float* kt = ks[cur][phase];
+      // Lane (lr, h) of step st reads K row acc_row(st, h), column 32 b + lr.
 #pragma unroll
       for (int b = 0; b < NB; ++b) {
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          // K^T[b*32 + lr][keys 8g + 4h .. +3]: one 128-bit read feeds 4 steps
-          const int kc_col = b * 32 + lr;
-          const f32x4 kf = *reinterpret_cast<const f32x4*>(kt + kc_col * kLdt + vt_swz<kSwz>(kc_col, 8 * g + 4 * h));
-#pragma unroll
-          for (int e = 0; e < 4; ++e) dq[b] = mfma32(kf[e], dsr[4 * g + e], dq[b]);
+        for (int st = 0; st < 16; ++st) {
+          const int off = Tile::ct_off(st, b) + (col_off ^ ((st & 3) << 2));
+          dq[b] = mfma32(kt[off], dsr[st], dq[b]);
         }
       }
     }
-    if (has_next) {
-      kc0.template store_t<kLdt, kSwz>(kts[cur ^ 1][0], tid);
-      kc1.template store_t<kLdt, kSwz>(kts[cur ^ 1][1], tid);
-    }
-    if (has_work(t + 2 + phase)) {
+    if (next_work) {
 #pragma unroll
       for (int st = 0; st < 16; ++st) dsr[st] = nxt[st];
     }
-    __syncthreads();
+    // This wave's DMAs and dS loads for the next pair have landed, and
+    // (after the barrier) every wave's have and every read of this pair is
+    // done.
+    wait_vm_lgkm0<0>();
+    ring_barrier();
   }
 
   // Phase 1 hands its dQ accumulators to phase 0 of the same query tile
-  // through the staging buffers (every wave is past the loop's last barrier),
-  // lane-major so the writes and reads are conflict free.
-  float* hq = &kts[0][0][0] + qt_local * (NB * 16 * kWave);
+  // through the staging buffers (every wave is past the loop's last barrier
+  // and no DMA is in flight), lane-major so the writes and reads are
+  // conflict free.
+  float* hq = &ks[0][0][0] + qt_local * (NB * 16 * kWave);
   if (phase == 1) {
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
@@ -1381,10 +1387,9 @@ flash_bwd_dq_ds_pair_kernel(FaIn Kv, const float* __restrict__ dS, FaOut dQv, in
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       const int dd = b * 32 + 8 * g + 4 * h;
-      if (dd >= d) continue;
       f32x4 v = {dq[b][4 * g] * scale, dq[b][4 * g + 1] * scale, dq[b][4 * g + 2] * scale,
                  dq[b][4 * g + 3] * scale};
-      store4<VEC>(qrow + dd, v, d - dd);
+      *reinterpret_cast<f32x4*>(qrow + dd) = v;
     }
   }
 }
@@ -1487,14 +1492,17 @@ int fa_fwd_resident() {
   return n;
 }
 
-// Queries per forward workgroup.  The 128-query kernel's longest items (the
-// last query block of each head, every key tile in turn) set the time when
-// its whole grid is one round of resident workgroups and the sequence is
-// short; there the paired 64-query kernel (two key phases per query tile)
-// halves that chain.  The paired kernel stages its tiles by DMA in a layout
-// built for causal d = 64 exactly, with 128-bit operands; other shapes take
-// 128.  A process-wide override (aar_flash_set_fwd_query_block) serves tuning
-// and tests.
+// Queries per forward workgroup.  The paired 64-query kernel (two key phases
+// per query tile, K and V staged by DMA) halves the longest chain of key
+// tiles of the 128-query kernel and has no staging registers; the 128-query
+// kernel shares each staged key tile among four query tiles.  Measured on
+// MI355X (causal, d = 64; R = 128-query grid / resident 128-query
+// workgroups), the paired kernel takes 0.81-0.86x the time at R <= 1
+// (T = 256..4096), 0.91-0.93x at R = 2 and 0.98x at R = 4 for T <= 1024, but
+// 1.01x at R = 4, T = 4096 and at R = 8, T = 256.  So: paired up to two
+// rounds, and up to four for T <= 1024.  It is built for causal d = 64
+// exactly, with 128-bit operands; other shapes take 128.  A process-wide
+// override (aar_flash_set_fwd_query_block) serves tuning and tests.
 std::atomic<int> g_fwd_query_block_override{0};
 int fa_fwd_query_block(int64_t bh, int64_t T, int64_t d, bool causal, bool vec) {
   if (!causal || d != 64 || !vec) return kBlock;
@@ -1502,7 +1510,7 @@ int fa_fwd_query_block(int64_t bh, int64_t T, int64_t d, bool causal, bool vec) 
   if (forced) return forced;
   const int64_t slots = (int64_t)device_cu_count() * fa_fwd_resident<64, true>();
   const int64_t grid = bh * ((T + kBlock - 1) / kBlock);
-  return (T <= 512 && grid <= slots) ? 64 : kBlock;
+  return (grid <= 2 * slots || (T <= 1024 && grid <= 4 * slots)) ? 64 : kBlock;
 }
 
 template <int DP, bool C, bool VEC>
@@ -1633,11 +1641,11 @@ struct BwdLaunch {
   // recomputing P and dP.
   static int run_dq(const BwdArgs& a) {
     const int nb = (a.T + kBlock - 1) / kBlock;
-    if constexpr (DP == 64) {
+    if constexpr (DP == 64 && VEC) {
       const int64_t nb2 = (a.T + 2 * kTile - 1) / (2 * kTile);
-      if (a.dS && a.key_block == 64 && nb2 * a.BH * kFaThreads <= (int64_t)UINT32_MAX) {
-        flash_bwd_dq_ds_pair_kernel<DP, C, VEC><<<dim3((unsigned)(nb2 * a.BH)), dim3(kFaThreads), 0, a.st>>>(
-            a.k, a.dS, a.dq, a.T, a.d, a.H, (int)nb2, a.BH, a.scale);
+      if (a.dS && a.key_block == 64 && a.d == DP && nb2 * a.BH * kFaThreads <= (int64_t)UINT32_MAX) {
+        flash_bwd_dq_ds_pair_kernel<DP, C><<<dim3((unsigned)(nb2 * a.BH)), dim3(kFaThreads), 0, a.st>>>(
+            a.k, a.dS, a.dq, a.T, a.H, (int)nb2, a.BH, a.scale);
         return launch_status();
       }
     }

@@ -282,9 +282,10 @@ int aar_flash_bwd_strided_f32(const float* q, const float* k, const float* v,
  * process (64 or 128; 0 restores the plan; head dims above 64 always take
  * 128); backward calls running on other threads meanwhile may see either.
  * aar_flash_fwd_query_block: queries per forward workgroup, 64 (the paired
- * kernel: two key phases per query tile, for short causal sequences whose
- * 128-query grid is one round) or 128; when it is 64 the forward does not
- * split and aar_flash_fwd_plan's count does not apply.
+ * kernel: two key phases per query tile, for causal grids of up to two
+ * rounds of resident 128-query workgroups, four when T <= 1024) or 128; when
+ * it is 64 the forward does not split and aar_flash_fwd_plan's count does not
+ * apply.
  * aar_flash_set_fwd_query_block forces it likewise (64 or 128; 0 restores
  * the plan; only causal d = 64 with 128-bit operands can take 64). */
 int aar_flash_fwd_plan(int64_t bh, int64_t T, int64_t d, int causal, int vec, size_t workspace_bytes,

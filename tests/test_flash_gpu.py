@@ -490,13 +490,15 @@ def test_flash_plans(gpu):
         assert (out.value > 0) == want_split, (bh, T, out.value)
         assert L.aar_flash_fwd_plan(bh, T, 64, 1, 1, 0, ctypes.byref(out)) == 0 and out.value == 0
         assert L.aar_flash_fwd_plan(bh, T, 64, 0, 1, wsb, ctypes.byref(out)) == 0 and out.value == 0
-    # forward query blocks: the paired 64-query kernel for short causal d = 64 grids of one round
+    # forward query blocks: the paired 64-query kernel for causal d = 64 grids of up
+    # to two rounds of 128-query workgroups (four for T <= 1024)
     assert _fwd_qb(L, 384, 256, 64, True) == 64      # the GPT step's attention
     assert _fwd_qb(L, 8, 100, 64, True) == 64
     assert _fwd_qb(L, 8, 512, 48, True) == 128       # the paired kernel's DMA layout is d = 64 exactly
-    assert _fwd_qb(L, 96, 1024, 64, True) == 128     # longer sequences split the key range instead
-    assert _fwd_qb(L, 96, 4096, 64, True) == 128
-    assert _fwd_qb(L, 4096, 256, 64, True) == 128    # several rounds of 128-query workgroups
+    assert _fwd_qb(L, 96, 1024, 64, True) == 64      # BASELINE config 4, T = 1024
+    assert _fwd_qb(L, 12, 4096, 64, True) == 64
+    assert _fwd_qb(L, 96, 4096, 64, True) == 128     # four rounds at T = 4096
+    assert _fwd_qb(L, 4096, 256, 64, True) == 128    # many rounds of 128-query workgroups
     assert _fwd_qb(L, 8, 256, 64, False) == 128
     for d in (32, 48, 63, 100, 128):
         assert _fwd_qb(L, 8, 256, d, True) == 128
