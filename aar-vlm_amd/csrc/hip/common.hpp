@@ -130,6 +130,23 @@ __device__ __forceinline__ void dma4_untracked(const void* g, lds_void_t* lds) {
 #endif
 }
 
+// The untracked DMAs with a wave-uniform 64-bit base in SGPRs and a 32-bit
+// per-lane byte offset (the global "saddr" form): a loop that walks tiles
+// moves only the scalar base, so issuing costs no vector arithmetic.
+__device__ __forceinline__ void dma16_untracked_s(uint32_t lane_off, const void* base, lds_void_t* lds) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  const unsigned m0 = __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)lds);
+  asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(lane_off), "s"(base), "{m0}"(m0) : "memory");
+#endif
+}
+
+__device__ __forceinline__ void dma4_untracked_s(uint32_t lane_off, const void* base, lds_void_t* lds) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  const unsigned m0 = __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)lds);
+  asm volatile("global_load_lds_dword %0, %1" ::"v"(lane_off), "s"(base), "{m0}"(m0) : "memory");
+#endif
+}
+
 // s_waitcnt vmcnt(N) lgkmcnt(0) (expcnt untouched): this wave's DMAs and
 // loads but the last N are done, and its LDS accesses are complete.
 template <int N>

@@ -436,15 +436,45 @@ struct FaDmaTile64 {
   static constexpr int kFloats = kTile * 64;
   static constexpr int kPerWave = kTile * kGroups / (kWave * 4);  // 2 DMA instructions per wave (4 waves)
 
-  __device__ __forceinline__ static void issue(const float* __restrict__ base, int64_t st, int row0, int T,
-                                               float* stage, int wave, int lane) {
+  // One operand as a wave stages it: the head's row 0 and row stride, and
+  // the byte offset of each of the wave's DMA lanes within a tile.  `wave`
+  // must be wave-uniform to the compiler (readfirstlane), so tile bases and
+  // LDS addresses stay scalar.
+  struct Src {
+    const float* base;
+    int64_t st;
+    uint32_t off[kPerWave];
+    bool small;  // 31 rows of stride st fit the 32-bit lane offsets
+  };
+  __device__ __forceinline__ static int lane_row(int wave, int i, int lane) {
+    return ((wave * kPerWave + i) * kWave + lane) / kGroups;
+  }
+  __device__ __forceinline__ static int lane_col(int wave, int i, int lane) {
+    const int u = (wave * kPerWave + i) * kWave + lane;
+    return ((u % kGroups) ^ ((u / kGroups) & 15)) * 4;
+  }
+  __device__ __forceinline__ static Src src(const float* __restrict__ base, int64_t st, int wave, int lane) {
+    Src s{base, st, {}, st < (int64_t(1) << 25)};
 #pragma unroll
-    for (int i = 0; i < kPerWave; ++i) {
-      const int u = (wave * kPerWave + i) * kWave + lane;
-      const int r = u / kGroups;
-      const int g = (u % kGroups) ^ (r & 15);
-      const int row = min(row0 + r, T - 1);
-      dma16_untracked(base + (int64_t)row * st + g * 4, (lds_void_t*)(stage + (wave * kPerWave + i) * kWave * 4));
+    for (int i = 0; i < kPerWave; ++i)
+      s.off[i] = (uint32_t)((lane_row(wave, i, lane) * st + lane_col(wave, i, lane)) * 4);
+    return s;
+  }
+  // Stages rows row0 .. row0 + 31 of `s`.  A tile inside [0, T) takes the
+  // scalar-base form; one that crosses T clamps its rows onto T - 1.
+  __device__ __forceinline__ static void issue(const Src& s, int row0, int T, float* stage, int wave, int lane) {
+    if (row0 + kTile <= T && s.small) {
+      const float* tile = s.base + (int64_t)row0 * s.st;
+#pragma unroll
+      for (int i = 0; i < kPerWave; ++i)
+        dma16_untracked_s(s.off[i], tile, (lds_void_t*)(stage + (wave * kPerWave + i) * kWave * 4));
+    } else {
+#pragma unroll
+      for (int i = 0; i < kPerWave; ++i) {
+        const int row = min(row0 + lane_row(wave, i, lane), T - 1);
+        dma16_untracked(s.base + (int64_t)row * s.st + lane_col(wave, i, lane),
+                        (lds_void_t*)(stage + (wave * kPerWave + i) * kWave * 4));
+      }
     }
   }
   // float4 group `grp` of row `row`
@@ -492,7 +522,8 @@ flash_fwd_pair_kernel(FaIn Qv, FaIn Kv, FaIn Vv, FaOut Ov, float* __restrict__ L
   __shared__ __attribute__((aligned(16))) float vs[2][2][Tile::kFloats];
   static_assert(2 * kHand <= 4 * Tile::kFloats, "phase hand-over fits in the K staging buffers");
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform to the compiler
   const int lr = lane & 31, h = lane >> 5;
   const int qt_local = wave & 1;  // query tile of this wave
   const int phase = wave >> 1;    // key tile t + phase of each staged pair
@@ -582,11 +613,12 @@ flash_fwd_pair_kernel(FaIn Qv, FaIn Kv, FaIn Vv, FaOut Ov, float* __restrict__ L
     }
   };
 
+  const Tile::Src ksrc = Tile::src(K, Kv.st, wave, lane), vsrc = Tile::src(V, Vv.st, wave, lane);
   auto issue_tiles = [&](int t, int buf) {
 #pragma unroll
     for (int p = 0; p < 2; ++p) {
-      Tile::issue(K, Kv.st, (t + p) * kTile, T, ks[buf][p], wave, lane);
-      Tile::issue(V, Vv.st, (t + p) * kTile, T, vs[buf][p], wave, lane);
+      Tile::issue(ksrc, (t + p) * kTile, T, ks[buf][p], wave, lane);
+      Tile::issue(vsrc, (t + p) * kTile, T, vs[buf][p], wave, lane);
     }
   };
   issue_tiles(0, 0);
@@ -900,7 +932,8 @@ flash_bwd_dkdv_pair_kernel(FaIn Qv, FaIn Kv, FaIn Vv, FaIn dOv, const float* __r
   static_assert(2 * kTile == kWave, "one 4-byte DMA per staged statistic");
   static_assert(Tile::kFloats >= NB * 16 * kWave, "phase hand-over of one key tile fits in one staged tile");
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform to the compiler
   const int lr = lane & 31, h = lane >> 5;
   const int kt_local = wave & 1;  // key tile of this wave
   const int phase = wave >> 1;    // query tile t + phase of each staged pair
@@ -940,16 +973,24 @@ flash_bwd_dkdv_pair_kernel(FaIn Qv, FaIn Kv, FaIn Vv, FaIn dOv, const float* __r
   // (two instructions per wave each), and the raw lse and D of the 64 rows
   // (one 4-byte-per-lane instruction each, waves 0 and 1; rows past T read
   // row T - 1 and are masked where P is formed).  No staging registers.
+  const Tile::Src qsrc = Tile::src(Q, Qv.st, wave, lane), dosrc = Tile::src(dO, dOv.st, wave, lane);
   auto issue_tiles = [&](int t, int buf) {
 #pragma unroll
     for (int p = 0; p < 2; ++p) {
-      Tile::issue(Q, Qv.st, (t + p) * kTile, T, qs[buf][p], wave, lane);
-      Tile::issue(dO, dOv.st, (t + p) * kTile, T, dos[buf][p], wave, lane);
+      Tile::issue(qsrc, (t + p) * kTile, T, qs[buf][p], wave, lane);
+      Tile::issue(dosrc, (t + p) * kTile, T, dos[buf][p], wave, lane);
     }
     // __lane_id() recomputes the lane index here (kept live, it would be
     // spilled, and its reload would wait for every DMA in flight)
-    if (wave == 0) dma4_untracked(Lb + min(t * kTile + (int)__lane_id(), T - 1), (lds_void_t*)ls[buf]);
-    if (wave == 1) dma4_untracked(Db + min(t * kTile + (int)__lane_id(), T - 1), (lds_void_t*)dsum[buf]);
+    if (wave < 2) {
+      const float* stat = wave == 0 ? Lb : Db;
+      float* dst = wave == 0 ? ls[buf] : dsum[buf];
+      if (t * kTile + kWave <= T) {
+        dma4_untracked_s(__lane_id() * 4, stat + t * kTile, (lds_void_t*)dst);
+      } else {
+        dma4_untracked(stat + min(t * kTile + (int)__lane_id(), T - 1), (lds_void_t*)dst);
+      }
+    }
   };
   // Lane offset of the column reads for st % 4 == 0; the one for st % 4 == k
   // is col_off ^ (k << 2) (see FaDmaTile64::lane_off: the XOR only touches
@@ -1292,7 +1333,8 @@ flash_bwd_dq_ds_pair_kernel(FaIn Kv, const float* __restrict__ dS, FaOut dQv, in
   __shared__ __attribute__((aligned(16))) float ks[2][2][Tile::kFloats];  // key tiles t, t+1 of a stage
   static_assert(2 * NB * 16 * kWave <= 4 * Tile::kFloats, "phase hand-over fits in the staging buffers");
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform to the compiler
   const int lr = lane & 31, h = lane >> 5;
   const int qt_local = wave & 1;  // query tile of this wave
   const int phase = wave >> 1;    // key tile t + phase of each staged pair
@@ -1320,9 +1362,10 @@ flash_bwd_dq_ds_pair_kernel(FaIn Kv, const float* __restrict__ dS, FaOut dQv, in
 #pragma unroll
     for (int st = 0; st < 16; ++st) r[st] = tile[(8 * (st >> 2) + (st & 3)) * kTile];
   };
+  const Tile::Src ksrc = Tile::src(K, Kv.st, wave, lane);
   auto issue_tiles = [&](int t, int buf) {
 #pragma unroll
-    for (int p = 0; p < 2; ++p) Tile::issue(K, Kv.st, (t + p) * kTile, T, ks[buf][p], wave, lane);
+    for (int p = 0; p < 2; ++p) Tile::issue(ksrc, (t + p) * kTile, T, ks[buf][p], wave, lane);
   };
   // Lane offset of the K column reads for st % 4 == 0 (st % 4 == k: XOR k << 2).
   const int col_off = Tile::lane_off(0, lr, h);
