@@ -498,7 +498,12 @@ struct FaDmaTile64 {
 // 128-query grid is about one round of resident workgroups and its longest
 // items (the last query block, every key tile in turn) set the time: four
 // waves as 2 query tiles x 2 key phases.  Each iteration stages key tiles t
-// and t + 1 of K and V by DMA (FaDmaTile64, double-buffered); wave (a, p)
+// and t + 1 of K and V by DMA (FaDmaTile64).  STAGES = 2 double-buffers
+// them (64 KB, two workgroups per CU: the next pair's DMA runs under this
+// pair's MFMA work); STAGES = 1 stages a pair after the previous one is
+// consumed (32 KB, three workgroups per CU that cover each other's DMA
+// latency), which is faster for short workgroups (T = 256: -6 %) and slower
+// for long ones (T = 4096: +9 %).  Wave (a, p)
 // runs the online softmax of query tile a over key tile t + p, so the two
 // phases of a query tile split its key range and the longest chain of tiles
 // is half that of the 128-query kernel.  S^T takes 128-bit K row reads; O +=
@@ -508,8 +513,8 @@ struct FaDmaTile64 {
 // fixed order (m = max(m0, m1), w_p = 2^(m_p - m), l = w0 l0 + w1 l1,
 // O = w0 O0 + w1 O1; deterministic), normalises and stores O and lse.
 // Requires d == DP == 64 and 16-byte aligned rows.
-template <int DP, bool CAUSAL>
-__global__ void __launch_bounds__(kFaThreads, 2)
+template <int DP, bool CAUSAL, int STAGES>
+__global__ void __launch_bounds__(kFaThreads, STAGES == 1 ? 3 : 2)
 flash_fwd_pair_kernel(FaIn Qv, FaIn Kv, FaIn Vv, FaOut Ov, float* __restrict__ Lse, int T, int H, int nqb,
                       int BH, float scale_log2) {
   static_assert(DP == 64, "the paired forward is built for head dim 64");
@@ -518,9 +523,10 @@ flash_fwd_pair_kernel(FaIn Qv, FaIn Kv, FaIn Vv, FaOut Ov, float* __restrict__ L
   constexpr int kQueries = 2 * kTile;           // queries per workgroup
   constexpr int kHand = (NB * 16 + 2) * kWave;  // one wave's O, m and l, lane-major
   using Tile = FaDmaTile64;
-  __shared__ __attribute__((aligned(16))) float ks[2][2][Tile::kFloats];
-  __shared__ __attribute__((aligned(16))) float vs[2][2][Tile::kFloats];
-  static_assert(2 * kHand <= 4 * Tile::kFloats, "phase hand-over fits in the K staging buffers");
+  static_assert(STAGES == 1 || STAGES == 2, "one or two staged tile pairs");
+  __shared__ __attribute__((aligned(16))) float ks[STAGES][2][Tile::kFloats];  // key tiles t, t + 1
+  __shared__ __attribute__((aligned(16))) float vs[STAGES][2][Tile::kFloats];
+  static_assert(kHand <= 2 * Tile::kFloats, "a query tile's hand-over fits in one stage's K (or V) tiles");
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform to the compiler
@@ -626,19 +632,28 @@ flash_fwd_pair_kernel(FaIn Qv, FaIn Kv, FaIn Vv, FaOut Ov, float* __restrict__ L
   ring_barrier();
 
   for (int t = 0; t < ntiles; t += 2) {
-    const int cur = (t >> 1) & 1;
-    if (t + 2 < ntiles) issue_tiles(t + 2, cur ^ 1);
+    const int cur = STAGES == 2 ? (t >> 1) & 1 : 0;
+    if (STAGES == 2 && t + 2 < ntiles) issue_tiles(t + 2, cur ^ 1);
     if (t + phase <= wlast) soft_pv(qk(ks[cur][phase]), vs[cur][phase], (t + phase) * kTile);
-    // This wave's DMAs for the next pair have landed, and (after the
-    // barrier) every wave's have and every read of this pair is done.
+    if (t + 2 >= ntiles) break;
+    if (STAGES == 1) {
+      // every read of this pair is done before the next pair lands in the
+      // same buffers
+      ring_barrier();
+      issue_tiles(t + 2, 0);
+    }
+    // the next pair's DMAs have landed before any wave reads them (two
+    // stages: and every read of this pair is done before the pair after
+    // next is issued into its buffers)
     wait_vm_lgkm0<0>();
     ring_barrier();
   }
+  __syncthreads();
 
   // Phase 1 hands (O, m, l) of its query tile to phase 0 (every wave is past
-  // the loop's last barrier and no DMA is in flight, so the K buffers are
-  // free).
-  float* const hs = &ks[0][0][0] + qt_local * kHand;
+  // the loop's last read of the staged tiles and no DMA is in flight):
+  // query tile 0 through the K tiles, query tile 1 through V.
+  float* const hs = qt_local == 0 ? &ks[0][0][0] : &vs[0][0][0];
   if (phase == 1) {
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
@@ -1563,8 +1578,13 @@ struct FwdLaunch {
       const int64_t nqb64 = (a.T + 2 * kTile - 1) / (2 * kTile);
       // (a dispatch holds the grid as a 32-bit work-item count)
       if (fa_fwd_query_block(a.BH, a.T, a.d, true, true) == 64 && nqb64 * a.BH * kFaThreads <= (int64_t)UINT32_MAX) {
-        flash_fwd_pair_kernel<DP, C><<<dim3((unsigned)(nqb64 * a.BH)), dim3(kFaThreads), 0, a.st>>>(
-            a.q, a.k, a.v, a.o, a.lse, a.T, a.H, (int)nqb64, a.BH, a.scale * kLog2e);
+        if (a.T <= 1024) {
+          flash_fwd_pair_kernel<DP, C, 1><<<dim3((unsigned)(nqb64 * a.BH)), dim3(kFaThreads), 0, a.st>>>(
+              a.q, a.k, a.v, a.o, a.lse, a.T, a.H, (int)nqb64, a.BH, a.scale * kLog2e);
+        } else {
+          flash_fwd_pair_kernel<DP, C, 2><<<dim3((unsigned)(nqb64 * a.BH)), dim3(kFaThreads), 0, a.st>>>(
+              a.q, a.k, a.v, a.o, a.lse, a.T, a.H, (int)nqb64, a.BH, a.scale * kLog2e);
+        }
         return launch_status();
       }
     }

@@ -520,12 +520,13 @@ def test_flash_plans(gpu):
 @pytest.mark.parametrize("query_block", [64, 128])
 @pytest.mark.parametrize("bh,T,d", [(3, 77, 64), (1, 1, 64), (2, 33, 64), (2, 257, 64), (4, 64, 64),
                                     (2, 130, 48), (5, 31, 64), (3, 200, 64), (1, 511, 64), (2, 96, 64),
-                                    (2, 448, 64), (1, 320, 64)])
+                                    (2, 448, 64), (1, 320, 64), (1, 1100, 64), (1, 2051, 64)])
 def test_fwd_query_blocks_vs_oracle(gpu, query_block, bh, T, d):
     """Both causal forward decompositions (forced) against the oracle: O and
     lse, then the backward through the forward's lse.  The paired kernel
     merges two key phases per query tile in a fixed order, so a rerun is bit
-    identical."""
+    identical.  T > 1024 takes its double-buffered form, T <= 1024 the
+    single-stage one."""
     L = _flash_plans()
     rng = np.random.default_rng(bh * 131 + T + d + query_block)
     q, k, v, do = (rng.standard_normal((bh, T, d)).astype(f32) for _ in range(4))
