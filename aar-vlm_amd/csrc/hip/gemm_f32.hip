@@ -560,6 +560,144 @@ gemm_f32_dma_kernel(const float* __restrict__ A, const float* __restrict__ B, fl
   store_tile<TM, TN, EPI>(acc, C, ep, M, N, ldc, m0 + wm0, n0 + wn0, lr, h);
 }
 
+// ------------------------------------------------------------ thin outputs
+// C[M, N] with N <= 128 and a short contraction (16 <= K <= 512, K % 16 == 0):
+// tall-skinny products such as a vocabulary head (16384 tokens x 65 classes
+// x 384).  The tile configurations waste most of their work there: a 64-wide
+// tile leaves a one-column remainder tile, and B's rows (N floats) are not
+// 16-byte aligned for NN/TN.  Instead a 16-wave workgroup holds all of B,
+// padded to NC = 16*NB columns, in LDS, staged by untracked 4-byte (NN/TN) or
+// 16-byte (NT) DMAs, and its 64 rows of A stream HBM -> registers.  Waves are
+// 4 row slabs x 4 K parts; a wave computes 16 rows x NC columns of its K
+// part with v_mfma_f32_16x16x4f32: in each 16-deep k block, lane (i, q)
+// supplies A[row i][4q .. 4q+3] as four consecutive k steps (one 128-bit
+// load), and B the same four k values of column 16*nb + i.  The four parts
+// of a slab are summed through LDS in a fixed order (deterministic).  Rows
+// past M are clamped onto row M - 1 and columns past N onto column N - 1;
+// both feed only outputs that are not stored.
+//   NN, TN: B is [K][N]; LDS holds it as [k][c], row stride NC + 4 (the
+//           four k rows of one 32-bit read land 16 banks apart).
+//   NT:     B is [N][K]; LDS holds it row for row as [c][k], row stride K + 4
+//           (128-bit reads of 16 consecutive columns are conflict free).
+constexpr int kThinThreads = 1024;
+constexpr int kThinSlabs = 4, kThinParts = 4;
+constexpr int kThinRows = 16 * kThinSlabs;  // rows per workgroup
+constexpr int kThinMaxKb = 8;               // 16-deep k blocks per part: K <= 512
+constexpr int kThinLds = 32768;             // floats of LDS (128 KB)
+
+__host__ __device__ constexpr int thin_ld_kn(int nb) { return 16 * nb + 4; }
+
+template <int NB, int OP>
+__global__ void __launch_bounds__(kThinThreads, 1)
+gemm_f32_thin_kernel(const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, int M,
+                     int N, int K, int64_t lda, int64_t ldb, int64_t ldc) {
+  constexpr bool kNT = OP == AAR_GEMM_NT;
+  constexpr bool kTN = OP == AAR_GEMM_TN;
+  constexpr int NC = 16 * NB;
+  constexpr int kLdKn = thin_ld_kn(NB);
+  static_assert(kThinParts * kThinSlabs * 64 == kThinThreads, "16 waves: 4 slabs x 4 K parts");
+  static_assert((kThinParts - 1) * kThinSlabs * NB * 256 <= kThinLds, "the part combine fits in LDS");
+  __shared__ __attribute__((aligned(16))) float lds[kThinLds];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int slab = wave % kThinSlabs, part = wave / kThinSlabs;
+  const int li = lane & 15, lq = lane >> 4;
+  const int kpart = (K / 16 + kThinParts - 1) / kThinParts * 16;
+  const int kbase = part * kpart;
+  const int nkb = max(0, min(K - kbase, kpart)) / 16;
+  const int ldk = kNT ? K + 4 : kLdKn;
+
+  // A fragments first, so their HBM latency overlaps the staging of B.
+  const int64_t row = min((int64_t)blockIdx.x * kThinRows + slab * 16 + li, (int64_t)M - 1);
+  f32x4 a[kThinMaxKb];
+#pragma unroll
+  for (int i = 0; i < kThinMaxKb; ++i) {
+    if (i < nkb) {
+      const int k = kbase + 16 * i + 4 * lq;
+      if constexpr (kTN) {
+        a[i] = f32x4{A[(int64_t)k * lda + row], A[(int64_t)(k + 1) * lda + row], A[(int64_t)(k + 2) * lda + row],
+                     A[(int64_t)(k + 3) * lda + row]};
+      } else {
+        a[i] = *reinterpret_cast<const f32x4*>(A + row * lda + k);
+      }
+    }
+  }
+
+  if constexpr (kNT) {
+    for (int c = wave; c < NC; c += kThinThreads / 64) {
+      const float* src = B + (int64_t)min(c, N - 1) * ldb;
+      float* dst = lds + c * ldk;
+      for (int k0 = 0; k0 < K; k0 += 256) {
+        if (lane * 4 < K - k0) dma16_untracked_s(lane * 16, src + k0, (lds_void_t*)(dst + k0));
+      }
+    }
+  } else {
+    for (int k = wave; k < K; k += kThinThreads / 64) {
+      const float* src = B + (int64_t)k * ldb;
+      float* dst = lds + k * kLdKn;
+      if (lane < NC) dma4_untracked_s(min(lane, N - 1) * 4, src, (lds_void_t*)dst);
+      if (NC > 64 && lane < NC - 64) dma4_untracked_s(min(64 + lane, N - 1) * 4, src, (lds_void_t*)(dst + 64));
+    }
+  }
+  wait_vm_lgkm0<0>();
+  __syncthreads();
+
+  f32x4 acc[NB];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) acc[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < kThinMaxKb; ++i) {
+    if (i < nkb) {
+      const int k = kbase + 16 * i + 4 * lq;
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        f32x4 b;
+        if constexpr (kNT) {
+          b = *reinterpret_cast<const f32x4*>(lds + (16 * nb + li) * ldk + k);
+        } else {
+          const float* col = lds + k * kLdKn + 16 * nb + li;
+          b = f32x4{col[0], col[kLdKn], col[2 * kLdKn], col[3 * kLdKn]};
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[nb] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i][j], b[j], acc[nb], 0, 0, 0);
+      }
+    }
+  }
+
+  // Parts 1..3 hand their sums to part 0 through LDS (B is no longer read),
+  // which adds them in part order.  Accumulator layout of a 16x16 block:
+  // lane (i, q), register r holds row 4q + r, column i.
+  __syncthreads();
+  float* const hand = lds + slab * NB * 256;
+  constexpr int kPartStride = kThinSlabs * NB * 256;
+  if (part > 0) {
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+      *reinterpret_cast<f32x4*>(hand + (part - 1) * kPartStride + nb * 256 + lane * 4) = acc[nb];
+  }
+  __syncthreads();
+  if (part > 0) return;
+#pragma unroll
+  for (int p = 1; p < kThinParts; ++p) {
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      const f32x4 v = *reinterpret_cast<const f32x4*>(hand + (p - 1) * kPartStride + nb * 256 + lane * 4);
+      acc[nb] += v;
+    }
+  }
+  const int64_t r0 = (int64_t)blockIdx.x * kThinRows + slab * 16 + 4 * lq;
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) {
+    const int col = 16 * nb + li;
+    if (col >= N) continue;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      if (r0 + r < M) C[(r0 + r) * ldc + col] = acc[nb][r];
+    }
+  }
+}
+
 // C[i] = sum_s W[s*stride + i], s in order 0..splits-1 (deterministic), four
 // consecutive outputs per thread with 128-bit loads (stride % 4 == 0 and
 // 16-byte aligned W/C); the split loop is unrolled so its loads overlap.
@@ -659,7 +797,37 @@ int64_t split_chunk(int64_t K, int splits, int bk) { return ceil_div(ceil_div(K,
 // of the GPT step plus a held-out shape set; the split counts tried are the
 // measured ones.
 constexpr int kPlanSplits[] = {1, 2, 3, 4, 6, 8, 12, 16, 24, 32};
-Plan plan_gemm(int op, int64_t M, int64_t N, int64_t K, size_t ws_bytes, bool allow_split, int64_t batch = 1) {
+
+// The thin-output kernel (gemm_f32_thin_kernel) has configuration id
+// kThinCfg, past the tile configurations.  thin_shape_ok: the shapes it
+// runs (B padded to 16-column blocks fits in its LDS); thin_operands_ok: the
+// alignment its 128-bit A loads and (NT) 16-byte B DMAs need.
+constexpr int kThinCfg = kNumCfgs;
+bool thin_shape_ok(int op, int64_t M, int64_t N, int64_t K) {
+  if (M < 1 || N < 1 || N > 128 || K < 16 || K > 16 * kThinMaxKb * kThinParts || K % 16 != 0) return false;
+  const int64_t nb = ceil_div(N, (int64_t)16);
+  const int64_t lds = op == AAR_GEMM_NT ? 16 * nb * (K + 4) : K * thin_ld_kn((int)nb);
+  return lds <= kThinLds && ceil_div(M, (int64_t)kThinRows) * kThinThreads <= (int64_t)UINT32_MAX;
+}
+bool thin_operands_ok(int op, const float* A, const float* B, int64_t lda, int64_t ldb) {
+  if (op != AAR_GEMM_TN && (!aligned16(A) || lda % 4 != 0)) return false;
+  if (op == AAR_GEMM_NT && (!aligned16(B) || ldb % 4 != 0)) return false;
+  return true;
+}
+// Where the thin kernel is planned.  Measured on MI355X (time against the
+// best tile configuration and split): at M = 16384, NN/TN 0.51-0.55 for
+// N = 65, K = 384 (the vocabulary head), 0.56-0.68 for N = 16, 0.77-0.83
+// for N = 96, 0.97-0.99 for N = 128; NT 0.93 at N = 65, 1.00 at N = 96, 1.18
+// at N = 128; M = 65536 0.77 (NN/TN); at M = 4096 (64 workgroups) it loses
+// (1.07-1.35).  A workgroup takes a fixed ~5 us of staging on top of its
+// MFMA work, so it needs rows enough to spread over most CUs.
+bool thin_plan_wins(int op, int64_t M, int64_t N, int64_t K) {
+  return M >= 8192 && K >= 64 && N <= (op == AAR_GEMM_NT ? 80 : 96);
+}
+
+Plan plan_gemm(int op, int64_t M, int64_t N, int64_t K, size_t ws_bytes, bool allow_split, int64_t batch = 1,
+               bool allow_thin = false) {
+  if (allow_thin && batch == 1 && thin_shape_ok(op, M, N, K) && thin_plan_wins(op, M, N, K)) return Plan{kThinCfg, 1, K};
   const int cus = device_cu_count();
   const double cu_flops = 157.3e12 / 256;  // fp32 MFMA FLOP/s per CU
   Plan best{3, 1, K};
@@ -805,6 +973,42 @@ int dispatch_op(int op, int cfg, bool vec, const float* A, const float* B, float
   }
 }
 
+template <int OP>
+int launch_thin(const float* A, const float* B, float* C, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb,
+                int64_t ldc, hipStream_t st) {
+  const dim3 grid((unsigned)ceil_div(M, (int64_t)kThinRows));
+  switch (ceil_div(N, (int64_t)16)) {
+#define AAR_THIN_NB(NBV)                                                                                  \
+  case NBV:                                                                                               \
+    gemm_f32_thin_kernel<NBV, OP><<<grid, dim3(kThinThreads), 0, st>>>(A, B, C, (int)M, (int)N, (int)K, lda, \
+                                                                       ldb, ldc);                         \
+    return launch_status();
+    AAR_THIN_NB(1)
+    AAR_THIN_NB(2)
+    AAR_THIN_NB(3)
+    AAR_THIN_NB(4)
+    AAR_THIN_NB(5)
+    AAR_THIN_NB(6)
+    AAR_THIN_NB(7)
+    AAR_THIN_NB(8)
+#undef AAR_THIN_NB
+    default:
+      return AAR_EUNSUPPORTED;
+  }
+}
+
+// The thin-output kernel on contiguous operands (no epilogue, no split).
+int run_thin(int op, int64_t M, int64_t N, int64_t K, const float* A, const float* B, float* C, hipStream_t st) {
+  int64_t lda, ldb;
+  default_ld(op, M, N, K, lda, ldb);
+  if (!thin_shape_ok(op, M, N, K) || !thin_operands_ok(op, A, B, lda, ldb)) return AAR_EUNSUPPORTED;
+  switch (op) {
+    case AAR_GEMM_NN: return launch_thin<AAR_GEMM_NN>(A, B, C, M, N, K, lda, ldb, N, st);
+    case AAR_GEMM_NT: return launch_thin<AAR_GEMM_NT>(A, B, C, M, N, K, lda, ldb, N, st);
+    default: return launch_thin<AAR_GEMM_TN>(A, B, C, M, N, K, lda, ldb, N, st);
+  }
+}
+
 // epi / ep: the epilogue (kEpi*), applied in an unsplit launch or after the
 // split-K reduction.  C is contiguous (ldc = N), and so is ep.aux.
 int run_gemm(int op, int64_t M, int64_t N, int64_t K, const float* A, const float* B, float* C,
@@ -853,7 +1057,7 @@ using namespace aar;
 
 extern "C" size_t aar_gemm_f32_workspace_bytes(int op, int64_t M, int64_t N, int64_t K) {
   if (op < 0 || op > 2 || M <= 0 || N <= 0 || K <= 0) return 0;
-  const Plan p = plan_gemm(op, M, N, K, (size_t)-1, true);
+  const Plan p = plan_gemm(op, M, N, K, (size_t)-1, true, 1, true);
   if (p.splits <= 1) return 0;
   return (size_t)p.splits * (size_t)M * (size_t)N * sizeof(float);
 }
@@ -862,7 +1066,11 @@ extern "C" int aar_gemm_f32(int op, int64_t M, int64_t N, int64_t K, const float
                             float* C, void* workspace, size_t workspace_bytes, void* stream) {
   const int chk = check_gemm_args(op, M, N, K, A, B, C, stream);
   if (chk != AAR_OK) return chk == 1 ? AAR_OK : chk;
-  const Plan p = plan_gemm(op, M, N, K, workspace ? workspace_bytes : 0, workspace != nullptr);
+  int64_t lda, ldb;
+  default_ld(op, M, N, K, lda, ldb);
+  const Plan p = plan_gemm(op, M, N, K, workspace ? workspace_bytes : 0, workspace != nullptr, 1,
+                           thin_operands_ok(op, A, B, lda, ldb));
+  if (p.cfg == kThinCfg) return run_thin(op, M, N, K, A, B, C, as_stream(stream));
   return run_gemm(op, M, N, K, A, B, C, workspace, p, as_stream(stream));
 }
 
@@ -916,7 +1124,7 @@ extern "C" int aar_gemm_f32_tile_config(int config, int* tile_m, int* tile_n, in
 extern "C" int aar_gemm_f32_plan(int op, int64_t M, int64_t N, int64_t K, size_t workspace_bytes,
                                  int* config, int* splits) {
   if (op < 0 || op > 2 || M <= 0 || N <= 0 || K <= 0) return AAR_EINVAL;
-  const Plan p = plan_gemm(op, M, N, K, workspace_bytes, workspace_bytes > 0);
+  const Plan p = plan_gemm(op, M, N, K, workspace_bytes, workspace_bytes > 0, 1, true);
   if (config) *config = p.cfg;
   if (splits) *splits = p.splits;
   return AAR_OK;
@@ -925,9 +1133,11 @@ extern "C" int aar_gemm_f32_plan(int op, int64_t M, int64_t N, int64_t K, size_t
 extern "C" int aar_gemm_f32_with_config(int op, int64_t M, int64_t N, int64_t K, const float* A,
                                         const float* B, float* C, void* workspace, size_t workspace_bytes,
                                         int config, int splits, void* stream) {
-  if (config < 0 || config >= kNumCfgs || splits < 1 || splits > kMaxSplits) return AAR_EINVAL;
+  if (config < 0 || config > kThinCfg || splits < 1 || splits > kMaxSplits) return AAR_EINVAL;
+  if (config == kThinCfg && splits != 1) return AAR_EINVAL;
   const int chk = check_gemm_args(op, M, N, K, A, B, C, stream);
   if (chk != AAR_OK) return chk == 1 ? AAR_OK : chk;
+  if (config == kThinCfg) return run_thin(op, M, N, K, A, B, C, as_stream(stream));
   const int64_t kps = split_chunk(K, splits, kCfgs[config].bk);
   const int real_splits = (int)ceil_div(K, kps);
   if (real_splits > 1 && (!workspace || workspace_bytes < (size_t)real_splits * M * N * sizeof(float)))

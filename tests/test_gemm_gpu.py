@@ -227,6 +227,59 @@ def test_every_tile_config_vs_oracle(gpu, op):
         abi.free()
 
 
+
+@pytest.mark.parametrize("op", [0, 1, 2])
+def test_thin_output_kernel_vs_oracle(gpu, op):
+    """The thin-output kernel (configuration id = the number of tile
+    configurations), forced through aar_gemm_f32_with_config: N up to 128 in
+    1..8 column blocks of 16 with ragged N and M, K a multiple of 16 up to 512
+    (4 K parts per row slab, some of them empty), misaligned A (NN/NT) or B
+    rows (N odd).  A rerun is bit identical (fixed-order part sum); shapes
+    outside its limits return AAR_EUNSUPPORTED; the plan takes it for the
+    vocabulary head 16384 x 65 x 384 in all three layouts."""
+    name = ["nn", "nt", "tn"][op]
+    abi = Abi()
+    try:
+        thin = len(gemm_configs(abi))
+        for (M, N, K) in [(300, 65, 384), (1000, 1, 16), (777, 128, 64), (64, 17, 512), (130, 96, 336),
+                          (4097, 33, 48), (65, 80, 400), (16, 16, 32)]:
+            if op == 1 and 16 * -(-N // 16) * (K + 4) > 32768:
+                continue  # B^T padded does not fit the kernel's LDS (checked below)
+            if op != 1 and K * (16 * -(-N // 16) + 4) > 32768:
+                continue
+            rng = np.random.default_rng(M * 7 + N + K + op)
+            a, b = operands(name, M, N, K, rng)
+            ref = O.matmul(name, a, b)
+            pa, pb = abi.put(a), abi.put(b)
+            outs = []
+            for _ in range(2):
+                pc = abi.empty(M * N)
+                abi.check(abi.L.aar_gemm_f32_with_config(op, M, N, K, pa, pb, pc, None, 0, thin, 1, None))
+                outs.append(abi.get(pc, (M, N)))
+            np.testing.assert_array_equal(outs[0], outs[1])
+            assert_close(outs[0], ref, gemm_tol(K), f"{name} thin {(M, N, K)}")
+        p = abi.alloc(4 << 20)
+        for (M, N, K) in [(256, 129, 64), (256, 64, 100), (256, 64, 528), (256, 64, 8)]:
+            assert abi.L.aar_gemm_f32_with_config(op, M, N, K, p, p, p, None, 0, thin, 1, None) == -3, (M, N, K)
+        if op == 1:  # B^T padded to 128 columns x (256 + 4) floats exceeds the 128 KB of LDS
+            assert abi.L.aar_gemm_f32_with_config(op, 256, 128, 256, p, p, p, None, 0, thin, 1, None) == -3
+        if op != 2:  # 128-bit A rows need a 16-byte aligned A
+            assert abi.L.aar_gemm_f32_with_config(op, 64, 65, 64, p + 4, p, p, None, 0, thin, 1, None) == -3
+        assert abi.L.aar_gemm_f32_with_config(op, 64, 65, 64, p, p, p, None, 0, thin, 2, None) == -1
+        cfg, sp = ctypes.c_int(-1), ctypes.c_int(-1)
+        abi.check(abi.L.aar_gemm_f32_plan(op, 16384, 65, 384, 1 << 30, ctypes.byref(cfg), ctypes.byref(sp)))
+        assert (cfg.value, sp.value) == (thin, 1)
+        # through aar_gemm_f32 with a misaligned A the plan falls back to a tile configuration
+        if op != 2:
+            rng = np.random.default_rng(5)
+            a, b = operands(name, 4096, 65, 64, rng)
+            pa, pb, pc = abi.put(a, offset_floats=1), abi.put(b), abi.empty(4096 * 65)
+            abi.check(abi.L.aar_gemm_f32(op, 4096, 65, 64, pa, pb, pc, None, 0, None))
+            assert_close(abi.get(pc, (4096, 65)), O.matmul(name, a, b), gemm_tol(64), f"{name} misaligned A")
+    finally:
+        abi.free()
+
+
 def test_plan_and_config_errors(gpu):
     abi = Abi()
     try:
@@ -235,7 +288,9 @@ def test_plan_and_config_errors(gpu):
         assert cfg.value >= 0 and sp.value == 1
         n = len(gemm_configs(abi))
         p = abi.alloc(4096)
-        assert abi.L.aar_gemm_f32_with_config(0, 8, 8, 8, p, p, p, None, 0, n, 1, None) == -1  # EINVAL
+        # id n is the thin-output kernel (K = 8 is below its 16-deep k blocks); n + 1 is invalid
+        assert abi.L.aar_gemm_f32_with_config(0, 8, 8, 8, p, p, p, None, 0, n, 1, None) == -3  # EUNSUPPORTED
+        assert abi.L.aar_gemm_f32_with_config(0, 8, 8, 8, p, p, p, None, 0, n + 1, 1, None) == -1  # EINVAL
         assert abi.L.aar_gemm_f32_with_config(0, 8, 8, 8, p, p, p, None, 0, 0, 0, None) == -1
         # a forced split needs workspace
         assert abi.L.aar_gemm_f32_with_config(0, 64, 64, 4096, p, p, p, None, 0, 0, 4, None) == -2
