@@ -587,16 +587,23 @@ constexpr int kThinLds = 32768;             // floats of LDS (128 KB)
 
 __host__ __device__ constexpr int thin_ld_kn(int nb) { return 16 * nb + 4; }
 
-template <int NB, int OP>
+// TAIL: the last column block holds 1..4 columns (N % 16 in 1..4).  Those
+// are computed with VALU FMAs from the same A fragments instead of a fifth of
+// the MFMA work (N = 65: 64 columns on MFMA, one by VALU); per lane the
+// partial dot products of its four k steps are summed over the four k lanes
+// of a row (lane ^ 16, then lane ^ 32) and over the K parts in part order.
+template <int NB, int OP, bool TAIL>
 __global__ void __launch_bounds__(kThinThreads, 1)
 gemm_f32_thin_kernel(const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, int M,
                      int N, int K, int64_t lda, int64_t ldb, int64_t ldc) {
   constexpr bool kNT = OP == AAR_GEMM_NT;
   constexpr bool kTN = OP == AAR_GEMM_TN;
   constexpr int NC = 16 * NB;
+  constexpr int NBM = TAIL ? NB - 1 : NB;  // column blocks on MFMA
+  static_assert(!TAIL || NB >= 2, "a tail follows at least one full column block");
   constexpr int kLdKn = thin_ld_kn(NB);
   static_assert(kThinParts * kThinSlabs * 64 == kThinThreads, "16 waves: 4 slabs x 4 K parts");
-  static_assert((kThinParts - 1) * kThinSlabs * NB * 256 <= kThinLds, "the part combine fits in LDS");
+  static_assert((kThinParts - 1) * kThinSlabs * (NB * 256 + 64) <= kThinLds, "the part combine fits in LDS");
   __shared__ __attribute__((aligned(16))) float lds[kThinLds];
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -646,12 +653,27 @@ gemm_f32_thin_kernel(const float* __restrict__ A, const float* __restrict__ B, f
   f32x4 acc[NB];
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) acc[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  f32x4 tail = {0.f, 0.f, 0.f, 0.f};  // tail columns 16 * NBM + t of row li, this lane's k steps
 #pragma unroll
   for (int i = 0; i < kThinMaxKb; ++i) {
     if (i < nkb) {
       const int k = kbase + 16 * i + 4 * lq;
+      if constexpr (TAIL) {
 #pragma unroll
-      for (int nb = 0; nb < NB; ++nb) {
+        for (int j = 0; j < 4; ++j) {
+          f32x4 bt;
+          if constexpr (kNT) {
+            bt = f32x4{lds[(16 * NBM) * ldk + k + j], lds[(16 * NBM + 1) * ldk + k + j],
+                       lds[(16 * NBM + 2) * ldk + k + j], lds[(16 * NBM + 3) * ldk + k + j]};
+          } else {
+            bt = *reinterpret_cast<const f32x4*>(lds + (k + j) * kLdKn + 16 * NBM);
+          }
+#pragma unroll
+          for (int t = 0; t < 4; ++t) tail[t] = fmaf(a[i][j], bt[t], tail[t]);
+        }
+      }
+#pragma unroll
+      for (int nb = 0; nb < NBM; ++nb) {
         f32x4 b;
         if constexpr (kNT) {
           b = *reinterpret_cast<const f32x4*>(lds + (16 * nb + li) * ldk + k);
@@ -668,27 +690,48 @@ gemm_f32_thin_kernel(const float* __restrict__ A, const float* __restrict__ B, f
   // Parts 1..3 hand their sums to part 0 through LDS (B is no longer read),
   // which adds them in part order.  Accumulator layout of a 16x16 block:
   // lane (i, q), register r holds row 4q + r, column i.
+  if constexpr (TAIL) {
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      tail[t] += __shfl_xor(tail[t], 16, 64);
+      tail[t] += __shfl_xor(tail[t], 32, 64);
+    }
+  }
   __syncthreads();
-  float* const hand = lds + slab * NB * 256;
-  constexpr int kPartStride = kThinSlabs * NB * 256;
+  // per part and slab: NBM accumulator blocks (256 floats each), then the
+  // tail sums of the slab's 16 rows (64 floats)
+  constexpr int kSlabFloats = NBM * 256 + (TAIL ? 64 : 0);
+  float* const hand = lds + slab * kSlabFloats;
+  constexpr int kPartStride = kThinSlabs * kSlabFloats;
   if (part > 0) {
 #pragma unroll
-    for (int nb = 0; nb < NB; ++nb)
+    for (int nb = 0; nb < NBM; ++nb)
       *reinterpret_cast<f32x4*>(hand + (part - 1) * kPartStride + nb * 256 + lane * 4) = acc[nb];
+    if (TAIL && lq == 0) *reinterpret_cast<f32x4*>(hand + (part - 1) * kPartStride + NBM * 256 + li * 4) = tail;
   }
   __syncthreads();
   if (part > 0) return;
 #pragma unroll
   for (int p = 1; p < kThinParts; ++p) {
 #pragma unroll
-    for (int nb = 0; nb < NB; ++nb) {
+    for (int nb = 0; nb < NBM; ++nb) {
       const f32x4 v = *reinterpret_cast<const f32x4*>(hand + (p - 1) * kPartStride + nb * 256 + lane * 4);
       acc[nb] += v;
+    }
+    if (TAIL) tail += *reinterpret_cast<const f32x4*>(hand + (p - 1) * kPartStride + NBM * 256 + li * 4);
+  }
+  if (TAIL && lq == 0) {
+    const int64_t trow = (int64_t)blockIdx.x * kThinRows + slab * 16 + li;
+    if (trow < M) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        if (16 * NBM + t < N) C[trow * ldc + 16 * NBM + t] = tail[t];
+      }
     }
   }
   const int64_t r0 = (int64_t)blockIdx.x * kThinRows + slab * 16 + 4 * lq;
 #pragma unroll
-  for (int nb = 0; nb < NB; ++nb) {
+  for (int nb = 0; nb < NBM; ++nb) {
     const int col = 16 * nb + li;
     if (col >= N) continue;
 #pragma unroll
@@ -977,11 +1020,19 @@ template <int OP>
 int launch_thin(const float* A, const float* B, float* C, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb,
                 int64_t ldc, hipStream_t st) {
   const dim3 grid((unsigned)ceil_div(M, (int64_t)kThinRows));
+  const bool tail = N > 16 && N % 16 >= 1 && N % 16 <= 4;
   switch (ceil_div(N, (int64_t)16)) {
-#define AAR_THIN_NB(NBV)                                                                                  \
-  case NBV:                                                                                               \
-    gemm_f32_thin_kernel<NBV, OP><<<grid, dim3(kThinThreads), 0, st>>>(A, B, C, (int)M, (int)N, (int)K, lda, \
-                                                                       ldb, ldc);                         \
+#define AAR_THIN_NB(NBV)                                                                                          \
+  case NBV:                                                                                                       \
+    if constexpr (NBV >= 2) {                                                                                     \
+      if (tail) {                                                                                                 \
+        gemm_f32_thin_kernel<NBV, OP, true><<<grid, dim3(kThinThreads), 0, st>>>(A, B, C, (int)M, (int)N, (int)K, \
+                                                                                 lda, ldb, ldc);                  \
+        return launch_status();                                                                                   \
+      }                                                                                                           \
+    }                                                                                                             \
+    gemm_f32_thin_kernel<NBV, OP, false><<<grid, dim3(kThinThreads), 0, st>>>(A, B, C, (int)M, (int)N, (int)K,    \
+                                                                              lda, ldb, ldc);                     \
     return launch_status();
     AAR_THIN_NB(1)
     AAR_THIN_NB(2)

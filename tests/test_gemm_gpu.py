@@ -232,7 +232,8 @@ def test_every_tile_config_vs_oracle(gpu, op):
 def test_thin_output_kernel_vs_oracle(gpu, op):
     """The thin-output kernel (configuration id = the number of tile
     configurations), forced through aar_gemm_f32_with_config: N up to 128 in
-    1..8 column blocks of 16 with ragged N and M, K a multiple of 16 up to 512
+    1..8 column blocks of 16 with ragged N and M (a last block of 1-4 columns
+    goes through VALU FMAs), K a multiple of 16 up to 512
     (4 K parts per row slab, some of them empty), misaligned A (NN/NT) or B
     rows (N odd).  A rerun is bit identical (fixed-order part sum); shapes
     outside its limits return AAR_EUNSUPPORTED; the plan takes it for the
@@ -241,8 +242,9 @@ def test_thin_output_kernel_vs_oracle(gpu, op):
     abi = Abi()
     try:
         thin = len(gemm_configs(abi))
+        # N % 16 in 1..4 (65, 17, 33, 50, 20) takes the VALU tail-column form
         for (M, N, K) in [(300, 65, 384), (1000, 1, 16), (777, 128, 64), (64, 17, 512), (130, 96, 336),
-                          (4097, 33, 48), (65, 80, 400), (16, 16, 32)]:
+                          (4097, 33, 48), (65, 80, 400), (16, 16, 32), (257, 50, 64), (300, 20, 128)]:
             if op == 1 and 16 * -(-N // 16) * (K + 4) > 32768:
                 continue  # B^T padded does not fit the kernel's LDS (checked below)
             if op != 1 and K * (16 * -(-N // 16) + 4) > 32768:
