@@ -723,35 +723,57 @@ flash_fwd_combine_kernel(FaSplit sp, FaOut Ov, float* __restrict__ Lse, int T, i
 
 // ------------------------------------------------------------- backward 0
 
-// D[bh*T + t] = sum_c dO[bh][t][c] * O[bh][t][c]; 16 lanes per row.  VEC
+// D[bh*T + t] = sum_c dO[bh][t][c] * O[bh][t][c]; 16 lanes per row, R
+// consecutive rows of one head per 16-lane group (R divides T).  VEC
 // (d % 4 == 0, 16-byte aligned rows): each lane takes float4 groups sub,
-// sub + 16, ... with 128-bit loads (one per operand for d <= 64), so a row
-// is two contiguous 256-byte reads; else element-wise.
-template <bool VEC>
+// sub + 16, ... with 128-bit loads, the first group of all R rows issued
+// before any is used (2R loads in flight per lane); else element-wise.
+template <bool VEC, int R>
 __global__ void __launch_bounds__(256)
 flash_bwd_dot_kernel(FaIn dOv, FaIn Ov, float* __restrict__ D, int64_t rows, int T, int H, int d) {
-  const int64_t row = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 4;
+  const int64_t row0 = (((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 4) * R;
   const int sub = threadIdx.x & 15;
-  float acc = 0.f;
-  if (row < rows) {
-    const int bh = (int)(row / T), t = (int)(row % T);
-    const float* a = dOv.head(bh, H) + (int64_t)t * dOv.st;
-    const float* b = Ov.head(bh, H) + (int64_t)t * Ov.st;
+  float acc[R];
+#pragma unroll
+  for (int i = 0; i < R; ++i) acc[i] = 0.f;
+  if (row0 < rows) {
+    const int bh = (int)(row0 / T), t0 = (int)(row0 - (int64_t)bh * T);
+    const float* a = dOv.head(bh, H) + (int64_t)t0 * dOv.st;
+    const float* b = Ov.head(bh, H) + (int64_t)t0 * Ov.st;
     if (VEC) {
-      for (int c = 4 * sub; c < d; c += 64) {
-        const f32x4 x = *reinterpret_cast<const f32x4*>(a + c);
-        const f32x4 y = *reinterpret_cast<const f32x4*>(b + c);
-        acc += x[0] * y[0] + x[1] * y[1] + x[2] * y[2] + x[3] * y[3];
+      // lanes past the row's end (d < 64) load nothing
+      const bool on = 4 * sub < d;
+      f32x4 x[R], y[R];
+#pragma unroll
+      for (int i = 0; i < R; ++i) {
+        x[i] = on ? *reinterpret_cast<const f32x4*>(a + i * dOv.st + 4 * sub) : f32x4{0.f, 0.f, 0.f, 0.f};
+        y[i] = on ? *reinterpret_cast<const f32x4*>(b + i * Ov.st + 4 * sub) : f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+#pragma unroll
+      for (int i = 0; i < R; ++i) acc[i] = x[i][0] * y[i][0] + x[i][1] * y[i][1] + x[i][2] * y[i][2] + x[i][3] * y[i][3];
+      for (int c = 4 * sub + 64; c < d; c += 64) {
+#pragma unroll
+        for (int i = 0; i < R; ++i) {
+          const f32x4 u = *reinterpret_cast<const f32x4*>(a + i * dOv.st + c);
+          const f32x4 v = *reinterpret_cast<const f32x4*>(b + i * Ov.st + c);
+          acc[i] += u[0] * v[0] + u[1] * v[1] + u[2] * v[2] + u[3] * v[3];
+        }
       }
     } else {
-      for (int c = sub; c < d; c += 16) acc += a[c] * b[c];
+#pragma unroll
+      for (int i = 0; i < R; ++i)
+        for (int c = sub; c < d; c += 16) acc[i] += a[i * dOv.st + c] * b[i * Ov.st + c];
     }
   }
-  acc += dpp_quad_xor1(acc);
-  acc += dpp_quad_xor2(acc);
-  acc += dpp_half_mirror(acc);
-  acc += dpp_row_mirror(acc);
-  if (row < rows && sub == 0) D[row] = acc;
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    float v = acc[i];
+    v += dpp_quad_xor1(v);
+    v += dpp_quad_xor2(v);
+    v += dpp_half_mirror(v);
+    v += dpp_row_mirror(v);
+    if (row0 < rows && sub == 0) D[row0 + i] = v;
+  }
 }
 
 // ------------------------------------------------------------- backward 1
@@ -1815,9 +1837,15 @@ extern "C" int aar_flash_bwd_strided_f32(const float* q, const float* k, const f
   float* D = static_cast<float*>(workspace);
   const int64_t rows = bh * T;
   const bool dot_vec = fa_vec_ok(d, {o, dout}, strides + 9, 6);
-  auto dot_kernel = dot_vec ? flash_bwd_dot_kernel<true> : flash_bwd_dot_kernel<false>;
-  dot_kernel<<<dim3((unsigned)ceil_div(rows * 16, (int64_t)256)), dim3(256), 0, st>>>(
-      fa_in(dout, strides + 12), fa_in(o, strides + 9), D, rows, (int)T, (int)H, (int)d);
+  // four rows per 16-lane group where they never straddle two heads
+  if (dot_vec && T % 4 == 0) {
+    flash_bwd_dot_kernel<true, 4><<<dim3((unsigned)ceil_div(rows / 4 * 16, (int64_t)256)), dim3(256), 0, st>>>(
+        fa_in(dout, strides + 12), fa_in(o, strides + 9), D, rows, (int)T, (int)H, (int)d);
+  } else {
+    auto dot_kernel = dot_vec ? flash_bwd_dot_kernel<true, 1> : flash_bwd_dot_kernel<false, 1>;
+    dot_kernel<<<dim3((unsigned)ceil_div(rows * 16, (int64_t)256)), dim3(256), 0, st>>>(
+        fa_in(dout, strides + 12), fa_in(o, strides + 9), D, rows, (int)T, (int)H, (int)d);
+  }
   int rc = launch_status();
   if (rc != AAR_OK) return rc;
   const bool vec = fa_vec_ok(d, {q, k, v, dout, dq, dk, dv}, strides, 24);
