@@ -140,13 +140,18 @@ int aar_gemm_f32_batched(int op, int64_t batch, int64_t M, int64_t N, int64_t K,
 
 /* Tuning and test access to the GEMM tile configurations (no counterpart in
  * the reference, whose launchers pick a tile size internally,
- * cppsrc/ops/matmul.cu:792-832).  Configurations are numbered 0..n-1;
- * aar_gemm_f32_tile_config returns AAR_EINVAL past the last one.
+ * cppsrc/ops/matmul.cu:792-832).  Tile configurations are numbered 0..n-1;
+ * aar_gemm_f32_tile_config returns AAR_EINVAL past the last one.  Id n is
+ * the thin-output kernel: N <= 128, 16 <= K <= 512 with K % 16 == 0, B
+ * padded to 16-column blocks in LDS (at most 128 KB), a 16-byte aligned A
+ * for NN/NT and B for NT, no split (splits must be 1); outside those limits
+ * it returns AAR_EUNSUPPORTED.
  * aar_gemm_f32_plan reports the configuration and split count aar_gemm_f32
- * would use with `workspace_bytes` of scratch.  aar_gemm_f32_with_config runs
- * a given configuration and split-K count (needs splits*M*N*4 bytes of
- * workspace when splits > 1, else AAR_EWORKSPACE); results agree with
- * aar_gemm_f32 up to summation order. */
+ * would use with `workspace_bytes` of scratch (id n for thin outputs such as
+ * a vocabulary head; aar_gemm_f32 takes it only when the operands' alignment
+ * allows).  aar_gemm_f32_with_config runs a given configuration and split-K
+ * count (needs splits*M*N*4 bytes of workspace when splits > 1, else
+ * AAR_EWORKSPACE); results agree with aar_gemm_f32 up to summation order. */
 int aar_gemm_f32_tile_config(int config, int* tile_m, int* tile_n, int* tile_k);
 int aar_gemm_f32_plan(int op, int64_t M, int64_t N, int64_t K, size_t workspace_bytes,
                       int* config, int* splits);
