@@ -592,7 +592,12 @@ __host__ __device__ constexpr int thin_ld_kn(int nb) { return 16 * nb + 4; }
 // the MFMA work (N = 65: 64 columns on MFMA, one by VALU); per lane the
 // partial dot products of its four k steps are summed over the four k lanes
 // of a row (lane ^ 16, then lane ^ 32) and over the K parts in part order.
-template <int NB, int OP, bool TAIL>
+// FLAT (NN/TN with B contiguous and 16-byte aligned): B is copied into LDS
+// as it lies in HBM ([k][c], row stride N) by 16-byte DMAs, a quarter of the
+// instructions of the padded form's 4-byte row DMAs (their staging time is
+// what the 16-byte form saves; the fragment reads then meet some bank
+// conflicts).
+template <int NB, int OP, bool TAIL, bool FLAT>
 __global__ void __launch_bounds__(kThinThreads, 1)
 gemm_f32_thin_kernel(const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, int M,
                      int N, int K, int64_t lda, int64_t ldb, int64_t ldc) {
@@ -602,6 +607,7 @@ gemm_f32_thin_kernel(const float* __restrict__ A, const float* __restrict__ B, f
   constexpr int NBM = TAIL ? NB - 1 : NB;  // column blocks on MFMA
   static_assert(!TAIL || NB >= 2, "a tail follows at least one full column block");
   constexpr int kLdKn = thin_ld_kn(NB);
+  static_assert(!(FLAT && OP == AAR_GEMM_NT), "the flat copy is the [K][N] layout of NN/TN");
   static_assert(kThinParts * kThinSlabs * 64 == kThinThreads, "16 waves: 4 slabs x 4 K parts");
   static_assert((kThinParts - 1) * kThinSlabs * (NB * 256 + 64) <= kThinLds, "the part combine fits in LDS");
   __shared__ __attribute__((aligned(16))) float lds[kThinLds];
@@ -613,7 +619,7 @@ gemm_f32_thin_kernel(const float* __restrict__ A, const float* __restrict__ B, f
   const int kpart = (K / 16 + kThinParts - 1) / kThinParts * 16;
   const int kbase = part * kpart;
   const int nkb = max(0, min(K - kbase, kpart)) / 16;
-  const int ldk = kNT ? K + 4 : kLdKn;
+  const int ldk = kNT ? K + 4 : (FLAT ? N : kLdKn);  // LDS row stride of the staged B
 
   // A fragments first, so their HBM latency overlaps the staging of B.
   const int64_t row = min((int64_t)blockIdx.x * kThinRows + slab * 16 + li, (int64_t)M - 1);
@@ -638,6 +644,12 @@ gemm_f32_thin_kernel(const float* __restrict__ A, const float* __restrict__ B, f
       for (int k0 = 0; k0 < K; k0 += 256) {
         if (lane * 4 < K - k0) dma16_untracked_s(lane * 16, src + k0, (lds_void_t*)(dst + k0));
       }
+    }
+  } else if constexpr (FLAT) {
+    // K * N floats (a multiple of 16: K % 16 == 0), 1 KB per instruction
+    const int n4 = K * N / 4;
+    for (int u = wave; u * 64 < n4; u += kThinThreads / 64) {
+      if (u * 64 + lane < n4) dma16_untracked_s(lane * 16, B + u * 256, (lds_void_t*)(lds + u * 256));
     }
   } else {
     for (int k = wave; k < K; k += kThinThreads / 64) {
@@ -665,6 +677,12 @@ gemm_f32_thin_kernel(const float* __restrict__ A, const float* __restrict__ B, f
           if constexpr (kNT) {
             bt = f32x4{lds[(16 * NBM) * ldk + k + j], lds[(16 * NBM + 1) * ldk + k + j],
                        lds[(16 * NBM + 2) * ldk + k + j], lds[(16 * NBM + 3) * ldk + k + j]};
+          } else if constexpr (FLAT) {
+            // columns past N read the next row (or, in the last row, past
+            // the copy: the launcher keeps 64 floats of LDS spare); they
+            // feed only tail sums that are never stored
+            const float* r = lds + (k + j) * ldk + 16 * NBM;
+            bt = f32x4{r[0], r[1], r[2], r[3]};
           } else {
             bt = *reinterpret_cast<const f32x4*>(lds + (k + j) * kLdKn + 16 * NBM);
           }
@@ -678,8 +696,8 @@ gemm_f32_thin_kernel(const float* __restrict__ A, const float* __restrict__ B, f
         if constexpr (kNT) {
           b = *reinterpret_cast<const f32x4*>(lds + (16 * nb + li) * ldk + k);
         } else {
-          const float* col = lds + k * kLdKn + 16 * nb + li;
-          b = f32x4{col[0], col[kLdKn], col[2 * kLdKn], col[3 * kLdKn]};
+          const float* col = lds + k * ldk + 16 * nb + li;
+          b = f32x4{col[0], col[ldk], col[2 * ldk], col[3 * ldk]};
         }
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[nb] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i][j], b[j], acc[nb], 0, 0, 0);
@@ -1021,30 +1039,38 @@ int launch_thin(const float* A, const float* B, float* C, int64_t M, int64_t N, 
                 int64_t ldc, hipStream_t st) {
   const dim3 grid((unsigned)ceil_div(M, (int64_t)kThinRows));
   const bool tail = N > 16 && N % 16 >= 1 && N % 16 <= 4;
+  // (the fragment reads of padding columns run up to 15 floats past the copy)
+  const bool flat = OP != AAR_GEMM_NT && ldb == N && aligned16(B) && K * N + 64 <= kThinLds;
+  auto go = [&](auto nb_tag) {
+    constexpr int NBV = decltype(nb_tag)::value;
+    auto launch = [&](auto kern) {
+      kern<<<grid, dim3(kThinThreads), 0, st>>>(A, B, C, (int)M, (int)N, (int)K, lda, ldb, ldc);
+      return launch_status();
+    };
+    if constexpr (OP != AAR_GEMM_NT) {
+      if constexpr (NBV >= 2) {
+        if (tail) return flat ? launch(gemm_f32_thin_kernel<NBV, OP, true, true>)
+                              : launch(gemm_f32_thin_kernel<NBV, OP, true, false>);
+      }
+      return flat ? launch(gemm_f32_thin_kernel<NBV, OP, false, true>)
+                  : launch(gemm_f32_thin_kernel<NBV, OP, false, false>);
+    } else {
+      if constexpr (NBV >= 2) {
+        if (tail) return launch(gemm_f32_thin_kernel<NBV, OP, true, false>);
+      }
+      return launch(gemm_f32_thin_kernel<NBV, OP, false, false>);
+    }
+  };
   switch (ceil_div(N, (int64_t)16)) {
-#define AAR_THIN_NB(NBV)                                                                                          \
-  case NBV:                                                                                                       \
-    if constexpr (NBV >= 2) {                                                                                     \
-      if (tail) {                                                                                                 \
-        gemm_f32_thin_kernel<NBV, OP, true><<<grid, dim3(kThinThreads), 0, st>>>(A, B, C, (int)M, (int)N, (int)K, \
-                                                                                 lda, ldb, ldc);                  \
-        return launch_status();                                                                                   \
-      }                                                                                                           \
-    }                                                                                                             \
-    gemm_f32_thin_kernel<NBV, OP, false><<<grid, dim3(kThinThreads), 0, st>>>(A, B, C, (int)M, (int)N, (int)K,    \
-                                                                              lda, ldb, ldc);                     \
-    return launch_status();
-    AAR_THIN_NB(1)
-    AAR_THIN_NB(2)
-    AAR_THIN_NB(3)
-    AAR_THIN_NB(4)
-    AAR_THIN_NB(5)
-    AAR_THIN_NB(6)
-    AAR_THIN_NB(7)
-    AAR_THIN_NB(8)
-#undef AAR_THIN_NB
-    default:
-      return AAR_EUNSUPPORTED;
+    case 1: return go(std::integral_constant<int, 1>{});
+    case 2: return go(std::integral_constant<int, 2>{});
+    case 3: return go(std::integral_constant<int, 3>{});
+    case 4: return go(std::integral_constant<int, 4>{});
+    case 5: return go(std::integral_constant<int, 5>{});
+    case 6: return go(std::integral_constant<int, 6>{});
+    case 7: return go(std::integral_constant<int, 7>{});
+    case 8: return go(std::integral_constant<int, 8>{});
+    default: return AAR_EUNSUPPORTED;
   }
 }
 

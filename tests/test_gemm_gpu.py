@@ -234,8 +234,9 @@ def test_thin_output_kernel_vs_oracle(gpu, op):
     configurations), forced through aar_gemm_f32_with_config: N up to 128 in
     1..8 column blocks of 16 with ragged N and M (a last block of 1-4 columns
     goes through VALU FMAs), K a multiple of 16 up to 512
-    (4 K parts per row slab, some of them empty), misaligned A (NN/NT) or B
-    rows (N odd).  A rerun is bit identical (fixed-order part sum); shapes
+    (4 K parts per row slab, some of them empty), misaligned A (NN/NT), B
+    rows that are not 16-byte aligned (N odd), B staged whole (flat) or row by
+    row (padded).  A rerun is bit identical (fixed-order part sum); shapes
     outside its limits return AAR_EUNSUPPORTED; the plan takes it for the
     vocabulary head 16384 x 65 x 384 in all three layouts."""
     name = ["nn", "nt", "tn"][op]
@@ -271,6 +272,15 @@ def test_thin_output_kernel_vs_oracle(gpu, op):
         cfg, sp = ctypes.c_int(-1), ctypes.c_int(-1)
         abi.check(abi.L.aar_gemm_f32_plan(op, 16384, 65, 384, 1 << 30, ctypes.byref(cfg), ctypes.byref(sp)))
         assert (cfg.value, sp.value) == (thin, 1)
+        # NN/TN copy a contiguous, 16-byte aligned B into LDS whole (flat form); a B
+        # one float off that alignment takes the padded row-by-row form
+        if op != 1:
+            for (M, N, K) in [(300, 65, 384), (130, 40, 96)]:
+                rng = np.random.default_rng(M + N + K + 100 * op)
+                a, b = operands(name, M, N, K, rng)
+                pa, pb, pc = abi.put(a), abi.put(b, offset_floats=1), abi.empty(M * N)
+                abi.check(abi.L.aar_gemm_f32_with_config(op, M, N, K, pa, pb, pc, None, 0, thin, 1, None))
+                assert_close(abi.get(pc, (M, N)), O.matmul(name, a, b), gemm_tol(K), f"{name} thin padded B {(M, N, K)}")
         # through aar_gemm_f32 with a misaligned A the plan falls back to a tile configuration
         if op != 2:
             rng = np.random.default_rng(5)
