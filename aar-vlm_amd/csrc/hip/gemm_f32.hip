@@ -75,10 +75,17 @@ struct GemmEpi {
 // Epilogue: a wave's (32*TM) x (32*TN) accumulators to C.  Accumulator
 // layout of a 32x32 block: lane (lr, h), register r holds row
 // 8*(r/4) + 4*h + (r%4), column lr.
+// A wave tile wholly inside C (the common case) stores without bounds tests;
+// element offsets from the lane's first element are a constant row count
+// times ldc, which the compiler forms once in scalar registers.
 template <int TM, int TN, int EPI>
 __device__ __forceinline__ void store_tile(const f32x16 (&acc)[TM][TN], float* __restrict__ C, const GemmEpi& ep,
                                            int64_t M, int64_t N, int64_t ldc, int64_t r0, int64_t c0, int lr,
                                            int h) {
+  const bool interior = r0 + 32 * TM <= M && c0 + 32 * TN <= N;
+  const int64_t lane0 = (r0 + 4 * h) * ldc + c0 + lr;  // offset of the lane's first element
+  float* const Cl = C + lane0;
+  const float* const Xl = EPI == kEpiMask ? ep.aux + lane0 : nullptr;
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
 #pragma unroll
@@ -88,13 +95,14 @@ __device__ __forceinline__ void store_tile(const f32x16 (&acc)[TM][TN], float* _
       if constexpr (EPI == kEpiBias || EPI == kEpiBiasRelu) b = col < N ? ep.bias[col] : 0.f;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int64_t row = r0 + 32 * i + 8 * (r / 4) + 4 * h + (r % 4);
-        if (row < M && col < N) {
+        const int dr = 32 * i + 8 * (r / 4) + (r % 4);  // row - r0 - 4h
+        const int64_t off = (int64_t)dr * ldc + 32 * j;
+        if (interior || (r0 + 4 * h + dr < M && col < N)) {
           float v = acc[i][j][r];
           if constexpr (EPI == kEpiBias) v = v + b;
           if constexpr (EPI == kEpiBiasRelu) v = fmaxf(0.0f, v + b);
-          if constexpr (EPI == kEpiMask) v = ep.aux[row * ldc + col] > 0.0f ? v : 0.0f;
-          C[row * ldc + col] = v;
+          if constexpr (EPI == kEpiMask) v = Xl[off] > 0.0f ? v : 0.0f;
+          Cl[off] = v;
         }
       }
     }
@@ -420,8 +428,11 @@ gemm_f32_dma_kernel(const float* __restrict__ A, const float* __restrict__ B, fl
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int grp = (tid >> 6) / NW;  // K group
-  const int wave = (tid >> 6) % NW;  // wave within the group
+  // Wave index read into a scalar register: the group's tile range, the
+  // ragged-tile test and the out-of-tiles test are then scalar branches.
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int grp = wv / NW;   // K group
+  const int wave = wv % NW;  // wave within the group
   const int lr = lane & 31;
   const int h = lane >> 5;
   const int wm0 = (wave % NWM) * WM;

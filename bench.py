@@ -389,8 +389,10 @@ def bench_gemm_sweep(ev: Events, iters: int = 20):
                 ws = abi.alloc(wsb) if wsb else None
                 flop = 2.0 * M * N * K
                 n_it = iters if flop < 2e11 else max(3, iters // 4)
-                # ~30 ms of warm-up per layout so the clock has ramped before timing
-                n_warm = int(min(200, max(3, 4e12 / max(flop, 1.0))))
+                # 30-40 ms of warm-up per layout so the clock has ramped before
+                # timing (launches of a 1024^3 product take ~22 us each: a cap
+                # of 200 left it timing the ramp)
+                n_warm = int(min(2000, max(3, 4e12 / max(flop, 1.0))))
                 for _ in range(n_warm):
                     assert L.aar_gemm_f32(op, M, N, K, pa, pb, pc, ws, wsb, None) == 0
                 ev.start()
