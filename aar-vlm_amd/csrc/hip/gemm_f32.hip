@@ -315,9 +315,10 @@ gemm_f32_kernel(const float* __restrict__ A, const float* __restrict__ B, float*
 // pass reads (8 or 16 consecutive rows, same q) land in distinct banks.
 template <int BK>
 __device__ __forceinline__ int kc_swz(int row) {
-  static_assert(BK == 16 || BK == 32, "swizzle defined for BK 16 and 32");
+  static_assert(BK == 16 || BK == 32 || BK == 64, "swizzle defined for BK 16, 32 and 64");
   if (BK == 16) return ((row >> 1) + (row >> 3)) & 3;
-  return (row ^ (row >> 3)) & 7;
+  if (BK == 32) return (row ^ (row >> 3)) & 7;
+  return row & 15;  // 16 float4 groups per row: 16 consecutive rows, 16 distinct groups
 }
 
 template <int BR, int BK, int NW, bool KC>
@@ -849,6 +850,9 @@ constexpr Cfg kCfgs[] = {
     {128, 128, 32, 64, 64, 1, 2, 0.826f, 1, kAllOps, 2},         // 10: 8 waves
     {64, 64, 32, 32, 32, 1, 3, 0.60f, 1, kAllOps, 2},            // 11: 8 waves
     {64, 96, 32, 32, 96, 1, 2, 0.55f, 1, 1 << AAR_GEMM_NT, 4},   // 12: 8 waves
+    // 13: 8 waves, BK 64: half the barriers of 11 per K (1024^3: 22.0-22.9
+    // us against 23.0-23.2 for 9 and 11)
+    {64, 64, 64, 32, 32, 1, 2, 0.615f, 1, kAllOps, 2},
 };
 constexpr int kNumCfgs = sizeof(kCfgs) / sizeof(kCfgs[0]);
 constexpr int kMaxSplits = 64;
@@ -998,12 +1002,13 @@ int launch_op(int cfg, bool vec, const float* A, const float* B, float* C, int64
     AAR_GEMM_CFG(10)
     AAR_GEMM_CFG(11)
     AAR_GEMM_CFG(12)
+    AAR_GEMM_CFG(13)
     default:
       return AAR_EINVAL;
   }
 #undef AAR_GEMM_CFG
 }
-static_assert(kNumCfgs == 13, "launch_op lists every configuration");
+static_assert(kNumCfgs == 14, "launch_op lists every configuration");
 
 // 128-bit loads need 16-byte aligned operands whose contiguous extents and
 // leading dimensions are multiples of 4, and the 32-bit per-thread offsets
