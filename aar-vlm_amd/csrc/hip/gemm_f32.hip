@@ -853,6 +853,10 @@ constexpr Cfg kCfgs[] = {
     // 13: 8 waves, BK 64: half the barriers of 11 per K (1024^3: 22.0-22.9
     // us against 23.0-23.2 for 9 and 11)
     {64, 64, 64, 32, 32, 1, 2, 0.615f, 1, kAllOps, 2},
+    // 14: 8 waves of 32x64 over a 128x128 tile, BK 64, one K group (128 KB
+    // of LDS): for grids of about one 128x128 tile per CU (2048^3: 129.2 /
+    // 128.8 / 127.2 TF NN/NT/TN against 127.2 / 123.5 / 127.6 for 10)
+    {128, 128, 64, 32, 64, 1, 2, 0.83f, 1, kAllOps},
 };
 constexpr int kNumCfgs = sizeof(kCfgs) / sizeof(kCfgs[0]);
 constexpr int kMaxSplits = 64;
@@ -1003,12 +1007,13 @@ int launch_op(int cfg, bool vec, const float* A, const float* B, float* C, int64
     AAR_GEMM_CFG(11)
     AAR_GEMM_CFG(12)
     AAR_GEMM_CFG(13)
+    AAR_GEMM_CFG(14)
     default:
       return AAR_EINVAL;
   }
 #undef AAR_GEMM_CFG
 }
-static_assert(kNumCfgs == 14, "launch_op lists every configuration");
+static_assert(kNumCfgs == 15, "launch_op lists every configuration");
 
 // 128-bit loads need 16-byte aligned operands whose contiguous extents and
 // leading dimensions are multiples of 4, and the 32-bit per-thread offsets
