@@ -826,7 +826,8 @@ struct Cfg {
   int bm, bn, bk, wm, wn, resident, stages;
   float eff;
   int slots, ops;
-  int kg = 1;  // K groups of the DMA path
+  int kg = 1;           // K groups of the DMA path
+  bool splitk = true;   // the planner may split its K
 };
 constexpr Cfg kCfgs[] = {
     {256, 256, 32, 64, 128, 1, 2, 0.866f, 1, kAllOps},  // 0: 8 waves, 2 waves/SIMD; BK 32 halves the barriers
@@ -852,7 +853,7 @@ constexpr Cfg kCfgs[] = {
     {64, 96, 32, 32, 96, 1, 2, 0.55f, 1, 1 << AAR_GEMM_NT, 4},   // 12: 8 waves
     // 13: 8 waves, BK 64: half the barriers of 11 per K (1024^3: 22.0-22.9
     // us against 23.0-23.2 for 9 and 11)
-    {64, 64, 64, 32, 32, 1, 2, 0.615f, 1, kAllOps, 2},
+    {64, 64, 64, 32, 32, 1, 2, 0.615f, 1, kAllOps, 2, false},
     // 14: 8 waves of 32x64 over a 128x128 tile, BK 64, one K group (128 KB
     // of LDS): for grids of about one 128x128 tile per CU (2048^3: 129.2 /
     // 128.8 / 127.2 TF NN/NT/TN against 127.2 / 123.5 / 127.6 for 10)
@@ -877,6 +878,7 @@ int64_t split_chunk(int64_t K, int splits, int bk) { return ceil_div(ceil_div(K,
 // of the GPT step plus a held-out shape set; the split counts tried are the
 // measured ones.
 constexpr int kPlanSplits[] = {1, 2, 3, 4, 6, 8, 12, 16, 24, 32};
+constexpr int kNumPlanSplits = sizeof(kPlanSplits) / sizeof(kPlanSplits[0]);
 
 // The thin-output kernel (gemm_f32_thin_kernel) has configuration id
 // kThinCfg, past the tile configurations.  thin_shape_ok: the shapes it
@@ -916,11 +918,22 @@ Plan plan_gemm(int op, int64_t M, int64_t N, int64_t K, size_t ws_bytes, bool al
     const Cfg& cf = kCfgs[c];
     if (!(cf.ops & (1 << op))) continue;
     const int64_t tiles = ceil_div(M, (int64_t)cf.bm) * ceil_div(N, (int64_t)cf.bn) * batch;
-    for (const int splits : kPlanSplits) {
+    // the measured split counts, then the one that fills the CUs' slots in
+    // one round
+    const int64_t fill = (int64_t)cus * cf.slots / std::max<int64_t>(tiles, 1);
+    for (int si = 0; si <= kNumPlanSplits; ++si) {
+      const int splits = si < kNumPlanSplits ? kPlanSplits[si] : (int)std::min<int64_t>(fill, 64);
+      if (si == kNumPlanSplits && (splits < 2 || std::count(kPlanSplits, kPlanSplits + kNumPlanSplits, splits))) break;
       if (splits > 1) {
-        if (!allow_split) break;
-        if (K / splits < 256) break;
-        if ((size_t)splits * M * N * sizeof(float) > ws_bytes) break;
+        if (!allow_split || !cf.splitk) break;
+        if (K / splits < 256) {
+          if (si < kNumPlanSplits) si = kNumPlanSplits - 1;  // still try the filling count
+          continue;
+        }
+        if ((size_t)splits * M * N * sizeof(float) > ws_bytes) {
+          if (si < kNumPlanSplits) si = kNumPlanSplits - 1;
+          continue;
+        }
       }
       const int64_t kps = split_chunk(K, splits, cf.bk);
       const int64_t real_splits = ceil_div(K, kps);
