@@ -589,8 +589,10 @@ gemm_f32_dma_kernel(const float* __restrict__ A, const float* __restrict__ B, fl
 // both feed only outputs that are not stored.
 //   NN, TN: B is [K][N]; LDS holds it as [k][c], row stride NC + 4 (the
 //           four k rows of one 32-bit read land 16 banks apart).
-//   NT:     B is [N][K]; LDS holds it row for row as [c][k], row stride K + 4
-//           (128-bit reads of 16 consecutive columns are conflict free).
+//   NT:     B is [N][K]; LDS holds it as [chunk][c][64] in 64-deep k chunks,
+//           float4 group g of column c at g ^ (c & 15), so the 128-bit reads
+//           of 16 consecutive columns at one k hit 16 distinct bank quads
+//           (measured 5 % faster than [c][k] rows of stride K + 4).
 constexpr int kThinThreads = 1024;
 constexpr int kThinSlabs = 4, kThinParts = 4;
 constexpr int kThinRows = 16 * kThinSlabs;  // rows per workgroup
@@ -631,7 +633,7 @@ gemm_f32_thin_kernel(const float* __restrict__ A, const float* __restrict__ B, f
   const int kpart = (K / 16 + kThinParts - 1) / kThinParts * 16;
   const int kbase = part * kpart;
   const int nkb = max(0, min(K - kbase, kpart)) / 16;
-  const int ldk = kNT ? K + 4 : (FLAT ? N : kLdKn);  // LDS row stride of the staged B
+  const int ldk = FLAT ? N : kLdKn;  // LDS row stride of the staged [k][c] B (NN/TN)
 
   // A fragments first, so their HBM latency overlaps the staging of B.
   const int64_t row = min((int64_t)blockIdx.x * kThinRows + slab * 16 + li, (int64_t)M - 1);
@@ -650,11 +652,16 @@ gemm_f32_thin_kernel(const float* __restrict__ A, const float* __restrict__ B, f
   }
 
   if constexpr (kNT) {
-    for (int c = wave; c < NC; c += kThinThreads / 64) {
-      const float* src = B + (int64_t)min(c, N - 1) * ldb;
-      float* dst = lds + c * ldk;
-      for (int k0 = 0; k0 < K; k0 += 256) {
-        if (lane * 4 < K - k0) dma16_untracked_s(lane * 16, src + k0, (lds_void_t*)(dst + k0));
+    // one 16-byte DMA per 4 columns of a 64-deep chunk; lane (cl, gl) takes
+    // float4 group gl ^ (col & 15) of column col = 4u + cl
+    const int nchk = (K + 63) / 64;
+    const int cl = lane >> 4, gl = lane & 15;
+    for (int v = wave; v < nchk * (NC / 4); v += kThinThreads / 64) {
+      const int ch = v / (NC / 4), u = v % (NC / 4);
+      const int col = 4 * u + cl;
+      const int k = 64 * ch + 4 * (gl ^ (col & 15));
+      if (k < K) {
+        dma16_untracked_s((uint32_t)(min(col, N - 1) * ldb + k) * 4u, B, (lds_void_t*)(lds + (ch * NC + 4 * u) * 64));
       }
     }
   } else if constexpr (FLAT) {
@@ -687,8 +694,11 @@ gemm_f32_thin_kernel(const float* __restrict__ A, const float* __restrict__ B, f
         for (int j = 0; j < 4; ++j) {
           f32x4 bt;
           if constexpr (kNT) {
-            bt = f32x4{lds[(16 * NBM) * ldk + k + j], lds[(16 * NBM + 1) * ldk + k + j],
-                       lds[(16 * NBM + 2) * ldk + k + j], lds[(16 * NBM + 3) * ldk + k + j]};
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+              const int c = 16 * NBM + t;
+              bt[t] = lds[((k >> 6) * NC + c) * 64 + 4 * (((k & 63) >> 2) ^ (c & 15)) + j];
+            }
           } else if constexpr (FLAT) {
             // columns past N read the next row (or, in the last row, past
             // the copy: the launcher keeps 64 floats of LDS spare); they
@@ -706,7 +716,8 @@ gemm_f32_thin_kernel(const float* __restrict__ A, const float* __restrict__ B, f
       for (int nb = 0; nb < NBM; ++nb) {
         f32x4 b;
         if constexpr (kNT) {
-          b = *reinterpret_cast<const f32x4*>(lds + (16 * nb + li) * ldk + k);
+          // column 16 nb + li: its low four bits are li
+          b = *reinterpret_cast<const f32x4*>(lds + ((k >> 6) * NC + 16 * nb + li) * 64 + 4 * (((k & 63) >> 2) ^ li));
         } else {
           const float* col = lds + k * ldk + 16 * nb + li;
           b = f32x4{col[0], col[ldk], col[2 * ldk], col[3 * ldk]};
@@ -888,7 +899,7 @@ constexpr int kThinCfg = kNumCfgs;
 bool thin_shape_ok(int op, int64_t M, int64_t N, int64_t K) {
   if (M < 1 || N < 1 || N > 128 || K < 16 || K > 16 * kThinMaxKb * kThinParts || K % 16 != 0) return false;
   const int64_t nb = ceil_div(N, (int64_t)16);
-  const int64_t lds = op == AAR_GEMM_NT ? 16 * nb * (K + 4) : K * thin_ld_kn((int)nb);
+  const int64_t lds = op == AAR_GEMM_NT ? ceil_div(K, (int64_t)64) * 64 * 16 * nb : K * thin_ld_kn((int)nb);
   return lds <= kThinLds && ceil_div(M, (int64_t)kThinRows) * kThinThreads <= (int64_t)UINT32_MAX;
 }
 bool thin_operands_ok(int op, const float* A, const float* B, int64_t lda, int64_t ldb) {

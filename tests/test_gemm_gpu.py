@@ -246,8 +246,8 @@ def test_thin_output_kernel_vs_oracle(gpu, op):
         # N % 16 in 1..4 (65, 17, 33, 50, 20) takes the VALU tail-column form
         for (M, N, K) in [(300, 65, 384), (1000, 1, 16), (777, 128, 64), (64, 17, 512), (130, 96, 336),
                           (4097, 33, 48), (65, 80, 400), (16, 16, 32), (257, 50, 64), (300, 20, 128)]:
-            if op == 1 and 16 * -(-N // 16) * (K + 4) > 32768:
-                continue  # B^T padded does not fit the kernel's LDS (checked below)
+            if op == 1 and 16 * -(-N // 16) * 64 * -(-K // 64) > 32768:
+                continue  # B^T in 64-deep chunks does not fit the kernel's LDS (checked below)
             if op != 1 and K * (16 * -(-N // 16) + 4) > 32768:
                 continue
             rng = np.random.default_rng(M * 7 + N + K + op)
@@ -264,8 +264,14 @@ def test_thin_output_kernel_vs_oracle(gpu, op):
         p = abi.alloc(4 << 20)
         for (M, N, K) in [(256, 129, 64), (256, 64, 100), (256, 64, 528), (256, 64, 8)]:
             assert abi.L.aar_gemm_f32_with_config(op, M, N, K, p, p, p, None, 0, thin, 1, None) == -3, (M, N, K)
-        if op == 1:  # B^T padded to 128 columns x (256 + 4) floats exceeds the 128 KB of LDS
-            assert abi.L.aar_gemm_f32_with_config(op, 256, 128, 256, p, p, p, None, 0, thin, 1, None) == -3
+        if op == 1:  # B^T as 128 columns x 5 chunks of 64 k exceeds the 128 KB of LDS
+            assert abi.L.aar_gemm_f32_with_config(op, 256, 128, 272, p, p, p, None, 0, thin, 1, None) == -3
+            # K = 256 fills it exactly
+            rng = np.random.default_rng(9)
+            a, b = operands(name, 256, 128, 256, rng)
+            pa, pb, pc = abi.put(a), abi.put(b), abi.empty(256 * 128)
+            abi.check(abi.L.aar_gemm_f32_with_config(op, 256, 128, 256, pa, pb, pc, None, 0, thin, 1, None))
+            assert_close(abi.get(pc, (256, 128)), O.matmul(name, a, b), gemm_tol(256), "nt thin full LDS")
         if op != 2:  # 128-bit A rows need a 16-byte aligned A
             assert abi.L.aar_gemm_f32_with_config(op, 64, 65, 64, p + 4, p, p, None, 0, thin, 1, None) == -3
         assert abi.L.aar_gemm_f32_with_config(op, 64, 65, 64, p, p, p, None, 0, thin, 2, None) == -1
