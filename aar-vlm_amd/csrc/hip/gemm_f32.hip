@@ -837,8 +837,8 @@ struct Cfg {
   int bm, bn, bk, wm, wn, resident, stages;
   float eff;
   int slots, ops;
-  int kg = 1;           // K groups of the DMA path
-  bool splitk = true;   // the planner may split its K
+  int kg = 1;                  // K groups of the DMA path
+  int split_ops = kAllOps;     // layouts for which the planner may split its K
 };
 constexpr Cfg kCfgs[] = {
     {256, 256, 32, 64, 128, 1, 2, 0.866f, 1, kAllOps},  // 0: 8 waves, 2 waves/SIMD; BK 32 halves the barriers
@@ -852,8 +852,11 @@ constexpr Cfg kCfgs[] = {
     // 8: 4 waves of 64x96; for NN with N a multiple of 192 (the dX products
     // of the GPT step: +4-5 % over the 64x128 tile).  It keeps full speed
     // with one workgroup per CU, hence one model slot; as NT it loses at
-    // N = 1152, so it is not planned there.
-    {128, 192, 32, 64, 96, 2, 2, 0.87f, 1, 1 << AAR_GEMM_NN},
+    // N = 1152, so it is not planned there.  Unsplit TN products with many
+    // rows take it too (16384 x 384 x 1536: 147.6 against 176.5 us); split
+    // TN products lose with it (+25-28 % at 8 or 32 splits), so only NN
+    // splits it.
+    {128, 192, 32, 64, 96, 2, 2, 0.87f, 1, (1 << AAR_GEMM_NN) | (1 << AAR_GEMM_TN), 1, 1 << AAR_GEMM_NN},
     // 9-12: K groups (see gemm_f32_dma_kernel), for grids of about one
     // workgroup per CU.  12 has a 96-wide N tile for thin outputs (the GPT
     // head, N = 65); its row-contiguous DMA layout needs BN % 64 == 0, so it
@@ -864,7 +867,7 @@ constexpr Cfg kCfgs[] = {
     {64, 96, 32, 32, 96, 1, 2, 0.55f, 1, 1 << AAR_GEMM_NT, 4},   // 12: 8 waves
     // 13: 8 waves, BK 64: half the barriers of 11 per K (1024^3: 22.0-22.9
     // us against 23.0-23.2 for 9 and 11)
-    {64, 64, 64, 32, 32, 1, 2, 0.615f, 1, kAllOps, 2, false},
+    {64, 64, 64, 32, 32, 1, 2, 0.615f, 1, kAllOps, 2, 0},
     // 14: 8 waves of 32x64 over a 128x128 tile, BK 64, one K group (128 KB
     // of LDS): for grids of about one 128x128 tile per CU (2048^3: 129.2 /
     // 128.8 / 127.2 TF NN/NT/TN against 127.2 / 123.5 / 127.6 for 10)
@@ -929,6 +932,15 @@ Plan plan_gemm(int op, int64_t M, int64_t N, int64_t K, size_t ws_bytes, bool al
     const Cfg& cf = kCfgs[c];
     if (!(cf.ops & (1 << op))) continue;
     const int64_t tiles = ceil_div(M, (int64_t)cf.bm) * ceil_div(N, (int64_t)cf.bn) * batch;
+    // Configuration 8 as TN: only grids of at most one round of its resident
+    // workgroups, or of two or three whole rounds.  Measured at 16384 rows
+    // (64 row tiles x N / 192), a partial last round loses to 3 and 6 by
+    // 9-17 % (N = 960, 1152) and grids of four or more rounds lose to 0 by
+    // up to 4 %, while whole short grids gain 5-18 %.
+    if (c == 8 && op == AAR_GEMM_TN) {
+      const int64_t round = (int64_t)cus * cf.resident;
+      if (!(tiles <= round || (tiles % round == 0 && tiles / round <= 3))) continue;
+    }
     // the measured split counts, then the one that fills the CUs' slots in
     // one round
     const int64_t fill = (int64_t)cus * cf.slots / std::max<int64_t>(tiles, 1);
@@ -936,7 +948,7 @@ Plan plan_gemm(int op, int64_t M, int64_t N, int64_t K, size_t ws_bytes, bool al
       const int splits = si < kNumPlanSplits ? kPlanSplits[si] : (int)std::min<int64_t>(fill, 64);
       if (si == kNumPlanSplits && (splits < 2 || std::count(kPlanSplits, kPlanSplits + kNumPlanSplits, splits))) break;
       if (splits > 1) {
-        if (!allow_split || !cf.splitk) break;
+        if (!allow_split || !(cf.split_ops & (1 << op))) break;
         if (K / splits < 256) {
           if (si < kNumPlanSplits) si = kNumPlanSplits - 1;  // still try the filling count
           continue;
