@@ -856,7 +856,7 @@ constexpr Cfg kCfgs[] = {
     // rows take it too (16384 x 384 x 1536: 147.6 against 176.5 us); split
     // TN products lose with it (+25-28 % at 8 or 32 splits), so only NN
     // splits it.
-    {128, 192, 32, 64, 96, 2, 2, 0.87f, 1, (1 << AAR_GEMM_NN) | (1 << AAR_GEMM_TN), 1, 1 << AAR_GEMM_NN},
+    {128, 192, 32, 64, 96, 2, 2, 0.87f, 1, kAllOps, 1, 1 << AAR_GEMM_NN},
     // 9-12: K groups (see gemm_f32_dma_kernel), for grids of about one
     // workgroup per CU.  12 has a 96-wide N tile for thin outputs (the GPT
     // head, N = 65); its row-contiguous DMA layout needs BN % 64 == 0, so it
@@ -922,7 +922,7 @@ bool thin_plan_wins(int op, int64_t M, int64_t N, int64_t K) {
 }
 
 Plan plan_gemm(int op, int64_t M, int64_t N, int64_t K, size_t ws_bytes, bool allow_split, int64_t batch = 1,
-               bool allow_thin = false) {
+               bool allow_thin = false, int epi = kEpiNone) {
   if (allow_thin && batch == 1 && thin_shape_ok(op, M, N, K) && thin_plan_wins(op, M, N, K)) return Plan{kThinCfg, 1, K};
   const int cus = device_cu_count();
   const double cu_flops = 157.3e12 / 256;  // fp32 MFMA FLOP/s per CU
@@ -932,14 +932,16 @@ Plan plan_gemm(int op, int64_t M, int64_t N, int64_t K, size_t ws_bytes, bool al
     const Cfg& cf = kCfgs[c];
     if (!(cf.ops & (1 << op))) continue;
     const int64_t tiles = ceil_div(M, (int64_t)cf.bm) * ceil_div(N, (int64_t)cf.bn) * batch;
-    // Configuration 8 as TN: only grids of at most one round of its resident
-    // workgroups, or of two or three whole rounds.  Measured at 16384 rows
-    // (64 row tiles x N / 192), a partial last round loses to 3 and 6 by
-    // 9-17 % (N = 960, 1152) and grids of four or more rounds lose to 0 by
-    // up to 4 %, while whole short grids gain 5-18 %.
-    if (c == 8 && op == AAR_GEMM_TN) {
+    // Configuration 8 as NT or TN: plain products only (with the bias or
+    // bias + relu epilogue it lost 1-3 % to 3 and 6 at the GPT MLP shapes),
+    // and only grids of at most one round of its resident workgroups, or of
+    // two or three whole rounds.  Measured at 16384 rows (64 row tiles x
+    // N / 192), a partial last round loses to 3 and 6 by 9-17 % (N = 960,
+    // 1152) and grids of four or more rounds lose to 0 by up to 4 %, while
+    // whole short grids gain 1-19 %.
+    if (c == 8 && op != AAR_GEMM_NN) {
       const int64_t round = (int64_t)cus * cf.resident;
-      if (!(tiles <= round || (tiles % round == 0 && tiles / round <= 3))) continue;
+      if (epi != kEpiNone || !(tiles <= round || (tiles % round == 0 && tiles / round <= 3))) continue;
     }
     // the measured split counts, then the one that fills the CUs' slots in
     // one round
@@ -1217,7 +1219,7 @@ extern "C" int aar_gemm_f32_bias(int op, int64_t M, int64_t N, int64_t K, const 
   if (K == 0) return AAR_EUNSUPPORTED;  // C = bias rows: not a product, left to the caller
   const int chk = check_gemm_args(op, M, N, K, A, B, C, stream);
   if (chk != AAR_OK) return chk;
-  const Plan p = plan_gemm(op, M, N, K, workspace ? workspace_bytes : 0, workspace != nullptr);
+  const Plan p = plan_gemm(op, M, N, K, workspace ? workspace_bytes : 0, workspace != nullptr, 1, false, kEpiBias);
   return run_gemm(op, M, N, K, A, B, C, workspace, p, as_stream(stream), kEpiBias, GemmEpi{bias, nullptr});
 }
 
@@ -1230,7 +1232,7 @@ extern "C" int aar_gemm_f32_bias_relu(int op, int64_t M, int64_t N, int64_t K, c
   if (op != AAR_GEMM_NT || K == 0) return AAR_EUNSUPPORTED;
   const int chk = check_gemm_args(op, M, N, K, A, B, C, stream);
   if (chk != AAR_OK) return chk;
-  const Plan p = plan_gemm(op, M, N, K, workspace ? workspace_bytes : 0, workspace != nullptr);
+  const Plan p = plan_gemm(op, M, N, K, workspace ? workspace_bytes : 0, workspace != nullptr, 1, false, kEpiBiasRelu);
   return run_gemm(op, M, N, K, A, B, C, workspace, p, as_stream(stream), kEpiBiasRelu, GemmEpi{bias, nullptr});
 }
 
@@ -1243,7 +1245,7 @@ extern "C" int aar_gemm_f32_relu_mask(int op, int64_t M, int64_t N, int64_t K, c
   if (op != AAR_GEMM_NN) return AAR_EUNSUPPORTED;
   const int chk = check_gemm_args(op, M, N, K, A, B, C, stream);
   if (chk != AAR_OK) return chk == 1 ? AAR_OK : chk;  // K == 0: C = 0, which the mask keeps
-  const Plan p = plan_gemm(op, M, N, K, workspace ? workspace_bytes : 0, workspace != nullptr);
+  const Plan p = plan_gemm(op, M, N, K, workspace ? workspace_bytes : 0, workspace != nullptr, 1, false, kEpiMask);
   return run_gemm(op, M, N, K, A, B, C, workspace, p, as_stream(stream), kEpiMask, GemmEpi{nullptr, mask});
 }
 
