@@ -448,43 +448,70 @@ layernorm_bwd_kernel(const float* __restrict__ gy, const float* __restrict__ x,
 }
 
 // Stage 2 of layernorm backward: dw[c] and db[c] from the partial rows
-// part[p][0..2C) (dgamma in [0,C), dbeta in [C,2C)) in one launch.  A
-// workgroup owns kRedCols consecutive columns of the 2C and kRedSlices
-// slices of the parts; slice j sums its contiguous run of parts in order
-// (all loads issued together), then a fixed pairwise tree over the slices
-// in LDS finishes the column.  Deterministic.
-constexpr int kRedCols = 16;
-constexpr int kRedThreads = 1024;
-constexpr int kRedSlices = kRedThreads / kRedCols;
+// part[p][0..2C) (dgamma in [0,C), dbeta in [C,2C)).  A workgroup of
+// kRedThreads threads owns V consecutive columns of the 2C (V = 4: one
+// 128-bit load per partial row, when C % 4 == 0 and the partials are 16-byte
+// aligned; else V = 1), so the grid has 2C / V workgroups and every load of a
+// thread is issued before the first add.  Thread t sums parts t, t + 256, ...
+// in that order; the 256 sums of a column then meet in a fixed tree (a wave
+// butterfly, then the four waves in order through LDS).  Deterministic.
+//
+// Workgroups are dealt round-robin over the 8 XCDs (hardware id b runs on
+// XCD b % 8).  Ids are remapped so each XCD owns one contiguous run of column
+// blocks: the 128-byte lines of a partial row are then fetched into one XCD's
+// L2 instead of up to eight.
+constexpr int kRedThreads = 256;
+constexpr int kXcds = 8;
 
+__device__ __forceinline__ int xcd_contiguous_block(int b, int nblk) {
+  const int q = nblk / kXcds, r = nblk % kXcds, x = b % kXcds;
+  return x * q + min(x, r) + b / kXcds;
+}
+
+template <int V>
 __global__ void __launch_bounds__(kRedThreads)
 layernorm_bwd_reduce_kernel(const float* __restrict__ part, float* __restrict__ dw, float* __restrict__ db,
                             int nparts, int cols) {
-  __shared__ float acc[kRedSlices][kRedCols];
-  const int cl = threadIdx.x % kRedCols, slice = threadIdx.x / kRedCols;
+  __shared__ float acc[kRedThreads / kWave][V];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int64_t ncol2 = 2 * (int64_t)cols;
-  const int64_t c = (int64_t)blockIdx.x * kRedCols + cl;
-  const int per = (nparts + kRedSlices - 1) / kRedSlices;
-  const int p0 = slice * per;
-  const int p1 = min(nparts, p0 + per);
-  float s = 0.f;
-  if (c < ncol2) {
-#pragma unroll 16
-    for (int p = p0; p < p1; ++p) s += part[(int64_t)p * ncol2 + c];
-  }
-  acc[slice][cl] = s;
-  __syncthreads();
+  const int64_t nblk = ncol2 / V;
+  // More blocks than one grid holds (over 2^16 of them) loop with the grid's stride.
+  for (int64_t blk = xcd_contiguous_block(blockIdx.x, gridDim.x); blk < nblk; blk += gridDim.x) {
+    const int64_t c0 = blk * V;
+    float s[V];
 #pragma unroll
-  for (int h = kRedSlices / 2; h >= 1; h /= 2) {
-    if (slice < h) acc[slice][cl] += acc[slice + h][cl];
-    __syncthreads();
-  }
-  if (slice == 0 && c < ncol2) {
-    if (c < cols) {
-      dw[c] = acc[0][cl];
-    } else {
-      db[c - cols] = acc[0][cl];
+    for (int v = 0; v < V; ++v) s[v] = 0.f;
+#pragma unroll 4
+    for (int p = threadIdx.x; p < nparts; p += kRedThreads) {
+      const float* src = part + (int64_t)p * ncol2 + c0;
+      if constexpr (V == 4) {
+        const f32x4 t = *reinterpret_cast<const f32x4*>(src);
+#pragma unroll
+        for (int v = 0; v < 4; ++v) s[v] += t[v];
+      } else {
+        s[0] += *src;
+      }
     }
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+      const float w = wave_sum(s[v]);
+      if (lane == 0) acc[wave][v] = w;
+    }
+    __syncthreads();
+    if (threadIdx.x < V) {
+      const int v = threadIdx.x;
+      float t = acc[0][v];
+#pragma unroll
+      for (int i = 1; i < kRedThreads / kWave; ++i) t += acc[i][v];
+      const int64_t c = c0 + v;
+      if (c < cols) {
+        dw[c] = t;
+      } else {
+        db[c - cols] = t;
+      }
+    }
+    __syncthreads();
   }
 }
 
@@ -849,8 +876,14 @@ int layernorm_bwd_run(const float* gy, const float* x, const float* w, const flo
   }
   rc = launch_status();
   if (rc != AAR_OK) return rc;
-  layernorm_bwd_reduce_kernel<<<dim3((unsigned)ceil_div(2 * cols, kRedCols)), dim3(kRedThreads), 0, st>>>(
-      part, dw, db, parts, (int)cols);
+  // Reduce grid: one workgroup per V columns of the 2C, at most 2^16.
+  const int64_t red_blocks = 2 * cols / ((cols % 4 == 0 && aligned16(part)) ? 4 : 1);
+  const unsigned red_grid = (unsigned)std::min<int64_t>(red_blocks, int64_t(1) << 16);
+  if (cols % 4 == 0 && aligned16(part)) {
+    layernorm_bwd_reduce_kernel<4><<<dim3(red_grid), dim3(kRedThreads), 0, st>>>(part, dw, db, parts, (int)cols);
+  } else {
+    layernorm_bwd_reduce_kernel<1><<<dim3(red_grid), dim3(kRedThreads), 0, st>>>(part, dw, db, parts, (int)cols);
+  }
   return launch_status();
 }
 
