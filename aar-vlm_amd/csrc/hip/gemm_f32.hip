@@ -78,10 +78,12 @@ struct GemmEpi {
 // A wave tile wholly inside C (the common case) stores without bounds tests;
 // element offsets from the lane's first element are a constant row count
 // times ldc, which the compiler forms once in scalar registers.
-template <int TM, int TN, int EPI>
+// NQ < 4: only register quads q0 .. q0 + NQ - 1 of each accumulator are
+// stored, their values held in quads 0 .. NQ - 1 of acc (a K group's share).
+template <int TM, int TN, int EPI, int NQ = 4>
 __device__ __forceinline__ void store_tile(const f32x16 (&acc)[TM][TN], float* __restrict__ C, const GemmEpi& ep,
                                            int64_t M, int64_t N, int64_t ldc, int64_t r0, int64_t c0, int lr,
-                                           int h) {
+                                           int h, int q0 = 0) {
   const bool interior = r0 + 32 * TM <= M && c0 + 32 * TN <= N;
   const int64_t lane0 = (r0 + 4 * h) * ldc + c0 + lr;  // offset of the lane's first element
   float* const Cl = C + lane0;
@@ -94,8 +96,8 @@ __device__ __forceinline__ void store_tile(const f32x16 (&acc)[TM][TN], float* _
       float b = 0.f;
       if constexpr (EPI == kEpiBias || EPI == kEpiBiasRelu) b = col < N ? ep.bias[col] : 0.f;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int dr = 32 * i + 8 * (r / 4) + (r % 4);  // row - r0 - 4h
+      for (int r = 0; r < 4 * NQ; ++r) {
+        const int dr = 32 * i + 8 * (q0 + r / 4) + (r % 4);  // row - r0 - 4h
         const int64_t off = (int64_t)dr * ldc + 32 * j;
         if (interior || (r0 + 4 * h + dr < M && col < N)) {
           float v = acc[i][j][r];
@@ -423,7 +425,7 @@ gemm_f32_dma_kernel(const float* __restrict__ A, const float* __restrict__ B, fl
   constexpr int kPerTile = TA::kPerWave + TB::kPerWave;  // DMA instructions per wave per tile
   static_assert((S - 2) * kPerTile < 64, "outstanding DMAs exceed the vmcnt range");
   constexpr int kAccFloats = TM * TN * 16 * 64;  // one wave's accumulators
-  static_assert((KG - 1) * NW * kAccFloats <= KG * S * kStage, "K-group hand-over fits in the rings");
+  static_assert(KG == 1 || KG * NW * kAccFloats <= KG * S * kStage, "K-group hand-over fits in the rings");
 
   __shared__ __attribute__((aligned(16))) float smem[KG * S * kStage];
 
@@ -536,10 +538,16 @@ gemm_f32_dma_kernel(const float* __restrict__ A, const float* __restrict__ B, fl
   if constexpr (KG > 1) {
     // Hand-over: every wave's DMAs have landed (the last trip waits for all),
     // and the barrier ends every read of the rings, which the partial sums
-    // then overwrite.  Lane-major float4s: conflict-free stores and loads.
+    // then overwrite.  Every group writes its sums (lane-major float4s:
+    // conflict-free stores and loads); group g then adds the KG groups'
+    // values of register quads [g*4/KG, (g+1)*4/KG) of each accumulator in
+    // group order and stores those rows, so the adds and the stores are
+    // spread over all groups.
+    static_assert(4 % KG == 0, "register quads split evenly over the K groups");
+    constexpr int QPG = 4 / KG;
     __syncthreads();
-    if (grp > 0) {
-      float* dst = smem + ((grp - 1) * NW + wave) * kAccFloats + lane * 4;
+    {
+      float* dst = smem + (grp * NW + wave) * kAccFloats + lane * 4;
 #pragma unroll
       for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -550,23 +558,23 @@ gemm_f32_dma_kernel(const float* __restrict__ A, const float* __restrict__ B, fl
                 f32x4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
     }
     __syncthreads();
-    if (grp > 0) return;
+    const int q0 = grp * QPG;
+    const float* src = smem + wave * kAccFloats + lane * 4;
 #pragma unroll
-    for (int g = 1; g < KG; ++g) {
-      const float* src = smem + ((g - 1) * NW + wave) * kAccFloats + lane * 4;
+    for (int i = 0; i < TM; ++i)
 #pragma unroll
-      for (int i = 0; i < TM; ++i)
+      for (int j = 0; j < TN; ++j)
 #pragma unroll
-        for (int j = 0; j < TN; ++j)
+        for (int qq = 0; qq < QPG; ++qq) {
+          const int o = ((i * TN + j) * 4 + q0 + qq) * 256;
+          f32x4 v = *reinterpret_cast<const f32x4*>(src + o);
 #pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const f32x4 v = *reinterpret_cast<const f32x4*>(src + ((i * TN + j) * 4 + q) * 256);
-            acc[i][j][4 * q] += v[0];
-            acc[i][j][4 * q + 1] += v[1];
-            acc[i][j][4 * q + 2] += v[2];
-            acc[i][j][4 * q + 3] += v[3];
-          }
-    }
+          for (int g = 1; g < KG; ++g) v += *reinterpret_cast<const f32x4*>(src + g * NW * kAccFloats + o);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) acc[i][j][4 * qq + e] = v[e];
+        }
+    store_tile<TM, TN, EPI, QPG>(acc, C, ep, M, N, ldc, m0 + wm0, n0 + wn0, lr, h, q0);
+    return;
   }
 
   store_tile<TM, TN, EPI>(acc, C, ep, M, N, ldc, m0 + wm0, n0 + wn0, lr, h);
@@ -623,7 +631,6 @@ gemm_f32_thin_kernel(const float* __restrict__ A, const float* __restrict__ B, f
   constexpr int kLdKn = thin_ld_kn(NB);
   static_assert(!(FLAT && OP == AAR_GEMM_NT), "the flat copy is the [K][N] layout of NN/TN");
   static_assert(kThinParts * kThinSlabs * 64 == kThinThreads, "16 waves: 4 slabs x 4 K parts");
-  static_assert((kThinParts - 1) * kThinSlabs * (NB * 256 + 64) <= kThinLds, "the part combine fits in LDS");
   __shared__ __attribute__((aligned(16))) float lds[kThinLds];
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -728,9 +735,11 @@ gemm_f32_thin_kernel(const float* __restrict__ A, const float* __restrict__ B, f
     }
   }
 
-  // Parts 1..3 hand their sums to part 0 through LDS (B is no longer read),
-  // which adds them in part order.  Accumulator layout of a 16x16 block:
-  // lane (i, q), register r holds row 4q + r, column i.
+  // Every part writes its sums to LDS (B is no longer read); then wave
+  // (slab, p) adds the four parts of column blocks p, p + 4, ... in part
+  // order and stores them, so the combine and the stores are spread over all
+  // 16 waves.  Accumulator layout of a 16x16 block: lane (i, q), register r
+  // holds row 4q + r, column i.
   if constexpr (TAIL) {
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
@@ -742,42 +751,38 @@ gemm_f32_thin_kernel(const float* __restrict__ A, const float* __restrict__ B, f
   // per part and slab: NBM accumulator blocks (256 floats each), then the
   // tail sums of the slab's 16 rows (64 floats)
   constexpr int kSlabFloats = NBM * 256 + (TAIL ? 64 : 0);
-  float* const hand = lds + slab * kSlabFloats;
   constexpr int kPartStride = kThinSlabs * kSlabFloats;
-  if (part > 0) {
+  static_assert(kThinParts * kPartStride <= kThinLds, "the part combine fits in LDS");
+  float* const hand = lds + slab * kSlabFloats;
 #pragma unroll
-    for (int nb = 0; nb < NBM; ++nb)
-      *reinterpret_cast<f32x4*>(hand + (part - 1) * kPartStride + nb * 256 + lane * 4) = acc[nb];
-    if (TAIL && lq == 0) *reinterpret_cast<f32x4*>(hand + (part - 1) * kPartStride + NBM * 256 + li * 4) = tail;
-  }
+  for (int nb = 0; nb < NBM; ++nb)
+    *reinterpret_cast<f32x4*>(hand + part * kPartStride + nb * 256 + lane * 4) = acc[nb];
+  if (TAIL && lq == 0) *reinterpret_cast<f32x4*>(hand + part * kPartStride + NBM * 256 + li * 4) = tail;
   __syncthreads();
-  if (part > 0) return;
+  if (TAIL && part == NBM % kThinParts && lq == 0) {
+    f32x4 t = *reinterpret_cast<const f32x4*>(hand + NBM * 256 + li * 4);
 #pragma unroll
-  for (int p = 1; p < kThinParts; ++p) {
-#pragma unroll
-    for (int nb = 0; nb < NBM; ++nb) {
-      const f32x4 v = *reinterpret_cast<const f32x4*>(hand + (p - 1) * kPartStride + nb * 256 + lane * 4);
-      acc[nb] += v;
-    }
-    if (TAIL) tail += *reinterpret_cast<const f32x4*>(hand + (p - 1) * kPartStride + NBM * 256 + li * 4);
-  }
-  if (TAIL && lq == 0) {
+    for (int q = 1; q < kThinParts; ++q) t += *reinterpret_cast<const f32x4*>(hand + q * kPartStride + NBM * 256 + li * 4);
     const int64_t trow = (int64_t)blockIdx.x * kThinRows + slab * 16 + li;
     if (trow < M) {
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        if (16 * NBM + t < N) C[trow * ldc + 16 * NBM + t] = tail[t];
+      for (int c = 0; c < 4; ++c) {
+        if (16 * NBM + c < N) C[trow * ldc + 16 * NBM + c] = t[c];
       }
     }
   }
   const int64_t r0 = (int64_t)blockIdx.x * kThinRows + slab * 16 + 4 * lq;
 #pragma unroll
   for (int nb = 0; nb < NBM; ++nb) {
+    if (nb % kThinParts != part) continue;
+    f32x4 v = *reinterpret_cast<const f32x4*>(hand + nb * 256 + lane * 4);
+#pragma unroll
+    for (int q = 1; q < kThinParts; ++q) v += *reinterpret_cast<const f32x4*>(hand + q * kPartStride + nb * 256 + lane * 4);
     const int col = 16 * nb + li;
     if (col >= N) continue;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      if (r0 + r < M) C[(r0 + r) * ldc + col] = acc[nb][r];
+      if (r0 + r < M) C[(r0 + r) * ldc + col] = v[r];
     }
   }
 }
