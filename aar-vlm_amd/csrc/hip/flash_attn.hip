@@ -508,10 +508,11 @@ struct FaDmaTile64 {
 // phases of a query tile split its key range and the longest chain of tiles
 // is half that of the 128-query kernel.  S^T takes 128-bit K row reads; O +=
 // V^T P takes one 32-bit V column read per MFMA (the layout of the dK/dV
-// pair kernel's dO^T P product).  At the end phase 1 hands (m, l, O) to
-// phase 0 through LDS, and phase 0 merges the two partial softmaxes in a
-// fixed order (m = max(m0, m1), w_p = 2^(m_p - m), l = w0 l0 + w1 l1,
-// O = w0 O0 + w1 O1; deterministic), normalises and stores O and lse.
+// pair kernel's dO^T P product).  At the end the two phases exchange
+// (m, l) and half of O through LDS, and each merges the two partial
+// softmaxes for its half of O's columns in a fixed order (m = max(m0, m1),
+// w_p = 2^(m_p - m), l = w0 l0 + w1 l1, O = w0 O0 + w1 O1; deterministic),
+// normalises and stores it; phase 0 stores lse.
 // Requires d == DP == 64 and 16-byte aligned rows.
 template <int DP, bool CAUSAL, int STAGES>
 __global__ void __launch_bounds__(kFaThreads, STAGES == 1 ? 3 : 2)
@@ -521,7 +522,7 @@ flash_fwd_pair_kernel(FaIn Qv, FaIn Kv, FaIn Vv, FaOut Ov, float* __restrict__ L
   constexpr int NC = DP / 8;   // head-dim chunks
   constexpr int NB = DP / 32;  // head-dim output blocks
   constexpr int kQueries = 2 * kTile;           // queries per workgroup
-  constexpr int kHand = (NB * 16 + 2) * kWave;  // one wave's O, m and l, lane-major
+  constexpr int kHand = (NB * 16 + 4) * kWave;  // O blocks, then m and l of both phases, lane-major
   using Tile = FaDmaTile64;
   static_assert(STAGES == 1 || STAGES == 2, "one or two staged tile pairs");
   __shared__ __attribute__((aligned(16))) float ks[STAGES][2][Tile::kFloats];  // key tiles t, t + 1
@@ -650,44 +651,54 @@ flash_fwd_pair_kernel(FaIn Qv, FaIn Kv, FaIn Vv, FaOut Ov, float* __restrict__ L
   }
   __syncthreads();
 
-  // Phase 1 hands (O, m, l) of its query tile to phase 0 (every wave is past
-  // the loop's last read of the staged tiles and no DMA is in flight):
-  // query tile 0 through the K tiles, query tile 1 through V.
+  // The two phases of a query tile exchange (O, m, l) through LDS (every
+  // wave is past the loop's last read of the staged tiles and no DMA is in
+  // flight): query tile 0 through the K tiles, query tile 1 through V.  Each
+  // phase merges and stores half of O's column blocks (phase p: blocks
+  // b % 2 == p), so each writes the blocks the other stores, plus its m and
+  // l.  Both compute the merge weights from the same values with the same
+  // operations, so every stored element is w0*O0 + w1*O1 as one phase would
+  // form it.
+  static_assert(NB % 2 == 0, "the column blocks of O split evenly over the two phases");
   float* const hs = qt_local == 0 ? &ks[0][0][0] : &vs[0][0][0];
-  if (phase == 1) {
-#pragma unroll
-    for (int b = 0; b < NB; ++b) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) hs[(b * 16 + r) * kWave + lane] = o[b][r];
-    }
-    hs[(NB * 16) * kWave + lane] = m;
-    hs[(NB * 16 + 1) * kWave + lane] = l;
-  }
-  __syncthreads();
-  if (phase == 1 || qi >= T) return;
-  const float m1 = hs[(NB * 16) * kWave + lane], l1 = hs[(NB * 16 + 1) * kWave + lane];
-  const float mm = fmaxf(m, m1);
-  const float mu = mm == -INFINITY ? 0.f : mm;
-  const float w0 = fast_exp2(m - mu), w1 = fast_exp2(m1 - mu);
-  l = w0 * l + w1 * l1;
 #pragma unroll
   for (int b = 0; b < NB; ++b) {
+    if (b % 2 == phase) continue;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) o[b][r] = w0 * o[b][r] + w1 * hs[(b * 16 + r) * kWave + lane];
+    for (int r = 0; r < 16; ++r) hs[(b * 16 + r) * kWave + lane] = o[b][r];
   }
-  m = mm;
+  hs[(NB * 16 + 2 * phase) * kWave + lane] = m;
+  hs[(NB * 16 + 2 * phase + 1) * kWave + lane] = l;
+  __syncthreads();
+  if (qi >= T) return;
+  const float mo = hs[(NB * 16 + 2 * (1 - phase)) * kWave + lane];
+  const float lo = hs[(NB * 16 + 2 * (1 - phase) + 1) * kWave + lane];
+  const float m0 = phase == 0 ? m : mo, l0 = phase == 0 ? l : lo;
+  const float m1 = phase == 0 ? mo : m, l1 = phase == 0 ? lo : l;
+  const float mm = fmaxf(m0, m1);
+  const float mu = mm == -INFINITY ? 0.f : mm;
+  const float w0 = fast_exp2(m0 - mu), w1 = fast_exp2(m1 - mu);
+  l = fmaf(w0, l0, w1 * l1);
   const float inv_l = 1.0f / l;
   float* orow = Ov.head(bh, H) + (int64_t)qi * Ov.st;
 #pragma unroll
   for (int b = 0; b < NB; ++b) {
+    if (b % 2 != phase) continue;
+    float ob[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const float x = o[b][r], y = hs[(b * 16 + r) * kWave + lane];
+      const float o0 = phase == 0 ? x : y, o1 = phase == 0 ? y : x;
+      ob[r] = fmaf(w0, o0, w1 * o1);  // w0 O0 + w1 O1, one form in both phases
+    }
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       const int dd = b * 32 + 8 * g + 4 * h;
-      f32x4 v = {o[b][4 * g] * inv_l, o[b][4 * g + 1] * inv_l, o[b][4 * g + 2] * inv_l, o[b][4 * g + 3] * inv_l};
+      f32x4 v = {ob[4 * g] * inv_l, ob[4 * g + 1] * inv_l, ob[4 * g + 2] * inv_l, ob[4 * g + 3] * inv_l};
       *reinterpret_cast<f32x4*>(orow + dd) = v;
     }
   }
-  if (h == 0) Lse[(int64_t)bh * T + qi] = (m + log2f(l)) * kLn2;
+  if (phase == 0 && h == 0) Lse[(int64_t)bh * T + qi] = (mm + log2f(l)) * kLn2;
 }
 
 // Merge of the two halves of every split row: with L_p = m_p + log2(l_p) and
@@ -941,8 +952,8 @@ flash_bwd_dkdv_kernel(FaIn Qv, FaIn Kv, FaIn Vv, FaIn dOv, const float* __restri
 // query range in step and each works half of it.  Against 128-key
 // workgroups this halves the longest work item and the idle diagonal steps
 // (causal T = 256, 384 heads: 8 instead of 12 rounds of tile work on 512
-// slots).  At the end phase 1 hands its dK/dV accumulators to phase 0
-// through LDS, and phase 0 adds them (phase 0 + phase 1, a fixed order):
+// slots).  At the end the two phases of a key tile add their accumulators
+// through LDS (phase 0 finishes dK, phase 1 dV; each a sum of two terms):
 // deterministic, no atomics.  Stored dS tiles are written exactly as by
 // flash_bwd_dkdv_kernel.
 //
@@ -1105,44 +1116,54 @@ flash_bwd_dkdv_pair_kernel(FaIn Qv, FaIn Kv, FaIn Vv, FaIn dOv, const float* __r
     ring_barrier();
   }
 
-  // Phase 1 hands its accumulators to phase 0 of the same key tile through
-  // the staging buffers (every wave is past the loop's last barrier, no DMA
-  // is in flight): dK in qs[0][kt_local], dV in dos[0][kt_local], lane-major
-  // so the writes and reads are conflict free.
+  // The two phases of a key tile exchange halves of their accumulators
+  // through the staging buffers (every wave is past the loop's last barrier,
+  // no DMA is in flight), lane-major so the writes and reads are conflict
+  // free: phase 1 hands its dK to phase 0 (qs[0][kt_local]), which adds and
+  // stores dK; phase 0 hands its dV to phase 1 (dos[0][kt_local]), which
+  // adds and stores dV.  Each sum has two terms, so it is the same in either
+  // order.
   float* hk = qs[0][kt_local];
   float* hv = dos[0][kt_local];
-  if (phase == 1) {
 #pragma unroll
-    for (int b = 0; b < NB; ++b) {
+  for (int b = 0; b < NB; ++b) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
+    for (int r = 0; r < 16; ++r) {
+      if (phase == 1) {
         hk[(b * 16 + r) * kWave + lane] = dk[b][r];
+      } else {
         hv[(b * 16 + r) * kWave + lane] = dv[b][r];
       }
     }
   }
   __syncthreads();
-  if (phase == 1 || !key_ok) return;
+  if (!key_ok) return;
+  if (phase == 0) {
+    float* krow = dKv.head(bh, H) + (int64_t)kj * dKv.st;
 #pragma unroll
-  for (int b = 0; b < NB; ++b) {
+    for (int b = 0; b < NB; ++b) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      dk[b][r] += hk[(b * 16 + r) * kWave + lane];
-      dv[b][r] += hv[(b * 16 + r) * kWave + lane];
+      for (int r = 0; r < 16; ++r) dk[b][r] += hk[(b * 16 + r) * kWave + lane];
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int dd = b * 32 + 8 * g + 4 * h;
+        f32x4 a = {dk[b][4 * g] * scale, dk[b][4 * g + 1] * scale, dk[b][4 * g + 2] * scale,
+                   dk[b][4 * g + 3] * scale};
+        *reinterpret_cast<f32x4*>(krow + dd) = a;
+      }
     }
-  }
-  float* krow = dKv.head(bh, H) + (int64_t)kj * dKv.st;
-  float* vrow = dVv.head(bh, H) + (int64_t)kj * dVv.st;
+  } else {
+    float* vrow = dVv.head(bh, H) + (int64_t)kj * dVv.st;
 #pragma unroll
-  for (int b = 0; b < NB; ++b) {
+    for (int b = 0; b < NB; ++b) {
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const int dd = b * 32 + 8 * g + 4 * h;
-      f32x4 a = {dk[b][4 * g] * scale, dk[b][4 * g + 1] * scale, dk[b][4 * g + 2] * scale,
-                 dk[b][4 * g + 3] * scale};
-      f32x4 c = {dv[b][4 * g], dv[b][4 * g + 1], dv[b][4 * g + 2], dv[b][4 * g + 3]};
-      *reinterpret_cast<f32x4*>(krow + dd) = a;
-      *reinterpret_cast<f32x4*>(vrow + dd) = c;
+      for (int r = 0; r < 16; ++r) dv[b][r] = hv[(b * 16 + r) * kWave + lane] + dv[b][r];
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int dd = b * 32 + 8 * g + 4 * h;
+        f32x4 c = {dv[b][4 * g], dv[b][4 * g + 1], dv[b][4 * g + 2], dv[b][4 * g + 3]};
+        *reinterpret_cast<f32x4*>(vrow + dd) = c;
+      }
     }
   }
 }
@@ -1355,9 +1376,9 @@ flash_bwd_dq_ds_kernel(FaIn Kv, const float* __restrict__ dS, FaOut dQv, int T, 
 // longest work item is half that of a 128-query workgroup.  dQ^T += K^T dS^T
 // reads K columns with 32-bit conflict-free reads (the layout of the dK/dV
 // pair kernel's dO^T P product); each wave's dS tile of the next pair is
-// loaded into registers during the current one.  At the end phase 1 hands
-// its dQ accumulators to phase 0 through LDS and phase 0 adds them (phase 0
-// + phase 1, a fixed order; deterministic).  Requires d == DP == 64 and
+// loaded into registers during the current one.  At the end the two phases
+// of a query tile add their dQ accumulators through LDS, each phase
+// finishing half of the column blocks (a sum of two terms; deterministic).  Requires d == DP == 64 and
 // 16-byte aligned rows.
 template <int DP, bool CAUSAL>
 __global__ void __launch_bounds__(kFaThreads, 4)
@@ -1442,28 +1463,28 @@ flash_bwd_dq_ds_pair_kernel(FaIn Kv, const float* __restrict__ dS, FaOut dQv, in
     ring_barrier();
   }
 
-  // Phase 1 hands its dQ accumulators to phase 0 of the same query tile
+  // The two phases of a query tile exchange halves of their dQ accumulators
   // through the staging buffers (every wave is past the loop's last barrier
   // and no DMA is in flight), lane-major so the writes and reads are
-  // conflict free.
+  // conflict free: phase p adds and stores the column blocks b % 2 == p and
+  // hands the others over.  Each sum has two terms, so it is the same in
+  // either order.
+  static_assert(NB % 2 == 0, "the column blocks of dQ split evenly over the two phases");
   float* hq = &ks[0][0][0] + qt_local * (NB * 16 * kWave);
-  if (phase == 1) {
-#pragma unroll
-    for (int b = 0; b < NB; ++b) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) hq[(b * 16 + r) * kWave + lane] = dq[b][r];
-    }
-  }
-  __syncthreads();
-  if (phase == 1 || qi >= T) return;
 #pragma unroll
   for (int b = 0; b < NB; ++b) {
+    if (b % 2 == phase) continue;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) dq[b][r] += hq[(b * 16 + r) * kWave + lane];
+    for (int r = 0; r < 16; ++r) hq[(b * 16 + r) * kWave + lane] = dq[b][r];
   }
+  __syncthreads();
+  if (qi >= T) return;
   float* qrow = dQv.head(bh, H) + (int64_t)qi * dQv.st;
 #pragma unroll
   for (int b = 0; b < NB; ++b) {
+    if (b % 2 != phase) continue;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) dq[b][r] += hq[(b * 16 + r) * kWave + lane];
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       const int dd = b * 32 + 8 * g + 4 * h;
