@@ -136,6 +136,24 @@ def test_odd_widths_vs_oracle(gpu, rows, cols):
     assert_close(host(gpu, tb.grad), db, TOL, "ln db")
 
 
+@pytest.mark.parametrize("rows,cols", [(3, 140000), (2, 140001)])
+def test_layernorm_backward_wide_reduce_grid(gpu, rows, cols):
+    """Rows so wide that the dgamma/dbeta reduce has more column blocks (70000
+    float4 blocks; 280002 single columns) than its 2^16-workgroup grid, which
+    then strides over them.  Layernorm only: at 140001 columns the oracle's
+    sequential softmax sum carries more rounding than the tolerance."""
+    x, w, b, g = config3_inputs(rows, cols, seed=rows * 31 + cols)
+    tx, tw, tb = dev(gpu, x, True), dev(gpu, w, True), dev(gpu, b, True)
+    yl = gpu.layernorm(tx, tw, tb, 1e-5)
+    yl.backward(dev(gpu, g))
+    yl_ref, mu, rs = O.layernorm(x, w, b, 1e-5, stats=True)
+    dx, dw, db = O.layernorm_backward(g, x, w, mu, rs)
+    assert_close(host(gpu, yl), yl_ref, TOL, "ln")
+    assert_close(host(gpu, tx.grad), dx, TOL, "ln dx")
+    assert_close(host(gpu, tw.grad), dw, TOL, "ln dw")
+    assert_close(host(gpu, tb.grad), db, TOL, "ln db")
+
+
 def test_layernorm_no_grad_matches_with_stats(gpu):
     x, w, b, _ = config3_inputs(1000, 384, seed=4)
     y0 = host(gpu, gpu.layernorm(dev(gpu, x), dev(gpu, w), dev(gpu, b)))
