@@ -38,7 +38,6 @@
 #include <math.h>
 
 #include <algorithm>
-#include <atomic>
 #include <initializer_list>
 #include <stdint.h>
 
@@ -1525,6 +1524,7 @@ struct FwdArgs {
   float scale;
   void* ws;  // split partials when non-null and large enough
   size_t ws_bytes;
+  int query_block;  // queries per workgroup: 64 (paired kernel) or 128
   hipStream_t st;
 };
 
@@ -1602,12 +1602,11 @@ int fa_fwd_resident() {
 // (T = 256..4096), 0.91-0.93x at R = 2 and 0.98x at R = 4 for T <= 1024, but
 // 1.01x at R = 4, T = 4096 and at R = 8, T = 256.  So: paired up to two
 // rounds, and up to four for T <= 1024.  It is built for causal d = 64
-// exactly, with 128-bit operands; other shapes take 128.  A process-wide
-// override (aar_flash_set_fwd_query_block) serves tuning and tests.
-std::atomic<int> g_fwd_query_block_override{0};
-int fa_fwd_query_block(int64_t bh, int64_t T, int64_t d, bool causal, bool vec) {
+// exactly, with 128-bit operands; other shapes take 128.  `forced` (64 or
+// 128, from a caller's per-call plan; 0 = none) overrides the choice for
+// the shapes that can take either.
+int fa_fwd_query_block(int64_t bh, int64_t T, int64_t d, bool causal, bool vec, int forced = 0) {
   if (!causal || d != 64 || !vec) return kBlock;
-  const int forced = g_fwd_query_block_override.load(std::memory_order_relaxed);
   if (forced) return forced;
   const int64_t slots = (int64_t)device_cu_count() * fa_fwd_resident<64, true>();
   const int64_t grid = bh * ((T + kBlock - 1) / kBlock);
@@ -1620,7 +1619,7 @@ struct FwdLaunch {
     if constexpr (C && VEC && DP == 64) {
       const int64_t nqb64 = (a.T + 2 * kTile - 1) / (2 * kTile);
       // (a dispatch holds the grid as a 32-bit work-item count)
-      if (fa_fwd_query_block(a.BH, a.T, a.d, true, true) == 64 && nqb64 * a.BH * kFaThreads <= (int64_t)UINT32_MAX) {
+      if (a.query_block == 64 && nqb64 * a.BH * kFaThreads <= (int64_t)UINT32_MAX) {
         if (a.T <= 1024) {
           flash_fwd_pair_kernel<DP, C, 1><<<dim3((unsigned)(nqb64 * a.BH)), dim3(kFaThreads), 0, a.st>>>(
               a.q, a.k, a.v, a.o, a.lse, a.T, a.H, (int)nqb64, a.BH, a.scale * kLog2e);
@@ -1693,12 +1692,11 @@ int fa_dkdv_resident() {
 // resident workgroups (short sequences, few heads) its longest items set the
 // time, and the paired 64-key kernel (half the longest item) is used instead.
 // The paired kernel stages its tiles by DMA in a layout built for d = 64
-// exactly, with 128-bit operands; other shapes take 128-key workgroups.  A process-wide
-// override (aar_flash_set_bwd_key_block) serves tuning and tests.
-std::atomic<int> g_bwd_key_block_override{0};
-int fa_bwd_key_block(int64_t bh, int64_t T, int64_t d, bool causal, bool vec) {
+// exactly, with 128-bit operands; other shapes take 128-key workgroups.
+// `forced` (64 or 128, from a caller's per-call plan; 0 = none) overrides
+// the choice for the shapes that can take either.
+int fa_bwd_key_block(int64_t bh, int64_t T, int64_t d, bool causal, bool vec, int forced = 0) {
   if (d != 64 || !vec) return 128;
-  const int forced = g_bwd_key_block_override.load(std::memory_order_relaxed);
   if (forced) return forced;
   const int resident =
       causal ? fa_dkdv_resident<64, true, true, false>() : fa_dkdv_resident<64, false, true, false>();
@@ -1795,10 +1793,11 @@ extern "C" size_t aar_flash_fwd_workspace_bytes(int64_t bh, int64_t T, int64_t d
   return fa_fwd_split_bytes(bh, T, d);
 }
 
-extern "C" int aar_flash_fwd_strided_f32(const float* q, const float* k, const float* v, float* o, float* lse,
-                                         int64_t B, int64_t H, int64_t T, int64_t d, const int64_t* strides,
-                                         int causal, float scale, void* workspace, size_t workspace_bytes,
-                                         void* stream) {
+extern "C" int aar_flash_fwd_strided_plan_f32(const float* q, const float* k, const float* v, float* o,
+                                              float* lse, int64_t B, int64_t H, int64_t T, int64_t d,
+                                              const int64_t* strides, int causal, float scale, int query_block,
+                                              void* workspace, size_t workspace_bytes, void* stream) {
+  if (query_block != 0 && query_block != 64 && query_block != 128) return AAR_EINVAL;
   if (B < 0 || H < 0 || T < 0 || d <= 0) return AAR_EINVAL;
   if (d > 128) return AAR_EINVAL;
   if (B == 0 || H == 0 || T == 0) return AAR_OK;
@@ -1808,8 +1807,16 @@ extern "C" int aar_flash_fwd_strided_f32(const float* q, const float* k, const f
   FwdArgs a{fa_in(q, strides),      fa_in(k, strides + 3), fa_in(v, strides + 6), fa_out(o, strides + 9),
             lse,                    (int)T,                (int)d,                (int)H,
             (int)(B * H),           scale,                 workspace,             workspace_bytes,
-            as_stream(stream)};
+            fa_fwd_query_block(B * H, T, d, causal != 0, vec, query_block), as_stream(stream)};
   return dispatch_fa<FwdLaunch>(pad_dim(d), causal != 0, vec, a);
+}
+
+extern "C" int aar_flash_fwd_strided_f32(const float* q, const float* k, const float* v, float* o, float* lse,
+                                         int64_t B, int64_t H, int64_t T, int64_t d, const int64_t* strides,
+                                         int causal, float scale, void* workspace, size_t workspace_bytes,
+                                         void* stream) {
+  return aar_flash_fwd_strided_plan_f32(q, k, v, o, lse, B, H, T, d, strides, causal, scale, 0, workspace,
+                                        workspace_bytes, stream);
 }
 
 extern "C" int aar_flash_fwd_f32(const float* q, const float* k, const float* v, float* o, float* lse,
@@ -1842,11 +1849,12 @@ extern "C" size_t aar_flash_bwd_fast_workspace_bytes(int64_t bh, int64_t T, int6
   return fa_d_bytes(bh, T) + (size_t)bh * (size_t)ds_pairs(nt, causal != 0) * kDsTile * sizeof(float);
 }
 
-extern "C" int aar_flash_bwd_strided_f32(const float* q, const float* k, const float* v, const float* o,
-                                         const float* lse, const float* dout, float* dq, float* dk, float* dv,
-                                         int64_t B, int64_t H, int64_t T, int64_t d, const int64_t* strides,
-                                         int causal, float scale, void* workspace, size_t workspace_bytes,
-                                         void* stream) {
+extern "C" int aar_flash_bwd_strided_plan_f32(const float* q, const float* k, const float* v, const float* o,
+                                              const float* lse, const float* dout, float* dq, float* dk,
+                                              float* dv, int64_t B, int64_t H, int64_t T, int64_t d,
+                                              const int64_t* strides, int causal, float scale, int key_block,
+                                              void* workspace, size_t workspace_bytes, void* stream) {
+  if (key_block != 0 && key_block != 64 && key_block != 128) return AAR_EINVAL;
   if (B < 0 || H < 0 || T < 0 || d <= 0) return AAR_EINVAL;
   if (d > 128) return AAR_EINVAL;
   if (B == 0 || H == 0 || T == 0) return AAR_OK;
@@ -1878,8 +1886,17 @@ extern "C" int aar_flash_bwd_strided_f32(const float* q, const float* k, const f
             fa_out(dq, strides + 15),   fa_out(dk, strides + 18),   fa_out(dv, strides + 21),
             dS,                         (int)T,                     (int)d,
             (int)H,                     (int)bh,                    scale,
-            fa_bwd_key_block(bh, T, d, causal != 0, vec),  st};
+            fa_bwd_key_block(bh, T, d, causal != 0, vec, key_block),  st};
   return dispatch_fa<BwdLaunch>(pad_dim(d), causal != 0, vec, a);
+}
+
+extern "C" int aar_flash_bwd_strided_f32(const float* q, const float* k, const float* v, const float* o,
+                                         const float* lse, const float* dout, float* dq, float* dk, float* dv,
+                                         int64_t B, int64_t H, int64_t T, int64_t d, const int64_t* strides,
+                                         int causal, float scale, void* workspace, size_t workspace_bytes,
+                                         void* stream) {
+  return aar_flash_bwd_strided_plan_f32(q, k, v, o, lse, dout, dq, dk, dv, B, H, T, d, strides, causal, scale, 0,
+                                        workspace, workspace_bytes, stream);
 }
 
 extern "C" int aar_flash_bwd_f32(const float* q, const float* k, const float* v, const float* o,
@@ -1925,22 +1942,10 @@ extern "C" int aar_flash_bwd_plan(int64_t bh, int64_t T, int64_t d, int causal, 
   return AAR_OK;
 }
 
-extern "C" int aar_flash_set_bwd_key_block(int key_block) {
-  if (key_block != 0 && key_block != 64 && key_block != 128) return AAR_EINVAL;
-  g_bwd_key_block_override.store(key_block, std::memory_order_relaxed);
-  return AAR_OK;
-}
-
 extern "C" int aar_flash_fwd_query_block(int64_t bh, int64_t T, int64_t d, int causal, int vec, int* query_block) {
   if (!query_block || bh <= 0 || T <= 0 || d <= 0) return AAR_EINVAL;
   if (d > 128) return AAR_EINVAL;
   if (!fa_shape_ok(bh, T, d)) return AAR_EUNSUPPORTED;
   *query_block = fa_fwd_query_block(bh, T, d, causal != 0, vec != 0);
-  return AAR_OK;
-}
-
-extern "C" int aar_flash_set_fwd_query_block(int query_block) {
-  if (query_block != 0 && query_block != 64 && query_block != 128) return AAR_EINVAL;
-  g_fwd_query_block_override.store(query_block, std::memory_order_relaxed);
   return AAR_OK;
 }

@@ -283,22 +283,36 @@ int aar_flash_bwd_strided_f32(const float* q, const float* k, const float* v,
  * splits over two workgroups given `workspace_bytes` of workspace (0: none).
  * aar_flash_bwd_plan: keys per dK/dV workgroup, 64 (the paired kernel: two
  * query phases per key tile, for grids of about one round) or 128.
- * aar_flash_set_bwd_key_block forces that choice for later calls in this
- * process (64 or 128; 0 restores the plan; head dims above 64 always take
- * 128); backward calls running on other threads meanwhile may see either.
  * aar_flash_fwd_query_block: queries per forward workgroup, 64 (the paired
  * kernel: two key phases per query tile, for causal grids of up to two
  * rounds of resident 128-query workgroups, four when T <= 1024) or 128; when
  * it is 64 the forward does not split and aar_flash_fwd_plan's count does not
- * apply.
- * aar_flash_set_fwd_query_block forces it likewise (64 or 128; 0 restores
- * the plan; only causal d = 64 with 128-bit operands can take 64). */
+ * apply.  The library keeps no plan state: these are pure functions of the
+ * shape and the device. */
 int aar_flash_fwd_plan(int64_t bh, int64_t T, int64_t d, int causal, int vec, size_t workspace_bytes,
                        int* split_blocks);
 int aar_flash_bwd_plan(int64_t bh, int64_t T, int64_t d, int causal, int vec, int* key_block);
-int aar_flash_set_bwd_key_block(int key_block);
 int aar_flash_fwd_query_block(int64_t bh, int64_t T, int64_t d, int causal, int vec, int* query_block);
-int aar_flash_set_fwd_query_block(int query_block);
+
+/* The strided calls with the plan forced for this call only (tuning and
+ * tests; no counterpart in the reference).  query_block / key_block: 64 or
+ * 128 forces the forward's queries per workgroup / the backward's keys per
+ * dK/dV workgroup, 0 takes the planner's choice (the plain strided calls pass
+ * 0); other values are AAR_EINVAL.  Only shapes that can take either plan are
+ * forced (causal d = 64 with 128-bit operands for the forward, d = 64 with
+ * 128-bit operands for the backward); others keep 128.  Calls on other
+ * threads are unaffected. */
+int aar_flash_fwd_strided_plan_f32(const float* q, const float* k, const float* v,
+                                   float* o, float* lse, int64_t B, int64_t H,
+                                   int64_t T, int64_t d, const int64_t* strides,
+                                   int causal, float scale, int query_block,
+                                   void* workspace, size_t workspace_bytes, void* stream);
+int aar_flash_bwd_strided_plan_f32(const float* q, const float* k, const float* v,
+                                   const float* o, const float* lse, const float* dout,
+                                   float* dq, float* dk, float* dv,
+                                   int64_t B, int64_t H, int64_t T, int64_t d,
+                                   const int64_t* strides, int causal, float scale, int key_block,
+                                   void* workspace, size_t workspace_bytes, void* stream);
 
 /* Strided fp32 copy of an ndim <= 8 view: dst[idx] = src[idx] for every index
  * of `shape`, element offsets given by the two stride arrays (host arrays, read

@@ -53,6 +53,13 @@ class Abi:
         L.aar_flash_bwd_f32.argtypes = [vp] * 9 + [i64, i64, i64, ctypes.c_int, ctypes.c_float, vp, sz, vp]
         L.aar_flash_bwd_fast_workspace_bytes.restype = sz
         L.aar_flash_bwd_fast_workspace_bytes.argtypes = [i64, i64, i64, ctypes.c_int]
+        L.aar_flash_fwd_workspace_bytes.restype = sz
+        L.aar_flash_fwd_workspace_bytes.argtypes = [i64, i64, i64, ctypes.c_int]
+        pi64 = ctypes.POINTER(i64)
+        L.aar_flash_fwd_strided_plan_f32.argtypes = [vp] * 5 + [i64] * 4 + [pi64, ctypes.c_int, ctypes.c_float,
+                                                                            ctypes.c_int, vp, sz, vp]
+        L.aar_flash_bwd_strided_plan_f32.argtypes = [vp] * 9 + [i64] * 4 + [pi64, ctypes.c_int, ctypes.c_float,
+                                                                            ctypes.c_int, vp, sz, vp]
         L.aar_add_f32.argtypes = [vp, vp, vp, i64, vp]
         L.aar_strided_copy_f32.argtypes = [vp, vp, ctypes.c_int, ctypes.POINTER(i64), ctypes.POINTER(i64),
                                            ctypes.POINTER(i64), vp]
@@ -91,3 +98,34 @@ class Abi:
         for p in self._bufs:
             self.L.aar_free(p)
         self._bufs.clear()
+
+
+def abi_flash(q, k, v, do, causal, query_block=0, key_block=0, fast=True, abi=None):
+    """Forward (O, lse) and backward (dq, dk, dv) of [bh, T, d] operands
+    through the C ABI's per-call plan entry points: query_block / key_block
+    64 or 128 force the forward's / backward's decomposition for these calls
+    only (0: the planner's).  The forward gets its split workspace; `fast`
+    gives the backward the stored-dS workspace, else the minimum (recompute
+    path)."""
+    bh, T, d = q.shape
+    own = abi is None
+    abi = abi if abi is not None else Abi()
+    L = abi.L
+    try:
+        pq, pk, pv, pdo = (abi.put(t) for t in (q, k, v, do))
+        po, pl = abi.empty(bh * T * d), abi.empty(bh * T)
+        s = 1.0 / float(np.sqrt(d))
+        st = (ctypes.c_int64 * 24)(*([bh * T * d, T * d, d] * 8))
+        fw = L.aar_flash_fwd_workspace_bytes(bh, T, d, int(causal))
+        abi.check(L.aar_flash_fwd_strided_plan_f32(pq, pk, pv, po, pl, 1, bh, T, d, st, int(causal), s, query_block,
+                                                   abi.alloc(fw) if fw else None, fw, None))
+        o, lse = abi.get(po, (bh, T, d)), abi.get(pl, (bh, T))
+        wsb = (L.aar_flash_bwd_fast_workspace_bytes(bh, T, d, int(causal)) if fast
+               else L.aar_flash_bwd_workspace_bytes(bh, T, d))
+        pdq, pdk, pdv = (abi.empty(bh * T * d) for _ in range(3))
+        abi.check(L.aar_flash_bwd_strided_plan_f32(pq, pk, pv, po, pl, pdo, pdq, pdk, pdv, 1, bh, T, d, st,
+                                                   int(causal), s, key_block, abi.alloc(wsb), wsb, None))
+        return o, lse, [abi.get(p, (bh, T, d)) for p in (pdq, pdk, pdv)]
+    finally:
+        if own:
+            abi.free()

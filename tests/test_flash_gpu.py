@@ -13,7 +13,7 @@ import pytest
 
 import oracle as O
 from conftest import TOL, assert_close
-from devutil import Abi, dev, host
+from devutil import Abi, abi_flash, dev, host
 
 pytestmark = pytest.mark.gpu
 f32 = np.float32
@@ -440,9 +440,7 @@ def _flash_plans():
                                      ctypes.c_size_t, ip]
     L.aar_flash_fwd_workspace_bytes.restype = ctypes.c_size_t
     L.aar_flash_fwd_workspace_bytes.argtypes = [ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int]
-    L.aar_flash_set_bwd_key_block.argtypes = [ctypes.c_int]
     L.aar_flash_fwd_query_block.argtypes = L.aar_flash_bwd_plan.argtypes
-    L.aar_flash_set_fwd_query_block.argtypes = [ctypes.c_int]
     return L
 
 
@@ -472,16 +470,6 @@ def test_flash_plans(gpu):
     assert _bwd_plan(L, 8, 256, 64, True, vec=0) == 128
     out = ctypes.c_int()
     assert L.aar_flash_bwd_plan(8, 256, 200, 1, 1, ctypes.byref(out)) == -1
-    assert L.aar_flash_set_bwd_key_block(96) == -1
-    try:
-        assert L.aar_flash_set_bwd_key_block(128) == 0
-        assert _bwd_plan(L, 384, 256, 64, True) == 128
-        assert L.aar_flash_set_bwd_key_block(64) == 0
-        assert _bwd_plan(L, 96, 4096, 64, True) == 64
-        assert _bwd_plan(L, 8, 256, 128, True) == 128  # other head dims never pair
-        assert _bwd_plan(L, 8, 256, 32, True) == 128
-    finally:
-        L.aar_flash_set_bwd_key_block(0)
     # forward split: with its workspace, a small causal grid splits, a full one does not
     for bh, T, want_split in ((2, 2048, True), (12, 1024, True), (96, 1024, True), (192, 512, False),
                               (96, 4096, False)):
@@ -504,17 +492,25 @@ def test_flash_plans(gpu):
         assert _fwd_qb(L, 8, 256, d, True) == 128
     assert _fwd_qb(L, 8, 256, 64, True, vec=0) == 128
     assert L.aar_flash_fwd_query_block(8, 256, 200, 1, 1, ctypes.byref(out)) == -1
-    assert L.aar_flash_set_fwd_query_block(96) == -1
-    try:
-        assert L.aar_flash_set_fwd_query_block(128) == 0
-        assert _fwd_qb(L, 384, 256, 64, True) == 128
-        assert L.aar_flash_set_fwd_query_block(64) == 0
-        assert _fwd_qb(L, 96, 4096, 64, True) == 64
-        assert _fwd_qb(L, 8, 256, 128, True) == 128   # other head dims never pair
-        assert _fwd_qb(L, 8, 256, 48, True) == 128
-        assert _fwd_qb(L, 8, 256, 64, False) == 128   # nor non-causal attention
-    finally:
-        L.aar_flash_set_fwd_query_block(0)
+
+
+def test_forced_plan_is_per_call(gpu):
+    """The plan entry points reject block sizes other than 0/64/128 before
+    any launch, and forcing a plan for one call leaves the planner's answer
+    (and so every later unforced call) unchanged: the library holds no plan
+    state."""
+    L = _flash_plans()
+    bh, T, d = 4, 96, 64
+    rng = np.random.default_rng(3)
+    q, k, v, do = (rng.standard_normal((bh, T, d)).astype(f32) for _ in range(4))
+    for bad in (96, -1, 1):
+        with pytest.raises(RuntimeError):
+            abi_flash(q, k, v, do, True, query_block=bad)
+        with pytest.raises(RuntimeError):
+            abi_flash(q, k, v, do, True, key_block=bad)
+    before = (_fwd_qb(L, 384, 256, 64, True), _bwd_plan(L, 384, 256, 64, True))
+    abi_flash(q, k, v, do, True, query_block=128, key_block=128)
+    assert (_fwd_qb(L, 384, 256, 64, True), _bwd_plan(L, 384, 256, 64, True)) == before == (64, 64)
 
 
 @pytest.mark.parametrize("query_block", [64, 128])
@@ -530,16 +526,9 @@ def test_fwd_query_blocks_vs_oracle(gpu, query_block, bh, T, d):
     L = _flash_plans()
     rng = np.random.default_rng(bh * 131 + T + d + query_block)
     q, k, v, do = (rng.standard_normal((bh, T, d)).astype(f32) for _ in range(4))
-    try:
-        assert L.aar_flash_set_fwd_query_block(query_block) == 0
-        assert _fwd_qb(L, bh, T, d, True) == (query_block if d == 64 else 128)  # pairs at d = 64 only
-        runs = [gpu._core._flash_attention_fwd(dev(gpu, q), dev(gpu, k), dev(gpu, v), True) for _ in range(2)]
-        tq, tk, tv = dev(gpu, q, True), dev(gpu, k, True), dev(gpu, v, True)
-        gpu.flash_attention(tq, tk, tv, True).backward(dev(gpu, do))
-        grads = [host(gpu, t.grad) for t in (tq, tk, tv)]
-    finally:
-        L.aar_flash_set_fwd_query_block(0)
-    (o, lse), (o2, lse2) = [(host(gpu, a), host(gpu, b)) for a, b in runs]
+    assert _fwd_qb(L, bh, T, d, True) in (64, 128)
+    o, lse, grads = abi_flash(q, k, v, do, True, query_block=query_block)
+    o2, lse2, _ = abi_flash(q, k, v, do, True, query_block=query_block)
     np.testing.assert_array_equal(o, o2)
     np.testing.assert_array_equal(lse, lse2)
     assert_close(o, O.attention(q, k, v, True), TOL, f"O (query block {query_block})")
@@ -559,15 +548,10 @@ def test_dkdv_key_blocks_vs_oracle(gpu, key_block, bh, T, d, causal):
     bit for bit; with 128-key blocks both dQ passes also run the key tiles in
     one sequential order (bit for bit), while the paired dQ pass sums two key
     phases and agrees with the recompute pass to rounding."""
-    L = _flash_plans()
     rng = np.random.default_rng(bh * 977 + T + d + causal)
     q, k, v, do = (rng.standard_normal((bh, T, d)).astype(f32) for _ in range(4))
-    try:
-        assert L.aar_flash_set_bwd_key_block(key_block) == 0
-        assert _bwd_plan(L, bh, T, d, causal) == key_block
-        o, slow, fast = _abi_bwd_both_paths(q, k, v, do, causal)
-    finally:
-        L.aar_flash_set_bwd_key_block(0)
+    o, _, fast = abi_flash(q, k, v, do, causal, key_block=key_block, fast=True)
+    _, _, slow = abi_flash(q, k, v, do, causal, key_block=key_block, fast=False)
     assert_close(o, O.attention(q, k, v, causal), TOL, "O")
     ref = O.attention_backward(q, k, v, do, causal)
     for g, r, n in zip(fast, ref, ("dq", "dk", "dv")):

@@ -75,3 +75,44 @@ def test_deferred_device_error_is_cleared_once_raised(gpu):
     with pytest.raises(IndexError):
         host(gpu, gpu.embedding(w, bad))
     np.testing.assert_array_equal(host(gpu, gpu.embedding(w, good)), np.ones((8, 4), f32))
+
+
+def test_forced_flash_plan_on_one_thread_leaves_another_on_the_default(gpu):
+    """One thread runs the flash calls with a forced plan (128-query forward,
+    128-key backward) through the C ABI's per-call plan entry points while
+    another runs the same shape with the planner's choice (the paired 64-query
+    and 64-key kernels at this shape).  The forced plan is an argument of the
+    call, not library state, so each thread's results equal its own serial
+    run bit for bit; the two plans themselves differ in rounding, so a plan
+    leaking across threads would show."""
+    from devutil import abi_flash
+
+    rng = np.random.default_rng(17)
+    q, k, v, do = (rng.standard_normal((8, 256, 64)).astype(f32) for _ in range(4))
+    forced = abi_flash(q, k, v, do, True, query_block=128, key_block=128)
+    default = abi_flash(q, k, v, do, True)
+    assert any(not np.array_equal(a, b) for a, b in zip([forced[0]] + forced[2], [default[0]] + default[2]))
+    results, errors = {"forced": [], "default": []}, []
+
+    def run(name, kw):
+        try:
+            for _ in range(12):
+                results[name].append(abi_flash(q, k, v, do, True, **kw))
+        except Exception as e:  # noqa: BLE001 - reported below
+            errors.append(repr(e))
+
+    threads = [threading.Thread(target=run, args=("forced", {"query_block": 128, "key_block": 128})),
+               threading.Thread(target=run, args=("default", {}))]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join(timeout=120)
+    assert not errors, errors
+    assert all(not t.is_alive() for t in threads)
+    for name, ref in (("forced", forced), ("default", default)):
+        assert len(results[name]) == 12
+        for o, lse, grads in results[name]:
+            np.testing.assert_array_equal(o, ref[0])
+            np.testing.assert_array_equal(lse, ref[1])
+            for g, r in zip(grads, ref[2]):
+                np.testing.assert_array_equal(g, r)
