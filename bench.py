@@ -113,14 +113,15 @@ def cpu_model() -> str:
 
 
 def load_traffic(name: str):
-    """HBM bytes per launch measured by rocprofv3 --pmc (FETCH_SIZE +
-    WRITE_SIZE, scaled by the copy-kernel calibration), committed under
-    profiles/ as JSON; None when not measured."""
+    """L2-to-fabric bytes per launch measured by rocprofv3 --pmc (FETCH_SIZE
+    + WRITE_SIZE count L2 misses and write-backs, scaled by the copy-kernel
+    calibration), committed under profiles/ as JSON; None when not
+    measured."""
     p = REPO / "profiles" / f"{name}_traffic.json"
     if not p.exists():
         return None
     try:
-        return float(json.loads(p.read_text())["hbm_bytes_per_launch"])
+        return float(json.loads(p.read_text())["l2_fabric_bytes_per_launch"])
     except (KeyError, ValueError):
         return None
 
@@ -366,8 +367,9 @@ def bench_copy(ev: Events, iters: int = 5, n: int = 1 << 26):
 
 
 def bench_gemm_sweep(ev: Events, iters: int = 20):
-    """BASELINE config 1 and 2 shapes in all three layouts through the C ABI
-    (kernel-level timing, workspace preallocated)."""
+    """BASELINE config 1 and 2 shapes and the reference bench's shapes in all
+    three layouts through the C ABI (kernel-level timing of back-to-back
+    launches, workspace preallocated)."""
     abi = Abi(ev.L)
     L = ev.L
     vp, i64, sz = ctypes.c_void_p, ctypes.c_int64, ctypes.c_size_t
@@ -376,7 +378,10 @@ def bench_gemm_sweep(ev: Events, iters: int = 20):
     L.aar_gemm_f32_workspace_bytes.argtypes = [ctypes.c_int, i64, i64, i64]
     shapes = [(1024, 1024, 1024), (2048, 2048, 2048), (4096, 4096, 4096), (8192, 8192, 8192),
               (16384, 1536, 384), (16384, 384, 1536), (1536, 384, 16384), (384, 1536, 16384),
-              (16384, 1152, 384), (16384, 65, 384), (1152, 384, 16384)]
+              (16384, 1152, 384), (16384, 65, 384), (1152, 384, 16384),
+              # the rest of the reference bench's shapes (bench/bench_matmul.cu:150-167)
+              (256, 256, 256), (512, 512, 512), (8192, 4096, 1024), (16384, 256, 256), (256, 16384, 256),
+              (128, 4096, 4096)]
     out = {}
     rng = np.random.default_rng(0)
     try:
@@ -404,6 +409,137 @@ def bench_gemm_sweep(ev: Events, iters: int = 20):
     finally:
         abi.free()
     return out
+
+
+# The reference bench's shapes, in its groups (bench/bench_matmul.cu:146-167),
+# and its published rows for its shipping matmul kernel v4 (A = [M,K] times
+# B = [K,N], i.e. our NN layout), NVIDIA A100 80GB PCIe, as (ms_med, TFLOPS)
+# from bench/baselines/matmul_a100_80gb.csv (lines 7, 13, ..., 85: every sixth
+# line from 7, in this order).  Other hardware: a reported yardstick only.
+REF_SHAPES = [
+    ("square", "sq256", 256, 256, 256), ("square", "sq512", 512, 512, 512),
+    ("square", "sq1024", 1024, 1024, 1024), ("square", "sq2048", 2048, 2048, 2048),
+    ("square", "sq4096", 4096, 4096, 4096), ("square", "sq8192", 8192, 8192, 8192),
+    ("transformer", "qkv_proj", 16384, 1152, 384), ("transformer", "ffn_up", 16384, 1536, 384),
+    ("transformer", "ffn_down", 16384, 384, 1536), ("transformer", "vocab_head", 16384, 65, 384),
+    ("transformer", "big_ffn", 8192, 4096, 1024),
+    ("skinny", "tall", 16384, 256, 256), ("skinny", "wide", 256, 16384, 256), ("skinny", "tiny_M", 128, 4096, 4096),
+]
+REF_A100_V4 = {
+    "sq256": (0.0156, 2.15), "sq512": (0.0444, 6.05), "sq1024": (0.1867, 11.50), "sq2048": (1.3702, 12.54),
+    "sq4096": (8.5775, 16.02), "sq8192": (63.7034, 17.26), "qkv_proj": (1.0287, 14.09), "ffn_up": (1.3594, 14.22),
+    "ffn_down": (1.2375, 15.62), "vocab_head": (0.1452, 5.63), "big_ffn": (4.2348, 16.23), "tall": (0.1488, 14.44),
+    "wide": (0.1478, 14.53), "tiny_M": (0.5338, 8.05),
+}
+LAYOUTS = {"nn": 0, "nt": 1, "tn": 2}
+
+
+def _quantile(v, q):
+    """The reference bench's quantile: the sorted sample at floor(n*q),
+    clamped to the last (bench/bench_matmul.cu:60-64)."""
+    v = sorted(v)
+    return v[min(len(v) - 1, int(len(v) * q))]
+
+
+def bench_reference_shapes(ev: Events, shapes, layouts=("nn", "nt", "tn"), warmup: int = 10, iters: int = 50,
+                           seed: int = 0xC0FFEE, min_warm_ms: float = 30.0, csv_path=None, table=None):
+    """The reference bench's GEMM protocol (bench/bench_matmul.cu:66-89,
+    :203-274) through the C ABI: per shape, A and B uniform in [0, 1) from
+    `seed`; per layout, `warmup` launches (and at least `min_warm_ms` of GPU
+    time, so the clock has ramped), then `iters` launches each timed alone
+    between two events with a synchronisation (median and p99 of those, the
+    reference's figures), plus the back-to-back rate of `iters` pipelined
+    launches.  The result is checked on sampled rows against float64 with
+    the reference's tolerance max(2e-3, 5e-3*sqrt(K)/32) on the max abs
+    error.  NN entries carry the reference's published A100 v4 figure."""
+    abi = Abi(ev.L)
+    L = ev.L
+    vp, i64, sz = ctypes.c_void_p, ctypes.c_int64, ctypes.c_size_t
+    L.aar_gemm_f32.argtypes = [ctypes.c_int, i64, i64, i64, vp, vp, vp, vp, sz, vp]
+    L.aar_gemm_f32_workspace_bytes.restype = sz
+    L.aar_gemm_f32_workspace_bytes.argtypes = [ctypes.c_int, i64, i64, i64]
+    rng = np.random.default_rng(seed)
+    check_rng = np.random.default_rng(seed + 1)
+    gpu_name = device_name(L)
+    out = {}
+    csv_rows = []
+    try:
+        for group, tag, M, N, K in shapes:
+            a = rng.random(M * K, dtype=np.float32)
+            b = rng.random(K * N, dtype=np.float32)
+            pa, pb, pc = abi.put(a), abi.put(b), abi.alloc(4 * M * N)
+            flop = 2.0 * M * N * K
+            for op in layouts:
+                opi = LAYOUTS[op]
+                wsb = L.aar_gemm_f32_workspace_bytes(opi, M, N, K)
+                ws = abi.alloc(wsb) if wsb else None
+
+                def call():
+                    return L.aar_gemm_f32(opi, M, N, K, pa, pb, pc, ws, wsb, None)
+
+                assert call() == 0
+                L.aar_synchronize()
+                rows = check_rng.choice(M, min(M, 16), replace=False)
+                A = a.reshape(M, K) if op != "tn" else a.reshape(K, M).T
+                B = b.reshape(K, N) if op != "nt" else b.reshape(N, K).T
+                ref = A[rows].astype(np.float64) @ B.astype(np.float64)
+                got = np.empty((len(rows), N), np.float32)
+                for i, r in enumerate(rows):
+                    assert L.aar_memcpy(got[i].ctypes.data, pc + 4 * int(r) * N, 4 * N, 2, None) == 0
+                err = float(np.abs(got - ref).max())
+                tol = max(2e-3, 5e-3 * np.sqrt(K) / 32.0)
+                if not err <= tol:
+                    raise SystemExit(f"bench: {op} {tag} check failed (max abs err {err:.3e} > {tol:.3e})")
+                n_warm = int(max(warmup, min(5000, min_warm_ms * 1e-3 / max(flop / 150e12, 1e-7))))
+                for _ in range(n_warm):
+                    call()
+                L.aar_synchronize()
+                ts = []
+                for _ in range(iters):
+                    ev.start()
+                    call()
+                    ts.append(ev.stop_ms())
+                ev.start()
+                for _ in range(iters):
+                    call()
+                pipe = ev.stop_ms() / iters
+                med, p99 = _quantile(ts, 0.5), _quantile(ts, 0.99)
+                e = {"tag": tag, "M": M, "N": N, "K": K, "ms_med": round(med, 5), "ms_p99": round(p99, 5),
+                     "tflops": round(flop / (med * 1e-3) / 1e12, 2),
+                     "tflops_pipelined": round(flop / (pipe * 1e-3) / 1e12, 2), "max_abs_err": err}
+                if op == "nn" and tag in REF_A100_V4:
+                    pub = REF_A100_V4[tag][1]
+                    e["a100_v4_published_tflops"] = pub
+                    e["ratio_vs_a100_v4"] = round(e["tflops"] / pub, 2)
+                out[f"{op}_{tag}"] = e
+                csv_rows.append(f"{gpu_name},aar_{op},{tag},{M},{N},{K},{iters},{med:.4f},{p99:.4f},"
+                                f"{e['tflops']:.2f},,,{err:.4g}")
+                if table is not None:
+                    pub = f"{e['ratio_vs_a100_v4']:9.2f}" if "ratio_vs_a100_v4" in e else f"{'-':>9s}"
+                    print(f"{'aar_' + op:<14s} {tag:<12s} {M:6d} {N:6d} {K:6d} {med:10.4f} {p99:10.4f} "
+                          f"{e['tflops']:9.2f} {e['tflops_pipelined']:9.2f} {pub}", file=table, flush=True)
+            abi.free()
+    finally:
+        abi.free()
+    if csv_path:
+        path = Path(csv_path)
+        if path.parent != Path(""):
+            path.parent.mkdir(parents=True, exist_ok=True)
+        new = not path.exists()
+        with open(path, "a") as f:
+            if new:
+                f.write("gpu,kernel,tag,M,N,K,iters,ms_med,ms_p99,tflops,vs_sgemm_pct,vs_tf32_pct,max_abs_err\n")
+            f.write("\n".join(csv_rows) + "\n")
+    return out
+
+
+def device_name(L) -> str:
+    cu, clk, lds = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+    arch = ctypes.create_string_buffer(64)
+    L.aar_device_info.argtypes = [ctypes.POINTER(ctypes.c_int)] * 3 + [ctypes.c_char_p, ctypes.c_int]
+    if L.aar_device_info(ctypes.byref(cu), ctypes.byref(clk), ctypes.byref(lds), arch, 64) != 0:
+        return "AMD GPU"
+    return f"AMD {arch.value.decode()} ({cu.value} CUs)"
 
 
 # ----------------------------------------------------------------- GPT step
@@ -695,7 +831,19 @@ def main() -> int:
                          "B8 H12; 256 is config 5's attention, B64 H6)")
     ap.add_argument("--only", choices=["all", "gemm", "flash", "rowwise", "extra", "copy", "gpt", "sweep"], default="all",
                     help="run one part (profiling runs); the JSON line is printed for 'all'")
+    # The reference bench's command line (bench/bench_matmul.cu:101-136): with
+    # --shape or --shapes, run its GEMM table protocol only, print the table
+    # and, with --csv, append rows in its CSV format.
+    ap.add_argument("--shape", default=None, help="one GEMM shape MxNxK (reference bench protocol)")
+    ap.add_argument("--shapes", default=None, choices=["all", "square", "transformer", "skinny"],
+                    help="a group of the reference bench's shapes (reference bench protocol)")
+    ap.add_argument("--iters", type=int, default=50, help="timed launches per shape and layout (table mode)")
+    ap.add_argument("--seed", type=lambda v: int(v, 0), default=0xC0FFEE, help="input seed (table mode)")
+    ap.add_argument("--csv", default=None, help="append the table's rows to this CSV (table mode)")
+    ap.add_argument("--kernel", default="all", choices=["all", "nn", "nt", "tn"],
+                    help="layout(s) to time in table mode: nn = matmul, nt = matmul_a_bt, tn = matmul_at_b")
     args = ap.parse_args()
+    warmup_given = any(a == "--warmup" or a.startswith("--warmup=") for a in sys.argv[1:])
     if args.gpus != 1:
         print(f"bench.py: this build targets one GPU; --gpus {args.gpus} is not supported "
               "(every kernel here runs on one GPU's share; no collectives are built)", file=sys.stderr)
@@ -709,6 +857,26 @@ def main() -> int:
     ev = Events()
     n = 4096
     flops = 2.0 * n ** 3
+
+    if args.shape or args.shapes:
+        if args.shape:
+            try:
+                M, N, K = (int(t) for t in args.shape.lower().split("x"))
+            except ValueError:
+                print(f"bad shape {args.shape} (want MxNxK)", file=sys.stderr)
+                return 1
+            shapes = [("single", "custom", M, N, K)]
+        else:
+            shapes = [s for s in REF_SHAPES if args.shapes in ("all", s[0])]
+        layouts = ("nn", "nt", "tn") if args.kernel == "all" else (args.kernel,)
+        print(f"# GPU={device_name(ev.L)} iters={args.iters} warmup={args.warmup if warmup_given else 10} "
+              f"seed={args.seed:#x}")
+        print(f"{'kernel':<14s} {'tag':<12s} {'M':>6s} {'N':>6s} {'K':>6s} {'ms_med':>10s} {'ms_p99':>10s} "
+              f"{'TFLOPS':>9s} {'TF_pipe':>9s} {'vs_A100v4':>9s}", flush=True)
+        res = bench_reference_shapes(ev, shapes, layouts, warmup=args.warmup if warmup_given else 10,
+                                     iters=args.iters, seed=args.seed, csv_path=args.csv, table=sys.stdout)
+        log(json.dumps(res))
+        return 0
 
     if args.only == "copy":
         log("copy calibration:", bench_copy(ev))
@@ -757,6 +925,11 @@ def main() -> int:
 
     sweep = bench_gemm_sweep(ev)
     log("GEMM sweep TFLOPS: " + ", ".join(f"{k} {v}" for k, v in sweep.items()))
+
+    ref_table = bench_reference_shapes(ev, REF_SHAPES)
+    log("reference bench shapes (its protocol: median of single timed launches), TFLOPS: " +
+        ", ".join(f"{k} {v['tflops']}" + (f" ({v['ratio_vs_a100_v4']}x A100 v4)" if "ratio_vs_a100_v4" in v else "")
+                  for k, v in ref_table.items()))
 
     rowwise = bench_rowwise(ev)
     for k, v in rowwise.items():
@@ -850,6 +1023,7 @@ def main() -> int:
             "config": "causal, B64 H6 T256 d64 (one GPT-step layer's attention), fwd+bwd",
         },
         "gemm_sweep_tflops": sweep,
+        "gemm_reference_bench_table": ref_table,
         "rowwise_hbm": rowwise,
         "attention_ops_and_dropout": extra,
         "gpt_train_step": gpt,
@@ -861,7 +1035,10 @@ def main() -> int:
             "unit": "TFLOP/s",
             "frac": round(tflops / PEAK_FP32_MFMA_TFLOPS, 4),
             "traffic": load_traffic("gemm_f32_nn_4096"),
-            "kernel": "gemm_f32_dma_kernel<256, 256, 32, 64, 128, 2, 2, true, false, 0> (NN, plain epilogue; one launch per step)",
+            "traffic_counts": "L2-to-fabric bytes per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-calibrated); "
+                              "HBM bytes proper are not counted separately",
+            "kernel": "gemm_f32_dma_kernel<256, 256, 32, 64, 128, 2, 2, true, false, 0, 1> (NN, plain epilogue; "
+                      "one launch per step)",
             "algorithmic_flops_per_launch": flops,
         },
         "cpu_baseline": cpu,
