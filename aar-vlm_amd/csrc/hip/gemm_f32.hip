@@ -66,7 +66,11 @@ __device__ __forceinline__ void map_tile(int tiles_m, int tiles_n, int& tm, int&
 //   kEpiMask      C = aux[row][col] > 0 ? acc : 0  (relu backward, aux = the
 //                 relu's output, which is positive exactly where its input is;
 //                 aux has C's layout)
-enum : int { kEpiNone = 0, kEpiBias = 1, kEpiBiasRelu = 2, kEpiMask = 3 };
+//   kEpiAdd       C = acc + aux[row][col]          (a residual add after the
+//                 product: x + y W^T)
+//   kEpiBiasAdd   C = (acc + bias[col]) + aux[row][col]  (the same after a
+//                 linear layer with a bias)
+enum : int { kEpiNone = 0, kEpiBias = 1, kEpiBiasRelu = 2, kEpiMask = 3, kEpiAdd = 4, kEpiBiasAdd = 5 };
 struct GemmEpi {
   const float* bias;
   const float* aux;
@@ -87,14 +91,33 @@ __device__ __forceinline__ void store_tile(const f32x16 (&acc)[TM][TN], float* _
   const bool interior = r0 + 32 * TM <= M && c0 + 32 * TN <= N;
   const int64_t lane0 = (r0 + 4 * h) * ldc + c0 + lr;  // offset of the lane's first element
   float* const Cl = C + lane0;
-  const float* const Xl = EPI == kEpiMask ? ep.aux + lane0 : nullptr;
+  constexpr bool kAux = EPI == kEpiMask || EPI == kEpiAdd || EPI == kEpiBiasAdd;
+  const float* const Xl = kAux ? ep.aux + lane0 : nullptr;
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
+    // The aux values of this row of blocks are all loaded before any of its
+    // stores: C and aux may alias (an in-place residual), so a load placed
+    // after a store would wait for it, one memory round trip per element.
+    // (Each element is read and then written by the same lane, so an
+    // aliased aux still reads the old values.)
+    float xv[TN][4 * NQ];
+    if constexpr (kAux) {
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int64_t col = c0 + 32 * j + lr;
+#pragma unroll
+        for (int r = 0; r < 4 * NQ; ++r) {
+          const int dr = 32 * i + 8 * (q0 + r / 4) + (r % 4);
+          const int64_t off = (int64_t)dr * ldc + 32 * j;
+          xv[j][r] = (interior || (r0 + 4 * h + dr < M && col < N)) ? Xl[off] : 0.0f;
+        }
+      }
+    }
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
       const int64_t col = c0 + 32 * j + lr;
       float b = 0.f;
-      if constexpr (EPI == kEpiBias || EPI == kEpiBiasRelu) b = col < N ? ep.bias[col] : 0.f;
+      if constexpr (EPI == kEpiBias || EPI == kEpiBiasRelu || EPI == kEpiBiasAdd) b = col < N ? ep.bias[col] : 0.f;
 #pragma unroll
       for (int r = 0; r < 4 * NQ; ++r) {
         const int dr = 32 * i + 8 * (q0 + r / 4) + (r % 4);  // row - r0 - 4h
@@ -103,7 +126,9 @@ __device__ __forceinline__ void store_tile(const f32x16 (&acc)[TM][TN], float* _
           float v = acc[i][j][r];
           if constexpr (EPI == kEpiBias) v = v + b;
           if constexpr (EPI == kEpiBiasRelu) v = fmaxf(0.0f, v + b);
-          if constexpr (EPI == kEpiMask) v = Xl[off] > 0.0f ? v : 0.0f;
+          if constexpr (EPI == kEpiMask) v = xv[j][r] > 0.0f ? v : 0.0f;
+          if constexpr (EPI == kEpiAdd) v = v + xv[j][r];
+          if constexpr (EPI == kEpiBiasAdd) v = (v + b) + xv[j][r];
           Cl[off] = v;
         }
       }
@@ -801,7 +826,7 @@ splitk_reduce_vec_kernel(const f32x4* __restrict__ W, f32x4* __restrict__ C, int
   f32x4 s = W[i];
 #pragma unroll 8
   for (int p = 1; p < splits; ++p) s += W[p * stride4 + i];
-  if (epi == kEpiBias || epi == kEpiBiasRelu) s += bias[i % n_cols4];
+  if (epi == kEpiBias || epi == kEpiBiasRelu || epi == kEpiBiasAdd) s += bias[i % n_cols4];
   if (epi == kEpiBiasRelu) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) s[e] = fmaxf(0.0f, s[e]);
@@ -811,6 +836,7 @@ splitk_reduce_vec_kernel(const f32x4* __restrict__ W, f32x4* __restrict__ C, int
 #pragma unroll
     for (int e = 0; e < 4; ++e) s[e] = a[e] > 0.0f ? s[e] : 0.0f;
   }
+  if (epi == kEpiAdd || epi == kEpiBiasAdd) s += aux[i];
   C[i] = s;
 }
 
@@ -823,9 +849,10 @@ splitk_reduce_kernel(const float* __restrict__ W, float* __restrict__ C, int64_t
   float s = W[i];
 #pragma unroll 8
   for (int p = 1; p < splits; ++p) s += W[p * stride + i];
-  if (epi == kEpiBias || epi == kEpiBiasRelu) s += bias[i % n_cols];
+  if (epi == kEpiBias || epi == kEpiBiasRelu || epi == kEpiBiasAdd) s += bias[i % n_cols];
   if (epi == kEpiBiasRelu) s = fmaxf(0.0f, s);
   if (epi == kEpiMask) s = aux[i] > 0.0f ? s : 0.0f;
+  if (epi == kEpiAdd || epi == kEpiBiasAdd) s += aux[i];
   C[i] = s;
 }
 
@@ -1011,13 +1038,19 @@ int launch_cfg(bool vec, const float* A, const float* B, float* C, int64_t M, in
           A, B, C, M, N, K, lda, ldb, ldc, kps, split_stride, tiles_m, tiles_n, bt.sA, bt.sB, bt.sC, ep);
     return launch_status();
   };
-  // bias + relu is instantiated for the linear layer's x W^T (NT) only, the
-  // relu mask for its input gradient dY W (NN) only.
+  // bias + relu and the residual adds are instantiated for the linear layer's
+  // x W^T (NT) only, the relu mask for its input gradient dY W (NN) only.
   switch (epi) {
     case kEpiNone: return go(std::integral_constant<int, kEpiNone>{});
     case kEpiBias: return go(std::integral_constant<int, kEpiBias>{});
     case kEpiBiasRelu:
       if constexpr (A_KC && B_KC) return go(std::integral_constant<int, kEpiBiasRelu>{});
+      return AAR_EUNSUPPORTED;
+    case kEpiAdd:
+      if constexpr (A_KC && B_KC) return go(std::integral_constant<int, kEpiAdd>{});
+      return AAR_EUNSUPPORTED;
+    case kEpiBiasAdd:
+      if constexpr (A_KC && B_KC) return go(std::integral_constant<int, kEpiBiasAdd>{});
       return AAR_EUNSUPPORTED;
     case kEpiMask:
       if constexpr (A_KC && !B_KC) return go(std::integral_constant<int, kEpiMask>{});
@@ -1241,6 +1274,44 @@ extern "C" int aar_gemm_f32_bias_relu(int op, int64_t M, int64_t N, int64_t K, c
   return run_gemm(op, M, N, K, A, B, C, workspace, p, as_stream(stream), kEpiBiasRelu, GemmEpi{bias, nullptr});
 }
 
+// C = op(A, B) + R (R with C's layout), the product planned as the plain
+// aar_gemm_f32 plans it, so C is bit for bit the plain product followed by
+// an add (a plan that takes the thin-output kernel, which has no epilogue,
+// runs the product and then the add).  NT only (the linear layer's layout).
+extern "C" int aar_gemm_f32_add(int op, int64_t M, int64_t N, int64_t K, const float* A, const float* B,
+                                const float* R, float* C, void* workspace, size_t workspace_bytes, void* stream) {
+  if (op < 0 || op > 2 || M < 0 || N < 0 || K < 0) return AAR_EINVAL;
+  if (M == 0 || N == 0) return AAR_OK;
+  if (!R) return AAR_EINVAL;
+  if (op != AAR_GEMM_NT || K == 0) return AAR_EUNSUPPORTED;
+  const int chk = check_gemm_args(op, M, N, K, A, B, C, stream);
+  if (chk != AAR_OK) return chk;
+  int64_t lda, ldb;
+  default_ld(op, M, N, K, lda, ldb);
+  const Plan p = plan_gemm(op, M, N, K, workspace ? workspace_bytes : 0, workspace != nullptr, 1,
+                           thin_operands_ok(op, A, B, lda, ldb));
+  if (p.cfg == kThinCfg) {
+    const int rc = run_thin(op, M, N, K, A, B, C, as_stream(stream));
+    return rc != AAR_OK ? rc : aar_add_f32(C, R, C, M * N, stream);
+  }
+  return run_gemm(op, M, N, K, A, B, C, workspace, p, as_stream(stream), kEpiAdd, GemmEpi{nullptr, R});
+}
+
+// C = (op(A, B) + bias) + R, planned as aar_gemm_f32_bias plans it: bit for
+// bit that call followed by an add.  NT only.
+extern "C" int aar_gemm_f32_bias_add(int op, int64_t M, int64_t N, int64_t K, const float* A, const float* B,
+                                     const float* bias, const float* R, float* C, void* workspace,
+                                     size_t workspace_bytes, void* stream) {
+  if (op < 0 || op > 2 || M < 0 || N < 0 || K < 0) return AAR_EINVAL;
+  if (M == 0 || N == 0) return AAR_OK;
+  if (!bias || !R) return AAR_EINVAL;
+  if (op != AAR_GEMM_NT || K == 0) return AAR_EUNSUPPORTED;
+  const int chk = check_gemm_args(op, M, N, K, A, B, C, stream);
+  if (chk != AAR_OK) return chk;
+  const Plan p = plan_gemm(op, M, N, K, workspace ? workspace_bytes : 0, workspace != nullptr, 1, false, kEpiBias);
+  return run_gemm(op, M, N, K, A, B, C, workspace, p, as_stream(stream), kEpiBiasAdd, GemmEpi{bias, R});
+}
+
 extern "C" int aar_gemm_f32_relu_mask(int op, int64_t M, int64_t N, int64_t K, const float* A, const float* B,
                                       const float* mask, float* C, void* workspace, size_t workspace_bytes,
                                       void* stream) {
@@ -1250,7 +1321,17 @@ extern "C" int aar_gemm_f32_relu_mask(int op, int64_t M, int64_t N, int64_t K, c
   if (op != AAR_GEMM_NN) return AAR_EUNSUPPORTED;
   const int chk = check_gemm_args(op, M, N, K, A, B, C, stream);
   if (chk != AAR_OK) return chk == 1 ? AAR_OK : chk;  // K == 0: C = 0, which the mask keeps
-  const Plan p = plan_gemm(op, M, N, K, workspace ? workspace_bytes : 0, workspace != nullptr, 1, false, kEpiMask);
+  // planned as aar_gemm_f32 plans the product (the mask does not change the
+  // NN plan), so C is bit for bit that product masked; a thin-kernel plan,
+  // which has no epilogue, runs the product and then the mask pass
+  int64_t lda, ldb;
+  default_ld(op, M, N, K, lda, ldb);
+  const Plan p = plan_gemm(op, M, N, K, workspace ? workspace_bytes : 0, workspace != nullptr, 1,
+                           thin_operands_ok(op, A, B, lda, ldb), kEpiMask);
+  if (p.cfg == kThinCfg) {
+    const int rc = run_thin(op, M, N, K, A, B, C, as_stream(stream));
+    return rc != AAR_OK ? rc : aar_relu_bwd_f32(C, mask, C, M * N, stream);
+  }
   return run_gemm(op, M, N, K, A, B, C, workspace, p, as_stream(stream), kEpiMask, GemmEpi{nullptr, mask});
 }
 

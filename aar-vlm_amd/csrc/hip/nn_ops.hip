@@ -296,48 +296,86 @@ ce_row_kernel(const float* __restrict__ L, const int64_t* __restrict__ T, float*
   }
 }
 
-// Mean over active rows: loss and count summed in double / int64 in a fixed
-// order by one workgroup; writes the float mean (0 when no row is active) and
-// the active count.
-__global__ void __launch_bounds__(256)
+// Mean over active rows and the active count: one workgroup of 1024 threads.
+// Thread t sums rows t, t + 1024, ... in order (loss in double, count in
+// int64), issuing a chunk's 16 loads before its first add; a wave butterfly
+// and the 16 waves in order finish.  The order is fixed, so the result is
+// deterministic.  Writes the float mean (0 when no row is active) and the
+// count.
+constexpr int kCeThreads = 1024;
+constexpr int kCeChunk = 16;  // rows per thread whose loads are in flight together
+
+template <typename T>
+__device__ __forceinline__ T wave_sum_any(T v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+__global__ void __launch_bounds__(kCeThreads)
 ce_mean_kernel(const float* __restrict__ row_loss, const int* __restrict__ active, int64_t n,
                float* __restrict__ out, long long* __restrict__ count_out) {
-  __shared__ double dsum[256];
-  __shared__ long long csum[256];
+  __shared__ double dsum[kCeThreads / 64];
+  __shared__ long long csum[kCeThreads / 64];
   double s = 0.0;
   long long c = 0;
-  for (int64_t i = threadIdx.x; i < n; i += 256) {
-    s += (double)row_loss[i];
-    c += active[i];
-  }
-  dsum[threadIdx.x] = s;
-  csum[threadIdx.x] = c;
-  __syncthreads();
-  for (int w = 128; w > 0; w >>= 1) {
-    if (threadIdx.x < w) {
-      dsum[threadIdx.x] += dsum[threadIdx.x + w];
-      csum[threadIdx.x] += csum[threadIdx.x + w];
+  for (int64_t base = 0; base < n; base += (int64_t)kCeThreads * kCeChunk) {
+    float l[kCeChunk];
+    int a[kCeChunk];
+#pragma unroll
+    for (int k = 0; k < kCeChunk; ++k) {
+      const int64_t i = base + (int64_t)k * kCeThreads + threadIdx.x;
+      l[k] = i < n ? row_loss[i] : 0.f;
+      a[k] = i < n ? active[i] : 0;
     }
-    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < kCeChunk; ++k) {
+      s += (double)l[k];
+      c += a[k];
+    }
   }
+  s = wave_sum_any(s);
+  c = wave_sum_any(c);
+  const int wave = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) {
+    dsum[wave] = s;
+    csum[wave] = c;
+  }
+  __syncthreads();
   if (threadIdx.x == 0) {
-    out[0] = csum[0] > 0 ? (float)(dsum[0] / (double)csum[0]) : 0.0f;
-    if (count_out) count_out[0] = csum[0];
+    double ts = dsum[0];
+    long long tc = csum[0];
+    for (int w = 1; w < kCeThreads / 64; ++w) {
+      ts += dsum[w];
+      tc += csum[w];
+    }
+    out[0] = tc > 0 ? (float)(ts / (double)tc) : 0.0f;
+    if (count_out) count_out[0] = tc;
   }
 }
 
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(kCeThreads)
 ce_count_kernel(const int64_t* __restrict__ T, int64_t n, int64_t ignore_index, long long* __restrict__ count) {
-  __shared__ long long csum[256];
+  __shared__ long long csum[kCeThreads / 64];
   long long c = 0;
-  for (int64_t i = threadIdx.x; i < n; i += 256) c += (T[i] != ignore_index) ? 1 : 0;
-  csum[threadIdx.x] = c;
-  __syncthreads();
-  for (int w = 128; w > 0; w >>= 1) {
-    if (threadIdx.x < w) csum[threadIdx.x] += csum[threadIdx.x + w];
-    __syncthreads();
+  for (int64_t base = 0; base < n; base += (int64_t)kCeThreads * kCeChunk) {
+    int64_t t[kCeChunk];
+#pragma unroll
+    for (int k = 0; k < kCeChunk; ++k) {
+      const int64_t i = base + (int64_t)k * kCeThreads + threadIdx.x;
+      t[k] = i < n ? T[i] : ignore_index;
+    }
+#pragma unroll
+    for (int k = 0; k < kCeChunk; ++k) c += (t[k] != ignore_index) ? 1 : 0;
   }
-  if (threadIdx.x == 0) count[0] = csum[0];
+  c = wave_sum_any(c);
+  if ((threadIdx.x & 63) == 0) csum[threadIdx.x >> 6] = c;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    long long tc = csum[0];
+    for (int w = 1; w < kCeThreads / 64; ++w) tc += csum[w];
+    count[0] = tc;
+  }
 }
 
 // dL[i][v] = (softmax(row)[v] - [v == t]) * go / active, zeros for ignored
@@ -748,7 +786,7 @@ int aar_cross_entropy_fwd_f32(const float* logits, const int64_t* targets, float
     const int rc = launch_status();
     if (rc != AAR_OK) return rc;
   }
-  ce_mean_kernel<<<dim3(1), dim3(256), 0, st>>>(row_loss, active, n, loss, count);
+  ce_mean_kernel<<<dim3(1), dim3(kCeThreads), 0, st>>>(row_loss, active, n, loss, count);
   return launch_status();
 }
 
@@ -761,7 +799,7 @@ int aar_cross_entropy_bwd_f32(const float* grad, const float* logits, const int6
   if (!workspace || workspace_bytes < 16) return AAR_EWORKSPACE;
   hipStream_t st = as_stream(stream);
   long long* count = static_cast<long long*>(workspace);
-  ce_count_kernel<<<dim3(1), dim3(256), 0, st>>>(targets, n, ignore_index, count);
+  ce_count_kernel<<<dim3(1), dim3(kCeThreads), 0, st>>>(targets, n, ignore_index, count);
   int rc = launch_status();
   if (rc != AAR_OK) return rc;
   ce_bwd_kernel<<<dim3((unsigned)ceil_div(n, 4)), dim3(256), 0, st>>>(logits, targets, grad, count, dlogits, n,

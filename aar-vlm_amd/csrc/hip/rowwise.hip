@@ -314,7 +314,11 @@ layernorm_fwd_kernel(const float* __restrict__ x, const float* __restrict__ w,
 //  * resident waves per CU the persistent grid is sized for.
 constexpr int ln_bwd_waves(int nv, int w) { return (w > 1 && nv <= 4) ? 8 : 4; }
 constexpr int ln_bwd_rows(int nv, int w) { return w == 1 && nv <= 4 ? 2 : 1; }
-constexpr int ln_bwd_min_waves(int nv, int w) { return w == 1 && nv == 3 ? 4 : 1; }
+constexpr int ln_bwd_min_waves(int nv, int w, bool acc = false) {
+  // (the accumulating 768-column instance holds an addend row besides the two
+  // rows in flight: at 4 waves per SIMD it spilled 25 VGPRs)
+  return w == 1 && nv == 3 ? (acc ? 3 : 4) : 1;
+}
 constexpr bool ln_bwd_prefetch(int, int) { return false; }
 constexpr int kLnBwdWavesPerCu = 16;
 
@@ -346,12 +350,15 @@ __device__ __forceinline__ void ln_bwd_load(RS (&sg)[U], RS (&sx)[U], float (&mu
 // part[blockIdx.x][2][cols].  Workgroups of NW waves are persistent (as many
 // as fit on the device at once, at most 16 waves per CU) and stride over the
 // rows.  PF: the next iteration's rows are loaded before the current ones
-// are reduced, so each wave keeps two row sets in flight.
-template <int NV, int W, bool VEC, int NW, bool PF>
-__global__ void __launch_bounds__(NW * 64, ln_bwd_min_waves(NV, W))
+// are reduced, so each wave keeps two row sets in flight.  ACC: dx is added
+// onto `addend` (dx = addend + value, the fp32 addition of a gradient
+// fan-in); the addend row is loaded once the row's reductions are done, so
+// it costs no registers while gy and x are held.
+template <int NV, int W, bool VEC, int NW, bool PF, bool ACC>
+__global__ void __launch_bounds__(NW * 64, ln_bwd_min_waves(NV, W, ACC))
 layernorm_bwd_kernel(const float* __restrict__ gy, const float* __restrict__ x,
                      const float* __restrict__ w, const float* __restrict__ mean,
-                     const float* __restrict__ rstd, float* __restrict__ dx,
+                     const float* __restrict__ rstd, const float* addend, float* dx,
                      float* __restrict__ part, int64_t rows, int cols) {
   constexpr int U = ln_bwd_rows(NV, W);
   constexpr int per_iter = NW / W;
@@ -395,10 +402,24 @@ layernorm_bwd_kernel(const float* __restrict__ gy, const float* __restrict__ x,
       }
       sum_g = group_reduce<W, false, NW>(sum_g, red, (((int)(it & 1) * U + u) * 2 + 0), grp, wr, lane);
       sum_gn = group_reduce<W, false, NW>(sum_gn, red, (((int)(it & 1) * U + u) * 2 + 1), grp, wr, lane);
+      RS sa;
+      if (ACC) {
+        // (the empty asm keeps the compiler from hoisting these loads above the
+        // reductions, where they would hold registers beside gy and x)
+        asm volatile("" ::: "memory");
+        if (row0 + u < rows) sa.load(addend + (row0 + u) * cols, cols, wr, lane);
+      }
 #pragma unroll
       for (int k = 0; k < RS::kN; ++k) {
         const float gg = sg[u].v[k] * sw.v[k];
         sg[u].v[k] = r[u] * (gg - sum_g * inv_d - sx[u].v[k] * sum_gn * inv_d);
+      }
+      if (ACC) {
+        // a separately rounded addition (no fma with the product above), as
+        // the add of a gradient fan-in performs it
+#pragma clang fp contract(off)
+#pragma unroll
+        for (int k = 0; k < RS::kN; ++k) sg[u].v[k] = sa.v[k] + sg[u].v[k];
       }
       if (row0 + u < rows) sg[u].store(dx + (row0 + u) * cols, cols, wr, lane);
     }
@@ -600,7 +621,7 @@ layernorm_fwd_wide_kernel(const float* __restrict__ x, const float* __restrict__
 __global__ void __launch_bounds__(kThreads)
 layernorm_bwd_wide_kernel(const float* __restrict__ gy, const float* __restrict__ x,
                           const float* __restrict__ w, const float* __restrict__ mean,
-                          const float* __restrict__ rstd, float* __restrict__ dx, int64_t cols) {
+                          const float* __restrict__ rstd, const float* addend, float* dx, int64_t cols) {
   __shared__ float red[kWaves];
   const int64_t off = (int64_t)blockIdx.x * cols;
   const float mu = mean[blockIdx.x], r = rstd[blockIdx.x];
@@ -617,7 +638,13 @@ layernorm_bwd_wide_kernel(const float* __restrict__ gy, const float* __restrict_
   for (int64_t c = threadIdx.x; c < cols; c += kThreads) {
     const float n = (x[off + c] - mu) * r;
     const float gg = gy[off + c] * w[c];
-    dx[off + c] = r * (gg - sg * inv_d - n * sgn * inv_d);
+    const float v = r * (gg - sg * inv_d - n * sgn * inv_d);
+    if (addend) {
+#pragma clang fp contract(off)
+      dx[off + c] = addend[off + c] + v;  // separately rounded, as the fan-in's add
+    } else {
+      dx[off + c] = v;
+    }
   }
 }
 
@@ -707,7 +734,7 @@ int ln_bwd_resident() {
     int b = 0;
     constexpr int nw = ln_bwd_waves(NV, W);
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-            &b, layernorm_bwd_kernel<NV, W, V, nw, ln_bwd_prefetch(NV, W)>, nw * kWave, 0) != hipSuccess) {
+            &b, layernorm_bwd_kernel<NV, W, V, nw, ln_bwd_prefetch(NV, W), false>, nw * kWave, 0) != hipSuccess) {
       b = 1;
     }
     return b > 0 ? b : 1;
@@ -840,8 +867,8 @@ size_t ln_bwd_need_bytes(int64_t rows, int64_t cols, bool vec) {
 }
 
 int layernorm_bwd_run(const float* gy, const float* x, const float* w, const float* mean, const float* rstd,
-                      float* dx, float* dw, float* db, int64_t rows, int64_t cols, void* workspace,
-                      size_t workspace_bytes, void* stream) {
+                      const float* addend, float* dx, float* dw, float* db, int64_t rows, int64_t cols,
+                      void* workspace, size_t workspace_bytes, void* stream) {
   if (rows < 0 || cols <= 0) return AAR_EINVAL;
   if (!dw || !db || cols > INT32_MAX) return AAR_EINVAL;
   hipStream_t st = as_stream(stream);
@@ -851,7 +878,7 @@ int layernorm_bwd_run(const float* gy, const float* x, const float* w, const flo
     return rc;
   }
   if (!gy || !x || !w || !mean || !rstd || !dx) return AAR_EINVAL;
-  const bool vec = ln_bwd_vec(gy, x, w, dx, workspace, cols);
+  const bool vec = ln_bwd_vec(gy, x, w, dx, workspace, cols) && (!addend || aligned16(addend));
   const RowPlan p = plan_rows(cols, vec);
   const int parts = ln_bwd_parts_for(rows, p);
   const size_t need = (size_t)parts * 2 * (size_t)cols * sizeof(float);
@@ -861,18 +888,27 @@ int layernorm_bwd_run(const float* gy, const float* x, const float* w, const flo
   if (p.nv == 0) {
     if (!wide_grid_ok(rows)) return AAR_EUNSUPPORTED;
     layernorm_bwd_wide_kernel<<<dim3((unsigned)rows), dim3(kThreads), 0, st>>>(gy, x, w, mean, rstd,
-                                                                                dx, cols);
+                                                                                addend, dx, cols);
     rc = launch_status();
     if (rc != AAR_OK) return rc;
     layernorm_bwd_wide_cols_kernel<<<dim3((unsigned)ceil_div(cols, kThreads), (unsigned)parts),
                                      dim3(kThreads), 0, st>>>(gy, x, mean, rstd, part, rows, cols);
   } else {
-#define L(NV, W, V)                                                                          \
-  layernorm_bwd_kernel<NV, W, V, ln_bwd_waves(NV, W), ln_bwd_prefetch(NV, W)>                    \
-      <<<dim3(parts), dim3(ln_bwd_waves(NV, W) * kWave), 0, st>>>(gy, x, w, mean, rstd, dx, part, \
+    if (addend) {
+#define L(NV, W, V)                                                                                  \
+  layernorm_bwd_kernel<NV, W, V, ln_bwd_waves(NV, W), ln_bwd_prefetch(NV, W), true>                      \
+      <<<dim3(parts), dim3(ln_bwd_waves(NV, W) * kWave), 0, st>>>(gy, x, w, mean, rstd, addend, dx, part, \
                                                                  rows, (int)cols)
-    AAR_ROW_DISPATCH(p, L);
+      AAR_ROW_DISPATCH(p, L);
 #undef L
+    } else {
+#define L(NV, W, V)                                                                                  \
+  layernorm_bwd_kernel<NV, W, V, ln_bwd_waves(NV, W), ln_bwd_prefetch(NV, W), false>                     \
+      <<<dim3(parts), dim3(ln_bwd_waves(NV, W) * kWave), 0, st>>>(gy, x, w, mean, rstd, nullptr, dx, part, \
+                                                                 rows, (int)cols)
+      AAR_ROW_DISPATCH(p, L);
+#undef L
+    }
   }
   rc = launch_status();
   if (rc != AAR_OK) return rc;
@@ -928,7 +964,17 @@ extern "C" int aar_layernorm_bwd_f32(const float* gy, const float* x, const floa
                                      const float* mean, const float* rstd, float* dx, float* dw,
                                      float* db, int64_t rows, int64_t cols, void* workspace,
                                      size_t workspace_bytes, void* stream) {
-  return layernorm_bwd_run(gy, x, w, mean, rstd, dx, dw, db, rows, cols, workspace, workspace_bytes, stream);
+  return layernorm_bwd_run(gy, x, w, mean, rstd, nullptr, dx, dw, db, rows, cols, workspace, workspace_bytes,
+                           stream);
+}
+
+extern "C" int aar_layernorm_bwd_acc_f32(const float* gy, const float* x, const float* w, const float* mean,
+                                         const float* rstd, const float* dx_addend, float* dx, float* dw,
+                                         float* db, int64_t rows, int64_t cols, void* workspace,
+                                         size_t workspace_bytes, void* stream) {
+  if (rows > 0 && !dx_addend) return AAR_EINVAL;
+  return layernorm_bwd_run(gy, x, w, mean, rstd, dx_addend, dx, dw, db, rows, cols, workspace, workspace_bytes,
+                           stream);
 }
 
 extern "C" size_t aar_layernorm_bwd_noalloc_max_bytes(void) { return kLnBwdScratchBytes; }
@@ -945,5 +991,5 @@ extern "C" int aar_layernorm_bwd_noalloc_f32(const float* gy, const float* x, co
   void* ws = nullptr;
   const int rc = scratch_ptr(&ws);
   if (rc != AAR_OK) return rc;
-  return layernorm_bwd_run(gy, x, w, mean, rstd, dx, dw, db, rows, cols, ws, kLnBwdScratchBytes, stream);
+  return layernorm_bwd_run(gy, x, w, mean, rstd, nullptr, dx, dw, db, rows, cols, ws, kLnBwdScratchBytes, stream);
 }

@@ -9,7 +9,10 @@
 //     slot (indexed by its position in the schedule); a gradient arriving at a
 //     slot that already holds one is added to it (held + new, on the GPU), so
 //     fan-in sums accumulate in the order the consumers run.  Gradients for
-//     leaves go straight into the leaf's grad slot the same way.
+//     leaves go straight into the leaf's grad slot the same way.  A node that
+//     fuses fan-ins (Function::fuses_fan_in) is handed the held gradients of
+//     its inputs and may return held + new computed by its own kernel, the
+//     same sum in the same order without a separate add pass.
 // This fixes the summation order of every fan-in to the reference's: its
 // stack walk pushes a node's inputs in order and pops the last one first,
 // which is the same post-order.  Error messages match the reference's.
@@ -107,7 +110,26 @@ void sweep(const std::vector<FnPtr>& nodes, const Tensor& seed) {
     const Tensor upstream = std::move(*pending[i]);
     pending[i].reset();
     Function& fn = *nodes[i];
-    const std::vector<Tensor> outs = fn.backward(upstream);
+    std::vector<bool> summed(fn.inputs.size(), false);
+    std::vector<Tensor> outs;
+    if (fn.fuses_fan_in()) {
+      // the gradients already held for this node's inputs, for it to add onto
+      std::vector<const Tensor*> held(fn.inputs.size(), nullptr);
+      for (size_t k = 0; k < fn.inputs.size(); ++k) {
+        Function::Input& in = fn.inputs[k];
+        if (!in.needs_grad) continue;
+        if (in.grad_fn) {
+          std::optional<Tensor>& slot = pending[position.at(in.grad_fn.get())];
+          if (slot) held[k] = &*slot;
+        } else if (in.leaf.grad_slot && *in.leaf.grad_slot) {
+          held[k] = in.leaf.grad_slot->get();
+        }
+      }
+      outs = fn.backward_into(upstream, held, summed);
+      summed.resize(fn.inputs.size(), false);
+    } else {
+      outs = fn.backward(upstream);
+    }
     if (outs.size() != fn.inputs.size()) {
       throw std::runtime_error("autograd: backward returned wrong number of grads");
     }
@@ -115,7 +137,14 @@ void sweep(const std::vector<FnPtr>& nodes, const Tensor& seed) {
       Function::Input& in = fn.inputs[k];
       if (!in.needs_grad) continue;
       if (in.grad_fn) {
-        deposit(pending[position.at(in.grad_fn.get())], outs[k]);
+        std::optional<Tensor>& slot = pending[position.at(in.grad_fn.get())];
+        if (summed[k]) {
+          slot = outs[k];  // held + new, summed by the producing kernel
+        } else {
+          deposit(slot, outs[k]);
+        }
+      } else if (summed[k]) {
+        if (in.leaf.grad_slot) *in.leaf.grad_slot = std::make_shared<Tensor>(outs[k]);
       } else {
         deposit_leaf(in.leaf, outs[k]);
       }

@@ -178,6 +178,13 @@ PYBIND11_MODULE(_core, m) {
         gil_release(),
         "linear(relu(linear(x, w1, b1)), w2, b2) with bias + relu in the first GEMM's epilogue: the "
         "values and gradients of the composition.");
+  m.def("_linear_residual", &linear_residual, py::arg("r"), py::arg("a"), py::arg("weight"), gil_release(),
+        "r + a W^T as one GEMM with the residual added in its epilogue: the values and gradients of "
+        "add(r, matmul_a_bt(a, W)).");
+  m.def("_mlp_relu_residual", &mlp_relu_residual, py::arg("r"), py::arg("x"), py::arg("w1"), py::arg("b1"),
+        py::arg("w2"), py::arg("b2"), gil_release(),
+        "r + _mlp_relu(x, w1, b1, w2, b2) with the residual added in the second GEMM's epilogue: the values "
+        "and gradients of the composition.");
   m.def("_token_windows", &token_windows, py::arg("tokens"), py::arg("starts"), py::arg("seq_len"),
         gil_release(),
         "(x, y) int64 [len(starts), seq_len] with x[b] = tokens[s:s+T], y[b] = tokens[s+1:s+T+1], "

@@ -396,10 +396,31 @@ class SoftmaxFunction : public Function {
 
 // ------------------------------------------------------------- layernorm
 
+// A layernorm input that also feeds a residual connection (x + f(LN(x)), the
+// pre-norm block) has a gradient fan-in: the residual's gradient arrives
+// first and the layernorm's is added to it.  The backward takes that held
+// gradient into its kernel (dx = held + value, aar_layernorm_bwd_acc_f32),
+// the same fp32 sum as add_grads(held, dx) without the separate add pass.
 class LayerNormFunction : public Function {
  public:
   Tensor saved_x, saved_w, saved_mean, saved_rstd;
-  std::vector<Tensor> backward(const Tensor& grad_y) override {
+  std::vector<Tensor> backward(const Tensor& grad_y) override { return run(grad_y, nullptr); }
+  bool fuses_fan_in() const override { return true; }
+  std::vector<Tensor> backward_into(const Tensor& grad_y, const std::vector<const Tensor*>& held,
+                                    std::vector<bool>& summed) override {
+    summed.assign(inputs.size(), false);
+    const Tensor* h = held.empty() ? nullptr : held[0];
+    if (h && h->shape == saved_x.shape && h->dtype == DType::Fp32 && h->device == Device::CUDA &&
+        h->is_contiguous()) {
+      summed[0] = true;
+      return run(grad_y, h);
+    }
+    return run(grad_y, nullptr);
+  }
+  const char* name() const override { return "LayerNormFunction"; }
+
+ private:
+  std::vector<Tensor> run(const Tensor& grad_y, const Tensor* addend) {
     if (saved_x.device == Device::CPU) throw_cpu_compute("layernorm backward");
     Tensor gy = as_contig(grad_y);
     Tensor dx = Tensor::empty(saved_x.shape, saved_x.dtype, saved_x.device);
@@ -408,13 +429,19 @@ class LayerNormFunction : public Function {
     const int64_t last = saved_x.shape.back();
     const int64_t outer = static_cast<int64_t>(saved_x.numel()) / last;
     Workspace ws(aar_layernorm_bwd_workspace_bytes(outer, last));
-    check_status(aar_layernorm_bwd_f32(fp(gy), fp(saved_x), fp(saved_w), fp(saved_mean), fp(saved_rstd),
-                                       fp(dx), fp(dw), fp(db), outer, last, ws.data(), ws.bytes(),
-                                       current_stream()),
-                 "layernorm backward");
+    if (addend) {
+      check_status(aar_layernorm_bwd_acc_f32(fp(gy), fp(saved_x), fp(saved_w), fp(saved_mean), fp(saved_rstd),
+                                             fp(*addend), fp(dx), fp(dw), fp(db), outer, last, ws.data(),
+                                             ws.bytes(), current_stream()),
+                   "layernorm backward");
+    } else {
+      check_status(aar_layernorm_bwd_f32(fp(gy), fp(saved_x), fp(saved_w), fp(saved_mean), fp(saved_rstd),
+                                         fp(dx), fp(dw), fp(db), outer, last, ws.data(), ws.bytes(),
+                                         current_stream()),
+                   "layernorm backward");
+    }
     return {dx, dw, db};
   }
-  const char* name() const override { return "LayerNormFunction"; }
 };
 
 // ------------------------------------------------------------- attention
@@ -814,8 +841,8 @@ class MlpReluFunction : public Function {
     }
     Tensor dw2 = matmul_at_b_no_grad(gc, saved_h);
     // dh = relu_backward(g W2): the plain GEMM, then the mask pass.  (The
-    // mask in the GEMM epilogue, aar_gemm_f32_relu_mask, measured slower at
-    // the GPT shape: 233 us against 152 + 47 us.)
+    // mask in the GEMM epilogue, aar_gemm_f32_relu_mask, measured slower in
+    // the GPT step's profile: 219.9 us against about 150 + 43.5 us.)
     Tensor dh = Tensor::empty({rows, H}, DType::Fp32, Device::CUDA);
     if (dh.numel() != 0) {
       Tensor dpost = matmul_no_grad(gc, saved_w2);
@@ -865,6 +892,121 @@ Tensor mlp_relu(const Tensor& x, const Tensor& w1, const Tensor& b1, const Tenso
   }
   auto fn = std::make_shared<MlpReluFunction>();
   for (const Tensor* t : {&xc, &w1c, &b1c, &w2c, &b2c}) fn->record_input(*t);
+  fn->saved_x = x2;
+  fn->saved_w1 = w1c;
+  fn->saved_w2 = w2c;
+  fn->saved_h = h;
+  fn->x_shape = x.shape;
+  out.requires_grad = true;
+  out.grad_fn = fn;
+  return out;
+}
+
+// r + a W^T: the attention output projection of a pre-norm block (bias-free,
+// python/shakespeare/scripts/model.py:12) with its residual add, as one GEMM
+// whose epilogue adds r (aar_gemm_f32_add; bit for bit matmul_a_bt followed
+// by add).  The node stands for the pair add(r, matmul_a_bt(a, W)): its
+// inputs are (r, a, W) in that order, so the autograd walk visits them as it
+// visits the pair's, and its backward returns the pair's gradients: g for r,
+// g W for a and g^T a for W, from the same kernels.
+class LinearResidualFunction : public Function {
+ public:
+  Tensor saved_a, saved_w;  // a as [rows, K]
+  std::vector<int64_t> a_shape;
+  std::vector<Tensor> backward(const Tensor& g) override {
+    const int64_t rows = saved_a.shape[0], N = saved_w.shape[0];
+    Tensor gc = as_view(as_contig(g), {rows, N});
+    return {g, as_view(matmul_no_grad(gc, saved_w), a_shape), matmul_at_b_no_grad(gc, saved_a)};
+  }
+  const char* name() const override { return "LinearResidualFunction"; }
+};
+
+Tensor linear_residual(const Tensor& r, const Tensor& a, const Tensor& w) {
+  if (w.shape.size() != 2 || a.shape.size() < 2 || a.shape.back() != w.shape[1] || a.shape.back() == 0 ||
+      w.shape[0] == 0 || a.dtype != DType::Fp32 || w.dtype != DType::Fp32 || r.dtype != DType::Fp32 ||
+      a.device != w.device || r.device != a.device) {
+    return add(r, matmul_a_bt(a, w));  // the composition's checks, messages and edge cases
+  }
+  std::vector<int64_t> out_shape(a.shape.begin(), a.shape.end() - 1);
+  out_shape.push_back(w.shape[0]);
+  if (r.shape != out_shape) return add(r, matmul_a_bt(a, w));  // raises as add does
+  if (a.device == Device::CPU) throw_cpu_compute("matmul_a_bt");
+  Tensor rc = as_contig(r), ac = as_contig(a), wc = as_contig(w);
+  const int64_t K = a.shape.back(), N = w.shape[0];
+  const int64_t rows = static_cast<int64_t>(a.numel()) / K;
+  Tensor out = Tensor::empty(out_shape, DType::Fp32, Device::CUDA);
+  if (out.numel() != 0) {
+    Workspace ws(aar_gemm_f32_workspace_bytes(AAR_GEMM_NT, rows, N, K));
+    check_status(aar_gemm_f32_add(AAR_GEMM_NT, rows, N, K, fp(ac), fp(wc), fp(rc), fp(out), ws.data(), ws.bytes(),
+                                  current_stream()),
+                 "matmul_a_bt");
+  }
+  if (!rc.requires_grad && !ac.requires_grad && !wc.requires_grad) return out;
+  auto fn = std::make_shared<LinearResidualFunction>();
+  fn->record_input(rc);
+  fn->record_input(ac);
+  fn->record_input(wc);
+  fn->saved_a = as_view(ac, {rows, K});
+  fn->saved_w = wc;
+  fn->a_shape = a.shape;
+  out.requires_grad = true;
+  out.grad_fn = fn;
+  return out;
+}
+
+// r + mlp_relu(x, W1, b1, W2, b2): the MLP branch of a pre-norm block with its
+// residual add in the second GEMM's epilogue (aar_gemm_f32_bias_add; bit for
+// bit the mlp_relu + add composition).  Inputs (r, x, W1, b1, W2, b2), in the
+// order the pair add(r, mlp_relu(.)) presents them to the autograd walk; the
+// backward is MlpReluFunction's plus g for r.
+class MlpReluResidualFunction : public MlpReluFunction {
+ public:
+  std::vector<Tensor> backward(const Tensor& g) override {
+    std::vector<Tensor> grads = MlpReluFunction::backward(g);
+    grads.insert(grads.begin(), g);
+    return grads;
+  }
+  const char* name() const override { return "MlpReluResidualFunction"; }
+};
+
+Tensor mlp_relu_residual(const Tensor& r, const Tensor& x, const Tensor& w1, const Tensor& b1, const Tensor& w2,
+                         const Tensor& b2) {
+  const bool shapes_ok = w1.shape.size() == 2 && w2.shape.size() == 2 && x.shape.size() >= 2 && w1.shape[0] != 0 &&
+                         w2.shape[0] != 0 && x.shape.back() != 0 && x.shape.back() == w1.shape[1] &&
+                         w2.shape[1] == w1.shape[0] && b1.shape.size() == 1 && b2.shape.size() == 1 &&
+                         b1.shape[0] == w1.shape[0] && b2.shape[0] == w2.shape[0];
+  const bool types_ok = x.dtype == DType::Fp32 && w1.dtype == DType::Fp32 && w2.dtype == DType::Fp32 &&
+                        b1.dtype == DType::Fp32 && b2.dtype == DType::Fp32 && r.dtype == DType::Fp32 &&
+                        x.device == w1.device && x.device == w2.device && x.device == b1.device &&
+                        x.device == b2.device && x.device == r.device;
+  std::vector<int64_t> out_shape(x.shape.begin(), x.shape.end() - 1);
+  if (shapes_ok) out_shape.push_back(w2.shape[0]);
+  if (!shapes_ok || !types_ok || r.shape != out_shape) {
+    return add(r, mlp_relu(x, w1, b1, w2, b2));  // the composition's checks, messages and edge cases
+  }
+  if (x.device == Device::CPU) throw_cpu_compute("linear");
+  Tensor rc = as_contig(r), xc = as_contig(x), w1c = as_contig(w1), b1c = as_contig(b1), w2c = as_contig(w2),
+         b2c = as_contig(b2);
+  const int64_t d = x.shape.back(), H = w1.shape[0], N2 = w2.shape[0];
+  const int64_t rows = static_cast<int64_t>(x.numel()) / d;
+  Tensor x2 = as_view(xc, {rows, d});
+  Tensor h = Tensor::empty({rows, H}, DType::Fp32, Device::CUDA);
+  Tensor out = Tensor::empty(out_shape, DType::Fp32, Device::CUDA);
+  if (h.numel() != 0) {
+    Workspace ws(aar_gemm_f32_workspace_bytes(AAR_GEMM_NT, rows, H, d));
+    check_status(aar_gemm_f32_bias_relu(AAR_GEMM_NT, rows, H, d, fp(x2), fp(w1c), fp(b1c), fp(h), ws.data(),
+                                        ws.bytes(), current_stream()),
+                 "linear");
+    Workspace ws2(aar_gemm_f32_workspace_bytes(AAR_GEMM_NT, rows, N2, H));
+    check_status(aar_gemm_f32_bias_add(AAR_GEMM_NT, rows, N2, H, fp(h), fp(w2c), fp(b2c), fp(rc), fp(out),
+                                       ws2.data(), ws2.bytes(), current_stream()),
+                 "linear");
+  }
+  const bool grad = rc.requires_grad || xc.requires_grad || w1c.requires_grad || b1c.requires_grad ||
+                    w2c.requires_grad || b2c.requires_grad;
+  if (!grad) return out;
+  auto fn = std::make_shared<MlpReluResidualFunction>();
+  for (const Tensor* t : {&rc, &xc, &w1c, &b1c, &w2c, &b2c}) fn->record_input(*t);
   fn->saved_x = x2;
   fn->saved_w1 = w1c;
   fn->saved_w2 = w2c;

@@ -26,6 +26,12 @@ Tensor linear(const Tensor& x, const Tensor& w, const Tensor& b);
 // linear(relu(linear(x, w1, b1)), w2, b2) with bias + relu in the first
 // GEMM's epilogue; same values and gradients as the composition.
 Tensor mlp_relu(const Tensor& x, const Tensor& w1, const Tensor& b1, const Tensor& w2, const Tensor& b2);
+// The pre-norm block's residual adds folded into the last GEMM's epilogue:
+// r + matmul_a_bt(a, w) and r + mlp_relu(x, w1, b1, w2, b2), with the values
+// and gradients (and fan-in order) of the add + op compositions.
+Tensor linear_residual(const Tensor& r, const Tensor& a, const Tensor& w);
+Tensor mlp_relu_residual(const Tensor& r, const Tensor& x, const Tensor& w1, const Tensor& b1, const Tensor& w2,
+                         const Tensor& b2);
 
 // Row-wise (cppsrc/ops/softmax.cpp:75-96, cppsrc/ops/layernorm.cpp:174-227).
 Tensor softmax(const Tensor& x);

@@ -112,6 +112,21 @@ class Function {
   virtual std::vector<Tensor> backward(const Tensor& grad_output) = 0;
   virtual const char* name() const { return "Function"; }
   void record_input(const Tensor& t);
+
+  // Gradient fan-in folded into the producing kernel.  When the engine holds
+  // a gradient for input k already (`held[k]`, null when none) and the
+  // function fuses fan-ins (`fuses_fan_in`), it calls backward_into, which
+  // may return held[k] + its own gradient for input k in one pass and set
+  // summed[k]: the engine then takes that tensor as the new held gradient in
+  // place of add_grads(held, new).  The sum must be that fp32 addition bit for
+  // bit.  The default fuses nothing.
+  virtual bool fuses_fan_in() const { return false; }
+  virtual std::vector<Tensor> backward_into(const Tensor& grad_output, const std::vector<const Tensor*>& held,
+                                            std::vector<bool>& summed) {
+    (void)held;
+    summed.assign(inputs.size(), false);
+    return backward(grad_output);
+  }
 };
 
 void run_backward(const Tensor& root, const Tensor& grad_output);

@@ -604,12 +604,13 @@ class GPT:
             # nn.MultiHeadAttention's composition (per-head views of the packed
             # projection, causal flash attention, heads merged) as one fused op
             a = ag._core._flash_attention_qkv(ag.matmul_a_bt(h, wqkv), H, True)
-            x = ag.add(x, ag.matmul_a_bt(a, wout))
+            # x + out_proj(a), the residual add in the projection GEMM's epilogue
+            x = ag._core._linear_residual(x, a, wout)
             h = ag.layernorm(x, l2w, l2b, 1e-5)
-            # the MLP linear -> relu -> linear (nn.Linear with bias) as one fused op:
-            # bias and relu in the first GEMM's epilogue, the second bias in its
-            # GEMM's epilogue
-            x = ag.add(x, ag._core._mlp_relu(h, f1w, f1b, f2w, f2b))
+            # x + (the MLP linear -> relu -> linear, nn.Linear with bias) as one
+            # fused op: bias and relu in the first GEMM's epilogue, the second
+            # bias and the residual add in its GEMM's epilogue
+            x = ag._core._mlp_relu_residual(x, h, f1w, f1b, f2w, f2b)
         x = ag.layernorm(x, p[-3], p[-2], 1e-5)
         return ag.matmul_a_bt(x, p[-1])
 

@@ -115,13 +115,29 @@ int aar_gemm_f32_bias(int op, int64_t M, int64_t N, int64_t K, const float* A, c
 int aar_gemm_f32_bias_relu(int op, int64_t M, int64_t N, int64_t K, const float* A, const float* B,
                            const float* bias, float* C, void* workspace, size_t workspace_bytes,
                            void* stream);
+/* C = A W^T + R (R [M, N] contiguous): a linear layer without bias followed
+ * by a residual add, the add in the GEMM epilogue.  Bit-identical to
+ * aar_gemm_f32 then aar_add_f32 (the same product plan, one fp32 addition per
+ * element).  op must be AAR_GEMM_NT (else AAR_EUNSUPPORTED, as is K == 0).
+ * Replaces matmul_a_bt_cuda + add_cuda of a pre-norm block's attention
+ * output projection and residual, x + proj(attn) (cppsrc/ops/matmul.cpp:11,
+ * elementwise.cpp:8; python/shakespeare/scripts/model.py:47-57). */
+int aar_gemm_f32_add(int op, int64_t M, int64_t N, int64_t K, const float* A, const float* B,
+                     const float* R, float* C, void* workspace, size_t workspace_bytes, void* stream);
+/* C = (A W^T + bias[col]) + R: the same after a linear layer with a bias;
+ * bit-identical to aar_gemm_f32_bias then aar_add_f32.  NT only.  Replaces
+ * matmul_a_bt_cuda + add_bias_cuda + add_cuda of the MLP's output layer and
+ * its residual (cppsrc/ops/matmul.cpp:11, elementwise.cpp:24 and :8). */
+int aar_gemm_f32_bias_add(int op, int64_t M, int64_t N, int64_t K, const float* A, const float* B,
+                          const float* bias, const float* R, float* C, void* workspace,
+                          size_t workspace_bytes, void* stream);
 /* C = mask > 0 ? A B : 0 elementwise (mask [M, N] contiguous, the relu's
  * output): the relu backward applied in the GEMM epilogue of the next layer's
  * input gradient dY W; bit-identical to aar_gemm_f32 then relu_backward.  op
  * must be AAR_GEMM_NN (else AAR_EUNSUPPORTED).  Replaces matmul_cuda +
  * relu_backward_cuda (cppsrc/ops/matmul.cpp:10, elementwise.cpp:17).  On
- * MI355X at 16384x1536x384 it runs slower than the GEMM plus the separate
- * mask pass, so the host MLP op uses those. */
+ * MI355X at the GPT step's 16384x1536x384 it runs slower than the GEMM plus
+ * the separate mask pass, so the host MLP op uses those. */
 int aar_gemm_f32_relu_mask(int op, int64_t M, int64_t N, int64_t K, const float* A, const float* B,
                            const float* mask, float* C, void* workspace, size_t workspace_bytes,
                            void* stream);
@@ -191,6 +207,19 @@ int aar_layernorm_bwd_f32(const float* gy, const float* x, const float* w,
                           float* dx, float* dw, float* db,
                           int64_t rows, int64_t cols,
                           void* workspace, size_t workspace_bytes, void* stream);
+
+/* aar_layernorm_bwd_f32 with the input gradient added onto `dx_addend`
+ * ([rows, cols] contiguous; may be dx itself): dx = dx_addend + the layernorm
+ * input gradient, bit-identical to aar_layernorm_bwd_f32 followed by
+ * aar_add_f32(dx_addend, dx).  dw and db as there.  Replaces the
+ * layernorm_backward_cuda + add_cuda pair of a gradient fan-in: the autograd
+ * sum of a layernorm input that also feeds a residual connection
+ * (cppsrc/ops/layernorm.cpp:15-17, cppsrc/autograd/backward.cpp:17-36). */
+int aar_layernorm_bwd_acc_f32(const float* gy, const float* x, const float* w,
+                              const float* mean, const float* rstd, const float* dx_addend,
+                              float* dx, float* dw, float* db,
+                              int64_t rows, int64_t cols,
+                              void* workspace, size_t workspace_bytes, void* stream);
 
 /* No counterpart in the reference: aar_layernorm_bwd_f32 for callers that
  * cannot allocate device memory (code under HIP graph capture, tight serving

@@ -7,7 +7,8 @@ each epilogue performs the same fp32 operation as the separate op.  Cases
 cover the unsplit DMA path, the register (unaligned) path and split-K with the
 vector and the scalar reduce; one case rechecks the result against the oracle
 at the GEMM tolerance.  The C-ABI relu-mask GEMM (aar_gemm_f32_relu_mask, which
-the op does not use) is checked against the GEMM followed by relu backward."""
+the op does not use) is checked against the GEMM followed by relu backward,
+including a shape the plain GEMM plans on the thin-output kernel."""
 from __future__ import annotations
 
 import numpy as np
@@ -91,7 +92,8 @@ def test_mlp_no_grad_and_errors(gpu):
         gpu._core._mlp_relu(*(dev(gpu, a) for a in (x, w1, b1, w2[:, :31], b2)))
 
 
-@pytest.mark.parametrize("M,N,K", [(64, 96, 8192), (33, 30, 4999), (150, 65, 17), (512, 256, 256)])
+@pytest.mark.parametrize("M,N,K", [(64, 96, 8192), (33, 30, 4999), (150, 65, 17), (512, 256, 256),
+                                   (16384, 96, 384)])
 def test_abi_relu_mask_gemm_matches_gemm_then_relu_backward(gpu, M, N, K):
     rng = np.random.default_rng(M + N + K)
     a = rng.standard_normal((M, K)).astype(f32)
