@@ -229,10 +229,12 @@ int aar_layernorm_bwd_acc_f32(const float* gy, const float* x, const float* w,
  * instead of a caller workspace; the call allocates nothing (no hipMalloc,
  * no allocating library routine).  Same kernels and results as
  * aar_layernorm_bwd_f32, bit for bit.  A shape whose partial rows exceed
- * the buffer returns AAR_ESCRATCH before any launch: with 16-byte aligned
- * operands and a column count divisible by 4, any number of rows fits up to
- * 4096 columns; unaligned operands or other column counts take the
- * element-wise plan, which fits up to 2048 columns.  Every
+ * the buffer returns AAR_ESCRATCH before any launch.  The partial rows number
+ * CUs x resident workgroups, so the limits scale with the device: on
+ * MI355X's 256 CUs, with 16-byte aligned operands and a column count
+ * divisible by 4, any number of rows fits up to 4096 columns; unaligned
+ * operands or other column counts take the element-wise plan, which fits up
+ * to 2048 columns (a device with more CUs fits proportionally fewer).  Every
  * call on one GPU shares that GPU's buffer: calls that overlap on one GPU
  * (several streams or host threads at once) race and must be serialised by
  * the caller; calls ordered on one stream are safe. */

@@ -107,3 +107,43 @@ def test_noalloc_rejects_oversize_and_keeps_working(gpu):
         np.testing.assert_array_equal(db1, db0)
     finally:
         abi.free()
+
+
+def _free_device_bytes():
+    hip = ctypes.CDLL("libamdhip64.so")
+    free, total = ctypes.c_size_t(), ctypes.c_size_t()
+    assert hip.hipMemGetInfo(ctypes.byref(free), ctypes.byref(total)) == 0
+    return free.value
+
+
+def test_noalloc_calls_allocate_nothing(gpu):
+    """The defining property: after a first call (which loads the code object
+    with its static buffer), further calls of several shapes leave the
+    device's free memory unchanged, to the byte."""
+    abi = Abi()
+    try:
+        L = _setup(abi)
+        shapes = [(4096, 384), (300, 768), (1000, 4096), (77, 100)]
+        bufs = {}
+        for rows, cols in shapes:  # operands allocated up front, outside the measured window
+            rng = np.random.default_rng(rows + cols)
+            x = (3 * rng.standard_normal((rows, cols))).astype(f32)
+            w = (1 + 0.02 * rng.standard_normal(cols)).astype(f32)
+            b = np.zeros(cols, f32)
+            gy = rng.standard_normal((rows, cols)).astype(f32)
+            px, pw, pb, pg = abi.put(x), abi.put(w), abi.put(b), abi.put(gy)
+            py, pm, pr = abi.empty(rows * cols), abi.empty(rows), abi.empty(rows)
+            abi.check(L.aar_layernorm_fwd_f32(px, pw, pb, py, pm, pr, rows, cols, ctypes.c_float(1e-5), None))
+            pdx, pdw, pdb = abi.empty(rows * cols), abi.empty(cols), abi.empty(cols)
+            bufs[(rows, cols)] = (pg, px, pw, pm, pr, pdx, pdw, pdb)
+        rows, cols = shapes[0]
+        abi.check(L.aar_layernorm_bwd_noalloc_f32(*bufs[(rows, cols)], rows, cols, None))  # warm-up
+        abi.check(L.aar_synchronize())
+        before = _free_device_bytes()
+        for _ in range(3):
+            for rows, cols in shapes:
+                abi.check(L.aar_layernorm_bwd_noalloc_f32(*bufs[(rows, cols)], rows, cols, None))
+        abi.check(L.aar_synchronize())
+        assert _free_device_bytes() == before
+    finally:
+        abi.free()
