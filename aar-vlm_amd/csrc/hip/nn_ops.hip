@@ -159,6 +159,33 @@ colsum_stage1_kernel(const float* __restrict__ g, float* __restrict__ part, int6
   part[(int64_t)blockIdx.y * cols + c] = s;
 }
 
+// Stage 1 fused with the relu backward that produces g: dx = x > 0 ? g : 0
+// is stored and summed in the same order as colsum_stage1_kernel sums dx, so
+// the partials are bit for bit those of the two kernels in sequence.  Each
+// thread owns 4 consecutive columns (128-bit accesses; cols % 4 == 0 and
+// 16-byte aligned rows), a workgroup 1024 columns of one row chunk.
+__global__ void __launch_bounds__(256)
+relu_bwd_colsum_stage1_kernel(const f32x4* __restrict__ g, const f32x4* __restrict__ x, f32x4* __restrict__ dx,
+                              float* __restrict__ part, int64_t rows, int64_t cols4, int64_t chunk) {
+  const int64_t c4 = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (c4 >= cols4) return;
+  const int64_t r0 = (int64_t)blockIdx.y * chunk;
+  const int64_t r1 = min(rows, r0 + chunk);
+  f32x4 s = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 8
+  for (int64_t r = r0; r < r1; ++r) {
+    const f32x4 gv = __builtin_nontemporal_load(g + r * cols4 + c4);
+    const f32x4 xv = __builtin_nontemporal_load(x + r * cols4 + c4);
+    f32x4 v;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = xv[e] > 0.0f ? gv[e] : 0.0f;
+    __builtin_nontemporal_store(v, dx + r * cols4 + c4);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) s[e] += v[e];
+  }
+  *reinterpret_cast<f32x4*>(part + (int64_t)blockIdx.y * cols4 * 4 + c4 * 4) = s;
+}
+
 // Stage 2: out[c] = sum over p of part[p][c].  A workgroup owns kCsCols
 // columns and kCsSlices slices of the parts: slice j sums its contiguous run
 // of parts in order, then a fixed pairwise tree over the slices in LDS
@@ -242,6 +269,26 @@ embedding_fwd_kernel(const float* __restrict__ w, const int64_t* __restrict__ id
       *err = 1;
     }
     out[e] = v;
+  }
+}
+
+// The same with one wave per row and 128-bit accesses (dim % 4 == 0,
+// 16-byte aligned w and out): the row's id is read once, lanes stride over
+// the row's float4 columns.
+__global__ void __launch_bounds__(256)
+embedding_fwd_vec_kernel(const f32x4* __restrict__ w, const int64_t* __restrict__ ids, f32x4* __restrict__ out,
+                         int64_t n, int64_t vocab, int64_t dim4, int* __restrict__ err) {
+  const int64_t i = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (i >= n) return;
+  const int64_t id = ids[i];
+  const bool ok = id >= 0 && id < vocab;
+  if (!ok && lane == 0 && err) *err = 1;
+  const f32x4* src = w + (ok ? id : 0) * dim4;
+  f32x4* dst = out + i * dim4;
+  for (int64_t k = lane; k < dim4; k += 64) {
+    const f32x4 v = ok ? src[k] : f32x4{0.f, 0.f, 0.f, 0.f};
+    __builtin_nontemporal_store(v, dst + k);
   }
 }
 
@@ -709,6 +756,31 @@ int aar_colsum_f32(const float* g, float* out, int64_t rows, int64_t cols, void*
   return launch_status();
 }
 
+int aar_relu_bwd_colsum_f32(const float* g, const float* x, float* dx, float* colsum, int64_t rows, int64_t cols,
+                            void* workspace, size_t workspace_bytes, void* stream) {
+  if (rows < 0 || cols <= 0) return AAR_EINVAL;
+  if (!colsum) return AAR_EINVAL;
+  if (rows == 0) return aar_memset_zero(colsum, (size_t)cols * sizeof(float), stream);
+  if (!g || !x || !dx) return AAR_EINVAL;
+  if (!workspace || workspace_bytes < aar_colsum_workspace_bytes(rows, cols)) return AAR_EWORKSPACE;
+  if (cols % 4 != 0 || !aligned16(g) || !aligned16(x) || !aligned16(dx) || !aligned16(workspace)) {
+    const int rc = aar_relu_bwd_f32(g, x, dx, rows * cols, stream);
+    return rc != AAR_OK ? rc : aar_colsum_f32(dx, colsum, rows, cols, workspace, workspace_bytes, stream);
+  }
+  hipStream_t st = as_stream(stream);
+  const int parts = colsum_parts(rows);
+  const int64_t chunk = ceil_div(rows, parts);
+  float* part = static_cast<float*>(workspace);
+  relu_bwd_colsum_stage1_kernel<<<dim3((unsigned)ceil_div(cols / 4, 256), (unsigned)parts), dim3(256), 0, st>>>(
+      reinterpret_cast<const f32x4*>(g), reinterpret_cast<const f32x4*>(x), reinterpret_cast<f32x4*>(dx), part,
+      rows, cols / 4, chunk);
+  int rc = launch_status();
+  if (rc != AAR_OK) return rc;
+  colsum_stage2_kernel<<<dim3((unsigned)ceil_div(cols, (int64_t)kCsCols)), dim3(kCsThreads), 0, st>>>(part, colsum,
+                                                                                                    parts, cols);
+  return launch_status();
+}
+
 size_t aar_sum_workspace_bytes(int64_t n) {
   (void)n;
   return (size_t)kSumBlocks * sizeof(float);
@@ -733,6 +805,11 @@ int aar_embedding_fwd_f32(const float* w, const int64_t* ids, float* out, int64_
   if (n < 0 || vocab < 0 || dim < 0) return AAR_EINVAL;
   if (n == 0 || dim == 0) return AAR_OK;
   if (!ids || !out || (vocab > 0 && !w)) return AAR_EINVAL;
+  if (dim % 4 == 0 && (vocab == 0 || aligned16(w)) && aligned16(out) && ceil_div(n, 4) <= (int64_t)UINT32_MAX) {
+    embedding_fwd_vec_kernel<<<dim3((unsigned)ceil_div(n, 4)), dim3(256), 0, as_stream(stream)>>>(
+        reinterpret_cast<const f32x4*>(w), ids, reinterpret_cast<f32x4*>(out), n, vocab, dim / 4, err);
+    return launch_status();
+  }
   embedding_fwd_kernel<<<dim3(stream_grid(n * dim)), dim3(256), 0, as_stream(stream)>>>(w, ids, out, n, vocab, dim,
                                                                                          err);
   return launch_status();

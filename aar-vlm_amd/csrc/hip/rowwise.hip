@@ -758,7 +758,10 @@ int ln_bwd_parts_for(int64_t rows, const RowPlan& p) {
     AAR_ROW_DISPATCH(p, R);
 #undef R
     cap = cus * std::min(resident, kLnBwdWavesPerCu / nw);
-    pass = (int64_t)(nw / p.w) * ln_bwd_rows(p.nv, p.w);
+    // at least 32 rows per workgroup: below the cap (short inputs) fewer,
+    // longer workgroups write fewer partial rows (16384 x 384: 20.8 -> 20.2 us,
+    // x 768: 35.7 -> 33.4 us; 64 rows was slower again)
+    pass = std::max<int64_t>((int64_t)(nw / p.w) * ln_bwd_rows(p.nv, p.w), 32);
   }
   const int64_t need = ceil_div(rows, pass);
   return (int)(need < cap ? need : cap);

@@ -844,13 +844,13 @@ class MlpReluFunction : public Function {
     // mask in the GEMM epilogue, aar_gemm_f32_relu_mask, measured slower in
     // the GPT step's profile: 219.9 us against about 150 + 43.5 us.)
     Tensor dh = Tensor::empty({rows, H}, DType::Fp32, Device::CUDA);
-    if (dh.numel() != 0) {
-      Tensor dpost = matmul_no_grad(gc, saved_w2);
-      check_status(aar_relu_bwd_f32(fp(dpost), fp(saved_h), fp(dh), rows * H, current_stream()), "mlp backward");
-    }
     {
+      // the mask pass and db1's column sum in one pass over dh (bit for bit the
+      // relu backward followed by bias_grad)
+      Tensor dpost = matmul_no_grad(gc, saved_w2);
       Workspace ws(aar_colsum_workspace_bytes(rows, H));
-      check_status(aar_colsum_f32(fp(dh), fp(db1), rows, H, ws.data(), ws.bytes(), current_stream()),
+      check_status(aar_relu_bwd_colsum_f32(fp(dpost), fp(saved_h), fp(dh), fp(db1), rows, H, ws.data(), ws.bytes(),
+                                           current_stream()),
                    "mlp backward");
     }
     Tensor dx = as_view(matmul_no_grad(dh, saved_w1), x_shape);

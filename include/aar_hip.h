@@ -121,13 +121,13 @@ int aar_gemm_f32_bias_relu(int op, int64_t M, int64_t N, int64_t K, const float*
  * element).  op must be AAR_GEMM_NT (else AAR_EUNSUPPORTED, as is K == 0).
  * Replaces matmul_a_bt_cuda + add_cuda of a pre-norm block's attention
  * output projection and residual, x + proj(attn) (cppsrc/ops/matmul.cpp:11,
- * elementwise.cpp:8; python/shakespeare/scripts/model.py:47-57). */
+ * elementwise.cpp:13; python/shakespeare/scripts/model.py:19-23). */
 int aar_gemm_f32_add(int op, int64_t M, int64_t N, int64_t K, const float* A, const float* B,
                      const float* R, float* C, void* workspace, size_t workspace_bytes, void* stream);
 /* C = (A W^T + bias[col]) + R: the same after a linear layer with a bias;
  * bit-identical to aar_gemm_f32_bias then aar_add_f32.  NT only.  Replaces
  * matmul_a_bt_cuda + add_bias_cuda + add_cuda of the MLP's output layer and
- * its residual (cppsrc/ops/matmul.cpp:11, elementwise.cpp:24 and :8). */
+ * its residual (cppsrc/ops/matmul.cpp:11, elementwise.cpp:24 and :13). */
 int aar_gemm_f32_bias_add(int op, int64_t M, int64_t N, int64_t K, const float* A, const float* B,
                           const float* bias, const float* R, float* C, void* workspace,
                           size_t workspace_bytes, void* stream);
@@ -362,7 +362,7 @@ int aar_add_f32(const float* a, const float* b, float* c, int64_t n, void* strea
 /* Elementwise over n floats; outputs may alias inputs.  Replace the reference
  * device legs sub_cuda / mul_cuda / scale_cuda / neg_cuda / relu_cuda /
  * relu_backward_cuda / gelu_cuda / gelu_backward_cuda / fill_cuda /
- * scaled_add_inplace_cuda (cppsrc/ops/elementwise.cpp:8-27, kernels
+ * scaled_add_inplace_cuda (cppsrc/ops/elementwise.cpp:13-26, kernels
  * cppsrc/ops/elementwise.cu:16-72). */
 int aar_sub_f32(const float* a, const float* b, float* c, int64_t n, void* stream);      /* c = a - b */
 int aar_mul_f32(const float* a, const float* b, float* c, int64_t n, void* stream);      /* c = a * b */
@@ -375,17 +375,26 @@ int aar_gelu_bwd_f32(const float* g, const float* x, float* dx, int64_t n, void*
 int aar_fill_f32(float* y, float value, int64_t n, void* stream);
 int aar_scaled_add_f32(float* dst, const float* src, float alpha, int64_t n, void* stream); /* dst += alpha*src (SGD) */
 
-/* y[r][c] = x[r][c] + bias[c].  Replaces add_bias_cuda (cppsrc/ops/elementwise.cpp:22). */
+/* y[r][c] = x[r][c] + bias[c].  Replaces add_bias_cuda (cppsrc/ops/elementwise.cpp:24). */
 int aar_add_bias_f32(const float* x, const float* bias, float* y, int64_t rows, int64_t cols, void* stream);
 
 /* out[c] = sum_r g[r][c], deterministic two-stage tree.  Replaces bias_grad_cuda
- * (cppsrc/ops/elementwise.cpp:23, atomicAdd kernel elementwise.cu:79-82). */
+ * (cppsrc/ops/elementwise.cpp:25, atomicAdd kernel elementwise.cu:79-82). */
 size_t aar_colsum_workspace_bytes(int64_t rows, int64_t cols);
 int aar_colsum_f32(const float* g, float* out, int64_t rows, int64_t cols,
                    void* workspace, size_t workspace_bytes, void* stream);
+/* dx = x > 0 ? g : 0 over [rows, cols] and colsum[c] = sum over rows of
+ * dx[r][c] in one pass over g, x and dx: the relu backward followed by the
+ * bias-gradient column sum of the layer below it, bit-identical to
+ * aar_relu_bwd_f32 then aar_colsum_f32 (the same row chunks summed in the same
+ * order; workspace as aar_colsum_workspace_bytes).  Replaces
+ * relu_backward_cuda + bias_grad_cuda of the MLP's first layer
+ * (cppsrc/ops/elementwise.cpp:17, :25). */
+int aar_relu_bwd_colsum_f32(const float* g, const float* x, float* dx, float* colsum, int64_t rows,
+                            int64_t cols, void* workspace, size_t workspace_bytes, void* stream);
 
 /* out[0] = sum of n floats, deterministic two-stage tree.  Replaces sum_all_cuda
- * (cppsrc/ops/elementwise.cpp:24, single-block kernel elementwise.cu:84-100). */
+ * (cppsrc/ops/elementwise.cpp:16, single-block kernel elementwise.cu:84-100). */
 size_t aar_sum_workspace_bytes(int64_t n);
 int aar_sum_f32(const float* x, float* out, int64_t n, void* workspace, size_t workspace_bytes, void* stream);
 

@@ -249,7 +249,7 @@ void flash_attention_backward_cuda(const Tensor& q, const Tensor& k, const Tenso
         "flash_attention backward");
 }
 
-// ------------------------------------------------------------ elementwise (cppsrc/ops/elementwise.cpp:8-27)
+// ------------------------------------------------------------ elementwise (cppsrc/ops/elementwise.cpp:13-26)
 Tensor add_cuda(const Tensor& a, const Tensor& b) { return binary(aar_add_f32, a, b, "add"); }
 Tensor sub_cuda(const Tensor& a, const Tensor& b) { return binary(aar_sub_f32, a, b, "sub"); }
 Tensor mul_cuda(const Tensor& a, const Tensor& b) { return binary(aar_mul_f32, a, b, "mul"); }

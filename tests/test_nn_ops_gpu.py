@@ -209,7 +209,7 @@ def test_optimizers_take_one_multi_tensor_step(gpu, ag):
 
 
 @pytest.mark.parametrize("vocab,dim,shape", [(7, 4, (2, 3)), (65, 384, (64, 256)), (256, 384, (64, 256)),
-                                             (5, 3, (6,))])
+                                             (5, 3, (6,)), (3, 260, (5, 7)), (9, 4100, (3,))])
 def test_embedding_fwd_bwd(gpu, vocab, dim, shape):
     rng = np.random.default_rng(vocab + dim)
     w = rng.standard_normal((vocab, dim)).astype(f32)
@@ -223,7 +223,12 @@ def test_embedding_fwd_bwd(gpu, vocab, dim, shape):
     assert_close(host(gpu, tw.grad), O.embedding_backward(g, ids, vocab), TOL, "embedding dW")
 
 
-def test_embedding_out_of_range_is_reported(gpu):
+@pytest.mark.parametrize("dim", [3, 8])  # the element-wise and the 128-bit row kernel
+def test_embedding_out_of_range_is_reported(gpu, dim):
+    w = dev(gpu, np.ones((5, dim), f32))
+    y = gpu.embedding(w, ids_dev(gpu, np.array([1, 5, -1, 4], np.int64)))
+    with pytest.raises(IndexError):
+        host(gpu, y)
     w = dev(gpu, np.ones((5, 3), f32))
     y = gpu.embedding(w, ids_dev(gpu, np.array([1, 5], np.int64)))  # 5 is out of range
     with pytest.raises(IndexError):
@@ -261,3 +266,42 @@ def test_cross_entropy_all_ignored_and_errors(gpu):
         host(gpu, bad)
     with pytest.raises(ValueError, match="targets must be Int64"):
         gpu.cross_entropy(logits, dev(gpu, np.zeros(3, f32)))
+
+
+@pytest.mark.parametrize("rows,cols,offset", [(16384, 1536, 0), (300, 96, 0), (17, 4100, 0), (64, 30, 0),
+                                              (100, 64, 1)])
+def test_relu_bwd_colsum_matches_the_two_passes(gpu, rows, cols, offset):
+    """aar_relu_bwd_colsum_f32 (the MLP backward's mask pass with db1's column
+    sum) against aar_relu_bwd_f32 then aar_colsum_f32, bit for bit: the fused
+    pass sums the same row chunks in the same order.  cols % 4 != 0 and an
+    offset of one float take the two-pass fallback."""
+    import ctypes
+    from devutil import Abi
+    rng = np.random.default_rng(rows + cols)
+    g = rng.standard_normal((rows, cols)).astype(f32)
+    x = rng.standard_normal((rows, cols)).astype(f32)
+    abi = Abi()
+    L = abi.L
+    vp, i64, sz = ctypes.c_void_p, ctypes.c_int64, ctypes.c_size_t
+    L.aar_relu_bwd_f32.argtypes = [vp, vp, vp, i64, vp]
+    L.aar_colsum_workspace_bytes.restype = sz
+    L.aar_colsum_workspace_bytes.argtypes = [i64, i64]
+    L.aar_colsum_f32.argtypes = [vp, vp, i64, i64, vp, sz, vp]
+    L.aar_relu_bwd_colsum_f32.argtypes = [vp, vp, vp, vp, i64, i64, vp, sz, vp]
+    try:
+        pg, px = abi.put(g, offset), abi.put(x, offset)
+        wsb = L.aar_colsum_workspace_bytes(rows, cols)
+        ws = abi.alloc(wsb)
+        pdx, pcs = abi.empty(rows * cols, offset), abi.empty(cols)
+        abi.check(L.aar_relu_bwd_f32(pg, px, pdx, rows * cols, None))
+        abi.check(L.aar_colsum_f32(pdx, pcs, rows, cols, ws, wsb, None))
+        pdx2, pcs2 = abi.empty(rows * cols, offset), abi.empty(cols)
+        abi.check(L.aar_relu_bwd_colsum_f32(pg, px, pdx2, pcs2, rows, cols, ws, wsb, None))
+        dx, cs = abi.get(pdx, (rows, cols)), abi.get(pcs, cols)
+        np.testing.assert_array_equal(abi.get(pdx2, (rows, cols)).view(np.uint32), dx.view(np.uint32))
+        np.testing.assert_array_equal(abi.get(pcs2, cols).view(np.uint32), cs.view(np.uint32))
+        ref = np.where(x > 0, g, 0).astype(np.float64).sum(0)
+        assert_close(cs, ref, TOL * np.sqrt(rows), "column sums of the masked gradient")
+        assert L.aar_relu_bwd_colsum_f32(pg, px, pdx2, pcs2, rows, cols, ws, 4, None) == -2
+    finally:
+        abi.free()
