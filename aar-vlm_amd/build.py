@@ -42,10 +42,13 @@ LIB_NAME = "libaar_hip.so"
 
 # Per-file extra flags.  The flash-attention kernels rescale their MFMA
 # accumulators with VALU ops every tile, so their accumulators are kept in
-# arch VGPRs (no accvgpr copies in the loop); the GEMM keeps its 256-register
-# accumulator tiles in AGPRs.
+# arch VGPRs (no accvgpr copies in the loop); so do the short-operand GEMMs,
+# whose few accumulators the compiler otherwise copied between AGPRs and
+# VGPRs every k tile; the tiled GEMM keeps its 256-register accumulator tiles
+# in AGPRs.
 HIP_FILE_FLAGS = {
     "flash_attn": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+    "gemm_small": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
 }
 
 

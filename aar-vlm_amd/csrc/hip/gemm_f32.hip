@@ -38,6 +38,7 @@
 #include <type_traits>
 
 #include "common.hpp"
+#include "gemm_small.hpp"
 
 namespace aar {
 namespace {
@@ -953,9 +954,36 @@ bool thin_plan_wins(int op, int64_t M, int64_t N, int64_t K) {
   return M >= 8192 && K >= 64 && N <= (op == AAR_GEMM_NT ? 80 : 96);
 }
 
+// The short-operand kernels (gemm_small.hip) have configuration id
+// kShortCfg: TN with at most 260 output rows (split over K) and NN with a
+// contraction of at most 128.  They are planned for plain products whose
+// operands the DMA path cannot stage (rows not 16-byte aligned), in place of
+// the predicated register path: at the GPT step's vocabulary-65 shapes
+// (16384 x 384 x 65 NN, 65 x 384 x 16384 TN) that path ran 20-27 us.
+constexpr int kShortCfg = kThinCfg + 1;
+bool short_plan_ok(int op, int64_t M, int64_t N, int64_t K) {
+  if (op == AAR_GEMM_TN) return shortm_shape_ok(M, N, K) && K >= 1024;
+  if (op == AAR_GEMM_NN) return shortk_shape_ok(M, N, K);
+  return false;
+}
+// gemm_vec_ok's shape conditions alone (contiguous operands, aligned bases)
+bool shape_vec_ok(int op, int64_t M, int64_t N, int64_t K) {
+  switch (op) {
+    case AAR_GEMM_NN: return K % 4 == 0 && N % 4 == 0;
+    case AAR_GEMM_NT: return K % 4 == 0;
+    default: return M % 4 == 0 && N % 4 == 0;
+  }
+}
+
+// vec_ok: whether the DMA path can stage the operands (gemm_vec_ok); when it
+// cannot, a plain product with a short operand takes the short kernels.
 Plan plan_gemm(int op, int64_t M, int64_t N, int64_t K, size_t ws_bytes, bool allow_split, int64_t batch = 1,
-               bool allow_thin = false, int epi = kEpiNone) {
+               bool allow_thin = false, int epi = kEpiNone, bool vec_ok = true) {
   if (allow_thin && batch == 1 && thin_shape_ok(op, M, N, K) && thin_plan_wins(op, M, N, K)) return Plan{kThinCfg, 1, K};
+  if (!vec_ok && batch == 1 && epi == kEpiNone && short_plan_ok(op, M, N, K)) {
+    const int s = op == AAR_GEMM_TN ? shortm_splits(M, N, K, allow_split ? ws_bytes : 0) : 1;
+    return Plan{kShortCfg, s, K};
+  }
   const int cus = device_cu_count();
   const double cu_flops = 157.3e12 / 256;  // fp32 MFMA FLOP/s per CU
   Plan best{3, 1, K};
@@ -1208,6 +1236,14 @@ int run_gemm(int op, int64_t M, int64_t N, int64_t K, const float* A, const floa
   return launch_status();
 }
 
+// The short-operand kernels on contiguous operands (no epilogue).
+int run_short(int op, int64_t M, int64_t N, int64_t K, const float* A, const float* B, float* C, int splits,
+              void* workspace, size_t ws_bytes, hipStream_t st) {
+  if (op == AAR_GEMM_TN) return run_shortm(A, nullptr, B, C, M, N, K, splits, workspace, ws_bytes, st);
+  if (op == AAR_GEMM_NN && splits == 1) return run_shortk(A, B, C, M, N, K, st);
+  return op == AAR_GEMM_NN ? AAR_EINVAL : AAR_EUNSUPPORTED;
+}
+
 // Shared argument checks; returns AAR_OK to proceed, 1 when there is nothing
 // to compute, or an error code.
 int check_gemm_args(int op, int64_t M, int64_t N, int64_t K, const float* A, const float* B, float* C,
@@ -1231,7 +1267,8 @@ using namespace aar;
 
 extern "C" size_t aar_gemm_f32_workspace_bytes(int op, int64_t M, int64_t N, int64_t K) {
   if (op < 0 || op > 2 || M <= 0 || N <= 0 || K <= 0) return 0;
-  const Plan p = plan_gemm(op, M, N, K, (size_t)-1, true, 1, true);
+  const Plan p = plan_gemm(op, M, N, K, (size_t)-1, true, 1, true, kEpiNone, shape_vec_ok(op, M, N, K));
+  if (p.cfg == kShortCfg) return shortm_workspace_bytes(M, N, K, p.splits);
   if (p.splits <= 1) return 0;
   return (size_t)p.splits * (size_t)M * (size_t)N * sizeof(float);
 }
@@ -1242,9 +1279,16 @@ extern "C" int aar_gemm_f32(int op, int64_t M, int64_t N, int64_t K, const float
   if (chk != AAR_OK) return chk == 1 ? AAR_OK : chk;
   int64_t lda, ldb;
   default_ld(op, M, N, K, lda, ldb);
-  const Plan p = plan_gemm(op, M, N, K, workspace ? workspace_bytes : 0, workspace != nullptr, 1,
-                           thin_operands_ok(op, A, B, lda, ldb));
+  const bool vec = gemm_vec_ok(op, M, N, K, A, B, lda, ldb);
+  Plan p = plan_gemm(op, M, N, K, workspace ? workspace_bytes : 0, workspace != nullptr, 1,
+                     thin_operands_ok(op, A, B, lda, ldb), kEpiNone, vec);
   if (p.cfg == kThinCfg) return run_thin(op, M, N, K, A, B, C, as_stream(stream));
+  if (p.cfg == kShortCfg) {
+    const int rc = run_short(op, M, N, K, A, B, C, p.splits, workspace, workspace_bytes, as_stream(stream));
+    if (rc != AAR_EUNSUPPORTED) return rc;
+    // (an operand alignment the short kernels do not take either)
+    p = plan_gemm(op, M, N, K, workspace ? workspace_bytes : 0, workspace != nullptr, 1, false);
+  }
   return run_gemm(op, M, N, K, A, B, C, workspace, p, as_stream(stream));
 }
 
@@ -1346,7 +1390,8 @@ extern "C" int aar_gemm_f32_tile_config(int config, int* tile_m, int* tile_n, in
 extern "C" int aar_gemm_f32_plan(int op, int64_t M, int64_t N, int64_t K, size_t workspace_bytes,
                                  int* config, int* splits) {
   if (op < 0 || op > 2 || M <= 0 || N <= 0 || K <= 0) return AAR_EINVAL;
-  const Plan p = plan_gemm(op, M, N, K, workspace_bytes, workspace_bytes > 0, 1, true);
+  const Plan p = plan_gemm(op, M, N, K, workspace_bytes, workspace_bytes > 0, 1, true, kEpiNone,
+                           shape_vec_ok(op, M, N, K));
   if (config) *config = p.cfg;
   if (splits) *splits = p.splits;
   return AAR_OK;
@@ -1355,11 +1400,16 @@ extern "C" int aar_gemm_f32_plan(int op, int64_t M, int64_t N, int64_t K, size_t
 extern "C" int aar_gemm_f32_with_config(int op, int64_t M, int64_t N, int64_t K, const float* A,
                                         const float* B, float* C, void* workspace, size_t workspace_bytes,
                                         int config, int splits, void* stream) {
-  if (config < 0 || config > kThinCfg || splits < 1 || splits > kMaxSplits) return AAR_EINVAL;
+  if (config < 0 || config > kShortCfg || splits < 1 || splits > kMaxSplits) return AAR_EINVAL;
   if (config == kThinCfg && splits != 1) return AAR_EINVAL;
   const int chk = check_gemm_args(op, M, N, K, A, B, C, stream);
   if (chk != AAR_OK) return chk == 1 ? AAR_OK : chk;
   if (config == kThinCfg) return run_thin(op, M, N, K, A, B, C, as_stream(stream));
+  if (config == kShortCfg) {
+    if ((op == AAR_GEMM_TN && !shortm_shape_ok(M, N, K)) || (op == AAR_GEMM_NN && !shortk_shape_ok(M, N, K)))
+      return AAR_EUNSUPPORTED;
+    return run_short(op, M, N, K, A, B, C, splits, workspace, workspace_bytes, as_stream(stream));
+  }
   const int64_t kps = split_chunk(K, splits, kCfgs[config].bk);
   const int real_splits = (int)ceil_div(K, kps);
   if (real_splits > 1 && (!workspace || workspace_bytes < (size_t)real_splits * M * N * sizeof(float)))

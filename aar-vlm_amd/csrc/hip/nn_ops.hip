@@ -12,16 +12,22 @@
 //  * Every reduction is a fixed-order two-stage tree (bias_grad = column sums,
 //    sum_all, cross-entropy mean), so results are bit-reproducible; the
 //    reference uses float atomicAdd for bias_grad and embedding backward.
-//  * Embedding backward is dW = onehot(ids)^T . dY, run on the MFMA GEMM
-//    (matmul_at_b layout): deterministic, and at the vocabularies of the GPT
-//    step (65, 256) far cheaper than atomics into a few hot rows.
+//  * Embedding backward is dW = onehot(ids)^T . dY on matrix cores:
+//    deterministic, and at the vocabularies of the GPT step (65, 256) far
+//    cheaper than atomics into a few hot rows.  Up to 260 rows it runs the
+//    short-M TN kernel (gemm_small.hip), which makes the one-hot values from
+//    the ids in registers and skips row blocks absent from a tile; larger
+//    vocabularies build the one-hot matrix and run the tiled GEMM.
 //  * Out-of-range ids/targets cannot throw on the device: the kernels write
 //    zeros for such rows (never reading out of bounds) and raise a flag in a
 //    caller-provided int that the host checks at its next synchronisation.
 #include <hip/hip_runtime.h>
 #include <math.h>
 
+#include <algorithm>
+
 #include "common.hpp"
+#include "gemm_small.hpp"
 
 namespace aar {
 namespace {
@@ -815,11 +821,20 @@ int aar_embedding_fwd_f32(const float* w, const int64_t* ids, float* out, int64_
   return launch_status();
 }
 
-// one-hot [n, vocab] followed by the GEMM's own workspace
+// The one-hot GEMM path: one-hot [n, vocab] followed by the GEMM's own
+// workspace.  Vocabularies up to 260 (with dim % 4 == 0) take the short-M
+// kernel with the one-hot values made from the ids in registers; its split
+// partial products need their own workspace.  The larger of the two is
+// reported, so either path runs with it.
 size_t aar_embedding_bwd_workspace_bytes(int64_t n, int64_t vocab, int64_t dim) {
   if (n <= 0 || vocab <= 0 || dim <= 0) return 0;
   const size_t oh = ((size_t)n * (size_t)vocab * sizeof(float) + 255) / 256 * 256;
-  return oh + aar_gemm_f32_workspace_bytes(AAR_GEMM_TN, vocab, dim, n);
+  size_t bytes = oh + aar_gemm_f32_workspace_bytes(AAR_GEMM_TN, vocab, dim, n);
+  if (shortm_shape_ok(vocab, dim, n)) {
+    const int s = shortm_splits(vocab, dim, n, (size_t)-1);
+    bytes = std::max(bytes, shortm_workspace_bytes(vocab, dim, n, s, true));
+  }
+  return bytes;
 }
 
 int aar_embedding_bwd_f32(const float* g, const int64_t* ids, float* dw, int64_t n, int64_t vocab, int64_t dim,
@@ -831,6 +846,12 @@ int aar_embedding_bwd_f32(const float* g, const int64_t* ids, float* dw, int64_t
   if (!g || !ids) return AAR_EINVAL;
   if ((double)n * (double)vocab > (double)(1ll << 30)) return AAR_EUNSUPPORTED;
   if (!workspace || workspace_bytes < aar_embedding_bwd_workspace_bytes(n, vocab, dim)) return AAR_EWORKSPACE;
+  if (shortm_shape_ok(vocab, dim, n) && aligned16(g) && aligned16(workspace)) {
+    // dW = onehot(ids)^T . g with the one-hot rows made from the ids in registers
+    const int s = shortm_splits(vocab, dim, n, workspace_bytes);
+    if (shortm_workspace_bytes(vocab, dim, n, s, true) <= workspace_bytes)
+      return run_shortm(nullptr, ids, g, dw, vocab, dim, n, s, workspace, workspace_bytes, as_stream(stream));
+  }
   float* oh = static_cast<float*>(workspace);
   const size_t oh_bytes = ((size_t)n * (size_t)vocab * sizeof(float) + 255) / 256 * 256;
   onehot_kernel<<<dim3(stream_grid(n * vocab)), dim3(256), 0, as_stream(stream)>>>(ids, oh, n, vocab);

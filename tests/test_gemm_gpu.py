@@ -349,11 +349,91 @@ def test_plan_and_config_errors(gpu):
         assert cfg.value >= 0 and sp.value == 1
         n = len(gemm_configs(abi))
         p = abi.alloc(4096)
-        # id n is the thin-output kernel (K = 8 is below its 16-deep k blocks); n + 1 is invalid
+        # id n is the thin-output kernel (K = 8 is below its 16-deep k blocks); n + 1
+        # the short-operand kernels (NN and TN only, NN unsplit); n + 2 is invalid
         assert abi.L.aar_gemm_f32_with_config(0, 8, 8, 8, p, p, p, None, 0, n, 1, None) == -3  # EUNSUPPORTED
-        assert abi.L.aar_gemm_f32_with_config(0, 8, 8, 8, p, p, p, None, 0, n + 1, 1, None) == -1  # EINVAL
+        assert abi.L.aar_gemm_f32_with_config(1, 8, 8, 8, p, p, p, None, 0, n + 1, 1, None) == -3
+        assert abi.L.aar_gemm_f32_with_config(0, 8, 8, 8, p, p, p, None, 0, n + 1, 2, None) == -1
+        assert abi.L.aar_gemm_f32_with_config(0, 8, 8, 8, p, p, p, None, 0, n + 2, 1, None) == -1  # EINVAL
         assert abi.L.aar_gemm_f32_with_config(0, 8, 8, 8, p, p, p, None, 0, 0, 0, None) == -1
         # a forced split needs workspace
         assert abi.L.aar_gemm_f32_with_config(0, 64, 64, 4096, p, p, p, None, 0, 0, 4, None) == -2
+    finally:
+        abi.free()
+
+
+def test_short_operand_kernels_vs_oracle(gpu):
+    """The short-operand kernels (configuration id = tile configurations + 1):
+    TN with at most 260 output rows split over K, NN with a contraction of at
+    most 128, for operands whose rows are not 16-byte aligned (a vocabulary of
+    65).  TN: MFMA over an even number of 32-row blocks plus up to 4 rows by
+    VALU (65, 68, 130 rows) or padded blocks (1, 3, 100; past 6 blocks, and
+    a misaligned A past 2, are refused and the plan falls back), N
+    ragged against the 64-column workgroup tile, K ragged against the 32-row
+    k tile, forced split counts 1, 3 and 17 and the planned one, A one float
+    off 16-byte alignment (4-byte DMAs).  NN: K below one 8-step MFMA chunk
+    (1, 7), K % 8 steps by VALU (65, 127), misaligned A.  Reruns are bit
+    identical; the plan takes this kernel for the GPT head's TN and NN
+    products, and aar_gemm_f32 runs them through it."""
+    abi = Abi()
+    try:
+        short = len(gemm_configs(abi)) + 1
+        tn_shapes = [(65, 384, 16384), (65, 388, 4099), (1, 4, 1024), (3, 64, 1000), (100, 100, 2048),
+                     (68, 100, 2048), (130, 128, 1500), (200, 388, 1111), (257, 64, 3000), (260, 68, 777)]
+        # (with_config is given pa as C where it must refuse before any launch)
+        for (M, N, K) in tn_shapes:
+            rng = np.random.default_rng(M + N + K)
+            a, b = operands("tn", M, N, K, rng)
+            ref = O.matmul("tn", a, b)
+            for off in ((0, 1) if M in (65, 130, 257) else (0,)):
+                pa, pb = abi.put(a, offset_floats=off), abi.put(b)
+                ws_bytes = 64 * M * N * 4 + 4096
+                ws = abi.alloc(ws_bytes)
+                # more than 6 row blocks of a dense A do not fit two LDS stages,
+                # and a misaligned A past 2 blocks needs more 4-byte DMAs than
+                # one vmcnt counts: refused, and the plan falls back to the
+                # tiled kernels
+                supported = M <= 196 and (off == 0 or M <= 68)
+                if not supported:
+                    assert abi.L.aar_gemm_f32_with_config(2, M, N, K, pa, pb, pa, ws, ws_bytes, short, 3, None) == -3
+                for splits in ((1, 3, 17) if supported else ()):
+                    outs = []
+                    for _ in range(2):
+                        pc = abi.empty(M * N)
+                        abi.check(abi.L.aar_gemm_f32_with_config(2, M, N, K, pa, pb, pc, ws, ws_bytes, short, splits,
+                                                                 None))
+                        outs.append(abi.get(pc, (M, N)))
+                    np.testing.assert_array_equal(outs[0], outs[1])
+                    assert_close(outs[0], ref, gemm_tol(K), f"tn short {(M, N, K)} splits {splits} off {off}")
+                pc = abi.empty(M * N)
+                abi.check(abi.L.aar_gemm_f32(2, M, N, K, pa, pb, pc, ws, ws_bytes, None))
+                assert_close(abi.get(pc, (M, N)), ref, gemm_tol(K), f"tn planned {(M, N, K)} off {off}")
+        for (M, N, K) in [(16384, 384, 65), (1000, 388, 7), (300, 100, 127), (77, 4, 1), (129, 260, 72)]:
+            rng = np.random.default_rng(M + N + K + 1)
+            a, b = operands("nn", M, N, K, rng)
+            ref = O.matmul("nn", a, b)
+            for off in (0, 1):
+                pa, pb = abi.put(a, offset_floats=off), abi.put(b)
+                outs = []
+                for _ in range(2):
+                    pc = abi.empty(M * N)
+                    abi.check(abi.L.aar_gemm_f32_with_config(0, M, N, K, pa, pb, pc, None, 0, short, 1, None))
+                    outs.append(abi.get(pc, (M, N)))
+                np.testing.assert_array_equal(outs[0], outs[1])
+                assert_close(outs[0], ref, gemm_tol(K), f"nn short {(M, N, K)} off {off}")
+                pc = abi.empty(M * N)
+                abi.check(abi.L.aar_gemm_f32(0, M, N, K, pa, pb, pc, None, 0, None))
+                assert_close(abi.get(pc, (M, N)), ref, gemm_tol(K), f"nn planned {(M, N, K)} off {off}")
+        cfg, sp = ctypes.c_int(-1), ctypes.c_int(-1)
+        for op, (M, N, K) in ((2, (65, 384, 16384)), (0, (16384, 384, 65))):
+            ws = abi.L.aar_gemm_f32_workspace_bytes(op, M, N, K)
+            abi.check(abi.L.aar_gemm_f32_plan(op, M, N, K, ws, ctypes.byref(cfg), ctypes.byref(sp)))
+            assert cfg.value == short, (op, M, N, K, cfg.value)
+            assert sp.value >= (2 if op == 2 else 1)
+            assert ws >= (sp.value * M * N * 4 if sp.value > 1 else 0)
+        p = abi.alloc(4096)
+        assert abi.L.aar_gemm_f32_with_config(2, 261, 64, 1024, p, p, p, None, 0, short, 1, None) == -3  # M > 260
+        assert abi.L.aar_gemm_f32_with_config(0, 64, 64, 129, p, p, p, None, 0, short, 1, None) == -3  # K > 128
+        assert abi.L.aar_gemm_f32_with_config(2, 65, 64, 4096, p, p, p, None, 0, short, 4, None) == -2  # workspace
     finally:
         abi.free()

@@ -223,6 +223,24 @@ def test_embedding_fwd_bwd(gpu, vocab, dim, shape):
     assert_close(host(gpu, tw.grad), O.embedding_backward(g, ids, vocab), TOL, "embedding dW")
 
 
+@pytest.mark.parametrize("vocab,dim,B,T", [(256, 384, 64, 256), (260, 8, 3, 200), (300, 8, 2, 100)])
+def test_embedding_backward_position_ids(gpu, vocab, dim, B, T):
+    """Position ids (arange(T) per sequence, as the GPT step looks up its
+    position table): in each 32-id tile only one 32-row block of the table
+    occurs, and the short-M kernel skips the others; vocab 300 is past its
+    260 rows and takes the one-hot GEMM path.  Rerun bit identical."""
+    rng = np.random.default_rng(vocab + T)
+    ids = np.tile(np.arange(T, dtype=np.int64), (B, 1))
+    g = rng.standard_normal((B, T, dim)).astype(f32)
+    outs = []
+    for _ in range(2):
+        tw = dev(gpu, rng.standard_normal((vocab, dim)).astype(f32), True)
+        gpu.embedding(tw, ids_dev(gpu, ids)).backward(dev(gpu, g))
+        outs.append(host(gpu, tw.grad))
+    np.testing.assert_array_equal(outs[0], outs[1])
+    assert_close(outs[0], O.embedding_backward(g, ids, vocab), TOL, "embedding dW at position ids")
+
+
 @pytest.mark.parametrize("dim", [3, 8])  # the element-wise and the 128-bit row kernel
 def test_embedding_out_of_range_is_reported(gpu, dim):
     w = dev(gpu, np.ones((5, dim), f32))
