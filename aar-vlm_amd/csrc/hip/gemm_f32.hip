@@ -85,14 +85,36 @@ struct GemmEpi {
 // times ldc, which the compiler forms once in scalar registers.
 // NQ < 4: only register quads q0 .. q0 + NQ - 1 of each accumulator are
 // stored, their values held in quads 0 .. NQ - 1 of acc (a K group's share).
+constexpr bool epi_has_bias(int epi) { return epi == kEpiBias || epi == kEpiBiasRelu || epi == kEpiBiasAdd; }
+
+// The bias values a lane's accumulator columns need (column c0 + 32 j + lr),
+// read before the main loop so their latency is hidden under it: read at
+// the epilogue, they cost a memory round trip per workgroup round (measured
+// +10 us on a 16384 x 1536 x 384 product with the bias epilogue).
+template <int TN, int EPI>
+__device__ __forceinline__ void load_bias(const GemmEpi& ep, int64_t N, int64_t c0, int lr, float (&bias)[TN]) {
+#pragma unroll
+  for (int j = 0; j < TN; ++j) {
+    const int64_t col = c0 + 32 * j + lr;
+    bias[j] = 0.f;
+    if constexpr (epi_has_bias(EPI)) bias[j] = col < N ? ep.bias[col] : 0.f;
+  }
+}
+
 template <int TM, int TN, int EPI, int NQ = 4>
 __device__ __forceinline__ void store_tile(const f32x16 (&acc)[TM][TN], float* __restrict__ C, const GemmEpi& ep,
-                                           int64_t M, int64_t N, int64_t ldc, int64_t r0, int64_t c0, int lr,
-                                           int h, int q0 = 0) {
+                                           const float (&bias)[TN], int64_t M, int64_t N, int64_t ldc, int64_t r0,
+                                           int64_t c0, int lr, int h, int q0 = 0) {
   const bool interior = r0 + 32 * TM <= M && c0 + 32 * TN <= N;
   const int64_t lane0 = (r0 + 4 * h) * ldc + c0 + lr;  // offset of the lane's first element
   float* const Cl = C + lane0;
   constexpr bool kAux = EPI == kEpiMask || EPI == kEpiAdd || EPI == kEpiBiasAdd;
+  // The loaded operands (bias, aux) are waited for once, explicitly, before
+  // the stores.  Left to the compiler, the per-element bounds branches made
+  // it wait for vmcnt(0) before every store that uses one (stores count in
+  // vmcnt), one memory round trip per element: measured +10 us on a
+  // 16384 x 1536 x 384 product with the bias epilogue.
+  if constexpr (epi_has_bias(EPI)) wait_vm_lgkm0<0>();
   const float* const Xl = kAux ? ep.aux + lane0 : nullptr;
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
@@ -113,12 +135,12 @@ __device__ __forceinline__ void store_tile(const f32x16 (&acc)[TM][TN], float* _
           xv[j][r] = (interior || (r0 + 4 * h + dr < M && col < N)) ? Xl[off] : 0.0f;
         }
       }
+      wait_vm_lgkm0<0>();
     }
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
       const int64_t col = c0 + 32 * j + lr;
-      float b = 0.f;
-      if constexpr (EPI == kEpiBias || EPI == kEpiBiasRelu || EPI == kEpiBiasAdd) b = col < N ? ep.bias[col] : 0.f;
+      const float b = bias[j];
 #pragma unroll
       for (int r = 0; r < 4 * NQ; ++r) {
         const int dr = 32 * i + 8 * (q0 + r / 4) + (r % 4);  // row - r0 - 4h
@@ -312,7 +334,9 @@ gemm_f32_kernel(const float* __restrict__ A, const float* __restrict__ B, float*
 
   // Accumulator layout of a 32x32 block: lane (lr, h), register r holds
   // row 8*(r/4) + 4*h + (r%4), column lr.
-  store_tile<TM, TN, EPI>(acc, C, ep, M, N, ldc, m0 + wm0, n0 + wn0, lr, h);
+  float bias[TN];
+  load_bias<TN, EPI>(ep, N, n0 + wn0, lr, bias);
+  store_tile<TM, TN, EPI>(acc, C, ep, bias, M, N, ldc, m0 + wm0, n0 + wn0, lr, h);
 }
 
 // ------------------------------------------------------------------ DMA path
@@ -502,6 +526,8 @@ gemm_f32_dma_kernel(const float* __restrict__ A, const float* __restrict__ B, fl
   TB tb;
   ta.init(lda, m0, M, wave, lane);
   tb.init(ldb, n0, N, wave, lane);
+  float bias[TN];
+  load_bias<TN, EPI>(ep, N, n0 + wn0, lr, bias);
   auto issue = [&](int t) {
     const int64_t k0 = kbeg + (int64_t)t * BK;
     float* st = ring + (t % S) * kStage;
@@ -599,11 +625,11 @@ gemm_f32_dma_kernel(const float* __restrict__ A, const float* __restrict__ B, fl
 #pragma unroll
           for (int e = 0; e < 4; ++e) acc[i][j][4 * qq + e] = v[e];
         }
-    store_tile<TM, TN, EPI, QPG>(acc, C, ep, M, N, ldc, m0 + wm0, n0 + wn0, lr, h, q0);
+    store_tile<TM, TN, EPI, QPG>(acc, C, ep, bias, M, N, ldc, m0 + wm0, n0 + wn0, lr, h, q0);
     return;
   }
 
-  store_tile<TM, TN, EPI>(acc, C, ep, M, N, ldc, m0 + wm0, n0 + wn0, lr, h);
+  store_tile<TM, TN, EPI>(acc, C, ep, bias, M, N, ldc, m0 + wm0, n0 + wn0, lr, h);
 }
 
 // ------------------------------------------------------------ thin outputs
@@ -992,16 +1018,17 @@ Plan plan_gemm(int op, int64_t M, int64_t N, int64_t K, size_t ws_bytes, bool al
     const Cfg& cf = kCfgs[c];
     if (!(cf.ops & (1 << op))) continue;
     const int64_t tiles = ceil_div(M, (int64_t)cf.bm) * ceil_div(N, (int64_t)cf.bn) * batch;
-    // Configuration 8 as NT or TN: plain products only (with the bias or
-    // bias + relu epilogue it lost 1-3 % to 3 and 6 at the GPT MLP shapes),
-    // and only grids of at most one round of its resident workgroups, or of
-    // two or three whole rounds.  Measured at 16384 rows (64 row tiles x
-    // N / 192), a partial last round loses to 3 and 6 by 9-17 % (N = 960,
-    // 1152) and grids of four or more rounds lose to 0 by up to 4 %, while
-    // whole short grids gain 1-19 %.
+    // Configuration 8 as NT or TN: only grids of at most one round of its
+    // resident workgroups, or of two or three whole rounds.  Measured at
+    // 16384 rows (64 row tiles x N / 192), a partial last round loses to 3
+    // and 6 by 9-17 % (N = 960, 1152) and grids of four or more rounds lose
+    // to 0 by up to 4 %, while whole short grids gain 1-19 %.  With the bias
+    // + relu and bias + residual epilogues of the GPT MLP it gains 1.5-2 %
+    // over 3 and 6 (16384 x 1536 x 384: 158.5 against 161.0 us;
+    // 16384 x 384 x 1536: 158.8 against 161.7 us).
     if (c == 8 && op != AAR_GEMM_NN) {
       const int64_t round = (int64_t)cus * cf.resident;
-      if (epi != kEpiNone || !(tiles <= round || (tiles % round == 0 && tiles / round <= 3))) continue;
+      if (!(tiles <= round || (tiles % round == 0 && tiles / round <= 3))) continue;
     }
     // the measured split counts, then the one that fills the CUs' slots in
     // one round

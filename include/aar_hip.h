@@ -161,7 +161,12 @@ int aar_gemm_f32_batched(int op, int64_t batch, int64_t M, int64_t N, int64_t K,
  * the thin-output kernel: N <= 128, 16 <= K <= 512 with K % 16 == 0, B
  * padded to 16-column blocks in LDS (at most 128 KB), a 16-byte aligned A
  * for NN/NT and B for NT, no split (splits must be 1); outside those limits
- * it returns AAR_EUNSUPPORTED.
+ * it returns AAR_EUNSUPPORTED.  Id n+1 is the short-operand kernels: TN with
+ * M <= 260 (split over K: `splits` partial products summed in order; a
+ * 16-byte aligned B, N % 4 == 0; up to 6 32-row blocks of M, 2 when A is not
+ * 16-byte aligned) and NN with K <= 128 (unsplit); aar_gemm_f32 plans them
+ * for plain products whose rows the tiled kernels cannot stage (not 16-byte
+ * aligned: a vocabulary of 65).
  * aar_gemm_f32_plan reports the configuration and split count aar_gemm_f32
  * would use with `workspace_bytes` of scratch (id n for thin outputs such as
  * a vocabulary head; aar_gemm_f32 takes it only when the operands' alignment
