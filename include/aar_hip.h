@@ -409,8 +409,11 @@ int aar_sum_f32(const float* x, float* out, int64_t n, void* workspace, size_t w
 int aar_embedding_fwd_f32(const float* w, const int64_t* ids, float* out, int64_t n, int64_t vocab,
                           int64_t dim, int* err, void* stream);
 
-/* dw[vocab, dim] = onehot(ids)^T . g[n, dim] on the MFMA GEMM (deterministic;
- * AAR_EUNSUPPORTED when n*vocab > 2^30).  Replaces embedding_backward_cuda
+/* dw[vocab, dim] = onehot(ids)^T . g[n, dim] on matrix cores (deterministic;
+ * AAR_EUNSUPPORTED when n*vocab > 2^30).  Up to 260 rows (dim % 4 == 0, g
+ * 16-byte aligned) the one-hot values are made from the ids in registers by
+ * the short-M GEMM kernel; larger vocabularies build the one-hot matrix in
+ * the workspace and run the tiled GEMM.  Replaces embedding_backward_cuda
  * (cppsrc/ops/embedding.cpp:10-11, atomicAdd kernel embedding.cu:19-26). */
 size_t aar_embedding_bwd_workspace_bytes(int64_t n, int64_t vocab, int64_t dim);
 int aar_embedding_bwd_f32(const float* g, const int64_t* ids, float* dw, int64_t n, int64_t vocab,
