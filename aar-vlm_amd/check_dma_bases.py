@@ -89,11 +89,11 @@ def _functions(asm: str) -> dict[str, list[str]]:
 def _spills(asm: str) -> dict[str, tuple[int, int]]:
     out, name = {}, None
     for ln in asm.split("\n"):
-        m = re.match(r"\s+\.name:\s+(\S+)", ln)
+        m = re.match(r"\s+(?:-\s+)?\.name:\s+(\S+)", ln)
         if m:
             name = m.group(1)
             out[name] = [0, 0]
-        m = re.match(r"\s+\.(private_segment_fixed_size|vgpr_spill_count):\s+(\d+)", ln)
+        m = re.match(r"\s+(?:-\s+)?\.(private_segment_fixed_size|vgpr_spill_count):\s+(\d+)", ln)
         if m and name:
             out[name][0 if m.group(1).startswith("private") else 1] = int(m.group(2))
     return {k: tuple(v) for k, v in out.items()}
