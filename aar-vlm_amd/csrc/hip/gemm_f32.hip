@@ -37,6 +37,7 @@
 
 #include <type_traits>
 
+#include "colsum.hpp"
 #include "common.hpp"
 #include "gemm_small.hpp"
 
@@ -71,11 +72,34 @@ __device__ __forceinline__ void map_tile(int tiles_m, int tiles_n, int& tm, int&
 //                 product: x + y W^T)
 //   kEpiBiasAdd   C = (acc + bias[col]) + aux[row][col]  (the same after a
 //                 linear layer with a bias)
-enum : int { kEpiNone = 0, kEpiBias = 1, kEpiBiasRelu = 2, kEpiMask = 3, kEpiAdd = 4, kEpiBiasAdd = 5 };
+// and two that carry a relu's mask as bits from the forward product to the
+// backward one (store_tile_bits), so the backward reads 1 bit per element
+// where kEpiMask reads the relu's whole output:
+//   kEpiBiasReluBits  C = max(0, acc + bias[col]) as kEpiBiasRelu, and bit
+//                     col % 32 of word bits[row * ldm + col / 32] set where
+//                     C > 0 (ldm = ceil(N / 32) words per row)
+//   kEpiMaskBits      C = bit(row, col) ? acc : 0 (the relu backward), and
+//                     part[row / 64][col] = the sum of C over the 64 rows of
+//                     that chunk, in row order from 0.f: the stage-1
+//                     partials of aar_colsum_f32 (a wave owns one chunk)
+enum : int {
+  kEpiNone = 0,
+  kEpiBias = 1,
+  kEpiBiasRelu = 2,
+  kEpiMask = 3,
+  kEpiAdd = 4,
+  kEpiBiasAdd = 5,
+  kEpiBiasReluBits = 6,
+  kEpiMaskBits = 7
+};
 struct GemmEpi {
   const float* bias;
   const float* aux;
+  uint32_t* bits = nullptr;  // kEpiBiasReluBits writes, kEpiMaskBits reads
+  int64_t ldm = 0;           // words per row of bits
+  float* part = nullptr;     // kEpiMaskBits: [M / 64][N] column partials
 };
+constexpr bool epi_bits(int epi) { return epi == kEpiBiasReluBits || epi == kEpiMaskBits; }
 
 // Epilogue: a wave's (32*TM) x (32*TN) accumulators to C.  Accumulator
 // layout of a 32x32 block: lane (lr, h), register r holds row
@@ -85,7 +109,9 @@ struct GemmEpi {
 // times ldc, which the compiler forms once in scalar registers.
 // NQ < 4: only register quads q0 .. q0 + NQ - 1 of each accumulator are
 // stored, their values held in quads 0 .. NQ - 1 of acc (a K group's share).
-constexpr bool epi_has_bias(int epi) { return epi == kEpiBias || epi == kEpiBiasRelu || epi == kEpiBiasAdd; }
+constexpr bool epi_has_bias(int epi) {
+  return epi == kEpiBias || epi == kEpiBiasRelu || epi == kEpiBiasAdd || epi == kEpiBiasReluBits;
+}
 
 // The bias values a lane's accumulator columns need (column c0 + 32 j + lr),
 // read before the main loop so their latency is hidden under it: read at
@@ -98,6 +124,112 @@ __device__ __forceinline__ void load_bias(const GemmEpi& ep, int64_t N, int64_t 
     const int64_t col = c0 + 32 * j + lr;
     bias[j] = 0.f;
     if constexpr (epi_has_bias(EPI)) bias[j] = col < N ? ep.bias[col] : 0.f;
+  }
+}
+
+// Mask words the kEpiMaskBits epilogue needs, read before the main loop like
+// the bias: for block (i, j) lane k (k < 32) holds the word of register
+// k % 16 of lane half k / 16, i.e. row r0 + 32 i + 8 (k%16 / 4) + 4 (k / 16)
+// + k % 4, columns c0 + 32 j .. + 31 (lanes 32..63 hold the same words).
+template <int TM, int TN, int EPI>
+__device__ __forceinline__ void load_bits(const GemmEpi& ep, int64_t M, int64_t N, int64_t r0, int64_t c0, int lane,
+                                          uint32_t (&words)[TM][TN]) {
+  const int k = lane & 31, rr = k & 15;
+  const int64_t row0 = r0 + 8 * (rr >> 2) + 4 * (k >> 4) + (rr & 3);
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      words[i][j] = 0u;
+      if constexpr (EPI == kEpiMaskBits) {
+        const int64_t row = row0 + 32 * i;
+        if (row < M && c0 + 32 * j < N) words[i][j] = ep.bits[row * ep.ldm + ((c0 + 32 * j) >> 5)];
+      }
+    }
+}
+
+// The two mask-bit epilogues (see kEpiBiasReluBits / kEpiMaskBits).  Column
+// blocks start at multiples of 32 (c0 and the tile widths are), so the 32
+// columns of a block are one mask word.
+//   kEpiBiasReluBits: for register r, __ballot(C > 0) gives the words of the
+//   block's rows 8(r/4) + r%4 (lanes 0-31) and that + 4 (lanes 32-63); lane k
+//   collects the word of register k % 16, half k / 16 and stores it.
+//   kEpiMaskBits (WM = 64: the wave's rows are one 64-row chunk): lane
+//   (lr, h) takes its bit from the word of its row, read out of the lane that
+//   loaded it (v_readlane), and the lanes of half 0 sum column c0 + 32 j + lr
+//   over the chunk's rows in order, the half-1 rows handed over by
+//   v_permlane32_swap.
+template <int TM, int TN, int EPI>
+__device__ __forceinline__ void store_tile_bits(const f32x16 (&acc)[TM][TN], float* __restrict__ C,
+                                                const GemmEpi& ep, const float (&bias)[TN],
+                                                const uint32_t (&words)[TM][TN], int64_t M, int64_t N, int64_t ldc,
+                                                int64_t r0, int64_t c0, int lr, int h) {
+  static_assert(epi_bits(EPI), "mask-bit epilogues only");
+  static_assert(EPI != kEpiMaskBits || TM == 2, "a kEpiMaskBits wave owns one 64-row chunk");
+  const int lane = lr + 32 * h;
+  wait_vm_lgkm0<0>();  // bias / mask words (see store_tile)
+#pragma unroll
+  for (int j = 0; j < TN; ++j) {
+    const int64_t col = c0 + 32 * j + lr;
+    const bool col_ok = col < N;
+    float vals[TM][16];
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      uint32_t w = 0u;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t row = r0 + 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
+        const bool ok = col_ok && row < M;
+        float v;
+        if constexpr (EPI == kEpiBiasReluBits) {
+          v = fmaxf(0.0f, acc[i][j][r] + bias[j]);
+          const uint64_t bal = __ballot(ok && v > 0.0f);
+          w = lane == r ? (uint32_t)bal : w;
+          w = lane == 16 + r ? (uint32_t)(bal >> 32) : w;
+        } else {
+          const uint32_t lo = __builtin_amdgcn_readlane(words[i][j], r);
+          const uint32_t hi = __builtin_amdgcn_readlane(words[i][j], 16 + r);
+          v = (((h ? hi : lo) >> lr) & 1u) ? acc[i][j][r] : 0.0f;
+          vals[i][r] = v;
+        }
+        if (ok) C[row * ldc + col] = v;
+      }
+      if constexpr (EPI == kEpiBiasReluBits) {
+        if (lane < 32) {
+          const int rr = lane & 15;
+          const int64_t row = r0 + 32 * i + 8 * (rr >> 2) + 4 * (lane >> 4) + (rr & 3);
+          if (row < M && c0 + 32 * j < N) ep.bits[row * ep.ldm + ((c0 + 32 * j) >> 5)] = w;
+        }
+      }
+    }
+    if constexpr (EPI == kEpiMaskBits) {
+      // rows 32 i + 8 g + {0..3} are half 0's registers 4g..4g+3, rows
+      // 32 i + 8 g + {4..7} half 1's
+      float s = 0.f;
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          float other[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+#if defined(__HIP_DEVICE_COMPILE__)
+            // the swap hands each lane its own value and its partner's, one
+            // in each result; where the two are equal either is the partner's
+            const uint32_t u = __float_as_uint(vals[i][4 * g + e]);
+            const auto sw = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+            other[e] = __uint_as_float(sw[0] == u ? sw[1] : sw[0]);
+#else
+            other[e] = vals[i][4 * g + e];
+#endif
+          }
+#pragma unroll
+          for (int e = 0; e < 4; ++e) s += vals[i][4 * g + e];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) s += other[e];
+        }
+      if (h == 0 && col_ok && r0 < M) ep.part[(r0 >> 6) * N + col] = s;
+    }
   }
 }
 
@@ -528,6 +660,8 @@ gemm_f32_dma_kernel(const float* __restrict__ A, const float* __restrict__ B, fl
   tb.init(ldb, n0, N, wave, lane);
   float bias[TN];
   load_bias<TN, EPI>(ep, N, n0 + wn0, lr, bias);
+  uint32_t words[TM][TN];
+  load_bits<TM, TN, EPI>(ep, M, N, m0 + wm0, n0 + wn0, lane, words);
   auto issue = [&](int t) {
     const int64_t k0 = kbeg + (int64_t)t * BK;
     float* st = ring + (t % S) * kStage;
@@ -629,7 +763,11 @@ gemm_f32_dma_kernel(const float* __restrict__ A, const float* __restrict__ B, fl
     return;
   }
 
-  store_tile<TM, TN, EPI>(acc, C, ep, bias, M, N, ldc, m0 + wm0, n0 + wn0, lr, h);
+  if constexpr (epi_bits(EPI)) {
+    store_tile_bits<TM, TN, EPI>(acc, C, ep, bias, words, M, N, ldc, m0 + wm0, n0 + wn0, lr, h);
+  } else {
+    store_tile<TM, TN, EPI>(acc, C, ep, bias, M, N, ldc, m0 + wm0, n0 + wn0, lr, h);
+  }
 }
 
 // ------------------------------------------------------------ thin outputs
@@ -1082,16 +1220,29 @@ int launch_cfg(bool vec, const float* A, const float* B, float* C, int64_t M, in
   dim3 grid((unsigned)(tiles_m * tiles_n), (unsigned)splits, (unsigned)bt.count);
   auto go = [&](auto epi_tag) {
     constexpr int E = decltype(epi_tag)::value;
-    if constexpr ((!A_KC && BM % 64 != 0) || (!B_KC && BN % 64 != 0)) {
-      if (vec) return AAR_EUNSUPPORTED;  // no DMA layout for this row-contiguous tile
-    } else if (vec) {
+    // The mask-bit epilogues run on the DMA path with one K group only, and
+    // kEpiMaskBits needs 64-row wave tiles (one column-sum chunk per wave).
+    if constexpr (epi_bits(E) && (KG > 1 || (E == kEpiMaskBits && WM != 64) || (!A_KC && BM % 64 != 0) ||
+                                  (!B_KC && BN % 64 != 0))) {
+      return AAR_EUNSUPPORTED;
+    } else if constexpr (epi_bits(E)) {
+      if (!vec) return AAR_EUNSUPPORTED;
       gemm_f32_dma_kernel<BM, BN, BK, WM, WN, kWpe, STAGES, A_KC, B_KC, E, KG><<<grid, dim3(kWaves * KG * 64), 0, st>>>(
           A, B, C, M, N, K, lda, ldb, ldc, kps, split_stride, tiles_m, tiles_n, bt.sA, bt.sB, bt.sC, ep);
       return launch_status();
-    }
-    gemm_f32_kernel<BM, BN, BK, WM, WN, kWpeReg, A_KC, B_KC, E><<<grid, dim3(kWaves * 64), 0, st>>>(
+    } else {
+      if constexpr ((!A_KC && BM % 64 != 0) || (!B_KC && BN % 64 != 0)) {
+        if (vec) return AAR_EUNSUPPORTED;  // no DMA layout for this row-contiguous tile
+      } else if (vec) {
+        gemm_f32_dma_kernel<BM, BN, BK, WM, WN, kWpe, STAGES, A_KC, B_KC, E, KG>
+            <<<grid, dim3(kWaves * KG * 64), 0, st>>>(A, B, C, M, N, K, lda, ldb, ldc, kps, split_stride, tiles_m,
+                                                      tiles_n, bt.sA, bt.sB, bt.sC, ep);
+        return launch_status();
+      }
+      gemm_f32_kernel<BM, BN, BK, WM, WN, kWpeReg, A_KC, B_KC, E><<<grid, dim3(kWaves * 64), 0, st>>>(
           A, B, C, M, N, K, lda, ldb, ldc, kps, split_stride, tiles_m, tiles_n, bt.sA, bt.sB, bt.sC, ep);
-    return launch_status();
+      return launch_status();
+    }
   };
   // bias + relu and the residual adds are instantiated for the linear layer's
   // x W^T (NT) only, the relu mask for its input gradient dY W (NN) only.
@@ -1109,6 +1260,12 @@ int launch_cfg(bool vec, const float* A, const float* B, float* C, int64_t M, in
       return AAR_EUNSUPPORTED;
     case kEpiMask:
       if constexpr (A_KC && !B_KC) return go(std::integral_constant<int, kEpiMask>{});
+      return AAR_EUNSUPPORTED;
+    case kEpiBiasReluBits:
+      if constexpr (A_KC && B_KC) return go(std::integral_constant<int, kEpiBiasReluBits>{});
+      return AAR_EUNSUPPORTED;
+    case kEpiMaskBits:
+      if constexpr (A_KC && !B_KC) return go(std::integral_constant<int, kEpiMaskBits>{});
       return AAR_EUNSUPPORTED;
     default: return AAR_EINVAL;
   }
@@ -1404,6 +1561,63 @@ extern "C" int aar_gemm_f32_relu_mask(int op, int64_t M, int64_t N, int64_t K, c
     return rc != AAR_OK ? rc : aar_relu_bwd_f32(C, mask, C, M * N, stream);
   }
   return run_gemm(op, M, N, K, A, B, C, workspace, p, as_stream(stream), kEpiMask, GemmEpi{nullptr, mask});
+}
+
+// aar_gemm_f32_bias_relu's plan and values, plus the relu's mask as bits
+// (kEpiBiasReluBits).  Plans without that epilogue return AAR_EUNSUPPORTED
+// before anything is launched.
+extern "C" int aar_gemm_f32_bias_relu_bits(int op, int64_t M, int64_t N, int64_t K, const float* A, const float* B,
+                                           const float* bias, float* C, uint32_t* bits, void* workspace,
+                                           size_t workspace_bytes, void* stream) {
+  if (op < 0 || op > 2 || M < 0 || N < 0 || K < 0) return AAR_EINVAL;
+  if (M == 0 || N == 0) return AAR_OK;
+  if (!bias || !bits) return AAR_EINVAL;
+  if (op != AAR_GEMM_NT || K == 0) return AAR_EUNSUPPORTED;
+  const int chk = check_gemm_args(op, M, N, K, A, B, C, stream);
+  if (chk != AAR_OK) return chk;
+  const Plan p = plan_gemm(op, M, N, K, workspace ? workspace_bytes : 0, workspace != nullptr, 1, false, kEpiBiasRelu);
+  if (p.splits > 1) return AAR_EUNSUPPORTED;
+  GemmEpi ep{bias, nullptr};
+  ep.bits = bits;
+  ep.ldm = ceil_div(N, (int64_t)32);
+  return run_gemm(op, M, N, K, A, B, C, nullptr, p, as_stream(stream), kEpiBiasReluBits, ep);
+}
+
+extern "C" size_t aar_gemm_f32_mask_bits_colsum_workspace_bytes(int64_t M, int64_t N) {
+  if (M <= 0 || N <= 0) return 0;
+  return (size_t)ceil_div(M, (int64_t)64) * (size_t)N * sizeof(float);
+}
+
+// The product planned as aar_gemm_f32 plans it with the workspace it asks
+// for, masked by the bits in the epilogue (kEpiMaskBits), which also writes
+// aar_colsum_f32's stage-1 partials of the masked product; colsum's stage 2
+// finishes them.  Plans without that epilogue return AAR_EUNSUPPORTED before
+// anything is launched.
+extern "C" int aar_gemm_f32_mask_bits_colsum(int op, int64_t M, int64_t N, int64_t K, const float* A,
+                                             const float* B, const uint32_t* bits, float* C, float* colsum,
+                                             void* workspace, size_t workspace_bytes, void* stream) {
+  if (op < 0 || op > 2 || M < 0 || N < 0 || K < 0) return AAR_EINVAL;
+  if (N == 0) return AAR_OK;
+  if (!colsum) return AAR_EINVAL;
+  if (M == 0) return aar_memset_zero(colsum, (size_t)N * sizeof(float), stream);
+  if (!bits) return AAR_EINVAL;
+  if (op != AAR_GEMM_NN || K == 0 || !colsum_chunks_of_64(M)) return AAR_EUNSUPPORTED;
+  const int chk = check_gemm_args(op, M, N, K, A, B, C, stream);
+  if (chk != AAR_OK) return chk;
+  if (!workspace || workspace_bytes < aar_gemm_f32_mask_bits_colsum_workspace_bytes(M, N)) return AAR_EWORKSPACE;
+  int64_t lda, ldb;
+  default_ld(op, M, N, K, lda, ldb);
+  const bool vec = gemm_vec_ok(op, M, N, K, A, B, lda, ldb);
+  const Plan p = plan_gemm(op, M, N, K, (size_t)-1, true, 1, thin_operands_ok(op, A, B, lda, ldb), kEpiNone, vec);
+  if (p.splits > 1 || p.cfg >= kNumCfgs) return AAR_EUNSUPPORTED;
+  GemmEpi ep{nullptr, nullptr};
+  ep.bits = const_cast<uint32_t*>(bits);
+  ep.ldm = ceil_div(N, (int64_t)32);
+  ep.part = static_cast<float*>(workspace);
+  hipStream_t st = as_stream(stream);
+  const int rc = run_gemm(op, M, N, K, A, B, C, nullptr, p, st, kEpiMaskBits, ep);
+  if (rc != AAR_OK) return rc;
+  return colsum_finish(ep.part, colsum, (int)(M / 64), N, st);
 }
 
 extern "C" int aar_gemm_f32_tile_config(int config, int* tile_m, int* tile_n, int* tile_k) {

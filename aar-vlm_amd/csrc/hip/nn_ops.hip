@@ -26,6 +26,7 @@
 
 #include <algorithm>
 
+#include "colsum.hpp"
 #include "common.hpp"
 #include "gemm_small.hpp"
 
@@ -686,6 +687,17 @@ causal_mask_kernel(const float* __restrict__ x, float* __restrict__ y, int64_t n
 }
 
 }  // namespace
+
+bool colsum_chunks_of_64(int64_t rows) {
+  return rows > 0 && rows % 64 == 0 && colsum_parts(rows) == rows / 64 && ceil_div(rows, colsum_parts(rows)) == 64;
+}
+
+int colsum_finish(const float* part, float* out, int nparts, int64_t cols, hipStream_t st) {
+  colsum_stage2_kernel<<<dim3((unsigned)ceil_div(cols, (int64_t)kCsCols)), dim3(kCsThreads), 0, st>>>(part, out, nparts,
+                                                                                                   cols);
+  return launch_status();
+}
+
 }  // namespace aar
 
 using namespace aar;

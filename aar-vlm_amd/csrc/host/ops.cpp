@@ -827,6 +827,9 @@ Tensor linear(const Tensor& x, const Tensor& w, const Tensor& b) {
 class MlpReluFunction : public Function {
  public:
   Tensor saved_x, saved_w1, saved_w2, saved_h;  // x and h as [rows, features]
+  // h > 0 as bits from the first GEMM's epilogue (aar_gemm_f32_bias_relu_bits),
+  // or null where that entry point did not take the product's plan
+  std::shared_ptr<Workspace> saved_bits;
   std::vector<int64_t> x_shape;
   std::vector<Tensor> backward(const Tensor& g) override {
     const int64_t N2 = saved_w2.shape[0], H = saved_w1.shape[0];
@@ -840,13 +843,26 @@ class MlpReluFunction : public Function {
                    "mlp backward");
     }
     Tensor dw2 = matmul_at_b_no_grad(gc, saved_h);
-    // dh = relu_backward(g W2): the plain GEMM, then the mask pass.  (The
-    // mask in the GEMM epilogue, aar_gemm_f32_relu_mask, measured slower in
-    // the GPT step's profile: 219.9 us against about 150 + 43.5 us.)
+    // dh = relu_backward(g W2) and db1 = its column sums.  With the mask bits,
+    // one GEMM does all three (aar_gemm_f32_mask_bits_colsum: the product, the
+    // mask and colsum's partials in its epilogue, bit for bit the separate
+    // passes).  Otherwise the plain GEMM, then the mask pass with db1's
+    // column sum in one pass over dh.  (The mask read as the relu's output in
+    // the epilogue, aar_gemm_f32_relu_mask, measured slower than the latter:
+    // 212 against 172 + 62 us at 16384 x 1536 x 384.)
     Tensor dh = Tensor::empty({rows, H}, DType::Fp32, Device::CUDA);
-    {
-      // the mask pass and db1's column sum in one pass over dh (bit for bit the
-      // relu backward followed by bias_grad)
+    bool fused = false;
+    if (saved_bits) {
+      Workspace ws(aar_gemm_f32_mask_bits_colsum_workspace_bytes(rows, H));
+      const int rc = aar_gemm_f32_mask_bits_colsum(AAR_GEMM_NN, rows, H, N2, fp(gc), fp(saved_w2),
+                                                   static_cast<const uint32_t*>(saved_bits->data()), fp(dh),
+                                                   fp(db1), ws.data(), ws.bytes(), current_stream());
+      if (rc != AAR_EUNSUPPORTED) {
+        check_status(rc, "mlp backward");
+        fused = true;
+      }
+    }
+    if (!fused) {
       Tensor dpost = matmul_no_grad(gc, saved_w2);
       Workspace ws(aar_colsum_workspace_bytes(rows, H));
       check_status(aar_relu_bwd_colsum_f32(fp(dpost), fp(saved_h), fp(dh), fp(db1), rows, H, ws.data(), ws.bytes(),
@@ -858,6 +874,31 @@ class MlpReluFunction : public Function {
   }
   const char* name() const override { return "MlpReluFunction"; }
 };
+
+// h = max(0, x W1^T + b1) (x2 [rows, d], h [rows, H]).  For a backward
+// (want_bits) also h > 0 as bits, returned for MlpReluFunction::saved_bits,
+// or null where aar_gemm_f32_bias_relu_bits does not take the product's plan
+// (h is then aar_gemm_f32_bias_relu's, the same values).
+std::shared_ptr<Workspace> mlp_hidden(const Tensor& x2, const Tensor& w1c, const Tensor& b1c, Tensor& h,
+                                      bool want_bits) {
+  const int64_t rows = h.shape[0], H = h.shape[1], d = x2.shape[1];
+  Workspace ws(aar_gemm_f32_workspace_bytes(AAR_GEMM_NT, rows, H, d));
+  if (want_bits) {
+    auto bits = std::make_shared<Workspace>(static_cast<size_t>(rows) * static_cast<size_t>((H + 31) / 32) *
+                                            sizeof(uint32_t));
+    const int rc = aar_gemm_f32_bias_relu_bits(AAR_GEMM_NT, rows, H, d, fp(x2), fp(w1c), fp(b1c), fp(h),
+                                               static_cast<uint32_t*>(bits->data()), ws.data(), ws.bytes(),
+                                               current_stream());
+    if (rc != AAR_EUNSUPPORTED) {
+      check_status(rc, "linear");
+      return bits;
+    }
+  }
+  check_status(aar_gemm_f32_bias_relu(AAR_GEMM_NT, rows, H, d, fp(x2), fp(w1c), fp(b1c), fp(h), ws.data(),
+                                      ws.bytes(), current_stream()),
+               "linear");
+  return nullptr;
+}
 
 Tensor mlp_relu(const Tensor& x, const Tensor& w1, const Tensor& b1, const Tensor& w2, const Tensor& b2) {
   if (w1.shape.size() != 2 || w2.shape.size() != 2 || x.shape.empty() || w1.shape[0] == 0 ||
@@ -878,24 +919,21 @@ Tensor mlp_relu(const Tensor& x, const Tensor& w1, const Tensor& b1, const Tenso
   const int64_t rows = static_cast<int64_t>(x.numel()) / d;
   Tensor x2 = as_view(xc, {rows, d});
   Tensor h = Tensor::empty({rows, H}, DType::Fp32, Device::CUDA);
-  if (h.numel() != 0) {
-    Workspace ws(aar_gemm_f32_workspace_bytes(AAR_GEMM_NT, rows, H, d));
-    check_status(aar_gemm_f32_bias_relu(AAR_GEMM_NT, rows, H, d, fp(x2), fp(w1c), fp(b1c), fp(h), ws.data(),
-                                        ws.bytes(), current_stream()),
-                 "linear");
-  }
+  const bool grad =
+      xc.requires_grad || w1c.requires_grad || b1c.requires_grad || w2c.requires_grad || b2c.requires_grad;
+  std::shared_ptr<Workspace> bits;
+  if (h.numel() != 0) bits = mlp_hidden(x2, w1c, b1c, h, grad);
   std::vector<int64_t> out_shape(x.shape.begin(), x.shape.end() - 1);
   out_shape.push_back(N2);
   Tensor out = as_view(linear_no_grad(h, w2c, b2c), out_shape);
-  if (!xc.requires_grad && !w1c.requires_grad && !b1c.requires_grad && !w2c.requires_grad && !b2c.requires_grad) {
-    return out;
-  }
+  if (!grad) return out;
   auto fn = std::make_shared<MlpReluFunction>();
   for (const Tensor* t : {&xc, &w1c, &b1c, &w2c, &b2c}) fn->record_input(*t);
   fn->saved_x = x2;
   fn->saved_w1 = w1c;
   fn->saved_w2 = w2c;
   fn->saved_h = h;
+  fn->saved_bits = bits;
   fn->x_shape = x.shape;
   out.requires_grad = true;
   out.grad_fn = fn;
@@ -992,18 +1030,16 @@ Tensor mlp_relu_residual(const Tensor& r, const Tensor& x, const Tensor& w1, con
   Tensor x2 = as_view(xc, {rows, d});
   Tensor h = Tensor::empty({rows, H}, DType::Fp32, Device::CUDA);
   Tensor out = Tensor::empty(out_shape, DType::Fp32, Device::CUDA);
+  const bool grad = rc.requires_grad || xc.requires_grad || w1c.requires_grad || b1c.requires_grad ||
+                    w2c.requires_grad || b2c.requires_grad;
+  std::shared_ptr<Workspace> bits;
   if (h.numel() != 0) {
-    Workspace ws(aar_gemm_f32_workspace_bytes(AAR_GEMM_NT, rows, H, d));
-    check_status(aar_gemm_f32_bias_relu(AAR_GEMM_NT, rows, H, d, fp(x2), fp(w1c), fp(b1c), fp(h), ws.data(),
-                                        ws.bytes(), current_stream()),
-                 "linear");
+    bits = mlp_hidden(x2, w1c, b1c, h, grad);
     Workspace ws2(aar_gemm_f32_workspace_bytes(AAR_GEMM_NT, rows, N2, H));
     check_status(aar_gemm_f32_bias_add(AAR_GEMM_NT, rows, N2, H, fp(h), fp(w2c), fp(b2c), fp(rc), fp(out),
                                        ws2.data(), ws2.bytes(), current_stream()),
                  "linear");
   }
-  const bool grad = rc.requires_grad || xc.requires_grad || w1c.requires_grad || b1c.requires_grad ||
-                    w2c.requires_grad || b2c.requires_grad;
   if (!grad) return out;
   auto fn = std::make_shared<MlpReluResidualFunction>();
   for (const Tensor* t : {&rc, &xc, &w1c, &b1c, &w2c, &b2c}) fn->record_input(*t);
@@ -1011,6 +1047,7 @@ Tensor mlp_relu_residual(const Tensor& r, const Tensor& x, const Tensor& w1, con
   fn->saved_w1 = w1c;
   fn->saved_w2 = w2c;
   fn->saved_h = h;
+  fn->saved_bits = bits;
   fn->x_shape = x.shape;
   out.requires_grad = true;
   out.grad_fn = fn;

@@ -141,6 +141,31 @@ int aar_gemm_f32_bias_add(int op, int64_t M, int64_t N, int64_t K, const float* 
 int aar_gemm_f32_relu_mask(int op, int64_t M, int64_t N, int64_t K, const float* A, const float* B,
                            const float* mask, float* C, void* workspace, size_t workspace_bytes,
                            void* stream);
+/* The MLP's relu carried as a bit mask from its forward product to its
+ * backward one, so the backward reads 1 bit per element instead of the relu's
+ * output.  aar_gemm_f32_bias_relu_bits: C as aar_gemm_f32_bias_relu (same
+ * plan, bit-identical) and bits[r * ldm + c / 32] bit (c % 32) = (C[r][c] > 0),
+ * ldm = (N + 31) / 32 words per row (uint32_t).  NT only.
+ * aar_gemm_f32_mask_bits_colsum: C = bit(r, c) ? A B : 0 (NN) and colsum[c] =
+ * sum over rows of C, bit-identical to aar_gemm_f32 (given the workspace
+ * aar_gemm_f32_workspace_bytes asks for), the relu backward and
+ * aar_colsum_f32; its workspace (aar_gemm_f32_mask_bits_colsum_workspace_bytes)
+ * holds colsum's per-64-row partials, which the GEMM epilogue writes.  Both
+ * return AAR_EUNSUPPORTED, launching nothing, where the product's plan splits
+ * K or has no such epilogue (register staging, K-group tiles, wave tiles of
+ * other than 64 rows for the mask) or, for the mask, where M is not a
+ * multiple of 64 up to 16384 (colsum's partials are not 64-row chunks
+ * there); the caller then runs the separate passes.  Replace
+ * matmul_a_bt_cuda + add_bias_cuda + relu_cuda and matmul_cuda +
+ * relu_backward_cuda + the bias gradient's column sum of the MLP
+ * (cppsrc/ops/matmul.cpp:10-11, elementwise.cpp:15-24). */
+int aar_gemm_f32_bias_relu_bits(int op, int64_t M, int64_t N, int64_t K, const float* A, const float* B,
+                                const float* bias, float* C, uint32_t* bits, void* workspace,
+                                size_t workspace_bytes, void* stream);
+size_t aar_gemm_f32_mask_bits_colsum_workspace_bytes(int64_t M, int64_t N);
+int aar_gemm_f32_mask_bits_colsum(int op, int64_t M, int64_t N, int64_t K, const float* A, const float* B,
+                                  const uint32_t* bits, float* C, float* colsum, void* workspace,
+                                  size_t workspace_bytes, void* stream);
 
 /* Batched GEMM with explicit leading dimensions: for b in [0, batch),
  * C_b = op(A_b, B_b) with A_b = A + b*strideA (and so on), op as in

@@ -69,6 +69,25 @@ def test_abi_validates_before_touching_the_device():
     assert lib.aar_gemm_f32_relu_mask(0, 2, 2, 2, None, None, None, None, None, 0, None) == -1  # no mask
     assert lib.aar_gemm_f32_relu_mask(1, 2, 2, 2, None, None, x, None, None, 0, None) == -3  # NT
     assert lib.aar_gemm_f32_relu_mask(3, 2, 2, 2, None, None, x, None, None, 0, None) == -1  # bad op
+    # the mask as bits: bias + relu + bits on NT only; the masked NN product with column sums needs
+    # bits, column sums and a row count of 64-row colsum chunks
+    lib.aar_gemm_f32_bias_relu_bits.argtypes = [ctypes.c_int, i64, i64, i64, vp, vp, vp, vp, vp, vp,
+                                                ctypes.c_size_t, vp]
+    lib.aar_gemm_f32_mask_bits_colsum.argtypes = lib.aar_gemm_f32_bias_relu_bits.argtypes
+    lib.aar_gemm_f32_mask_bits_colsum_workspace_bytes.restype = ctypes.c_size_t
+    lib.aar_gemm_f32_mask_bits_colsum_workspace_bytes.argtypes = [i64, i64]
+    assert lib.aar_gemm_f32_bias_relu_bits(1, 2, 2, 2, None, None, x, None, None, None, 0, None) == -1  # no bits
+    assert lib.aar_gemm_f32_bias_relu_bits(1, 2, 2, 2, None, None, None, None, x, None, 0, None) == -1  # no bias
+    assert lib.aar_gemm_f32_bias_relu_bits(0, 2, 2, 2, None, None, x, None, x, None, 0, None) == -3  # NN
+    assert lib.aar_gemm_f32_bias_relu_bits(1, 0, 2, 2, None, None, None, None, None, None, 0, None) == 0
+    assert lib.aar_gemm_f32_mask_bits_colsum(0, 64, 2, 2, None, None, x, None, None, None, 0, None) == -1
+    assert lib.aar_gemm_f32_mask_bits_colsum(0, 64, 2, 2, None, None, None, None, x, None, 0, None) == -1
+    assert lib.aar_gemm_f32_mask_bits_colsum(1, 64, 2, 2, None, None, x, None, x, None, 0, None) == -3  # NT
+    assert lib.aar_gemm_f32_mask_bits_colsum(0, 100, 2, 2, None, None, x, None, x, None, 0, None) == -3
+    assert lib.aar_gemm_f32_mask_bits_colsum(0, 64, 2, 0, None, None, x, None, x, None, 0, None) == -3  # K = 0
+    assert lib.aar_gemm_f32_mask_bits_colsum(0, 64, 0, 2, None, None, None, None, None, None, 0, None) == 0
+    assert lib.aar_gemm_f32_mask_bits_colsum_workspace_bytes(16384, 1536) == 256 * 1536 * 4
+    assert lib.aar_gemm_f32_mask_bits_colsum_workspace_bytes(0, 1536) == 0
     assert lib.aar_gemm_f32_bias(1, 2, 2, 0, None, None, 16, None, None, 0, None) == -3  # K = 0: not a product
     lib.aar_softmax_fwd_f32.argtypes = [vp, vp, i64, i64, vp]
     assert lib.aar_softmax_fwd_f32(None, None, 4, 0, None) == -1

@@ -1,6 +1,8 @@
 """The fused feed-forward block _mlp_relu(x, W1, b1, W2, b2): bias + relu in
 the first GEMM's epilogue; the backward takes the relu mask from the saved
-output h.  Against the composition
+output h, or, where the GEMM plans allow (the 16384-row GPT case), from bits
+the first GEMM's epilogue wrote, applying it and db1's column-sum partials in
+the dh GEMM's epilogue.  Against the composition
 linear(relu(linear(x, W1, b1)), W2, b2) of the same backend (aargrad/nn.py:101-122,
 the GPT block's MLP) the values and all five gradients must be bit-identical:
 each epilogue performs the same fp32 operation as the separate op.  Cases
@@ -27,6 +29,7 @@ f32 = np.float32
 # (leading dims of x, d, hidden, out)
 CASES = [
     ((4, 64), 384, 1536, 384),   # GPT block shape (256 rows), unsplit
+    ((64, 256), 384, 1536, 384),  # GPT block at config 5 (16384 rows): the mask-bits epilogues
     ((3, 50), 17, 33, 65),       # unaligned everywhere: register path, scalar epilogue
     ((64,), 4096, 96, 64),       # forward bias+relu under split-K, vector reduce
     ((33,), 4999, 30, 7),        # forward split-K, scalar reduce
