@@ -76,12 +76,14 @@ __device__ __forceinline__ void map_tile(int tiles_m, int tiles_n, int& tm, int&
 // backward one (store_tile_bits), so the backward reads 1 bit per element
 // where kEpiMask reads the relu's whole output:
 //   kEpiBiasReluBits  C = max(0, acc + bias[col]) as kEpiBiasRelu, and bit
-//                     col % 32 of word bits[row * ldm + col / 32] set where
-//                     C > 0 (ldm = ceil(N / 32) words per row)
+//                     row % 32 of word bits[(row / 32) * N + col] set where
+//                     C > 0: a word holds one column of a 32-row block, the
+//                     rows of one accumulator block
 //   kEpiMaskBits      C = bit(row, col) ? acc : 0 (the relu backward), and
 //                     part[row / 64][col] = the sum of C over the 64 rows of
-//                     that chunk, in row order from 0.f: the stage-1
-//                     partials of aar_colsum_f32 (a wave owns one chunk)
+//                     that chunk, in aar_colsum_f32's stage-1 order (two
+//                     running sums, see colsum_stage1_kernel): its partials
+//                     (a wave owns one chunk)
 enum : int {
   kEpiNone = 0,
   kEpiBias = 1,
@@ -95,8 +97,7 @@ enum : int {
 struct GemmEpi {
   const float* bias;
   const float* aux;
-  uint32_t* bits = nullptr;  // kEpiBiasReluBits writes, kEpiMaskBits reads
-  int64_t ldm = 0;           // words per row of bits
+  uint32_t* bits = nullptr;  // [ceil(M / 32)][N]: kEpiBiasReluBits writes, kEpiMaskBits reads
   float* part = nullptr;     // kEpiMaskBits: [M / 64][N] column partials
 };
 constexpr bool epi_bits(int epi) { return epi == kEpiBiasReluBits || epi == kEpiMaskBits; }
@@ -128,37 +129,46 @@ __device__ __forceinline__ void load_bias(const GemmEpi& ep, int64_t N, int64_t 
 }
 
 // Mask words the kEpiMaskBits epilogue needs, read before the main loop like
-// the bias: for block (i, j) lane k (k < 32) holds the word of register
-// k % 16 of lane half k / 16, i.e. row r0 + 32 i + 8 (k%16 / 4) + 4 (k / 16)
-// + k % 4, columns c0 + 32 j .. + 31 (lanes 32..63 hold the same words).
+// the bias: lane (lr, h) holds, for block (i, j), the word of column
+// c0 + 32 j + lr over rows r0 + 32 i .. + 31 (both halves read the same word,
+// 128 contiguous bytes per half-wave).
 template <int TM, int TN, int EPI>
-__device__ __forceinline__ void load_bits(const GemmEpi& ep, int64_t M, int64_t N, int64_t r0, int64_t c0, int lane,
+__device__ __forceinline__ void load_bits(const GemmEpi& ep, int64_t M, int64_t N, int64_t r0, int64_t c0, int lr,
                                           uint32_t (&words)[TM][TN]) {
-  const int k = lane & 31, rr = k & 15;
-  const int64_t row0 = r0 + 8 * (rr >> 2) + 4 * (k >> 4) + (rr & 3);
 #pragma unroll
   for (int i = 0; i < TM; ++i)
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
       words[i][j] = 0u;
       if constexpr (EPI == kEpiMaskBits) {
-        const int64_t row = row0 + 32 * i;
-        if (row < M && c0 + 32 * j < N) words[i][j] = ep.bits[row * ep.ldm + ((c0 + 32 * j) >> 5)];
+        const int64_t col = c0 + 32 * j + lr;
+        if (r0 + 32 * i < M && col < N) words[i][j] = ep.bits[((r0 + 32 * i) >> 5) * N + col];
       }
     }
 }
 
-// The two mask-bit epilogues (see kEpiBiasReluBits / kEpiMaskBits).  Column
-// blocks start at multiples of 32 (c0 and the tile widths are), so the 32
-// columns of a block are one mask word.
-//   kEpiBiasReluBits: for register r, __ballot(C > 0) gives the words of the
-//   block's rows 8(r/4) + r%4 (lanes 0-31) and that + 4 (lanes 32-63); lane k
-//   collects the word of register k % 16, half k / 16 and stores it.
-//   kEpiMaskBits (WM = 64: the wave's rows are one 64-row chunk): lane
-//   (lr, h) takes its bit from the word of its row, read out of the lane that
-//   loaded it (v_readlane), and the lanes of half 0 sum column c0 + 32 j + lr
-//   over the chunk's rows in order, the half-1 rows handed over by
-//   v_permlane32_swap.
+// The two mask-bit epilogues (see kEpiBiasReluBits / kEpiMaskBits).  Wave
+// tiles start at multiples of 32 rows, so accumulator block (i, j) covers
+// whole mask words: lane (lr, h) holds the bits 8 (r / 4) + 4 h + r % 4 of the
+// word of its column c0 + 32 j + lr, its half's 16 rows.
+//   kEpiBiasReluBits: each lane sets its 16 bits, the two halves OR their
+//   words (v_permlane32_swap) and half 0 stores the word.
+//   kEpiMaskBits (WM = 64: the wave's rows are one 64-row chunk): each lane
+//   tests its 16 bits of the prefetched word and sums its 32 rows of the
+//   chunk in order, the row set (row & 4 == 4h) of one of colsum's two
+//   running sums; half 0 adds its partner's (v_permlane32_swap) and stores
+//   the chunk partial s0 + s1.
+// The swap hands each lane its own value and its partner's, one in each
+// result; where the two are equal either is the partner's.
+__device__ __forceinline__ uint32_t partner_u32(uint32_t u) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  const auto sw = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return sw[0] == u ? sw[1] : sw[0];
+#else
+  return u;
+#endif
+}
+
 template <int TM, int TN, int EPI>
 __device__ __forceinline__ void store_tile_bits(const f32x16 (&acc)[TM][TN], float* __restrict__ C,
                                                 const GemmEpi& ep, const float (&bias)[TN],
@@ -166,69 +176,60 @@ __device__ __forceinline__ void store_tile_bits(const f32x16 (&acc)[TM][TN], flo
                                                 int64_t r0, int64_t c0, int lr, int h) {
   static_assert(epi_bits(EPI), "mask-bit epilogues only");
   static_assert(EPI != kEpiMaskBits || TM == 2, "a kEpiMaskBits wave owns one 64-row chunk");
-  const int lane = lr + 32 * h;
+  // addressing as store_tile: a lane base and row offsets dr * ldc that the
+  // compiler forms in scalar registers, bounds tests only off the interior
+  const bool interior = r0 + 32 * TM <= M && c0 + 32 * TN <= N;
+  float* const Cl = C + (r0 + 4 * h) * ldc + c0 + lr;
   wait_vm_lgkm0<0>();  // bias / mask words (see store_tile)
 #pragma unroll
   for (int j = 0; j < TN; ++j) {
     const int64_t col = c0 + 32 * j + lr;
-    const bool col_ok = col < N;
     float vals[TM][16];
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
-      uint32_t w = 0u;
+      uint32_t w = 0u;                           // this half's bits, at 8 (r / 4) + r % 4
+      const uint32_t mine = words[i][j] >> (4 * h);  // kEpiMaskBits: the same positions
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int64_t row = r0 + 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
-        const bool ok = col_ok && row < M;
+        const int dr = 32 * i + 8 * (r >> 2) + (r & 3);  // row - r0 - 4h
+        const int bit = 8 * (r >> 2) + (r & 3);
+        const bool ok = interior || (r0 + 4 * h + dr < M && col < N);
         float v;
+        // (the bit tests stay free of the bounds test: with it, the compiler
+        // kept every element's lane mask live and spilled them to VGPR lanes)
         if constexpr (EPI == kEpiBiasReluBits) {
           v = fmaxf(0.0f, acc[i][j][r] + bias[j]);
-          const uint64_t bal = __ballot(ok && v > 0.0f);
-          w = lane == r ? (uint32_t)bal : w;
-          w = lane == 16 + r ? (uint32_t)(bal >> 32) : w;
+          w |= v > 0.0f ? (1u << bit) : 0u;
         } else {
-          const uint32_t lo = __builtin_amdgcn_readlane(words[i][j], r);
-          const uint32_t hi = __builtin_amdgcn_readlane(words[i][j], 16 + r);
-          v = (((h ? hi : lo) >> lr) & 1u) ? acc[i][j][r] : 0.0f;
+          // all ones where the bit is set: acc, else +0.0f
+#if defined(__HIP_DEVICE_COMPILE__)
+          const uint32_t keep = (uint32_t)__builtin_amdgcn_sbfe((int)mine, bit, 1);
+#else
+          const uint32_t keep = ((mine >> bit) & 1u) ? ~0u : 0u;
+#endif
+          v = __uint_as_float(__float_as_uint(acc[i][j][r]) & keep);
           vals[i][r] = v;
         }
-        if (ok) C[row * ldc + col] = v;
+        if (ok) Cl[(int64_t)dr * ldc + 32 * j] = v;
       }
       if constexpr (EPI == kEpiBiasReluBits) {
-        if (lane < 32) {
-          const int rr = lane & 15;
-          const int64_t row = r0 + 32 * i + 8 * (rr >> 2) + 4 * (lane >> 4) + (rr & 3);
-          if (row < M && c0 + 32 * j < N) ep.bits[row * ep.ldm + ((c0 + 32 * j) >> 5)] = w;
-        }
+        w <<= 4 * h;
+        w |= partner_u32(w);
+        const int64_t rows = M - (r0 + 32 * i);  // rows of this word inside C
+        if (rows < 32) w &= (1u << (rows > 0 ? rows : 0)) - 1u;
+        if (h == 0 && rows > 0 && col < N) ep.bits[((r0 + 32 * i) >> 5) * N + col] = w;
       }
     }
     if constexpr (EPI == kEpiMaskBits) {
-      // rows 32 i + 8 g + {0..3} are half 0's registers 4g..4g+3, rows
-      // 32 i + 8 g + {4..7} half 1's
+      // colsum's chunk partial: half h's running sum over its rows (row & 4
+      // == 4h) in row order, i.e. its registers in order, then s0 + s1
       float s = 0.f;
 #pragma unroll
       for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          float other[4];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-#if defined(__HIP_DEVICE_COMPILE__)
-            // the swap hands each lane its own value and its partner's, one
-            // in each result; where the two are equal either is the partner's
-            const uint32_t u = __float_as_uint(vals[i][4 * g + e]);
-            const auto sw = __builtin_amdgcn_permlane32_swap(u, u, false, false);
-            other[e] = __uint_as_float(sw[0] == u ? sw[1] : sw[0]);
-#else
-            other[e] = vals[i][4 * g + e];
-#endif
-          }
-#pragma unroll
-          for (int e = 0; e < 4; ++e) s += vals[i][4 * g + e];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) s += other[e];
-        }
-      if (h == 0 && col_ok && r0 < M) ep.part[(r0 >> 6) * N + col] = s;
+        for (int r = 0; r < 16; ++r) s += vals[i][r];
+      s += __uint_as_float(partner_u32(__float_as_uint(s)));
+      if (h == 0 && col < N && r0 < M) ep.part[(r0 >> 6) * N + col] = s;
     }
   }
 }
@@ -661,7 +662,7 @@ gemm_f32_dma_kernel(const float* __restrict__ A, const float* __restrict__ B, fl
   float bias[TN];
   load_bias<TN, EPI>(ep, N, n0 + wn0, lr, bias);
   uint32_t words[TM][TN];
-  load_bits<TM, TN, EPI>(ep, M, N, m0 + wm0, n0 + wn0, lane, words);
+  load_bits<TM, TN, EPI>(ep, M, N, m0 + wm0, n0 + wn0, lr, words);
   auto issue = [&](int t) {
     const int64_t k0 = kbeg + (int64_t)t * BK;
     float* st = ring + (t % S) * kStage;
@@ -1579,7 +1580,6 @@ extern "C" int aar_gemm_f32_bias_relu_bits(int op, int64_t M, int64_t N, int64_t
   if (p.splits > 1) return AAR_EUNSUPPORTED;
   GemmEpi ep{bias, nullptr};
   ep.bits = bits;
-  ep.ldm = ceil_div(N, (int64_t)32);
   return run_gemm(op, M, N, K, A, B, C, nullptr, p, as_stream(stream), kEpiBiasReluBits, ep);
 }
 
@@ -1612,7 +1612,6 @@ extern "C" int aar_gemm_f32_mask_bits_colsum(int op, int64_t M, int64_t N, int64
   if (p.splits > 1 || p.cfg >= kNumCfgs) return AAR_EUNSUPPORTED;
   GemmEpi ep{nullptr, nullptr};
   ep.bits = const_cast<uint32_t*>(bits);
-  ep.ldm = ceil_div(N, (int64_t)32);
   ep.part = static_cast<float*>(workspace);
   hipStream_t st = as_stream(stream);
   const int rc = run_gemm(op, M, N, K, A, B, C, nullptr, p, st, kEpiMaskBits, ep);

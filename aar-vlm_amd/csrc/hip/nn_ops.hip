@@ -152,7 +152,12 @@ add_bias_vec_kernel(const f32x4* __restrict__ x, const f32x4* __restrict__ bias,
 }
 
 // Column sums, stage 1: part[p][c] = sum of g[r][c] for rows r in chunk p
-// (rows p*chunk .. p*chunk+chunk-1, in order).
+// (rows r0 = p*chunk .. r0+chunk-1) as two running sums from 0.f, in row
+// order: s0 over the rows with (r - r0) & 4 == 0, s1 over the others, then
+// s0 + s1.  The two sets are the row sets of the two lane halves of a 32x32
+// MFMA accumulator block, so a GEMM epilogue holding 64-row chunks
+// (kEpiMaskBits, gemm_f32.hip) forms the same partials with one exchange
+// between the halves.
 __global__ void __launch_bounds__(256)
 colsum_stage1_kernel(const float* __restrict__ g, float* __restrict__ part, int64_t rows, int64_t cols,
                      int64_t chunk) {
@@ -160,10 +165,17 @@ colsum_stage1_kernel(const float* __restrict__ g, float* __restrict__ part, int6
   if (c >= cols) return;
   const int64_t r0 = (int64_t)blockIdx.y * chunk;
   const int64_t r1 = min(rows, r0 + chunk);
-  float s = 0.f;
+  float s0 = 0.f, s1 = 0.f;
 #pragma unroll 8
-  for (int64_t r = r0; r < r1; ++r) s += g[r * cols + c];
-  part[(int64_t)blockIdx.y * cols + c] = s;
+  for (int64_t r = r0; r < r1; ++r) {
+    const float v = g[r * cols + c];
+    if ((r - r0) & 4) {
+      s1 += v;
+    } else {
+      s0 += v;
+    }
+  }
+  part[(int64_t)blockIdx.y * cols + c] = s0 + s1;
 }
 
 // Stage 1 fused with the relu backward that produces g: dx = x > 0 ? g : 0
@@ -178,7 +190,7 @@ relu_bwd_colsum_stage1_kernel(const f32x4* __restrict__ g, const f32x4* __restri
   if (c4 >= cols4) return;
   const int64_t r0 = (int64_t)blockIdx.y * chunk;
   const int64_t r1 = min(rows, r0 + chunk);
-  f32x4 s = {0.f, 0.f, 0.f, 0.f};
+  f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll 8
   for (int64_t r = r0; r < r1; ++r) {
     const f32x4 gv = __builtin_nontemporal_load(g + r * cols4 + c4);
@@ -187,10 +199,13 @@ relu_bwd_colsum_stage1_kernel(const f32x4* __restrict__ g, const f32x4* __restri
 #pragma unroll
     for (int e = 0; e < 4; ++e) v[e] = xv[e] > 0.0f ? gv[e] : 0.0f;
     __builtin_nontemporal_store(v, dx + r * cols4 + c4);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) s[e] += v[e];
+    if ((r - r0) & 4) {
+      s1 += v;
+    } else {
+      s0 += v;
+    }
   }
-  *reinterpret_cast<f32x4*>(part + (int64_t)blockIdx.y * cols4 * 4 + c4 * 4) = s;
+  *reinterpret_cast<f32x4*>(part + (int64_t)blockIdx.y * cols4 * 4 + c4 * 4) = s0 + s1;
 }
 
 // Stage 2: out[c] = sum over p of part[p][c].  A workgroup owns kCsCols

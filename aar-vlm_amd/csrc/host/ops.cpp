@@ -884,7 +884,7 @@ std::shared_ptr<Workspace> mlp_hidden(const Tensor& x2, const Tensor& w1c, const
   const int64_t rows = h.shape[0], H = h.shape[1], d = x2.shape[1];
   Workspace ws(aar_gemm_f32_workspace_bytes(AAR_GEMM_NT, rows, H, d));
   if (want_bits) {
-    auto bits = std::make_shared<Workspace>(static_cast<size_t>(rows) * static_cast<size_t>((H + 31) / 32) *
+    auto bits = std::make_shared<Workspace>(static_cast<size_t>((rows + 31) / 32) * static_cast<size_t>(H) *
                                             sizeof(uint32_t));
     const int rc = aar_gemm_f32_bias_relu_bits(AAR_GEMM_NT, rows, H, d, fp(x2), fp(w1c), fp(b1c), fp(h),
                                                static_cast<uint32_t*>(bits->data()), ws.data(), ws.bytes(),

@@ -144,8 +144,9 @@ int aar_gemm_f32_relu_mask(int op, int64_t M, int64_t N, int64_t K, const float*
 /* The MLP's relu carried as a bit mask from its forward product to its
  * backward one, so the backward reads 1 bit per element instead of the relu's
  * output.  aar_gemm_f32_bias_relu_bits: C as aar_gemm_f32_bias_relu (same
- * plan, bit-identical) and bits[r * ldm + c / 32] bit (c % 32) = (C[r][c] > 0),
- * ldm = (N + 31) / 32 words per row (uint32_t).  NT only.
+ * plan, bit-identical) and bits[(r / 32) * N + c] bit (r % 32) = (C[r][c] > 0):
+ * one uint32_t word per column of each 32-row block, (M + 31) / 32 * N words,
+ * bits past row M zero.  NT only.
  * aar_gemm_f32_mask_bits_colsum: C = bit(r, c) ? A B : 0 (NN) and colsum[c] =
  * sum over rows of C, bit-identical to aar_gemm_f32 (given the workspace
  * aar_gemm_f32_workspace_bytes asks for), the relu backward and

@@ -1,8 +1,8 @@
 """The MLP's relu carried as a bit mask between its GEMMs, through the C ABI:
 
 * aar_gemm_f32_bias_relu_bits (NT): C bit-identical to aar_gemm_f32_bias_relu
-  and the bits equal to C > 0 packed 32 columns a word (bit c % 32 of word
-  c / 32, zero past N);
+  and the bits equal to C > 0 packed 32 rows a word (bit r % 32 of word
+  (r / 32) * N + c, zero past M);
 * aar_gemm_f32_mask_bits_colsum (NN): C bit-identical to aar_gemm_f32 then
   aar_relu_bwd_f32 against the forward's C, and colsum bit-identical to
   aar_colsum_f32 of that C (its 64-row chunk partials come from the GEMM
@@ -42,12 +42,13 @@ def _bind(L):
 
 
 def _pack(c):
-    """bits[r][w] bit b = c[r][32 w + b] > 0 (zero past the last column)."""
+    """bits[rb][col] bit b = c[32 rb + b][col] > 0 (zero past the last row)."""
     M, N = c.shape
-    ldm = (N + 31) // 32
-    pos = np.zeros((M, ldm * 32), bool)
-    pos[:, :N] = c > 0
-    return np.packbits(pos, axis=1, bitorder="little").view("<u4").reshape(M, ldm)
+    nb = (M + 31) // 32
+    pos = np.zeros((nb * 32, N), bool)
+    pos[:M] = c > 0
+    pos = np.ascontiguousarray(pos.reshape(nb, 32, N).transpose(0, 2, 1))
+    return np.packbits(pos, axis=2, bitorder="little").view("<u4").reshape(nb, N)
 
 
 def _words(abi, p, shape):
@@ -55,8 +56,8 @@ def _words(abi, p, shape):
     return raw.view(np.uint32)
 
 
-def _sentinel_words(abi, M, ldm):
-    arr = np.full((M, ldm), SENTINEL, np.uint32).view(f32)
+def _sentinel_words(abi, rows, cols):
+    arr = np.full((rows, cols), SENTINEL, np.uint32).view(f32)
     return abi.put(arr)
 
 
@@ -66,7 +67,8 @@ SHAPES = [
     (16384, 1536, 384, 384),  # GPT block (must be fused)
     (4096, 1536, 384, 384),
     (2048, 960, 384, 128),
-    (1024, 200, 64, 96),      # N not a multiple of 32: a partial last word
+    (1000, 200, 64, 96),      # M not a multiple of 32: a partial last word (forward only)
+    (1024, 200, 64, 96),      # N not a multiple of the tile width
     (512, 96, 64, 33),
     (128, 1536, 384, 384),
 ]
@@ -80,7 +82,7 @@ def test_bits_forward_and_masked_backward(gpu, M, H, d, N2):
     b1 = (0.1 * rng.standard_normal(H)).astype(f32)
     g = rng.standard_normal((M, N2)).astype(f32)
     w2 = (rng.standard_normal((N2, H)) / np.sqrt(N2)).astype(f32)
-    ldm = (H + 31) // 32
+    nb = (M + 31) // 32
     abi = Abi()
     L = abi.L
     _bind(L)
@@ -90,7 +92,7 @@ def test_bits_forward_and_masked_backward(gpu, M, H, d, N2):
         wf = abi.alloc(wsf) if wsf else None
         # forward: the plain bias + relu product, then the bits entry point
         ph_ref, ph = abi.empty(M * H), abi.put(np.full((M, H), 7.0, f32))
-        pbits = _sentinel_words(abi, M, ldm)
+        pbits = _sentinel_words(abi, nb, H)
         abi.check(L.aar_gemm_f32_bias_relu(NT, M, H, d, px, pw1, pb1, ph_ref, wf, wsf, None))
         rc = L.aar_gemm_f32_bias_relu_bits(NT, M, H, d, px, pw1, pb1, ph, pbits, wf, wsf, None)
         assert rc in (0, -3), rc
@@ -99,12 +101,12 @@ def test_bits_forward_and_masked_backward(gpu, M, H, d, N2):
         if rc == -3:
             assert M != 16384, "the GPT block shape must take the bits epilogue"
             assert (abi.get(ph, (M, H)) == 7.0).all()
-            assert (_words(abi, pbits, (M, ldm)) == SENTINEL).all()
+            assert (_words(abi, pbits, (nb, H)) == SENTINEL).all()
             bits = _pack(h_ref)
             pbits = abi.put(bits.view(f32))
         else:
             np.testing.assert_array_equal(abi.get(ph, (M, H)), h_ref)
-            bits = _words(abi, pbits, (M, ldm))
+            bits = _words(abi, pbits, (nb, H))
             np.testing.assert_array_equal(bits, _pack(h_ref))
 
         # backward: the plain product, relu backward against h, colsum
@@ -145,7 +147,7 @@ def test_mask_bits_refusals(gpu):
     try:
         H, N2 = 192, 64
         pg, pw2 = abi.put(np.ones((16448, N2), f32)), abi.put(np.ones((N2, H), f32))
-        pbits = abi.put(np.zeros((16448, H // 32), f32))
+        pbits = abi.put(np.zeros((16448 // 32, H), f32))
         pdh, pcs = abi.empty(16448 * H), abi.put(np.full(H, 7.0, f32))
         ws = abi.alloc(L.aar_gemm_f32_mask_bits_colsum_workspace_bytes(16448, H))
         wsb = L.aar_gemm_f32_mask_bits_colsum_workspace_bytes(16448, H)
