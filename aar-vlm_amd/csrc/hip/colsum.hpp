@@ -17,4 +17,33 @@ bool colsum_chunks_of_64(int64_t rows);
 // fixed order.
 int colsum_finish(const float* part, float* out, int nparts, int64_t cols, hipStream_t st);
 
+// That order, for a workgroup of kColsumSlices * COLS threads owning columns
+// c0 .. c0 + COLS - 1: slice j sums its contiguous run of the parts in order,
+// then a fixed pairwise tree over the slices in LDS finishes each column.
+// The result does not depend on COLS, so launches of any width agree bit for
+// bit.
+constexpr int kColsumSlices = 64;
+template <int COLS>
+__device__ __forceinline__ void colsum_stage2_block(const float* __restrict__ part, float* __restrict__ out,
+                                                    int nparts, int64_t cols, int64_t c0,
+                                                    float (&acc)[kColsumSlices][COLS]) {
+  const int cl = threadIdx.x % COLS, slice = threadIdx.x / COLS;
+  const int64_t c = c0 + cl;
+  const int per = (nparts + kColsumSlices - 1) / kColsumSlices;
+  const int p0 = slice * per;
+  const int p1 = nparts < p0 + per ? nparts : p0 + per;
+  float s = 0.f;
+  if (c < cols) {
+    for (int p = p0; p < p1; ++p) s += part[(int64_t)p * cols + c];
+  }
+  acc[slice][cl] = s;
+  __syncthreads();
+#pragma unroll
+  for (int h = kColsumSlices / 2; h >= 1; h /= 2) {
+    if (slice < h) acc[slice][cl] += acc[slice + h][cl];
+    __syncthreads();
+  }
+  if (slice == 0 && c < cols) out[c] = acc[0][cl];
+}
+
 }  // namespace aar

@@ -173,7 +173,7 @@ inline int launch_status() {
   return e == hipSuccess ? AAR_OK : static_cast<int>(e);
 }
 
-inline bool aligned16(const void* p) {
+__host__ __device__ inline bool aligned16(const void* p) {
   return (reinterpret_cast<uintptr_t>(p) & 15u) == 0;
 }
 

@@ -92,15 +92,24 @@ enum : int {
   kEpiAdd = 4,
   kEpiBiasAdd = 5,
   kEpiBiasReluBits = 6,
-  kEpiMaskBits = 7
+  kEpiMaskBits = 7,
+  kEpiColsumA = 8
 };
+// kEpiColsumA is not an epilogue but work in the main loop (TN only): C is
+// stored plainly, and the waves of the first column of waves also sum the
+// staged A tile's columns: part[k / 64][m] = the sum of A[k][m] over the
+// 64-row chunk of k, in aar_colsum_f32's stage-1 order.  A lane holds the
+// k's with k & 4 == 4h of its column in order, i.e. one of that order's two
+// running sums; the halves add them at the chunk's end.  Chunk q is summed by
+// the workgroups with tn == q % tiles_n, so the work spreads over the grid.
 struct GemmEpi {
   const float* bias;
   const float* aux;
   uint32_t* bits = nullptr;  // [ceil(M / 32)][N]: kEpiBiasReluBits writes, kEpiMaskBits reads
-  float* part = nullptr;     // kEpiMaskBits: [M / 64][N] column partials
+  float* part = nullptr;     // kEpiMaskBits: [M / 64][N] column partials; kEpiColsumA: [K / 64][M]
 };
 constexpr bool epi_bits(int epi) { return epi == kEpiBiasReluBits || epi == kEpiMaskBits; }
+constexpr bool epi_dma_only(int epi) { return epi_bits(epi) || epi == kEpiColsumA; }
 
 // Epilogue: a wave's (32*TM) x (32*TN) accumulators to C.  Accumulator
 // layout of a 32x32 block: lane (lr, h), register r holds row
@@ -229,7 +238,7 @@ __device__ __forceinline__ void store_tile_bits(const f32x16 (&acc)[TM][TN], flo
 #pragma unroll
         for (int r = 0; r < 16; ++r) s += vals[i][r];
       s += __uint_as_float(partner_u32(__float_as_uint(s)));
-      if (h == 0 && col < N && r0 < M) ep.part[(r0 >> 6) * N + col] = s;
+      if (ep.part && h == 0 && col < N && r0 < M) ep.part[(r0 >> 6) * N + col] = s;
     }
   }
 }
@@ -663,6 +672,7 @@ gemm_f32_dma_kernel(const float* __restrict__ A, const float* __restrict__ B, fl
   load_bias<TN, EPI>(ep, N, n0 + wn0, lr, bias);
   uint32_t words[TM][TN];
   load_bits<TM, TN, EPI>(ep, M, N, m0 + wm0, n0 + wn0, lr, words);
+  float csum[TM] = {};  // kEpiColsumA: this lane's running sum of A column wm0 + 32 i + lr
   auto issue = [&](int t) {
     const int64_t k0 = kbeg + (int64_t)t * BK;
     float* st = ring + (t % S) * kStage;
@@ -693,6 +703,10 @@ gemm_f32_dma_kernel(const float* __restrict__ A, const float* __restrict__ B, fl
 
     const float* as = ring + (t % S) * kStage;
     const float* bs = as + TA::kFloats;
+    // kEpiColsumA: whether this wave sums the A columns of this K tile (a
+    // wave-uniform branch)
+    const int64_t k0 = kbeg + (int64_t)t * BK;
+    const bool cs_on = EPI == kEpiColsumA && wave < NWM && (k0 >> 6) % tiles_n == tn;
     // With K groups four waves share a SIMD; the one issuing matrix ops
     // keeps priority over those issuing loads (measured +2.5 % at 1024^3;
     // the one-group kernels lose slightly with it).
@@ -718,8 +732,27 @@ gemm_f32_dma_kernel(const float* __restrict__ A, const float* __restrict__ B, fl
 #pragma unroll
           for (int j = 0; j < TN; ++j)
             acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[p][i][s], bf[p][j][s], acc[i][j], 0, 0, 0);
+      if constexpr (EPI == kEpiColsumA) {
+        if (cs_on) {
+#pragma unroll
+          for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) csum[i] += af[p][i][e];
+        }
+      }
     }
     if constexpr (KG > 1) __builtin_amdgcn_s_setprio(0);
+    if constexpr (EPI == kEpiColsumA) {
+      if (cs_on && ((k0 + BK) & 63) == 0) {  // the chunk's last K tile
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+          const float tot = csum[i] + __uint_as_float(partner_u32(__float_as_uint(csum[i])));
+          const int64_t m = m0 + wm0 + 32 * i + lr;
+          if (h == 0 && m < M) ep.part[(k0 >> 6) * M + m] = tot;
+          csum[i] = 0.f;
+        }
+      }
+    }
   }
 
   if constexpr (KG > 1) {
@@ -981,6 +1014,29 @@ gemm_f32_thin_kernel(const float* __restrict__ A, const float* __restrict__ B, f
 // C[i] = sum_s W[s*stride + i], s in order 0..splits-1 (deterministic), four
 // consecutive outputs per thread with 128-bit loads (stride % 4 == 0 and
 // 16-byte aligned W/C); the split loop is unrolled so its loads overlap.
+// The split-K sum of splitk_reduce_vec_kernel (no epilogue) in workgroups
+// 0 .. nb_reduce - 1 and aar_colsum_f32's stage 2 of the A column sums
+// (kEpiColsumA) in the rest, 4 columns each: one launch for both reductions
+// of aar_gemm_f32_colsum_a.
+constexpr int kCsaCols = 4;
+__global__ void __launch_bounds__(kColsumSlices * kCsaCols)
+splitk_reduce_colsum_kernel(const f32x4* __restrict__ W, f32x4* __restrict__ C, int64_t n4, int64_t stride4,
+                            int splits, int nb_reduce, const float* __restrict__ part, float* __restrict__ colsum,
+                            int nparts, int64_t cols) {
+  static_assert(kColsumSlices * kCsaCols == 256, "the reduce workgroups take 256 float4s");
+  __shared__ float acc[kColsumSlices][kCsaCols];
+  if ((int)blockIdx.x < nb_reduce) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n4) return;
+    f32x4 s = W[i];
+#pragma unroll 8
+    for (int p = 1; p < splits; ++p) s += W[p * stride4 + i];
+    C[i] = s;
+    return;
+  }
+  colsum_stage2_block<kCsaCols>(part, colsum, nparts, cols, (int64_t)(blockIdx.x - nb_reduce) * kCsaCols, acc);
+}
+
 // The epilogue (kEpi*; bias row-broadcast over the N columns, aux with C's
 // layout; the vector kernel needs N % 4 == 0) is applied to the finished sum.
 __global__ void __launch_bounds__(256)
@@ -1221,12 +1277,14 @@ int launch_cfg(bool vec, const float* A, const float* B, float* C, int64_t M, in
   dim3 grid((unsigned)(tiles_m * tiles_n), (unsigned)splits, (unsigned)bt.count);
   auto go = [&](auto epi_tag) {
     constexpr int E = decltype(epi_tag)::value;
-    // The mask-bit epilogues run on the DMA path with one K group only, and
-    // kEpiMaskBits needs 64-row wave tiles (one column-sum chunk per wave).
-    if constexpr (epi_bits(E) && (KG > 1 || (E == kEpiMaskBits && WM != 64) || (!A_KC && BM % 64 != 0) ||
-                                  (!B_KC && BN % 64 != 0))) {
+    // The mask-bit epilogues and the A column sums run on the DMA path with
+    // one K group only; kEpiMaskBits needs 64-row wave tiles (one column-sum
+    // chunk per wave), kEpiColsumA K tiles that divide the 64-row chunks.
+    if constexpr (epi_dma_only(E) && (KG > 1 || (E == kEpiMaskBits && WM != 64) ||
+                                      (E == kEpiColsumA && 64 % BK != 0) || (!A_KC && BM % 64 != 0) ||
+                                      (!B_KC && BN % 64 != 0))) {
       return AAR_EUNSUPPORTED;
-    } else if constexpr (epi_bits(E)) {
+    } else if constexpr (epi_dma_only(E)) {
       if (!vec) return AAR_EUNSUPPORTED;
       gemm_f32_dma_kernel<BM, BN, BK, WM, WN, kWpe, STAGES, A_KC, B_KC, E, KG><<<grid, dim3(kWaves * KG * 64), 0, st>>>(
           A, B, C, M, N, K, lda, ldb, ldc, kps, split_stride, tiles_m, tiles_n, bt.sA, bt.sB, bt.sC, ep);
@@ -1267,6 +1325,9 @@ int launch_cfg(bool vec, const float* A, const float* B, float* C, int64_t M, in
       return AAR_EUNSUPPORTED;
     case kEpiMaskBits:
       if constexpr (A_KC && !B_KC) return go(std::integral_constant<int, kEpiMaskBits>{});
+      return AAR_EUNSUPPORTED;
+    case kEpiColsumA:
+      if constexpr (!A_KC && !B_KC) return go(std::integral_constant<int, kEpiColsumA>{});
       return AAR_EUNSUPPORTED;
     default: return AAR_EINVAL;
   }
@@ -1405,9 +1466,13 @@ int run_gemm(int op, int64_t M, int64_t N, int64_t K, const float* A, const floa
   const bool vec = gemm_vec_ok(op, M, N, K, A, B, lda, ldb);
   float* out = p.splits > 1 ? static_cast<float*>(workspace) : C;
   const int64_t split_stride = p.splits > 1 ? M * N : 0;
+  // kEpiColsumA works in the main loop of every split; the others apply to
+  // the finished sum, in the reduction when K is split
+  const int main_epi = p.splits > 1 && epi != kEpiColsumA ? kEpiNone : epi;
   int rc = dispatch_op(op, p.cfg, vec, A, B, out, M, N, K, lda, ldb, N, p.splits, p.k_per_split, split_stride,
-                       kSingle, st, p.splits > 1 ? kEpiNone : epi, ep);
+                       kSingle, st, main_epi, ep);
   if (rc != AAR_OK || p.splits <= 1) return rc;
+  if (epi == kEpiColsumA) epi = kEpiNone;
   const int64_t n = M * N;
   if (n % 4 == 0 && aligned16(out) && aligned16(C) && (!ep.bias || (N % 4 == 0 && aligned16(ep.bias))) &&
       (!ep.aux || aligned16(ep.aux))) {
@@ -1598,13 +1663,14 @@ extern "C" int aar_gemm_f32_mask_bits_colsum(int op, int64_t M, int64_t N, int64
                                              void* workspace, size_t workspace_bytes, void* stream) {
   if (op < 0 || op > 2 || M < 0 || N < 0 || K < 0) return AAR_EINVAL;
   if (N == 0) return AAR_OK;
-  if (!colsum) return AAR_EINVAL;
-  if (M == 0) return aar_memset_zero(colsum, (size_t)N * sizeof(float), stream);
+  if (M == 0) return colsum ? aar_memset_zero(colsum, (size_t)N * sizeof(float), stream) : AAR_OK;
   if (!bits) return AAR_EINVAL;
-  if (op != AAR_GEMM_NN || K == 0 || !colsum_chunks_of_64(M)) return AAR_EUNSUPPORTED;
+  if (op != AAR_GEMM_NN || K == 0 || (colsum && !colsum_chunks_of_64(M))) return AAR_EUNSUPPORTED;
   const int chk = check_gemm_args(op, M, N, K, A, B, C, stream);
   if (chk != AAR_OK) return chk;
-  if (!workspace || workspace_bytes < aar_gemm_f32_mask_bits_colsum_workspace_bytes(M, N)) return AAR_EWORKSPACE;
+  if (colsum && (!workspace || workspace_bytes < aar_gemm_f32_mask_bits_colsum_workspace_bytes(M, N))) {
+    return AAR_EWORKSPACE;
+  }
   int64_t lda, ldb;
   default_ld(op, M, N, K, lda, ldb);
   const bool vec = gemm_vec_ok(op, M, N, K, A, B, lda, ldb);
@@ -1612,11 +1678,78 @@ extern "C" int aar_gemm_f32_mask_bits_colsum(int op, int64_t M, int64_t N, int64
   if (p.splits > 1 || p.cfg >= kNumCfgs) return AAR_EUNSUPPORTED;
   GemmEpi ep{nullptr, nullptr};
   ep.bits = const_cast<uint32_t*>(bits);
-  ep.part = static_cast<float*>(workspace);
+  ep.part = colsum ? static_cast<float*>(workspace) : nullptr;  // no colsum: the mask only
   hipStream_t st = as_stream(stream);
   const int rc = run_gemm(op, M, N, K, A, B, C, nullptr, p, st, kEpiMaskBits, ep);
-  if (rc != AAR_OK) return rc;
+  if (rc != AAR_OK || !colsum) return rc;
   return colsum_finish(ep.part, colsum, (int)(M / 64), N, st);
+}
+
+// The product planned as aar_gemm_f32 plans it with the workspace it asks for
+// (its split partials first in the workspace), with aar_colsum_f32's stage-1
+// partials of A ([K, M]) summed in the main loop (kEpiColsumA) after them;
+// colsum's stage 2 finishes them.
+namespace aar {
+namespace {
+Plan colsum_a_plan(int op, int64_t M, int64_t N, int64_t K, const float* A, const float* B, bool& vec) {
+  int64_t lda, ldb;
+  default_ld(op, M, N, K, lda, ldb);
+  vec = gemm_vec_ok(op, M, N, K, A, B, lda, ldb);
+  return plan_gemm(op, M, N, K, (size_t)-1, true, 1, thin_operands_ok(op, A, B, lda, ldb), kEpiNone, vec);
+}
+size_t colsum_a_split_bytes(const Plan& p, int64_t M, int64_t N) {
+  return p.splits > 1 ? ceil_div((int64_t)p.splits * M * N * (int64_t)sizeof(float), (int64_t)256) * 256 : 0;
+}
+}  // namespace
+}  // namespace aar
+
+extern "C" size_t aar_gemm_f32_colsum_a_workspace_bytes(int op, int64_t M, int64_t N, int64_t K) {
+  if (op != AAR_GEMM_TN || M <= 0 || N <= 0 || K <= 0) return 0;
+  bool vec;
+  const Plan p = colsum_a_plan(op, M, N, K, nullptr, nullptr, vec);  // the shape's plan (aligned operands)
+  return colsum_a_split_bytes(p, M, N) + (size_t)ceil_div(K, (int64_t)64) * (size_t)M * sizeof(float);
+}
+
+extern "C" int aar_gemm_f32_colsum_a(int op, int64_t M, int64_t N, int64_t K, const float* A, const float* B,
+                                     float* C, float* colsum, void* workspace, size_t workspace_bytes,
+                                     void* stream) {
+  if (op < 0 || op > 2 || M < 0 || N < 0 || K < 0) return AAR_EINVAL;
+  if (M == 0) return AAR_OK;
+  if (!colsum) return AAR_EINVAL;
+  if (op != AAR_GEMM_TN || N == 0 || K == 0 || !colsum_chunks_of_64(K)) return AAR_EUNSUPPORTED;
+  const int chk = check_gemm_args(op, M, N, K, A, B, C, stream);
+  if (chk != AAR_OK) return chk;
+  bool vec;
+  const Plan p = colsum_a_plan(op, M, N, K, A, B, vec);
+  if (!vec || p.cfg >= kNumCfgs || p.k_per_split % 64 != 0) return AAR_EUNSUPPORTED;
+  const size_t split_bytes = colsum_a_split_bytes(p, M, N);
+  if (!workspace || workspace_bytes < split_bytes + (size_t)(K / 64) * (size_t)M * sizeof(float)) {
+    return AAR_EWORKSPACE;
+  }
+  GemmEpi ep{nullptr, nullptr};
+  ep.part = reinterpret_cast<float*>(static_cast<char*>(workspace) + split_bytes);
+  hipStream_t st = as_stream(stream);
+  const int nparts = (int)(K / 64);
+  float* out = p.splits > 1 ? static_cast<float*>(workspace) : C;
+  if (p.splits <= 1 || !aligned16(C) || !aligned16(workspace)) {
+    const int rc = run_gemm(op, M, N, K, A, B, C, workspace, p, st, kEpiColsumA, ep);
+    if (rc != AAR_OK) return rc;
+    return colsum_finish(ep.part, colsum, nparts, M, st);
+  }
+  // split: the products, then one launch for the split-K sum and colsum's
+  // stage 2 (M * N % 4 == 0: TN on the DMA path has M % 4 == N % 4 == 0)
+  int64_t lda, ldb;
+  default_ld(op, M, N, K, lda, ldb);
+  const int64_t split_stride = M * N;
+  int rc = dispatch_op(op, p.cfg, vec, A, B, out, M, N, K, lda, ldb, N, p.splits, p.k_per_split, split_stride,
+                       kSingle, st, kEpiColsumA, ep);
+  if (rc != AAR_OK) return rc;
+  const int64_t n4 = M * N / 4;
+  const int nb = (int)ceil_div(n4, (int64_t)256);
+  splitk_reduce_colsum_kernel<<<dim3((unsigned)(nb + ceil_div(M, (int64_t)kCsaCols))), dim3(256), 0, st>>>(
+      reinterpret_cast<const f32x4*>(out), reinterpret_cast<f32x4*>(C), n4, split_stride / 4, p.splits, nb, ep.part,
+      colsum, nparts, M);
+  return launch_status();
 }
 
 extern "C" int aar_gemm_f32_tile_config(int config, int* tile_m, int* tile_n, int* tile_k) {

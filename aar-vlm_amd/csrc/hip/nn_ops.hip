@@ -155,9 +155,9 @@ add_bias_vec_kernel(const f32x4* __restrict__ x, const f32x4* __restrict__ bias,
 // (rows r0 = p*chunk .. r0+chunk-1) as two running sums from 0.f, in row
 // order: s0 over the rows with (r - r0) & 4 == 0, s1 over the others, then
 // s0 + s1.  The two sets are the row sets of the two lane halves of a 32x32
-// MFMA accumulator block, so a GEMM epilogue holding 64-row chunks
-// (kEpiMaskBits, gemm_f32.hip) forms the same partials with one exchange
-// between the halves.
+// MFMA accumulator block (and of the A fragments of a TN product's K tile),
+// so the GEMM paths holding 64-row chunks (kEpiMaskBits, kEpiColsumA,
+// gemm_f32.hip) form the same partials with one exchange between the halves.
 __global__ void __launch_bounds__(256)
 colsum_stage1_kernel(const float* __restrict__ g, float* __restrict__ part, int64_t rows, int64_t cols,
                      int64_t chunk) {
@@ -208,35 +208,18 @@ relu_bwd_colsum_stage1_kernel(const f32x4* __restrict__ g, const f32x4* __restri
   *reinterpret_cast<f32x4*>(part + (int64_t)blockIdx.y * cols4 * 4 + c4 * 4) = s0 + s1;
 }
 
-// Stage 2: out[c] = sum over p of part[p][c].  A workgroup owns kCsCols
-// columns and kCsSlices slices of the parts: slice j sums its contiguous run
-// of parts in order, then a fixed pairwise tree over the slices in LDS
-// finishes each column.  Deterministic; one thread per column and part run
-// instead of one per column keeps the few-column case off the latency floor.
+// Stage 2: out[c] = sum over p of part[p][c] (colsum_stage2_block: a
+// workgroup owns kCsCols columns and kColsumSlices slices of the parts, a
+// slice sums its run of parts in order, a fixed tree finishes each column).
+// Deterministic; one thread per column and part run instead of one per
+// column keeps the few-column case off the latency floor.
 constexpr int kCsCols = 16;
-constexpr int kCsThreads = 1024;
-constexpr int kCsSlices = kCsThreads / kCsCols;
+constexpr int kCsThreads = kColsumSlices * kCsCols;
 
 __global__ void __launch_bounds__(kCsThreads)
 colsum_stage2_kernel(const float* __restrict__ part, float* __restrict__ out, int nparts, int64_t cols) {
-  __shared__ float acc[kCsSlices][kCsCols];
-  const int cl = threadIdx.x % kCsCols, slice = threadIdx.x / kCsCols;
-  const int64_t c = (int64_t)blockIdx.x * kCsCols + cl;
-  const int per = (nparts + kCsSlices - 1) / kCsSlices;
-  const int p0 = slice * per;
-  const int p1 = min(nparts, p0 + per);
-  float s = 0.f;
-  if (c < cols) {
-    for (int p = p0; p < p1; ++p) s += part[(int64_t)p * cols + c];
-  }
-  acc[slice][cl] = s;
-  __syncthreads();
-#pragma unroll
-  for (int h = kCsSlices / 2; h >= 1; h /= 2) {
-    if (slice < h) acc[slice][cl] += acc[slice + h][cl];
-    __syncthreads();
-  }
-  if (slice == 0 && c < cols) out[c] = acc[0][cl];
+  __shared__ float acc[kColsumSlices][kCsCols];
+  colsum_stage2_block<kCsCols>(part, out, nparts, cols, (int64_t)blockIdx.x * kCsCols, acc);
 }
 
 int colsum_parts(int64_t rows) {
@@ -539,7 +522,36 @@ multi_update_kernel(MultiArgs A, float alpha, float lr, float beta1, float beta2
   const int64_t i1 = min(A.n[t], i0 + kMultiChunk);
   float* a = A.a[t];  // may alias b (dst += alpha * dst)
   const float* b = A.b[t];
-  for (int64_t i = i0 + threadIdx.x; i < i1; i += 256) {
+  int64_t tail = i0;  // first element left to the scalar loop
+  if (!ADAMW && aligned16(a) && aligned16(b)) {
+    // 128-bit accesses: thread x takes float4s x, x + 256, ... of the chunk,
+    // every load issued before the first store (each element is read and
+    // written by this thread only, so an aliased b still reads old values).
+    // (AdamW keeps the scalar loop: in this form the compiler contracted its
+    // update into FMAs differently from the single-tensor kernel, 1 ulp off.)
+    constexpr int kU = kMultiChunk / (4 * 256);
+    const int64_t q0 = i0 / 4, q1 = i1 / 4;  // whole float4s
+    f32x4 pa[kU], pb[kU];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const int64_t q = q0 + threadIdx.x + 256 * u;
+      if (q < q1) {
+        pa[u] = reinterpret_cast<const f32x4*>(a)[q];
+        pb[u] = reinterpret_cast<const f32x4*>(b)[q];
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const int64_t q = q0 + threadIdx.x + 256 * u;
+      if (q < q1) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) pa[u][e] = ew<Ew::ScaledAdd>(pa[u][e], pb[u][e], alpha);
+        reinterpret_cast<f32x4*>(a)[q] = pa[u];
+      }
+    }
+    tail = q1 * 4;
+  }
+  for (int64_t i = tail + threadIdx.x; i < i1; i += 256) {
     if (ADAMW)
       adamw_elem(a[i], b[i], A.m[t][i], A.v[t][i], lr, beta1, beta2, eps, wd_factor, bc1, bc2);
     else

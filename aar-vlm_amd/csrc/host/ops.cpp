@@ -350,6 +350,27 @@ Tensor linear_no_grad(const Tensor& x, const Tensor& w, const Tensor& b) {
 
 // dx = g W, dW = g^T x (MatmulABTFunction) and db = column sums of g
 // (AddBiasFunction), the same kernels as the two-op composition.
+// A linear layer's dW = G^T X and db = colsum(G) (G [rows, N], X [rows, K],
+// contiguous): one pass of aar_gemm_f32_colsum_a over G where it takes the
+// product's plan, else the product and aar_colsum_f32 (the same values).
+std::pair<Tensor, Tensor> weight_bias_grads(const Tensor& g2, const Tensor& x2, const char* what) {
+  const int64_t rows = g2.shape[0], N = g2.shape[1], K = x2.shape[1];
+  Tensor db = Tensor::empty({N}, DType::Fp32, Device::CUDA);
+  {
+    Tensor dw = Tensor::empty({N, K}, DType::Fp32, Device::CUDA);
+    Workspace ws(aar_gemm_f32_colsum_a_workspace_bytes(AAR_GEMM_TN, N, K, rows));
+    const int rc = aar_gemm_f32_colsum_a(AAR_GEMM_TN, N, K, rows, fp(g2), fp(x2), fp(dw), fp(db), ws.data(),
+                                         ws.bytes(), current_stream());
+    if (rc != AAR_EUNSUPPORTED) {
+      check_status(rc, what);
+      return {dw, db};
+    }
+  }
+  Workspace ws(aar_colsum_workspace_bytes(rows, N));
+  check_status(aar_colsum_f32(fp(g2), fp(db), rows, N, ws.data(), ws.bytes(), current_stream()), what);
+  return {matmul_at_b_no_grad(g2, x2), db};
+}
+
 class LinearFunction : public Function {
  public:
   Tensor saved_x, saved_w;
@@ -357,10 +378,8 @@ class LinearFunction : public Function {
     Tensor gc = as_contig(g);
     const int64_t N = saved_w.shape[0], K = saved_w.shape[1];  // linear() routes N == 0 and K == 0 elsewhere
     const int64_t rows = static_cast<int64_t>(saved_x.numel()) / K;
-    Tensor db = Tensor::empty({N}, DType::Fp32, Device::CUDA);
-    Workspace ws(aar_colsum_workspace_bytes(rows, N));
-    check_status(aar_colsum_f32(fp(gc), fp(db), rows, N, ws.data(), ws.bytes(), current_stream()), "linear backward");
-    return {matmul_no_grad(gc, saved_w), matmul_at_b_no_grad(gc, saved_x), db};
+    auto [dw, db] = weight_bias_grads(as_view(gc, {rows, N}), as_view(saved_x, {rows, K}), "linear backward");
+    return {matmul_no_grad(gc, saved_w), dw, db};
   }
   const char* name() const override { return "LinearFunction"; }
 };
@@ -835,42 +854,32 @@ class MlpReluFunction : public Function {
     const int64_t N2 = saved_w2.shape[0], H = saved_w1.shape[0];
     const int64_t rows = saved_h.shape[0];
     Tensor gc = as_view(as_contig(g), {rows, N2});
-    Tensor db2 = Tensor::empty({N2}, DType::Fp32, Device::CUDA);
-    Tensor db1 = Tensor::empty({H}, DType::Fp32, Device::CUDA);
-    {
-      Workspace ws(aar_colsum_workspace_bytes(rows, N2));
-      check_status(aar_colsum_f32(fp(gc), fp(db2), rows, N2, ws.data(), ws.bytes(), current_stream()),
-                   "mlp backward");
-    }
-    Tensor dw2 = matmul_at_b_no_grad(gc, saved_h);
-    // dh = relu_backward(g W2) and db1 = its column sums.  With the mask bits,
-    // one GEMM does all three (aar_gemm_f32_mask_bits_colsum: the product, the
-    // mask and colsum's partials in its epilogue, bit for bit the separate
-    // passes).  Otherwise the plain GEMM, then the mask pass with db1's
-    // column sum in one pass over dh.  (The mask read as the relu's output in
-    // the epilogue, aar_gemm_f32_relu_mask, measured slower than the latter:
-    // 212 against 172 + 62 us at 16384 x 1536 x 384.)
+    auto [dw2, db2] = weight_bias_grads(gc, saved_h, "mlp backward");
+    // dh = relu_backward(g W2): with the mask bits, one GEMM applies the mask
+    // in its epilogue (aar_gemm_f32_mask_bits_colsum without column sums),
+    // else the plain GEMM and the mask pass.  db1 = colsum(dh) comes with dW1
+    // (dh is that product's A operand), bit for bit aar_colsum_f32's.  (The
+    // mask read as the relu's output in the epilogue, aar_gemm_f32_relu_mask,
+    // measured slower than the separate pass: 212 against 172 + 62 us at
+    // 16384 x 1536 x 384.)
     Tensor dh = Tensor::empty({rows, H}, DType::Fp32, Device::CUDA);
-    bool fused = false;
+    bool masked = false;
     if (saved_bits) {
-      Workspace ws(aar_gemm_f32_mask_bits_colsum_workspace_bytes(rows, H));
       const int rc = aar_gemm_f32_mask_bits_colsum(AAR_GEMM_NN, rows, H, N2, fp(gc), fp(saved_w2),
                                                    static_cast<const uint32_t*>(saved_bits->data()), fp(dh),
-                                                   fp(db1), ws.data(), ws.bytes(), current_stream());
+                                                   nullptr, nullptr, 0, current_stream());
       if (rc != AAR_EUNSUPPORTED) {
         check_status(rc, "mlp backward");
-        fused = true;
+        masked = true;
       }
     }
-    if (!fused) {
+    if (!masked) {
       Tensor dpost = matmul_no_grad(gc, saved_w2);
-      Workspace ws(aar_colsum_workspace_bytes(rows, H));
-      check_status(aar_relu_bwd_colsum_f32(fp(dpost), fp(saved_h), fp(dh), fp(db1), rows, H, ws.data(), ws.bytes(),
-                                           current_stream()),
-                   "mlp backward");
+      check_status(aar_relu_bwd_f32(fp(dpost), fp(saved_h), fp(dh), rows * H, current_stream()), "mlp backward");
     }
     Tensor dx = as_view(matmul_no_grad(dh, saved_w1), x_shape);
-    return {dx, matmul_at_b_no_grad(dh, saved_x), db1, dw2, db2};
+    auto [dw1, db1] = weight_bias_grads(dh, saved_x, "mlp backward");
+    return {dx, dw1, db1, dw2, db2};
   }
   const char* name() const override { return "MlpReluFunction"; }
 };

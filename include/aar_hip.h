@@ -151,10 +151,11 @@ int aar_gemm_f32_relu_mask(int op, int64_t M, int64_t N, int64_t K, const float*
  * sum over rows of C, bit-identical to aar_gemm_f32 (given the workspace
  * aar_gemm_f32_workspace_bytes asks for), the relu backward and
  * aar_colsum_f32; its workspace (aar_gemm_f32_mask_bits_colsum_workspace_bytes)
- * holds colsum's per-64-row partials, which the GEMM epilogue writes.  Both
- * return AAR_EUNSUPPORTED, launching nothing, where the product's plan splits
- * K or has no such epilogue (register staging, K-group tiles, wave tiles of
- * other than 64 rows for the mask) or, for the mask, where M is not a
+ * holds colsum's per-64-row partials, which the GEMM epilogue writes.  With
+ * colsum NULL it applies the mask only (no workspace).  Both return
+ * AAR_EUNSUPPORTED, launching nothing, where the product's plan splits K or
+ * has no such epilogue (register staging, K-group tiles, wave tiles of other
+ * than 64 rows for the mask) or, for the column sums, where M is not a
  * multiple of 64 up to 16384 (colsum's partials are not 64-row chunks
  * there); the caller then runs the separate passes.  Replace
  * matmul_a_bt_cuda + add_bias_cuda + relu_cuda and matmul_cuda +
@@ -167,6 +168,22 @@ size_t aar_gemm_f32_mask_bits_colsum_workspace_bytes(int64_t M, int64_t N);
 int aar_gemm_f32_mask_bits_colsum(int op, int64_t M, int64_t N, int64_t K, const float* A, const float* B,
                                   const uint32_t* bits, float* C, float* colsum, void* workspace,
                                   size_t workspace_bytes, void* stream);
+/* A linear layer's weight and bias gradients from one pass over its output
+ * gradient G: C = A^T B (TN; A = G [K, M], B = the layer input [K, N]) and
+ * colsum[m] = sum over k of A[k][m].  C is bit-identical to aar_gemm_f32 given
+ * the workspace aar_gemm_f32_workspace_bytes asks for (the same plan), colsum
+ * to aar_colsum_f32 over A: the GEMM's main loop sums the A tiles it stages
+ * into colsum's per-64-row partials.  The workspace
+ * (aar_gemm_f32_colsum_a_workspace_bytes) holds the split-K partials and those.
+ * Returns AAR_EUNSUPPORTED, launching nothing, for op other than TN, K not a
+ * multiple of 64 up to 16384 (colsum's partials are not 64-row chunks there),
+ * or a plan without the path (unaligned operands, the thin or short kernels,
+ * K-group tiles, K splits not on 64-row chunks); the caller then runs the two
+ * passes.  Replaces matmul_at_b_cuda + bias_grad_cuda of nn.Linear's backward
+ * (cppsrc/ops/matmul.cpp:12, elementwise.cpp:25). */
+size_t aar_gemm_f32_colsum_a_workspace_bytes(int op, int64_t M, int64_t N, int64_t K);
+int aar_gemm_f32_colsum_a(int op, int64_t M, int64_t N, int64_t K, const float* A, const float* B, float* C,
+                          float* colsum, void* workspace, size_t workspace_bytes, void* stream);
 
 /* Batched GEMM with explicit leading dimensions: for b in [0, batch),
  * C_b = op(A_b, B_b) with A_b = A + b*strideA (and so on), op as in

@@ -88,6 +88,16 @@ def test_abi_validates_before_touching_the_device():
     assert lib.aar_gemm_f32_mask_bits_colsum(0, 64, 0, 2, None, None, None, None, None, None, 0, None) == 0
     assert lib.aar_gemm_f32_mask_bits_colsum_workspace_bytes(16384, 1536) == 256 * 1536 * 4
     assert lib.aar_gemm_f32_mask_bits_colsum_workspace_bytes(0, 1536) == 0
+    # weight + bias gradients in one TN pass: TN only, whole 64-row colsum chunks
+    lib.aar_gemm_f32_colsum_a.argtypes = [ctypes.c_int, i64, i64, i64, vp, vp, vp, vp, vp, ctypes.c_size_t, vp]
+    lib.aar_gemm_f32_colsum_a_workspace_bytes.restype = ctypes.c_size_t
+    lib.aar_gemm_f32_colsum_a_workspace_bytes.argtypes = [ctypes.c_int, i64, i64, i64]
+    assert lib.aar_gemm_f32_colsum_a(2, 2, 2, 64, None, None, None, None, None, 0, None) == -1  # no colsum
+    assert lib.aar_gemm_f32_colsum_a(0, 2, 2, 64, None, None, None, x, None, 0, None) == -3  # NN
+    assert lib.aar_gemm_f32_colsum_a(2, 2, 2, 100, None, None, None, x, None, 0, None) == -3  # K not 64-row chunks
+    assert lib.aar_gemm_f32_colsum_a(2, 0, 2, 64, None, None, None, None, None, 0, None) == 0  # empty
+    assert lib.aar_gemm_f32_colsum_a_workspace_bytes(0, 384, 1536, 16384) == 0
+    assert lib.aar_gemm_f32_colsum_a_workspace_bytes(2, 384, 1536, 16384) >= 256 * 384 * 4
     assert lib.aar_gemm_f32_bias(1, 2, 2, 0, None, None, 16, None, None, 0, None) == -3  # K = 0: not a product
     lib.aar_softmax_fwd_f32.argtypes = [vp, vp, i64, i64, vp]
     assert lib.aar_softmax_fwd_f32(None, None, 4, 0, None) == -1

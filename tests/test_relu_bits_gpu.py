@@ -4,9 +4,10 @@
   and the bits equal to C > 0 packed 32 rows a word (bit r % 32 of word
   (r / 32) * N + c, zero past M);
 * aar_gemm_f32_mask_bits_colsum (NN): C bit-identical to aar_gemm_f32 then
-  aar_relu_bwd_f32 against the forward's C, and colsum bit-identical to
-  aar_colsum_f32 of that C (its 64-row chunk partials come from the GEMM
-  epilogue), and within the float64 bound of the exact column sums.
+  aar_relu_bwd_f32 against the forward's C, with column sums requested and
+  without; and colsum bit-identical to aar_colsum_f32 of that C (its 64-row
+  chunk partials come from the GEMM epilogue), and within the float64 bound
+  of the exact column sums.
 
 The GPT block's MLP shape (16384 rows, 384 -> 1536 -> 384) must take both
 entry points; other shapes either take them (and are checked the same way) or
@@ -119,6 +120,16 @@ def test_bits_forward_and_masked_backward(gpu, M, H, d, N2):
         pcs_ref = abi.empty(H)
         abi.check(L.aar_colsum_f32(pdh_ref, pcs_ref, M, H, abi.alloc(csb), csb, None))
         dh_ref, cs_ref = abi.get(pdh_ref, (M, H)), abi.get(pcs_ref, (H,))
+
+        # the mask only (no column sums, no workspace, any row count)
+        pdh = abi.put(np.full((M, H), 7.0, f32))
+        rc = L.aar_gemm_f32_mask_bits_colsum(NN, M, H, N2, pg, pw2, pbits, pdh, None, None, 0, None)
+        assert rc in (0, -3), rc
+        if rc == 0:
+            np.testing.assert_array_equal(abi.get(pdh, (M, H)), dh_ref)
+        else:
+            assert M != 16384, "the GPT block shape must take the mask-bits epilogue"
+            assert (abi.get(pdh, (M, H)) == 7.0).all()
 
         pdh, pcs = abi.put(np.full((M, H), 7.0, f32)), abi.put(np.full(H, 7.0, f32))
         wm = L.aar_gemm_f32_mask_bits_colsum_workspace_bytes(M, H)
