@@ -297,6 +297,47 @@ embedding_fwd_vec_kernel(const f32x4* __restrict__ w, const int64_t* __restrict_
   }
 }
 
+// Two lookups and their sum, out[i] = w1[ids1[i]] + w2[ids2[i]] (the token +
+// position embeddings of a GPT): each table row as embedding_fwd reads it (a
+// zero row for an id out of range, which sets *err), then one fp32 add, so
+// the result is bit for bit the two lookups followed by an add, with one
+// write of the sum instead of two rows written and read back.
+__global__ void __launch_bounds__(256)
+embedding_add_fwd_vec_kernel(const f32x4* __restrict__ w1, const int64_t* __restrict__ ids1, int64_t vocab1,
+                             const f32x4* __restrict__ w2, const int64_t* __restrict__ ids2, int64_t vocab2,
+                             f32x4* __restrict__ out, int64_t n, int64_t dim4, int* __restrict__ err) {
+  const int64_t i = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (i >= n) return;
+  const int64_t id1 = ids1[i], id2 = ids2[i];
+  const bool ok1 = id1 >= 0 && id1 < vocab1, ok2 = id2 >= 0 && id2 < vocab2;
+  if ((!ok1 || !ok2) && lane == 0 && err) *err = 1;
+  const f32x4* s1 = w1 + (ok1 ? id1 : 0) * dim4;
+  const f32x4* s2 = w2 + (ok2 ? id2 : 0) * dim4;
+  f32x4* dst = out + i * dim4;
+  const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+  for (int64_t k = lane; k < dim4; k += 64) {
+    const f32x4 a = ok1 ? s1[k] : z, b = ok2 ? s2[k] : z;
+    __builtin_nontemporal_store(a + b, dst + k);
+  }
+}
+
+__global__ void __launch_bounds__(256)
+embedding_add_fwd_kernel(const float* __restrict__ w1, const int64_t* __restrict__ ids1, int64_t vocab1,
+                         const float* __restrict__ w2, const int64_t* __restrict__ ids2, int64_t vocab2,
+                         float* __restrict__ out, int64_t n, int64_t dim, int* __restrict__ err) {
+  const int64_t total = n * dim;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += stride) {
+    const int64_t i = e / dim, k = e - i * dim;
+    const int64_t id1 = ids1[i], id2 = ids2[i];
+    const bool ok1 = id1 >= 0 && id1 < vocab1, ok2 = id2 >= 0 && id2 < vocab2;
+    if ((!ok1 || !ok2) && k == 0 && err) *err = 1;
+    const float a = ok1 ? w1[id1 * dim + k] : 0.f, b = ok2 ? w2[id2 * dim + k] : 0.f;
+    out[e] = a + b;
+  }
+}
+
 // onehot[i][v] = (ids[i] == v)  (row-major [n, vocab])
 __global__ void __launch_bounds__(256)
 onehot_kernel(const int64_t* __restrict__ ids, float* __restrict__ oh, int64_t n, int64_t vocab) {
@@ -857,6 +898,25 @@ int aar_embedding_fwd_f32(const float* w, const int64_t* ids, float* out, int64_
   }
   embedding_fwd_kernel<<<dim3(stream_grid(n * dim)), dim3(256), 0, as_stream(stream)>>>(w, ids, out, n, vocab, dim,
                                                                                          err);
+  return launch_status();
+}
+
+int aar_embedding_add_fwd_f32(const float* w1, const int64_t* ids1, int64_t vocab1, const float* w2,
+                              const int64_t* ids2, int64_t vocab2, float* out, int64_t n, int64_t dim, int* err,
+                              void* stream) {
+  if (n < 0 || vocab1 < 0 || vocab2 < 0 || dim < 0) return AAR_EINVAL;
+  if (n == 0 || dim == 0) return AAR_OK;
+  if (!ids1 || !ids2 || !out || (vocab1 > 0 && !w1) || (vocab2 > 0 && !w2)) return AAR_EINVAL;
+  hipStream_t st = as_stream(stream);
+  if (dim % 4 == 0 && (vocab1 == 0 || aligned16(w1)) && (vocab2 == 0 || aligned16(w2)) && aligned16(out) &&
+      ceil_div(n, 4) <= (int64_t)UINT32_MAX) {
+    embedding_add_fwd_vec_kernel<<<dim3((unsigned)ceil_div(n, 4)), dim3(256), 0, st>>>(
+        reinterpret_cast<const f32x4*>(w1), ids1, vocab1, reinterpret_cast<const f32x4*>(w2), ids2, vocab2,
+        reinterpret_cast<f32x4*>(out), n, dim / 4, err);
+    return launch_status();
+  }
+  embedding_add_fwd_kernel<<<dim3(stream_grid(n * dim)), dim3(256), 0, st>>>(w1, ids1, vocab1, w2, ids2, vocab2, out,
+                                                                              n, dim, err);
   return launch_status();
 }
 

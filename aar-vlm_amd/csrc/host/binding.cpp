@@ -181,6 +181,10 @@ PYBIND11_MODULE(_core, m) {
   m.def("_linear_residual", &linear_residual, py::arg("r"), py::arg("a"), py::arg("weight"), gil_release(),
         "r + a W^T as one GEMM with the residual added in its epilogue: the values and gradients of "
         "add(r, matmul_a_bt(a, W)).");
+  m.def("_embedding_add", &embedding_add, py::arg("w1"), py::arg("ids1"), py::arg("w2"), py::arg("ids2"),
+        gil_release(),
+        "add(embedding(w1, ids1), embedding(w2, ids2)) in one lookup-and-add pass: the values and gradients of "
+        "the composition.");
   m.def("_mlp_relu_residual", &mlp_relu_residual, py::arg("r"), py::arg("x"), py::arg("w1"), py::arg("b1"),
         py::arg("w2"), py::arg("b2"), gil_release(),
         "r + _mlp_relu(x, w1, b1, w2, b2) with the residual added in the second GEMM's epilogue: the values "

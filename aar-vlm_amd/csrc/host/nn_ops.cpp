@@ -200,6 +200,28 @@ class EmbeddingFunction : public Function {
   const char* name() const override { return "EmbeddingFunction"; }
 };
 
+// add(embedding(w1, ids1), embedding(w2, ids2)) as one node: the gradient of
+// each table is the embedding backward of the same g.
+class EmbeddingAddFunction : public Function {
+ public:
+  Tensor saved_ids1, saved_ids2;
+  int64_t vocab1 = 0, vocab2 = 0;
+  std::vector<Tensor> backward(const Tensor& g) override {
+    Tensor gc = as_contig(g);
+    const int64_t D = gc.shape.back();
+    auto table_grad = [&](const Tensor& ids, int64_t V) {
+      const int64_t n = n_of(ids);
+      Tensor dW = Tensor::empty({V, D}, DType::Fp32, Device::CUDA);
+      Workspace ws(aar_embedding_bwd_workspace_bytes(n, V, D));
+      check_status(aar_embedding_bwd_f32(fp(gc), ip(ids), fp(dW), n, V, D, ws.data(), ws.bytes(), current_stream()),
+                   "embedding backward");
+      return dW;
+    };
+    return {table_grad(saved_ids1, vocab1), table_grad(saved_ids2, vocab2)};
+  }
+  const char* name() const override { return "EmbeddingAddFunction"; }
+};
+
 class CrossEntropyFunction : public Function {
  public:
   Tensor saved_logits, saved_targets;
@@ -364,6 +386,37 @@ Tensor embedding(const Tensor& weight, const Tensor& ids) {
   fn->record_input(wc);
   fn->saved_ids = ic;
   fn->vocab_size = V;
+  return attach(fn, out);
+}
+
+// add(embedding(w1, ids1), embedding(w2, ids2)), the token + position
+// embeddings of a GPT (python/shakespeare/scripts/model.py:53), as one
+// lookup-and-add pass (aar_embedding_add_fwd_f32): the same values, and the
+// same gradients for both tables.  Anything the fused pass does not cover
+// (other dtypes or ranks, id shapes that differ, host tensors) takes the
+// composition, with its checks and messages.
+Tensor embedding_add(const Tensor& w1, const Tensor& ids1, const Tensor& w2, const Tensor& ids2) {
+  const bool plain = w1.dtype == DType::Fp32 && w2.dtype == DType::Fp32 && ids1.dtype == DType::Int64 &&
+                     ids2.dtype == DType::Int64 && w1.shape.size() == 2 && w2.shape.size() == 2 &&
+                     w1.shape[1] == w2.shape[1] && ids1.shape == ids2.shape && w1.device == Device::CUDA &&
+                     w2.device == Device::CUDA && ids1.device == Device::CUDA && ids2.device == Device::CUDA;
+  if (!plain) return add(embedding(w1, ids1), embedding(w2, ids2));
+  Tensor wc1 = as_contig(w1), wc2 = as_contig(w2), ic1 = as_contig(ids1), ic2 = as_contig(ids2);
+  const int64_t V1 = wc1.shape[0], V2 = wc2.shape[0], D = wc1.shape[1];
+  std::vector<int64_t> out_shape = ic1.shape;
+  out_shape.push_back(D);
+  Tensor out = Tensor::empty(out_shape, DType::Fp32, Device::CUDA);
+  check_status(aar_embedding_add_fwd_f32(fp(wc1), ip(ic1), V1, fp(wc2), ip(ic2), V2, fp(out), n_of(ic1), D,
+                                         device_error_word(kErrEmbeddingId), current_stream()),
+               "embedding");
+  if (!wc1.requires_grad && !wc2.requires_grad) return out;
+  auto fn = std::make_shared<EmbeddingAddFunction>();
+  fn->record_input(wc1);
+  fn->record_input(wc2);
+  fn->saved_ids1 = ic1;
+  fn->saved_ids2 = ic2;
+  fn->vocab1 = V1;
+  fn->vocab2 = V2;
   return attach(fn, out);
 }
 

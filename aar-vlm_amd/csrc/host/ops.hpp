@@ -62,6 +62,8 @@ Tensor sum_all(const Tensor& a);
 Tensor add_bias(const Tensor& x, const Tensor& bias);
 void scaled_add_inplace(Tensor& dst, const Tensor& src, float alpha);
 Tensor embedding(const Tensor& weight, const Tensor& ids);
+// add(embedding(w1, ids1), embedding(w2, ids2)) in one pass, same values and gradients.
+Tensor embedding_add(const Tensor& w1, const Tensor& ids1, const Tensor& w2, const Tensor& ids2);
 Tensor cross_entropy(const Tensor& logits, const Tensor& targets, int64_t ignore_index);
 void adamw_step(Tensor& param, const Tensor& grad, Tensor& m, Tensor& v, float lr, float beta1, float beta2,
                 float eps, float weight_decay, float bias_correction1, float bias_correction2);

@@ -597,7 +597,8 @@ class GPT:
         ag, c, p = self.ag, self.cfg, self.p
         B, T = ids.shape
         d, H = c["d_model"], c["heads"]
-        x = ag.add(ag.embedding(p[0], ids), ag.embedding(p[1], pos))
+        # add(embedding(tok), embedding(pos)) as one lookup-and-add pass
+        x = ag._core._embedding_add(p[0], ids, p[1], pos)
         for i in range(c["layers"]):
             (l1w, l1b, wqkv, wout, l2w, l2b, f1w, f1b, f2w, f2b) = p[2 + 10 * i: 12 + 10 * i]
             h = ag.layernorm(x, l1w, l1b, 1e-5)

@@ -451,6 +451,15 @@ int aar_sum_f32(const float* x, float* out, int64_t n, void* workspace, size_t w
  * Replaces embedding_cuda (cppsrc/ops/embedding.cpp:9). */
 int aar_embedding_fwd_f32(const float* w, const int64_t* ids, float* out, int64_t n, int64_t vocab,
                           int64_t dim, int* err, void* stream);
+/* out[i][:] = w1[ids1[i]][:] + w2[ids2[i]][:] (both tables [vocab_k, dim]): two
+ * lookups and their sum in one pass, bit-identical to two
+ * aar_embedding_fwd_f32 calls then aar_add_f32 (an id out of range gives a
+ * zero row and sets *err = 1).  Replaces embedding_cuda x2 + add_cuda of the
+ * GPT's token + position embeddings (cppsrc/ops/embedding.cpp:9,
+ * elementwise.cpp:13; python/shakespeare/scripts/model.py:53). */
+int aar_embedding_add_fwd_f32(const float* w1, const int64_t* ids1, int64_t vocab1, const float* w2,
+                              const int64_t* ids2, int64_t vocab2, float* out, int64_t n, int64_t dim, int* err,
+                              void* stream);
 
 /* dw[vocab, dim] = onehot(ids)^T . g[n, dim] on matrix cores (deterministic;
  * AAR_EUNSUPPORTED when n*vocab > 2^30).  Up to 260 rows (dim % 4 == 0, g

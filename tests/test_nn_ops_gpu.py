@@ -256,6 +256,38 @@ def test_embedding_out_of_range_is_reported(gpu, dim):
                                   np.ones((1, 3), f32))
 
 
+@pytest.mark.parametrize("dim,B,T", [(384, 64, 256), (8, 3, 50), (3, 2, 7)])  # 128-bit rows, element-wise
+def test_embedding_add_matches_composition(gpu, dim, B, T):
+    """_embedding_add (the GPT's token + position embeddings in one pass):
+    output and both table gradients bit-identical to add(embedding, embedding),
+    and against the oracle."""
+    rng = np.random.default_rng(dim + T)
+    tok, pos = rng.standard_normal((65, dim)).astype(f32), rng.standard_normal((T, dim)).astype(f32)
+    ids = rng.integers(0, 65, (B, T))
+    pids = np.tile(np.arange(T, dtype=np.int64), (B, 1))
+    g = rng.standard_normal((B, T, dim)).astype(f32)
+    res = []
+    for fused in (True, False):
+        tw, pw = dev(gpu, tok, True), dev(gpu, pos, True)
+        a, b = ids_dev(gpu, ids), ids_dev(gpu, pids)
+        if fused:
+            y = gpu._core._embedding_add(tw, a, pw, b)
+        else:
+            y = gpu.add(gpu.embedding(tw, a), gpu.embedding(pw, b))
+        y.backward(dev(gpu, g))
+        res.append((host(gpu, y), host(gpu, tw.grad), host(gpu, pw.grad)))
+    for x, y, name in zip(res[0], res[1], ("out", "d tok", "d pos")):
+        np.testing.assert_array_equal(x, y, err_msg=name)
+    np.testing.assert_array_equal(res[0][0], O.add(O.embedding(tok, ids), O.embedding(pos, pids)))
+    # an id out of range is reported as by embedding; differing id shapes take the composition
+    w = dev(gpu, np.ones((5, dim), f32))
+    y = gpu._core._embedding_add(w, ids_dev(gpu, np.array([1, 5], np.int64)), w, ids_dev(gpu, np.array([0, 1])))
+    with pytest.raises(IndexError):
+        host(gpu, y)
+    with pytest.raises(ValueError):
+        gpu._core._embedding_add(w, ids_dev(gpu, np.array([1, 2], np.int64)), w, ids_dev(gpu, np.array([0])))
+
+
 @pytest.mark.parametrize("N,V", [(6, 5), (4, 6), (16384, 65), (1000, 300)])
 def test_cross_entropy_fwd_bwd(gpu, N, V):
     rng = np.random.default_rng(N + V)
