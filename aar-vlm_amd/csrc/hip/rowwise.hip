@@ -353,8 +353,13 @@ __device__ __forceinline__ void ln_bwd_load(RS (&sg)[U], RS (&sx)[U], float (&mu
 // are reduced, so each wave keeps two row sets in flight.  ACC: dx is added
 // onto `addend` (dx = addend + value, the fp32 addition of a gradient
 // fan-in); the addend row is loaded once the row's reductions are done, so
-// it costs no registers while gy and x are held.
-template <int NV, int W, bool VEC, int NW, bool PF, bool ACC>
+// it costs no registers while gy and x are held.  EARLY (narrow rows, NV <=
+// 2, without PF): the addend rows are loaded with gy and x instead, so a row
+// waits for one memory round trip, not two; the host takes it for grids
+// below the resident cap (short inputs: 16384 x 384, 27.2 -> 23.5 us), where
+// each workgroup runs only a few row iterations (at 65536 rows, persistent
+// workgroups, it measured 75.0 -> 77.5 us).
+template <int NV, int W, bool VEC, int NW, bool PF, bool ACC, bool EARLY = false>
 __global__ void __launch_bounds__(NW * 64, ln_bwd_min_waves(NV, W, ACC))
 layernorm_bwd_kernel(const float* __restrict__ gy, const float* __restrict__ x,
                      const float* __restrict__ w, const float* __restrict__ mean,
@@ -377,10 +382,17 @@ layernorm_bwd_kernel(const float* __restrict__ gy, const float* __restrict__ x,
   const float inv_d = 1.0f / (float)cols;
   RS sg[U], sx[U];
   float mu[U], r[U];
+  constexpr bool kEarlyAddend = ACC && EARLY && !PF && NV <= 2;
+  RS sa_early[kEarlyAddend ? U : 1];
   if (PF) ln_bwd_load<U>(sg, sx, mu, r, gy, x, mean, rstd, group_row0(0, per_iter, grp, U), rows, cols, wr, lane);
   for (int64_t it = 0; it < iters; ++it) {
     const int64_t row0 = group_row0(it, per_iter, grp, U);
     if (!PF) ln_bwd_load<U>(sg, sx, mu, r, gy, x, mean, rstd, row0, rows, cols, wr, lane);
+    if constexpr (kEarlyAddend) {
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+        if (row0 + u < rows) sa_early[u].load(addend + (row0 + u) * cols, cols, wr, lane);
+    }
     RS ng[U], nx[U];
     float nmu[U], nr[U];
     if (PF && it + 1 < iters) {
@@ -403,7 +415,9 @@ layernorm_bwd_kernel(const float* __restrict__ gy, const float* __restrict__ x,
       sum_g = group_reduce<W, false, NW>(sum_g, red, (((int)(it & 1) * U + u) * 2 + 0), grp, wr, lane);
       sum_gn = group_reduce<W, false, NW>(sum_gn, red, (((int)(it & 1) * U + u) * 2 + 1), grp, wr, lane);
       RS sa;
-      if (ACC) {
+      if constexpr (kEarlyAddend) {
+        sa = sa_early[u];
+      } else if (ACC) {
         // (the empty asm keeps the compiler from hoisting these loads above the
         // reductions, where they would hold registers beside gy and x)
         asm volatile("" ::: "memory");
@@ -745,7 +759,7 @@ int ln_bwd_resident() {
 // Number of dgamma/dbeta partial rows = persistent workgroups of the
 // backward kernel: as many as are resident at once, at most
 // kLnBwdWavesPerCu waves per CU, so no workgroup waits for a second round.
-int ln_bwd_parts_for(int64_t rows, const RowPlan& p) {
+int ln_bwd_parts_for(int64_t rows, const RowPlan& p, bool* below_cap = nullptr) {
   const int64_t cus = device_cu_count();
   int64_t cap, pass;
   if (p.nv == 0) {
@@ -764,6 +778,7 @@ int ln_bwd_parts_for(int64_t rows, const RowPlan& p) {
     pass = std::max<int64_t>((int64_t)(nw / p.w) * ln_bwd_rows(p.nv, p.w), 32);
   }
   const int64_t need = ceil_div(rows, pass);
+  if (below_cap) *below_cap = need < cap;
   return (int)(need < cap ? need : cap);
 }
 // Workspace sizing does not know the pointers' alignment: cover both plans.
@@ -883,7 +898,8 @@ int layernorm_bwd_run(const float* gy, const float* x, const float* w, const flo
   if (!gy || !x || !w || !mean || !rstd || !dx) return AAR_EINVAL;
   const bool vec = ln_bwd_vec(gy, x, w, dx, workspace, cols) && (!addend || aligned16(addend));
   const RowPlan p = plan_rows(cols, vec);
-  const int parts = ln_bwd_parts_for(rows, p);
+  bool short_grid = false;
+  const int parts = ln_bwd_parts_for(rows, p, &short_grid);
   const size_t need = (size_t)parts * 2 * (size_t)cols * sizeof(float);
   if (!workspace || workspace_bytes < need) return AAR_EWORKSPACE;
   float* part = static_cast<float*>(workspace);
@@ -897,7 +913,14 @@ int layernorm_bwd_run(const float* gy, const float* x, const float* w, const flo
     layernorm_bwd_wide_cols_kernel<<<dim3((unsigned)ceil_div(cols, kThreads), (unsigned)parts),
                                      dim3(kThreads), 0, st>>>(gy, x, mean, rstd, part, rows, cols);
   } else {
-    if (addend) {
+    if (addend && short_grid) {
+#define L(NV, W, V)                                                                                  \
+  layernorm_bwd_kernel<NV, W, V, ln_bwd_waves(NV, W), ln_bwd_prefetch(NV, W), true, true>                \
+      <<<dim3(parts), dim3(ln_bwd_waves(NV, W) * kWave), 0, st>>>(gy, x, w, mean, rstd, addend, dx, part, \
+                                                                 rows, (int)cols)
+      AAR_ROW_DISPATCH(p, L);
+#undef L
+    } else if (addend) {
 #define L(NV, W, V)                                                                                  \
   layernorm_bwd_kernel<NV, W, V, ln_bwd_waves(NV, W), ln_bwd_prefetch(NV, W), true>                      \
       <<<dim3(parts), dim3(ln_bwd_waves(NV, W) * kWave), 0, st>>>(gy, x, w, mean, rstd, addend, dx, part, \
