@@ -230,6 +230,7 @@ __device__ __forceinline__ void store_tile_bits(const f32x16 (&acc)[TM][TN], flo
       }
     }
     if constexpr (EPI == kEpiMaskBits) {
+      if (!ep.part) continue;  // the mask only
       // colsum's chunk partial: half h's running sum over its rows (row & 4
       // == 4h) in row order, i.e. its registers in order, then s0 + s1
       float s = 0.f;
@@ -238,7 +239,7 @@ __device__ __forceinline__ void store_tile_bits(const f32x16 (&acc)[TM][TN], flo
 #pragma unroll
         for (int r = 0; r < 16; ++r) s += vals[i][r];
       s += __uint_as_float(partner_u32(__float_as_uint(s)));
-      if (ep.part && h == 0 && col < N && r0 < M) ep.part[(r0 >> 6) * N + col] = s;
+      if (h == 0 && col < N && r0 < M) ep.part[(r0 >> 6) * N + col] = s;
     }
   }
 }
@@ -708,9 +709,13 @@ gemm_f32_dma_kernel(const float* __restrict__ A, const float* __restrict__ B, fl
     const int64_t k0 = kbeg + (int64_t)t * BK;
     const bool cs_on = EPI == kEpiColsumA && wave < NWM && (k0 >> 6) % tiles_n == tn;
     // With K groups four waves share a SIMD; the one issuing matrix ops
-    // keeps priority over those issuing loads (measured +2.5 % at 1024^3;
-    // the one-group kernels lose slightly with it).
-    if constexpr (KG > 1) __builtin_amdgcn_s_setprio(1);
+    // keeps priority over those issuing loads (measured +2.5 % at 1024^3).
+    // One-group kernels lose slightly with it, except the 128x128x64 tile on
+    // TN products (A/B in one process: 2048^3 127.0 -> 129.0 TF, the GPT
+    // step's weight gradients 384 x 1536 x 16384 and 1536 x 384 x 16384 -2
+    // us of 161; its NN and NT lose up to 1 %).
+    constexpr bool kPrio = KG > 1 || (!A_KC && !B_KC && BM == 128 && BN == 128 && BK == 64 && WM == 32);
+    if constexpr (kPrio) __builtin_amdgcn_s_setprio(1);
     f32x4 af[2][TM], bf[2][TN];
 #pragma unroll
     for (int i = 0; i < TM; ++i) af[0][i] = TA::frag(as, wm0 + 32 * i + lr, 0, h);
@@ -741,7 +746,7 @@ gemm_f32_dma_kernel(const float* __restrict__ A, const float* __restrict__ B, fl
         }
       }
     }
-    if constexpr (KG > 1) __builtin_amdgcn_s_setprio(0);
+    if constexpr (kPrio) __builtin_amdgcn_s_setprio(0);
     if constexpr (EPI == kEpiColsumA) {
       if (cs_on && ((k0 + BK) & 63) == 0) {  // the chunk's last K tile
 #pragma unroll
