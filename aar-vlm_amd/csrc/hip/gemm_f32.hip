@@ -1131,8 +1131,20 @@ constexpr Cfg kCfgs[] = {
     // of LDS): for grids of about one 128x128 tile per CU (2048^3: 129.2 /
     // 128.8 / 127.2 TF NN/NT/TN against 127.2 / 123.5 / 127.6 for 10)
     {128, 128, 64, 32, 64, 1, 2, 0.83f, 1, kAllOps},
+    // 15: configuration 6 with two resident workgroups per CU and a 4-deep
+    // ring (48 KB).  Not a candidate of its own: the planner substitutes it
+    // for an unsplit plan on 6 whose grid holds at least 3 tiles per CU
+    // (kDeepRingFor6).  A/B in one process, 6 -> 15, over 8 shapes of 3 to 16
+    // tiles per CU (384 x 16384 x 384, 192 x 32768 x 1024, 16384 x 1152 x
+    // 1536, 16384 x 2048 x 256, ...): faster in all 24 shape/layout pairs by
+    // 0.7-4.6 %, e.g. the GPT qkv shape 16384 x 1152 x 384 NN/NT/TN 126.8 /
+    // 124.7 / 130.2 -> 123.9 / 122.6 / 126.6 us.  (Changing 6 itself in the
+    // planner's model moved 1140 of 17496 plans over a shape grid, mostly
+    // small-M split products that were not measured, so 6 keeps its role.)
+    {64, 128, 16, 32, 64, 2, 4, 0.80f, 3, kAllOps},
 };
 constexpr int kNumCfgs = sizeof(kCfgs) / sizeof(kCfgs[0]);
+constexpr int kDeepRingFor6 = 15;
 constexpr int kMaxSplits = 64;
 
 struct Plan {
@@ -1216,7 +1228,7 @@ Plan plan_gemm(int op, int64_t M, int64_t N, int64_t K, size_t ws_bytes, bool al
   double best_t = 1e300;
   for (int c = 0; c < kNumCfgs; ++c) {
     const Cfg& cf = kCfgs[c];
-    if (!(cf.ops & (1 << op))) continue;
+    if (!(cf.ops & (1 << op)) || c == kDeepRingFor6) continue;
     const int64_t tiles = ceil_div(M, (int64_t)cf.bm) * ceil_div(N, (int64_t)cf.bn) * batch;
     // Configuration 8 as NT or TN: only grids of at most one round of its
     // resident workgroups, or of two or three whole rounds.  Measured at
@@ -1258,6 +1270,10 @@ Plan plan_gemm(int op, int64_t M, int64_t N, int64_t K, size_t ws_bytes, bool al
         best = Plan{c, (int)real_splits, kps};
       }
     }
+  }
+  if (best.cfg == 6 && best.splits == 1) {
+    const int64_t tiles = ceil_div(M, (int64_t)kCfgs[6].bm) * ceil_div(N, (int64_t)kCfgs[6].bn) * batch;
+    if (tiles >= 3 * (int64_t)cus) best.cfg = kDeepRingFor6;
   }
   return best;
 }
@@ -1363,12 +1379,13 @@ int launch_op(int cfg, bool vec, const float* A, const float* B, float* C, int64
     AAR_GEMM_CFG(12)
     AAR_GEMM_CFG(13)
     AAR_GEMM_CFG(14)
+    AAR_GEMM_CFG(15)
     default:
       return AAR_EINVAL;
   }
 #undef AAR_GEMM_CFG
 }
-static_assert(kNumCfgs == 15, "launch_op lists every configuration");
+static_assert(kNumCfgs == 16, "launch_op lists every configuration");
 
 // 128-bit loads need 16-byte aligned operands whose contiguous extents and
 // leading dimensions are multiples of 4, and the 32-bit per-thread offsets
