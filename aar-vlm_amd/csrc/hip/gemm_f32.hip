@@ -1254,13 +1254,16 @@ Plan plan_gemm(int op, int64_t M, int64_t N, int64_t K, size_t ws_bytes, bool al
           if (si < kNumPlanSplits) si = kNumPlanSplits - 1;  // still try the filling count
           continue;
         }
-        if ((size_t)splits * M * N * sizeof(float) > ws_bytes) {
-          if (si < kNumPlanSplits) si = kNumPlanSplits - 1;
-          continue;
-        }
       }
       const int64_t kps = split_chunk(K, splits, cf.bk);
       const int64_t real_splits = ceil_div(K, kps);
+      // the workspace the plan uses: its real split count, which rounding the
+      // chunk to the tile depth can make smaller than the one asked for (and
+      // the one aar_gemm_f32_workspace_bytes reports)
+      if (real_splits > 1 && (size_t)real_splits * M * N * sizeof(float) > ws_bytes) {
+        if (si < kNumPlanSplits) si = kNumPlanSplits - 1;
+        continue;
+      }
       const int64_t per_cu = ceil_div(tiles * real_splits, (int64_t)cus);
       const double occ = std::min(1.0, 0.6 + 0.4 * (double)per_cu / cf.slots);
       double t = (double)per_cu * 2.0 * cf.bm * cf.bn * (double)kps / (cf.eff * occ * cu_flops);

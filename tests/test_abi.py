@@ -151,6 +151,39 @@ def test_abi_validates_before_touching_the_device():
     assert lib.aar_adamw_multi_f32(1, ptrs, ptrs, ptrs, ptrs, sizes, *([0.1] * 7), None) == 0  # all empty: no launch
 
 
+def test_gemm_workspace_query_buys_the_unlimited_plan():
+    """A caller that passes the bytes aar_gemm_f32_workspace_bytes reports
+    gets the plan an unlimited workspace gets (planning only, no launch; the
+    CU count is the device's, 256 without one).  Split counts the planner
+    asks for can shrink when the K chunk is rounded to the tile depth
+    (384 x 384 x 16384 TN: 28 asked, 27 real); the plan's workspace is the
+    real count's."""
+    lib = ctypes.CDLL(str(LIB))
+    i64, sz, ip = ctypes.c_int64, ctypes.c_size_t, ctypes.POINTER(ctypes.c_int)
+    lib.aar_gemm_f32_plan.argtypes = [ctypes.c_int, i64, i64, i64, sz, ip, ip]
+    lib.aar_gemm_f32_workspace_bytes.restype = sz
+    lib.aar_gemm_f32_workspace_bytes.argtypes = [ctypes.c_int, i64, i64, i64]
+
+    def plan(op, M, N, K, ws):
+        cfg, sp = ctypes.c_int(), ctypes.c_int()
+        assert lib.aar_gemm_f32_plan(op, M, N, K, ws, ctypes.byref(cfg), ctypes.byref(sp)) == 0
+        return cfg.value, sp.value
+
+    checked = split = 0
+    dims = (64, 65, 128, 384, 1000, 1152, 1536, 4096)
+    for op in (0, 1, 2):
+        for M in dims:
+            for N in dims:
+                for K in (384, 4096, 16384, 65536):
+                    ws = lib.aar_gemm_f32_workspace_bytes(op, M, N, K)
+                    want = plan(op, M, N, K, 1 << 40)
+                    assert plan(op, M, N, K, ws) == want, (op, M, N, K, ws)
+                    checked += 1
+                    split += want[1] > 1
+    assert split > 50, (checked, split)
+    assert plan(2, 384, 384, 16384, lib.aar_gemm_f32_workspace_bytes(2, 384, 384, 16384))[1] == 27
+
+
 def test_core_exports_reference_api(ag):
     for name in ("Tensor", "DType", "Device", "from_numpy", "to_numpy", "add", "sub", "mul", "relu",
                  "gelu", "sum_all", "add_bias", "scale", "matmul", "matmul_a_bt", "matmul_at_b",
