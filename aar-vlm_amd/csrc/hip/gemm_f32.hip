@@ -244,7 +244,7 @@ __device__ __forceinline__ void store_tile_bits(const f32x16 (&acc)[TM][TN], flo
   }
 }
 
-template <int TM, int TN, int EPI, int NQ = 4>
+template <int TM, int TN, int EPI, int NQ = 4, bool BATCH = false>
 __device__ __forceinline__ void store_tile(const f32x16 (&acc)[TM][TN], float* __restrict__ C, const GemmEpi& ep,
                                            const float (&bias)[TN], int64_t M, int64_t N, int64_t ldc, int64_t r0,
                                            int64_t c0, int lr, int h, int q0 = 0) {
@@ -259,43 +259,57 @@ __device__ __forceinline__ void store_tile(const f32x16 (&acc)[TM][TN], float* _
   // 16384 x 1536 x 384 product with the bias epilogue.
   if constexpr (epi_has_bias(EPI)) wait_vm_lgkm0<0>();
   const float* const Xl = kAux ? ep.aux + lane0 : nullptr;
-#pragma unroll
-  for (int i = 0; i < TM; ++i) {
-    // The aux values of this row of blocks are all loaded before any of its
-    // stores: C and aux may alias (an in-place residual), so a load placed
-    // after a store would wait for it, one memory round trip per element.
-    // (Each element is read and then written by the same lane, so an
-    // aliased aux still reads the old values.)
-    float xv[TN][4 * NQ];
-    if constexpr (kAux) {
-#pragma unroll
-      for (int j = 0; j < TN; ++j) {
-        const int64_t col = c0 + 32 * j + lr;
-#pragma unroll
-        for (int r = 0; r < 4 * NQ; ++r) {
-          const int dr = 32 * i + 8 * (q0 + r / 4) + (r % 4);
-          const int64_t off = (int64_t)dr * ldc + 32 * j;
-          xv[j][r] = (interior || (r0 + 4 * h + dr < M && col < N)) ? Xl[off] : 0.0f;
-        }
-      }
-      wait_vm_lgkm0<0>();
-    }
+  // The aux values are loaded before any store they feed: C and aux may
+  // alias (an in-place residual), so a load placed after a store would wait
+  // for it, one memory round trip per element.  (Each element is read and
+  // then written by the same lane, so an aliased aux still reads the old
+  // values.)  BATCH (the DMA kernels, whose staging registers are free by
+  // the epilogue): when the wave tile's aux values fit in 96 registers (the
+  // accumulators' count for a 64 x 96 wave tile), all rows of blocks are
+  // loaded in one batch and waited for once, one memory round trip per wave
+  // instead of one per row of blocks.  Otherwise a row of blocks at a time
+  // (in the register path the batch cost occupancy).
+  constexpr int kRowsPerBatch = BATCH && kAux && TM * TN * 4 * NQ <= 96 ? TM : 1;
+  auto load_aux = [&](int i, float (&xv)[TN][4 * NQ]) {
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
       const int64_t col = c0 + 32 * j + lr;
-      const float b = bias[j];
 #pragma unroll
       for (int r = 0; r < 4 * NQ; ++r) {
-        const int dr = 32 * i + 8 * (q0 + r / 4) + (r % 4);  // row - r0 - 4h
+        const int dr = 32 * i + 8 * (q0 + r / 4) + (r % 4);
         const int64_t off = (int64_t)dr * ldc + 32 * j;
-        if (interior || (r0 + 4 * h + dr < M && col < N)) {
-          float v = acc[i][j][r];
-          if constexpr (EPI == kEpiBias) v = v + b;
-          if constexpr (EPI == kEpiBiasRelu) v = fmaxf(0.0f, v + b);
-          if constexpr (EPI == kEpiMask) v = xv[j][r] > 0.0f ? v : 0.0f;
-          if constexpr (EPI == kEpiAdd) v = v + xv[j][r];
-          if constexpr (EPI == kEpiBiasAdd) v = (v + b) + xv[j][r];
-          Cl[off] = v;
+        xv[j][r] = (interior || (r0 + 4 * h + dr < M && col < N)) ? Xl[off] : 0.0f;
+      }
+    }
+  };
+#pragma unroll
+  for (int i0 = 0; i0 < TM; i0 += kRowsPerBatch) {
+    float xv[kRowsPerBatch][TN][4 * NQ];
+    if constexpr (kAux) {
+#pragma unroll
+      for (int ib = 0; ib < kRowsPerBatch; ++ib) load_aux(i0 + ib, xv[ib]);
+      wait_vm_lgkm0<0>();
+    }
+#pragma unroll
+    for (int ib = 0; ib < kRowsPerBatch; ++ib) {
+      const int i = i0 + ib;
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int64_t col = c0 + 32 * j + lr;
+        const float b = bias[j];
+#pragma unroll
+        for (int r = 0; r < 4 * NQ; ++r) {
+          const int dr = 32 * i + 8 * (q0 + r / 4) + (r % 4);  // row - r0 - 4h
+          const int64_t off = (int64_t)dr * ldc + 32 * j;
+          if (interior || (r0 + 4 * h + dr < M && col < N)) {
+            float v = acc[i][j][r];
+            if constexpr (EPI == kEpiBias) v = v + b;
+            if constexpr (EPI == kEpiBiasRelu) v = fmaxf(0.0f, v + b);
+            if constexpr (EPI == kEpiMask) v = xv[ib][j][r] > 0.0f ? v : 0.0f;
+            if constexpr (EPI == kEpiAdd) v = v + xv[ib][j][r];
+            if constexpr (EPI == kEpiBiasAdd) v = (v + b) + xv[ib][j][r];
+            Cl[off] = v;
+          }
         }
       }
     }
@@ -798,14 +812,14 @@ gemm_f32_dma_kernel(const float* __restrict__ A, const float* __restrict__ B, fl
 #pragma unroll
           for (int e = 0; e < 4; ++e) acc[i][j][4 * qq + e] = v[e];
         }
-    store_tile<TM, TN, EPI, QPG>(acc, C, ep, bias, M, N, ldc, m0 + wm0, n0 + wn0, lr, h, q0);
+    store_tile<TM, TN, EPI, QPG, true>(acc, C, ep, bias, M, N, ldc, m0 + wm0, n0 + wn0, lr, h, q0);
     return;
   }
 
   if constexpr (epi_bits(EPI)) {
     store_tile_bits<TM, TN, EPI>(acc, C, ep, bias, words, M, N, ldc, m0 + wm0, n0 + wn0, lr, h);
   } else {
-    store_tile<TM, TN, EPI>(acc, C, ep, bias, M, N, ldc, m0 + wm0, n0 + wn0, lr, h);
+    store_tile<TM, TN, EPI, 4, true>(acc, C, ep, bias, M, N, ldc, m0 + wm0, n0 + wn0, lr, h);
   }
 }
 
@@ -1142,9 +1156,20 @@ constexpr Cfg kCfgs[] = {
     // planner's model moved 1140 of 17496 plans over a shape grid, mostly
     // small-M split products that were not measured, so 6 keeps its role.)
     {64, 128, 16, 32, 64, 2, 4, 0.80f, 3, kAllOps},
+    // 16: configuration 8's 128x192 tile as 8 waves of 32x96 (one K group,
+    // 80 KB).  Not a candidate of its own: the planner substitutes it for an
+    // unsplit NN or NT plan on 8 whose grid is one workgroup per CU or a bit
+    // less (kEightWaveFor8), where 8 runs one 4-wave workgroup per CU, one
+    // wave per SIMD.  Timed against 8 in one process: 16384 x 384 x 384 NN /
+    // NT 45.3 / 45.7 -> 42.5 / 42.6 us, x 1152 114.9 / 118.2 -> 110.9 /
+    // 113.1, x 1536 150.7 / 155.1 -> 145.7 / 149.1 (bit-identical); TN lost
+    // 1 %, and grids of four tiles per CU lost up to 9 %.  Its 32-row wave
+    // tiles do not take the mask-bit epilogue.
+    {128, 192, 32, 32, 96, 1, 2, 0.87f, 1, kAllOps},
 };
 constexpr int kNumCfgs = sizeof(kCfgs) / sizeof(kCfgs[0]);
 constexpr int kDeepRingFor6 = 15;
+constexpr int kEightWaveFor8 = 16;
 constexpr int kMaxSplits = 64;
 
 struct Plan {
@@ -1228,7 +1253,7 @@ Plan plan_gemm(int op, int64_t M, int64_t N, int64_t K, size_t ws_bytes, bool al
   double best_t = 1e300;
   for (int c = 0; c < kNumCfgs; ++c) {
     const Cfg& cf = kCfgs[c];
-    if (!(cf.ops & (1 << op)) || c == kDeepRingFor6) continue;
+    if (!(cf.ops & (1 << op)) || c == kDeepRingFor6 || c == kEightWaveFor8) continue;
     const int64_t tiles = ceil_div(M, (int64_t)cf.bm) * ceil_div(N, (int64_t)cf.bn) * batch;
     // Configuration 8 as NT or TN: only grids of at most one round of its
     // resident workgroups, or of two or three whole rounds.  Measured at
@@ -1277,6 +1302,10 @@ Plan plan_gemm(int op, int64_t M, int64_t N, int64_t K, size_t ws_bytes, bool al
   if (best.cfg == 6 && best.splits == 1) {
     const int64_t tiles = ceil_div(M, (int64_t)kCfgs[6].bm) * ceil_div(N, (int64_t)kCfgs[6].bn) * batch;
     if (tiles >= 3 * (int64_t)cus) best.cfg = kDeepRingFor6;
+  }
+  if (best.cfg == 8 && best.splits == 1 && op != AAR_GEMM_TN && vec_ok && epi != kEpiMaskBits) {
+    const int64_t tiles = ceil_div(M, (int64_t)kCfgs[8].bm) * ceil_div(N, (int64_t)kCfgs[8].bn) * batch;
+    if (2 * tiles > (int64_t)cus && tiles <= (int64_t)cus) best.cfg = kEightWaveFor8;
   }
   return best;
 }
@@ -1383,12 +1412,13 @@ int launch_op(int cfg, bool vec, const float* A, const float* B, float* C, int64
     AAR_GEMM_CFG(13)
     AAR_GEMM_CFG(14)
     AAR_GEMM_CFG(15)
+    AAR_GEMM_CFG(16)
     default:
       return AAR_EINVAL;
   }
 #undef AAR_GEMM_CFG
 }
-static_assert(kNumCfgs == 16, "launch_op lists every configuration");
+static_assert(kNumCfgs == 17, "launch_op lists every configuration");
 
 // 128-bit loads need 16-byte aligned operands whose contiguous extents and
 // leading dimensions are multiples of 4, and the 32-bit per-thread offsets
@@ -1699,7 +1729,7 @@ extern "C" int aar_gemm_f32_mask_bits_colsum(int op, int64_t M, int64_t N, int64
   int64_t lda, ldb;
   default_ld(op, M, N, K, lda, ldb);
   const bool vec = gemm_vec_ok(op, M, N, K, A, B, lda, ldb);
-  const Plan p = plan_gemm(op, M, N, K, (size_t)-1, true, 1, thin_operands_ok(op, A, B, lda, ldb), kEpiNone, vec);
+  const Plan p = plan_gemm(op, M, N, K, (size_t)-1, true, 1, thin_operands_ok(op, A, B, lda, ldb), kEpiMaskBits, vec);
   if (p.splits > 1 || p.cfg >= kNumCfgs) return AAR_EUNSUPPORTED;
   GemmEpi ep{nullptr, nullptr};
   ep.bits = const_cast<uint32_t*>(bits);
