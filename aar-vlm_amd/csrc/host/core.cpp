@@ -298,7 +298,19 @@ Tensor Tensor::zeros(std::vector<int64_t> shape, DType dtype, Device device) {
 }
 
 Tensor Tensor::ones(std::vector<int64_t> shape, DType dtype, Device device) {
-  // Host fill then upload, as the reference does (tensor.cpp:78-87).
+  // fp32 on the device: a fill kernel on the current stream.  The upload the
+  // other dtypes take (a host fill, as the reference does, tensor.cpp:78-87)
+  // synchronizes the stream; for backward()'s seed gradient that drained the
+  // queue between a training step's forward and backward.
+  if (device == Device::CUDA && dtype == DType::Fp32) {
+    Tensor t = empty(std::move(shape), dtype, device);
+    if (t.storage) {
+      check_status(aar_fill_f32(static_cast<float*>(t.storage->data()), 1.0f, static_cast<int64_t>(t.numel()),
+                                current_stream()),
+                   "ones");
+    }
+    return t;
+  }
   Tensor cpu = empty(shape, dtype, Device::CPU);
   if (cpu.storage) {
     const size_t n = cpu.numel();
