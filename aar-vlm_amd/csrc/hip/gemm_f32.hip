@@ -1303,9 +1303,16 @@ Plan plan_gemm(int op, int64_t M, int64_t N, int64_t K, size_t ws_bytes, bool al
     const int64_t tiles = ceil_div(M, (int64_t)kCfgs[6].bm) * ceil_div(N, (int64_t)kCfgs[6].bn) * batch;
     if (tiles >= 3 * (int64_t)cus) best.cfg = kDeepRingFor6;
   }
-  if (best.cfg == 8 && best.splits == 1 && op != AAR_GEMM_TN && vec_ok && epi != kEpiMaskBits) {
+  if (best.splits == 1 && vec_ok && epi != kEpiMaskBits) {
     const int64_t tiles = ceil_div(M, (int64_t)kCfgs[8].bm) * ceil_div(N, (int64_t)kCfgs[8].bn) * batch;
-    if (2 * tiles > (int64_t)cus && tiles <= (int64_t)cus) best.cfg = kEightWaveFor8;
+    // an NN or NT plan on 8 over at most one tile per CU
+    if (best.cfg == 8 && op != AAR_GEMM_TN && 2 * tiles > (int64_t)cus && tiles <= (int64_t)cus)
+      best.cfg = kEightWaveFor8;
+    // an NT or TN plan on 6 (or 15) whose 128 x 192 grid is three or more
+    // whole rounds (16384 x 1152 x 384 to 32768 x 1152 x 384: -1.2 to -1.8 %
+    // against 15; a partial last round, 4.5 rounds, lost 5 %)
+    if ((best.cfg == 6 || best.cfg == kDeepRingFor6) && op != AAR_GEMM_NN && tiles % cus == 0 && tiles >= 3 * cus)
+      best.cfg = kEightWaveFor8;
   }
   return best;
 }
