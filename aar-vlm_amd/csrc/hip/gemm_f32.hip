@@ -1160,7 +1160,8 @@ constexpr Cfg kCfgs[] = {
     // 80 KB).  Not a candidate of its own: the planner substitutes it for an
     // unsplit NN or NT plan on 8 whose grid is one workgroup per CU or a bit
     // less (kEightWaveFor8), where 8 runs one 4-wave workgroup per CU, one
-    // wave per SIMD.  Timed against 8 in one process: 16384 x 384 x 384 NN /
+    // wave per SIMD, and for an unsplit NT or TN plan on 6 whose 128 x 192
+    // grid is three or more whole rounds (see plan_gemm).  Timed against 8 in one process: 16384 x 384 x 384 NN /
     // NT 45.3 / 45.7 -> 42.5 / 42.6 us, x 1152 114.9 / 118.2 -> 110.9 /
     // 113.1, x 1536 150.7 / 155.1 -> 145.7 / 149.1 (bit-identical); TN lost
     // 1 %, and grids of four tiles per CU lost up to 9 %.  Its 32-row wave
