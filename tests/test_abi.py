@@ -308,3 +308,29 @@ def test_backward_arity_and_shape_errors(ag):
     assert x.grad is None
     with pytest.raises(RuntimeError, match="non-leaf"):
         y.requires_grad = True
+
+
+def test_gemm_plan_substitutions():
+    """The planner's substitutions (planning only, 256 CUs without a device):
+    configuration 16 (the 128 x 192 tile as 8 waves) for NN/NT plans on 8
+    over at most one tile per CU and for NT/TN plans on 6 whose 128 x 192
+    grid is three or more whole rounds; configuration 15 (6 with a deeper
+    ring) for other unsplit plans on 6 of three or more tiles per CU."""
+    lib = ctypes.CDLL(str(LIB))
+    i64, sz, ip = ctypes.c_int64, ctypes.c_size_t, ctypes.POINTER(ctypes.c_int)
+    lib.aar_gemm_f32_plan.argtypes = [ctypes.c_int, i64, i64, i64, sz, ip, ip]
+
+    def cfg(op, M, N, K):
+        c, s = ctypes.c_int(), ctypes.c_int()
+        assert lib.aar_gemm_f32_plan(op, M, N, K, 1 << 30, ctypes.byref(c), ctypes.byref(s)) == 0
+        return c.value
+
+    NN, NT, TN = 0, 1, 2
+    for K in (384, 1152, 1536):  # the GPT step's one-tile-per-CU products
+        assert cfg(NN, 16384, 384, K) == 16 and cfg(NT, 16384, 384, K) == 16
+    assert cfg(TN, 16384, 384, 384) == 8  # TN keeps 8
+    assert cfg(NT, 16384, 1152, 384) == 16 and cfg(TN, 16384, 1152, 384) == 16  # 3 whole rounds
+    assert cfg(NT, 24576, 1152, 384) != 16  # 4.5 rounds: a partial last round
+    assert cfg(NT, 16384, 1536, 384) == 8  # two tiles per CU: 8 itself
+    # unsplit plans on 6 of three or more 64 x 128 tiles per CU whose 128 x 192 grid is not whole rounds
+    assert cfg(NN, 384, 16384, 384) == 15 and cfg(NT, 16384, 640, 384) == 15 and cfg(TN, 16384, 640, 1024) == 15
