@@ -1300,7 +1300,9 @@ Plan plan_gemm(int op, int64_t M, int64_t N, int64_t K, size_t ws_bytes, bool al
       }
     }
   }
-  if (best.cfg == 6 && best.splits == 1) {
+  // (the substitutions were measured on the DMA path; unaligned operands keep
+  // the planned configuration)
+  if (best.cfg == 6 && best.splits == 1 && vec_ok) {
     const int64_t tiles = ceil_div(M, (int64_t)kCfgs[6].bm) * ceil_div(N, (int64_t)kCfgs[6].bn) * batch;
     if (tiles >= 3 * (int64_t)cus) best.cfg = kDeepRingFor6;
   }
