@@ -1870,7 +1870,11 @@ extern "C" int aar_gemm_f32_batched(int op, int64_t batch, int64_t M, int64_t N,
   if (lda < need_a || ldb < need_b) return AAR_EINVAL;
   if (M > INT32_MAX / 2 || N > INT32_MAX / 2) return AAR_EUNSUPPORTED;
   const bool vec = gemm_vec_ok(op, M, N, K, A, B, lda, ldb) && strideA % 4 == 0 && strideB % 4 == 0;
-  const Plan p = plan_gemm(op, M, N, K, 0, false, batch);
+  // the operands' alignment keeps the DMA-path substitutions off unaligned
+  // batches; a short-kernel plan (one unaligned matrix) is not run here, so
+  // that case plans the tile kernels
+  Plan p = plan_gemm(op, M, N, K, 0, false, batch, false, kEpiNone, vec);
+  if (p.cfg >= kNumCfgs) p = plan_gemm(op, M, N, K, 0, false, batch);
   // Batches ride blockIdx.z (at most 65535 per launch): larger counts go in
   // consecutive launches (offsets keep the 16-byte alignment, strides % 4 == 0).
   constexpr int64_t kMaxGridZ = 65535;
