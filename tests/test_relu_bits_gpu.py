@@ -67,6 +67,7 @@ def _sentinel_words(abi, rows, cols):
 SHAPES = [
     (16384, 1536, 384, 384),  # GPT block (must be fused)
     (4096, 1536, 384, 384),
+    (4004, 1536, 384, 384),   # forward on the 32-row wave tiles of configuration 16, a 4-row last word
     (2048, 960, 384, 128),
     (1000, 200, 64, 96),      # M not a multiple of 32: a partial last word (forward only)
     (1024, 200, 64, 96),      # N not a multiple of the tile width
