@@ -702,6 +702,12 @@ gemm_f32_dma_kernel(const float* __restrict__ A, const float* __restrict__ B, fl
 #pragma unroll
   for (int p = 0; p < S - 1; ++p)
     if (p < ntiles) issue(p);
+  // kEpiColsumA (one K group, kbeg a multiple of 64): the residue mod tiles_n
+  // of the 64-row chunk of the current K tile, stepped at each chunk end
+  // rather than divided out in every trip (a 64-bit modulo by a runtime value
+  // in the loop cost the 1536 x 384 x 16384 product several microseconds)
+  int cs_res = 0;
+  if constexpr (EPI == kEpiColsumA) cs_res = (int)((kbeg >> 6) % tiles_n);
 
   for (int t = 0; t < ntg; ++t) {
     // Tile t has landed once at most the DMAs of the tiles issued after it
@@ -721,7 +727,7 @@ gemm_f32_dma_kernel(const float* __restrict__ A, const float* __restrict__ B, fl
     // kEpiColsumA: whether this wave sums the A columns of this K tile (a
     // wave-uniform branch)
     const int64_t k0 = kbeg + (int64_t)t * BK;
-    const bool cs_on = EPI == kEpiColsumA && wave < NWM && (k0 >> 6) % tiles_n == tn;
+    const bool cs_on = EPI == kEpiColsumA && wave < NWM && cs_res == tn;
     // With K groups four waves share a SIMD; the one issuing matrix ops
     // keeps priority over those issuing loads (measured +2.5 % at 1024^3).
     // One-group kernels lose slightly with it, except the 128x128x64 tile on
@@ -762,14 +768,17 @@ gemm_f32_dma_kernel(const float* __restrict__ A, const float* __restrict__ B, fl
     }
     if constexpr (kPrio) __builtin_amdgcn_s_setprio(0);
     if constexpr (EPI == kEpiColsumA) {
-      if (cs_on && ((k0 + BK) & 63) == 0) {  // the chunk's last K tile
+      if (((k0 + BK) & 63) == 0) {  // the chunk's last K tile
+        if (cs_on) {
 #pragma unroll
-        for (int i = 0; i < TM; ++i) {
-          const float tot = csum[i] + __uint_as_float(partner_u32(__float_as_uint(csum[i])));
-          const int64_t m = m0 + wm0 + 32 * i + lr;
-          if (h == 0 && m < M) ep.part[(k0 >> 6) * M + m] = tot;
-          csum[i] = 0.f;
+          for (int i = 0; i < TM; ++i) {
+            const float tot = csum[i] + __uint_as_float(partner_u32(__float_as_uint(csum[i])));
+            const int64_t m = m0 + wm0 + 32 * i + lr;
+            if (h == 0 && m < M) ep.part[(k0 >> 6) * M + m] = tot;
+            csum[i] = 0.f;
+          }
         }
+        cs_res = cs_res + 1 == tiles_n ? 0 : cs_res + 1;
       }
     }
   }
