@@ -1170,11 +1170,12 @@ constexpr Cfg kCfgs[] = {
     // unsplit NN or NT plan on 8 whose grid is one workgroup per CU or a bit
     // less (kEightWaveFor8), where 8 runs one 4-wave workgroup per CU, one
     // wave per SIMD, and for an unsplit NT or TN plan on 6 whose 128 x 192
-    // grid is three or more whole rounds (see plan_gemm).  Timed against 8 in one process: 16384 x 384 x 384 NN /
-    // NT 45.3 / 45.7 -> 42.5 / 42.6 us, x 1152 114.9 / 118.2 -> 110.9 /
-    // 113.1, x 1536 150.7 / 155.1 -> 145.7 / 149.1 (bit-identical); TN lost
-    // 1 %, and grids of four tiles per CU lost up to 9 %.  Its 32-row wave
-    // tiles do not take the mask-bit epilogue.
+    // grid is three or more whole rounds (see plan_gemm).  Timed against 8
+    // in one process: 16384 x 384 x 384 NN / NT 45.3 / 45.7 -> 42.5 / 42.6
+    // us, x 1152 114.9 / 118.2 -> 110.9 / 113.1, x 1536 150.7 / 155.1 ->
+    // 145.7 / 149.1 (bit-identical); TN lost 1 %, and grids of four tiles per
+    // CU lost up to 9 %.  Its 32-row wave tiles do not take the mask-bit
+    // epilogue.
     {128, 192, 32, 32, 96, 1, 2, 0.87f, 1, kAllOps},
 };
 constexpr int kNumCfgs = sizeof(kCfgs) / sizeof(kCfgs[0]);
