@@ -201,11 +201,13 @@ def test_abi_layernorm_bwd_acc(gpu, rows, cols, offset):
         abi.free()
 
 
-@pytest.mark.parametrize("M,N,K,offset", [(256, 384, 384, 0), (50, 65, 17, 1), (64, 96, 4096, 0), (33, 7, 4999, 0)])
+@pytest.mark.parametrize("M,N,K,offset", [(256, 384, 384, 0), (50, 65, 17, 1), (64, 96, 4096, 0), (33, 7, 4999, 0),
+                                          (16100, 384, 384, 0), (16100, 384, 1536, 0)])
 def test_abi_gemm_add_epilogues(gpu, M, N, K, offset):
     """aar_gemm_f32_add / aar_gemm_f32_bias_add against aar_gemm_f32 /
     aar_gemm_f32_bias followed by aar_add_f32, bit for bit; other layouts are
-    unsupported and a missing R is invalid."""
+    unsupported and a missing R is invalid.  16100 rows: the 8-wave 128 x 192
+    tile with a ragged last row tile and the residual loaded in one batch."""
     rng = np.random.default_rng(M + N + K)
     a = rng.standard_normal((M, K)).astype(f32)
     w = rng.standard_normal((N, K)).astype(f32)
