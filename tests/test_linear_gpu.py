@@ -30,6 +30,8 @@ CASES = [
     ((64,), 8192, 100),        # split-K, N % 4 == 0 with 100 columns
     ((33,), 4999, 30),         # split-K, register path, scalar reduce
     ((3, 50), 17, 65),         # unaligned K and N, register path
+    ((372,), 384, 16384),      # configuration 15 (64 x 128, deep ring), ragged last row tile
+    ((480,), 384, 20000),      # configuration 15, ragged last column tile
 ]
 
 
