@@ -628,6 +628,22 @@ class GPT:
         return loss
 
 
+def gpt_steps(ag, n: int = 5, cfg=GPT5):
+    """n config-5 steps, each synchronised and logged, with no event timing:
+    the mode counter passes (rocprofv3 --pmc) run, one line per step."""
+    B, T = cfg["batch"], cfg["ctx"]
+    model = GPT(ag, cfg, gpt_init_params(cfg))
+    ids_np, tgt_np = gpt_tokens(cfg, B)
+    ids = ag.from_numpy(ids_np).to(ag.Device.CUDA)
+    tgt = ag.from_numpy(tgt_np.reshape(-1)).to(ag.Device.CUDA)
+    pos = ag.from_numpy(np.tile(np.arange(T, dtype=np.int64), (B, 1))).to(ag.Device.CUDA)
+    for i in range(n):
+        t0 = time.time()
+        model.step(ids, pos, tgt, 1e-3)
+        ag.cuda_synchronize()
+        log(f"gpt step {i}: {(time.time() - t0) * 1e3:.1f} ms (synchronised)")
+
+
 def gpt_flops_per_step(cfg, batch):
     d, L, T, V, H = cfg["d_model"], cfg["layers"], cfg["ctx"], cfg["vocab"], cfg["heads"]
     linear_weights = L * (3 * d * d + d * d + 2 * 4 * d * d) + V * d
@@ -831,7 +847,8 @@ def main() -> int:
     ap.add_argument("--flash-t", type=int, default=4096, choices=[256, 1024, 4096],
                     help="sequence length of the --only flash run (BASELINE config 4 has 1024 and 4096 at "
                          "B8 H12; 256 is config 5's attention, B64 H6)")
-    ap.add_argument("--only", choices=["all", "gemm", "flash", "rowwise", "extra", "copy", "gpt", "sweep"], default="all",
+    ap.add_argument("--only", choices=["all", "gemm", "flash", "rowwise", "extra", "copy", "gpt", "gpt-steps", "sweep"],
+                    default="all",
                     help="run one part (profiling runs); the JSON line is printed for 'all'")
     # The reference bench's command line (bench/bench_matmul.cu:101-136): with
     # --shape or --shapes, run its GEMM table protocol only, print the table
@@ -891,6 +908,9 @@ def main() -> int:
         return 0
     if args.only == "sweep":
         log(json.dumps(bench_gemm_sweep(ev)))
+        return 0
+    if args.only == "gpt-steps":
+        gpt_steps(ag)
         return 0
     if args.only == "gpt":
         log(json.dumps(bench_gpt(ag, ev)))
