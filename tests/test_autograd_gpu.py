@@ -23,6 +23,14 @@ def test_device_round_trip_and_zeros(gpu):
     np.testing.assert_array_equal(host(gpu, z), np.zeros((3, 5), f32))
     o = gpu.Tensor.ones([7], gpu.DType.Fp32, gpu.Device.CUDA)
     np.testing.assert_array_equal(host(gpu, o), np.ones(7, f32))
+    # fp32 ones on the device are a fill kernel (several workgroups here, none
+    # for an empty shape); other dtypes are uploaded
+    o = gpu.Tensor.ones([3, 1000, 7], gpu.DType.Fp32, gpu.Device.CUDA)
+    np.testing.assert_array_equal(host(gpu, o), np.ones((3, 1000, 7), f32))
+    o = gpu.Tensor.ones([0, 4], gpu.DType.Fp32, gpu.Device.CUDA)
+    assert host(gpu, o).shape == (0, 4)
+    o = gpu.Tensor.ones([5], gpu.DType.Int64, gpu.Device.CUDA)
+    np.testing.assert_array_equal(gpu.to_numpy(o.to(gpu.Device.CPU)), np.ones(5, np.int64))
     gpu.cuda_synchronize()
 
 
