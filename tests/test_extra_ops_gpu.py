@@ -169,6 +169,27 @@ def _bmm_oracle(op, a, b):
 
 
 @pytest.mark.parametrize("op", O.BMM_OPS)
+def test_bmm_one_tile_per_cu_grid(gpu, op):
+    """2 x 8192 x 384 x 384: a batched grid of one 128 x 192 tile per CU (256
+    tiles, as the single 16384 x 384 x 384 product), which the planner runs on
+    the 8-wave 128 x 192 tile for bmm and bmm_a_bt.  Forward only, against a
+    float64 numpy product (the oracle's loops take seconds per product at
+    this size)."""
+    rng = np.random.default_rng(8192)
+    a, b = _bmm_case(op, (2,), 8192, 384, 384, rng)
+    c = getattr(gpu, op)(dev(gpu, a), dev(gpu, b))
+    a64, b64 = a.astype(np.float64), b.astype(np.float64)
+    if op == "bmm":
+        want = a64 @ b64
+    elif op == "bmm_a_bt":
+        want = a64 @ b64.transpose(0, 2, 1)
+    else:
+        want = a64.transpose(0, 2, 1) @ b64
+    assert tuple(c.shape) == want.shape
+    assert_close(host(gpu, c), want, gemm_tol(384), op)
+
+
+@pytest.mark.parametrize("op", O.BMM_OPS)
 @pytest.mark.parametrize("lead,M,N,K", [((2, 3), 4, 6, 5), ((6,), 1, 1, 1), ((12,), 256, 256, 64),
                                         ((4,), 300, 77, 129), ((2, 2), 64, 520, 33), ((3,), 5, 7, 0),
                                         ((0,), 4, 4, 4)])
